@@ -1,0 +1,141 @@
+"""ctypes binding of libdecik_nf4.so (include/decik_nf4.h) and the tensor -> descriptor glue.
+
+The library is built in-tree by `python -m decik_amd.build` (or __graft_entry__.build()). There
+is no fallback: every entry point raises if the library is missing or returns an error.
+"""
+
+import ctypes
+import os
+import threading
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libdecik_nf4.so")
+MAX_GROUPS = 4
+
+_lib = None
+_lock = threading.Lock()
+
+c_i64, c_i32, c_vp, c_f32 = ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p, ctypes.c_float
+
+
+class NF4Weight(ctypes.Structure):
+    _fields_ = [("packed", c_vp), ("absmax", c_vp), ("absmax2", c_vp), ("code2", c_vp),
+                ("offset", c_vp), ("code", c_vp), ("n", c_i64), ("k", c_i64),
+                ("blocksize", c_i32), ("blocksize2", c_i32), ("nested", c_i32),
+                ("reserved", c_i32)]
+
+
+class LinearFwdGroup(ctypes.Structure):
+    _fields_ = [("w", NF4Weight), ("bias", c_vp), ("lora_u", c_vp), ("lora_b", c_vp),
+                ("lora_scale", c_f32), ("reserved", c_i32), ("y", c_vp), ("ldy", c_i64)]
+
+
+class LinearBwdGroup(ctypes.Structure):
+    _fields_ = [("w", NF4Weight), ("dy", c_vp), ("lddy", c_i64), ("lora_gu", c_vp),
+                ("lora_a", c_vp)]
+
+
+EXPORTS = {
+    "dk_nf4_dequant": ([ctypes.POINTER(NF4Weight), c_vp, c_vp], c_i32),
+    "dk_nf4_dequant_batched": ([ctypes.POINTER(NF4Weight), ctypes.POINTER(c_vp), c_i32, c_vp], c_i32),
+    "dk_nf4_linear_fwd_workspace": ([c_i64, c_i64, ctypes.POINTER(c_i64), c_i32], c_i64),
+    "dk_nf4_linear_fwd": ([c_vp, c_i64, c_i64, c_i64, ctypes.POINTER(LinearFwdGroup), c_i32, c_i32,
+                           c_vp, c_i64, c_vp], c_i32),
+    "dk_nf4_linear_bwd_workspace": ([c_i64, c_i64, ctypes.POINTER(c_i64), c_i32], c_i64),
+    "dk_nf4_linear_bwd": ([ctypes.POINTER(LinearBwdGroup), c_i32, c_i64, c_i64, c_vp, c_i64, c_i32,
+                           c_i32, c_vp, c_i64, c_vp], c_i32),
+    "dk_lora_down": ([c_vp, c_i64, c_i64, c_i64, c_vp, c_i32, c_vp, c_vp], c_i32),
+    "dk_lora_bwd": ([c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_i32, c_f32, c_vp,
+                     c_vp, c_vp, c_vp], c_i32),
+    "dk_swiglu_fwd": ([c_vp, c_vp, c_vp, c_i64, c_vp], c_i32),
+    "dk_swiglu_bwd": ([c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp], c_i32),
+    "dk_last_error": ([], ctypes.c_char_p),
+    "dk_version": ([], c_i32),
+}
+
+
+class DecikError(RuntimeError):
+    pass
+
+
+def lib():
+    """The loaded library (raises DecikError if it was not built)."""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not os.path.exists(LIB_PATH):
+                    raise DecikError(f"{LIB_PATH} is missing: build it with `python -m decik_amd.build`")
+                L = ctypes.CDLL(LIB_PATH)
+                for name, (args, res) in EXPORTS.items():
+                    fn = getattr(L, name)
+                    fn.argtypes = args
+                    fn.restype = res
+                _lib = L
+    return _lib
+
+
+def check(rc):
+    if rc != 0:
+        raise DecikError(lib().dk_last_error().decode())
+
+
+def stream_of(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def weight_desc(packed, qs, device):
+    """NF4Weight of a packed uint8 tensor and its QuantState (fields of solution/nf4.py:70-79)."""
+    n, k = (int(s) for s in qs.shape)
+    code = qs.code if qs.code.device == device else qs.code.to(device)
+    w = NF4Weight()
+    w.packed = packed.data_ptr()
+    w.code = code.data_ptr()
+    w.n, w.k = n, k
+    w.blocksize = int(qs.blocksize)
+    w.nested = 1 if qs.nested else 0
+    keep = [packed, code]
+    if qs.nested:
+        w.absmax = qs.absmax.data_ptr()
+        w.absmax2 = qs.state2.absmax.data_ptr()
+        w.code2 = qs.state2.code.data_ptr()
+        offset = qs.offset
+        if not torch.is_tensor(offset):
+            offset = torch.tensor(float(offset), dtype=torch.float32, device=device)
+        w.offset = offset.data_ptr()
+        w.blocksize2 = int(qs.state2.blocksize)
+        keep += [qs.absmax, qs.state2.absmax, qs.state2.code, offset]
+    else:
+        w.absmax = qs.absmax.data_ptr()
+        w.blocksize2 = 256
+        keep.append(qs.absmax)
+    return w, keep
+
+
+class Workspace:
+    """Zero-filled split-K workspaces, one per (device, stream); the kernels leave them zeroed."""
+
+    def __init__(self):
+        self._bufs = {}
+        self._lock = threading.Lock()
+
+    def get(self, nbytes, device):
+        if nbytes <= 0:
+            return None, 0
+        key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+        with self._lock:
+            buf = self._bufs.get(key)
+            if buf is None or buf.numel() < nbytes:
+                size = max(nbytes, 0 if buf is None else 2 * buf.numel())
+                buf = torch.zeros(size, dtype=torch.uint8, device=device)
+                self._bufs[key] = buf
+        return buf, buf.numel()
+
+
+WORKSPACE = Workspace()

@@ -1,0 +1,413 @@
+// C ABI (include/decik_nf4.h): argument checks, launch planning and launches.
+#include <mutex>
+#include <string>
+
+#include "dk_internal.h"
+
+namespace dk {
+namespace {
+
+thread_local std::string g_error;
+
+int fail(const std::string& msg) {
+    g_error = msg;
+    return 1;
+}
+
+int check_hip(hipError_t e, const char* what) {
+    if (e == hipSuccess) return 0;
+    return fail(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+int log2_exact(int64_t v) {
+    if (v <= 0 || (v & (v - 1)) != 0) return -1;
+    int s = 0;
+    while ((int64_t(1) << s) < v) ++s;
+    return s;
+}
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+int to_dev(const dk_nf4_weight* w, NF4Dev* d, const char* who) {
+    if (w == nullptr) return fail(std::string(who) + ": null weight descriptor");
+    if (w->packed == nullptr || w->absmax == nullptr || w->code == nullptr)
+        return fail(std::string(who) + ": packed, absmax and code must be set");
+    if (w->n < 0 || w->k < 0 || ((w->n * w->k) & 1))
+        return fail(std::string(who) + ": n*k must be even and non-negative");
+    if (w->blocksize < 2 || (w->blocksize & 1))
+        return fail(std::string(who) + ": blocksize must be even and >= 2");
+    if (w->nested) {
+        if (w->absmax2 == nullptr || w->code2 == nullptr || w->offset == nullptr || w->blocksize2 < 1)
+            return fail(std::string(who) + ": nested weights need absmax2, code2, offset, blocksize2");
+    }
+    d->packed = w->packed;
+    d->absmax8 = w->nested ? static_cast<const uint8_t*>(w->absmax) : nullptr;
+    d->absmaxf = w->nested ? nullptr : static_cast<const float*>(w->absmax);
+    d->absmax2 = w->absmax2;
+    d->code2 = w->code2;
+    d->offset = w->offset;
+    d->code = w->code;
+    d->n = w->n;
+    d->k = w->k;
+    d->blocksize = w->blocksize;
+    d->blocksize2 = w->nested ? w->blocksize2 : 256;
+    d->bs_shift = log2_exact(w->blocksize);
+    d->bs2_shift = log2_exact(d->blocksize2);
+    return 0;
+}
+
+int num_cus() {
+    static int cus = 0;
+    static std::mutex mu;
+    std::lock_guard<std::mutex> lock(mu);
+    if (cus == 0) {
+        int dev = 0;
+        hipDeviceProp_t prop;
+        if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess)
+            cus = prop.multiProcessorCount;
+        if (cus <= 0) cus = 256;
+    }
+    return cus;
+}
+
+int pad8(int g) { return (g + 7) & ~7; }
+
+// ---- planning -----------------------------------------------------------------------------
+
+int choose_mt(int64_t m) {
+    // rows per tile = 16 * mt. Cost = tiles * (rows + 64): padded rows plus a per-tile share of
+    // the weight unpacking, which every m-tile repeats.
+    static const int cand[] = {1, 2, 4, 8, 13};
+    int best = 1;
+    int64_t best_cost = INT64_MAX;
+    for (int mt : cand) {
+        const int64_t rows = 16 * mt;
+        const int64_t tiles = (m + rows - 1) / rows;
+        const int64_t cost = tiles * (rows + 64);
+        if (cost < best_cost) {
+            best_cost = cost;
+            best = mt;
+        }
+    }
+    return best;
+}
+
+// Split the contraction so that tiles * splits work-groups cover the CUs evenly. Model: a
+// work-group step costs 1; the last work-group of a split tile reads the other partial tiles
+// at `fix` step-costs each.
+int choose_splits(int64_t tiles, int steps, double fix) {
+    const int cus = num_cus();
+    int best = 1;
+    double best_cost = 1e300;
+    const int max_s = steps < 64 ? steps : 64;
+    for (int s = 1; s <= max_s; ++s) {
+        const int per = (steps + s - 1) / s;
+        const int used = (steps + per - 1) / per;  // splits that actually get work
+        if (used != s) continue;
+        const double rounds = (double)((tiles * s + cus - 1) / cus);
+        const double cost = rounds * per + (s > 1 ? fix * s : 0.0);
+        if (cost < best_cost - 1e-9) {
+            best_cost = cost;
+            best = s;
+        }
+    }
+    return best;
+}
+
+GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
+    GemmPlan p{};
+    p.mt = choose_mt(m);
+    p.m_tiles = (int)((m + 16 * p.mt - 1) / (16 * p.mt));
+    p.n_tiles = 0;
+    for (int g = 0; g < ngroups; ++g) p.n_tiles += (int)((ns[g] + kFwdBN - 1) / kFwdBN);
+    p.steps = (int)((k + kFwdBK - 1) / kFwdBK);
+    const int64_t tiles = (int64_t)p.m_tiles * p.n_tiles;
+    p.splits = p.steps > 0 ? choose_splits(tiles, p.steps, 1.0) : 1;
+    p.steps_per_split = p.steps > 0 ? (p.steps + p.splits - 1) / p.splits : 0;
+    p.counters = p.splits > 1 ? (int)tiles : 0;
+    p.partial_floats = p.splits > 1 ? tiles * p.splits * (int64_t)(16 * p.mt) * kFwdBN : 0;
+    return p;
+}
+
+GemmPlan plan_bwd(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
+    GemmPlan p{};
+    p.mt = choose_mt(m);
+    p.m_tiles = (int)((m + 16 * p.mt - 1) / (16 * p.mt));
+    p.n_tiles = (int)((k + kBwdBN - 1) / kBwdBN);
+    p.steps = 0;
+    for (int g = 0; g < ngroups; ++g) p.steps += (int)((ns[g] + kBwdBC - 1) / kBwdBC);
+    const int64_t tiles = (int64_t)p.m_tiles * p.n_tiles;
+    p.splits = p.steps > 0 ? choose_splits(tiles, p.steps, 2.0) : 1;
+    p.steps_per_split = p.steps > 0 ? (p.steps + p.splits - 1) / p.splits : 0;
+    p.counters = p.splits > 1 ? (int)tiles : 0;
+    p.partial_floats = p.splits > 1 ? tiles * p.splits * (int64_t)(16 * p.mt) * kBwdBN : 0;
+    return p;
+}
+
+int64_t workspace_bytes(const GemmPlan& p) {
+    if (p.splits <= 1) return 0;
+    const int64_t counter_bytes = ((int64_t)p.counters * 4 + 255) & ~int64_t(255);
+    return counter_bytes + p.partial_floats * 4;
+}
+
+}  // namespace
+}  // namespace dk
+
+using namespace dk;
+
+extern "C" {
+
+const char* dk_last_error(void) { return g_error.c_str(); }
+
+int dk_version(void) { return 100; }
+
+int dk_nf4_dequant_batched(const dk_nf4_weight* ws, uint16_t* const* outs, int count, void* stream) {
+    g_error.clear();
+    if (count < 0 || (count > 0 && (ws == nullptr || outs == nullptr)))
+        return fail("dk_nf4_dequant_batched: bad arguments");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    for (int base = 0; base < count; base += kMaxDequantBatch) {
+        DequantArgs a{};
+        int wg = 0;
+        a.count = 0;
+        for (int i = 0; i < kMaxDequantBatch && base + i < count; ++i) {
+            const dk_nf4_weight* w = &ws[base + i];
+            if (to_dev(w, &a.w[i], "dk_nf4_dequant")) return 1;
+            if (outs[base + i] == nullptr && w->n * w->k > 0) return fail("dk_nf4_dequant: null output");
+            a.out[i] = outs[base + i];
+            a.nbytes[i] = w->n * w->k / 2;
+            a.wg_begin[i] = wg;
+            const int64_t chunks = (a.nbytes[i] + 15) / 16;
+            const int64_t g = (chunks + kDequantThreads - 1) / kDequantThreads;
+            if (wg + g > INT32_MAX / 2) return fail("dk_nf4_dequant: tensor too large");
+            wg += (int)g;
+            a.fast[i] = (w->blocksize % 32 == 0) && aligned(w->packed, 16) && aligned(outs[base + i], 16);
+            a.count = i + 1;
+        }
+        a.wg_begin[a.count] = wg;
+        for (int i = a.count; i < kMaxDequantBatch; ++i) a.wg_begin[i] = wg;
+        if (wg == 0) continue;
+        hipLaunchKernelGGL(nf4_dequant_kernel, dim3(wg), dim3(kDequantThreads), 0, s, a);
+        if (check_hip(hipGetLastError(), "dk_nf4_dequant launch")) return 1;
+    }
+    return 0;
+}
+
+int dk_nf4_dequant(const dk_nf4_weight* w, uint16_t* out, void* stream) {
+    return dk_nf4_dequant_batched(w, &out, 1, stream);
+}
+
+int64_t dk_nf4_linear_fwd_workspace(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
+    if (ngroups < 1 || ngroups > kMaxGroups || ns == nullptr || m <= 0 || k <= 0) return 0;
+    return workspace_bytes(plan_fwd(m, k, ns, ngroups));
+}
+
+int64_t dk_nf4_linear_bwd_workspace(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
+    if (ngroups < 1 || ngroups > kMaxGroups || ns == nullptr || m <= 0 || k <= 0) return 0;
+    return workspace_bytes(plan_bwd(m, k, ns, ngroups));
+}
+
+int dk_nf4_linear_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
+                      const dk_linear_fwd_group* groups, int ngroups, int lora_rank, void* workspace,
+                      int64_t workspace_bytes_, void* stream) {
+    g_error.clear();
+    if (ngroups < 1 || ngroups > kMaxGroups || groups == nullptr)
+        return fail("dk_nf4_linear_fwd: need 1..4 groups");
+    if (m < 0 || k <= 0 || (k % 32) != 0)
+        return fail("dk_nf4_linear_fwd: k must be a positive multiple of 32");
+    if (m > INT32_MAX / 2 || k > INT32_MAX / 2) return fail("dk_nf4_linear_fwd: m or k too large");
+    if (x == nullptr || !aligned(x, 16) || ldx < k || (ldx % 8) != 0)
+        return fail("dk_nf4_linear_fwd: x must be 16-byte aligned with ldx >= k, ldx % 8 == 0");
+    if (lora_rank != 0 && lora_rank != 16 && lora_rank != 32)
+        return fail("dk_nf4_linear_fwd: lora_rank must be 0, 16 or 32");
+    FwdArgs a{};
+    int64_t ns[kMaxGroups];
+    int nested = -1;
+    int tile = 0;
+    for (int g = 0; g < ngroups; ++g) {
+        const dk_linear_fwd_group& G = groups[g];
+        if (to_dev(&G.w, &a.g[g].w, "dk_nf4_linear_fwd")) return 1;
+        if (G.w.k != k) return fail("dk_nf4_linear_fwd: weight k differs from x");
+        if (G.w.blocksize % 32 != 0) return fail("dk_nf4_linear_fwd: blocksize must be a multiple of 32");
+        if (!aligned(G.w.packed, 16)) return fail("dk_nf4_linear_fwd: packed weights must be 16-byte aligned");
+        if (nested >= 0 && nested != G.w.nested)
+            return fail("dk_nf4_linear_fwd: all groups must be nested or all plain");
+        nested = G.w.nested;
+        if (G.y == nullptr || !aligned(G.y, 16) || G.ldy < G.w.n || (G.ldy % 8) != 0)
+            return fail("dk_nf4_linear_fwd: y must be 16-byte aligned with ldy >= n, ldy % 8 == 0");
+        if (G.lora_u != nullptr && (lora_rank == 0 || G.lora_b == nullptr))
+            return fail("dk_nf4_linear_fwd: LoRA needs lora_rank > 0 and lora_b");
+        if (G.lora_u != nullptr && (!aligned(G.lora_u, 8) || !aligned(G.lora_b, 8)))
+            return fail("dk_nf4_linear_fwd: LoRA operands must be 8-byte aligned");
+        a.g[g].bias = reinterpret_cast<const _Float16*>(G.bias);
+        a.g[g].lora_u = reinterpret_cast<const _Float16*>(G.lora_u);
+        a.g[g].lora_b = reinterpret_cast<const _Float16*>(G.lora_b);
+        a.g[g].lora_scale = G.lora_scale;
+        a.g[g].y = reinterpret_cast<_Float16*>(G.y);
+        a.g[g].ldy = G.ldy;
+        a.g[g].tile_begin = tile;
+        tile += (int)((G.w.n + kFwdBN - 1) / kFwdBN);
+        ns[g] = G.w.n;
+    }
+    if (m == 0 || tile == 0) return 0;
+    const GemmPlan p = plan_fwd(m, k, ns, ngroups);
+    const int64_t need = workspace_bytes(p);
+    if (need > 0 && (workspace == nullptr || workspace_bytes_ < need || !aligned(workspace, 256)))
+        return fail("dk_nf4_linear_fwd: workspace too small (need " + std::to_string(need) + " bytes)");
+    a.x = reinterpret_cast<const _Float16*>(x);
+    a.ldx = ldx;
+    a.m = (int)m;
+    a.k = (int)k;
+    a.ngroups = ngroups;
+    a.lora_rank = lora_rank;
+    a.m_tiles = p.m_tiles;
+    a.n_tiles = p.n_tiles;
+    a.splits = p.splits;
+    a.ksteps = p.steps;
+    a.ksteps_per_split = p.steps_per_split;
+    a.nested = nested;
+    if (need > 0) {
+        const int64_t counter_bytes = ((int64_t)p.counters * 4 + 255) & ~int64_t(255);
+        a.counters = static_cast<int32_t*>(workspace);
+        a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + counter_bytes);
+    }
+    const int64_t wgs = (int64_t)p.m_tiles * p.n_tiles * p.splits;
+    if (wgs > INT32_MAX / 2) return fail("dk_nf4_linear_fwd: problem too large");
+    return check_hip(launch_fwd(a, p.mt, pad8((int)wgs), static_cast<hipStream_t>(stream)),
+                     "dk_nf4_linear_fwd launch");
+}
+
+int dk_nf4_linear_bwd(const dk_linear_bwd_group* groups, int ngroups, int64_t m, int64_t k, void* dx,
+                      int64_t lddx, int dx_fp32, int lora_rank, void* workspace,
+                      int64_t workspace_bytes_, void* stream) {
+    g_error.clear();
+    if (ngroups < 1 || ngroups > kMaxGroups || groups == nullptr)
+        return fail("dk_nf4_linear_bwd: need 1..4 groups");
+    if (m < 0 || k <= 0 || (k % 32) != 0)
+        return fail("dk_nf4_linear_bwd: k must be a positive multiple of 32");
+    if (m > INT32_MAX / 2 || k > INT32_MAX / 2) return fail("dk_nf4_linear_bwd: m or k too large");
+    if (dx == nullptr || !aligned(dx, 16) || lddx < k || (lddx % 8) != 0)
+        return fail("dk_nf4_linear_bwd: dx must be 16-byte aligned with lddx >= k, lddx % 8 == 0");
+    if (lora_rank != 0 && lora_rank != 16 && lora_rank != 32)
+        return fail("dk_nf4_linear_bwd: lora_rank must be 0, 16 or 32");
+    BwdArgs a{};
+    int64_t ns[kMaxGroups];
+    int nested = -1;
+    int step = 0;
+    for (int g = 0; g < ngroups; ++g) {
+        const dk_linear_bwd_group& G = groups[g];
+        if (to_dev(&G.w, &a.g[g].w, "dk_nf4_linear_bwd")) return 1;
+        if (G.w.k != k) return fail("dk_nf4_linear_bwd: weight k differs from dx");
+        if (G.w.blocksize % 32 != 0) return fail("dk_nf4_linear_bwd: blocksize must be a multiple of 32");
+        if (!aligned(G.w.packed, 16)) return fail("dk_nf4_linear_bwd: packed weights must be 16-byte aligned");
+        if ((G.w.n % 8) != 0) return fail("dk_nf4_linear_bwd: weight rows must be a multiple of 8");
+        if (nested >= 0 && nested != G.w.nested)
+            return fail("dk_nf4_linear_bwd: all groups must be nested or all plain");
+        nested = G.w.nested;
+        if (G.dy == nullptr || !aligned(G.dy, 16) || G.lddy < G.w.n || (G.lddy % 8) != 0)
+            return fail("dk_nf4_linear_bwd: dy must be 16-byte aligned with lddy >= n, lddy % 8 == 0");
+        if (G.lora_gu != nullptr && (lora_rank == 0 || G.lora_a == nullptr || !aligned(G.lora_gu, 8)))
+            return fail("dk_nf4_linear_bwd: LoRA needs lora_rank > 0, lora_a and 8-byte aligned gu");
+        a.g[g].dy = reinterpret_cast<const _Float16*>(G.dy);
+        a.g[g].lddy = G.lddy;
+        a.g[g].lora_gu = reinterpret_cast<const _Float16*>(G.lora_gu);
+        a.g[g].lora_a = reinterpret_cast<const _Float16*>(G.lora_a);
+        a.g[g].step_begin = step;
+        a.g[g].nsteps = (int)((G.w.n + kBwdBC - 1) / kBwdBC);
+        step += a.g[g].nsteps;
+        ns[g] = G.w.n;
+    }
+    if (m == 0) return 0;
+    const GemmPlan p = plan_bwd(m, k, ns, ngroups);
+    const int64_t need = workspace_bytes(p);
+    if (need > 0 && (workspace == nullptr || workspace_bytes_ < need || !aligned(workspace, 256)))
+        return fail("dk_nf4_linear_bwd: workspace too small (need " + std::to_string(need) + " bytes)");
+    a.dx = dx;
+    a.lddx = lddx;
+    a.m = (int)m;
+    a.k = (int)k;
+    a.ngroups = ngroups;
+    a.lora_rank = lora_rank;
+    a.m_tiles = p.m_tiles;
+    a.k_tiles = p.n_tiles;
+    a.splits = p.splits;
+    a.csteps = p.steps;
+    a.csteps_per_split = p.steps_per_split;
+    a.dx_fp32 = dx_fp32 ? 1 : 0;
+    a.nested = nested;
+    if (need > 0) {
+        const int64_t counter_bytes = ((int64_t)p.counters * 4 + 255) & ~int64_t(255);
+        a.counters = static_cast<int32_t*>(workspace);
+        a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + counter_bytes);
+    }
+    const int64_t wgs = (int64_t)p.m_tiles * p.n_tiles * p.splits;
+    if (wgs > INT32_MAX / 2) return fail("dk_nf4_linear_bwd: problem too large");
+    return check_hip(launch_bwd(a, p.mt, pad8((int)wgs), static_cast<hipStream_t>(stream)),
+                     "dk_nf4_linear_bwd launch");
+}
+
+int dk_lora_down(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const uint16_t* a, int rank,
+                 uint16_t* u, void* stream) {
+    g_error.clear();
+    if (rank != 16 && rank != 32) return fail("dk_lora_down: rank must be 16 or 32");
+    if (m < 0 || k <= 0 || (k % 8) != 0 || ldx < k || (ldx % 8) != 0)
+        return fail("dk_lora_down: k and ldx must be multiples of 8");
+    if (x == nullptr || a == nullptr || u == nullptr || !aligned(x, 16) || !aligned(a, 16))
+        return fail("dk_lora_down: x and a must be 16-byte aligned");
+    return check_hip(launch_lora_down(reinterpret_cast<const _Float16*>(x), m, k, ldx,
+                                      reinterpret_cast<const _Float16*>(a), rank,
+                                      reinterpret_cast<_Float16*>(u), static_cast<hipStream_t>(stream)),
+                     "dk_lora_down launch");
+}
+
+int dk_lora_bwd(const uint16_t* dy, int64_t lddy, const uint16_t* u, const uint16_t* x, int64_t ldx,
+                const uint16_t* b, int64_t m, int64_t n, int64_t k, int rank, float scale, uint16_t* gu,
+                float* da, float* db, void* stream) {
+    g_error.clear();
+    if (rank != 16 && rank != 32) return fail("dk_lora_bwd: rank must be 16 or 32");
+    if (m < 0 || n <= 0 || k <= 0 || lddy < n || ldx < k)
+        return fail("dk_lora_bwd: bad shapes");
+    if (dy == nullptr || u == nullptr || x == nullptr || b == nullptr || gu == nullptr)
+        return fail("dk_lora_bwd: null pointer");
+    if (!aligned(u, 16) || !aligned(b, 16) || !aligned(gu, 16))
+        return fail("dk_lora_bwd: u, b, gu must be 16-byte aligned");
+    return check_hip(launch_lora_bwd(reinterpret_cast<const _Float16*>(dy), lddy,
+                                     reinterpret_cast<const _Float16*>(u),
+                                     reinterpret_cast<const _Float16*>(x), ldx,
+                                     reinterpret_cast<const _Float16*>(b), m, n, k, rank, scale,
+                                     reinterpret_cast<_Float16*>(gu), da, db,
+                                     static_cast<hipStream_t>(stream)),
+                     "dk_lora_bwd launch");
+}
+
+int dk_swiglu_fwd(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n, void* stream) {
+    g_error.clear();
+    if (n < 0 || (n > 0 && (gate == nullptr || up == nullptr || out == nullptr)))
+        return fail("dk_swiglu_fwd: bad arguments");
+    if (!aligned(gate, 16) || !aligned(up, 16) || !aligned(out, 16))
+        return fail("dk_swiglu_fwd: pointers must be 16-byte aligned");
+    return check_hip(launch_swiglu_fwd(reinterpret_cast<const _Float16*>(gate),
+                                       reinterpret_cast<const _Float16*>(up),
+                                       reinterpret_cast<_Float16*>(out), n,
+                                       static_cast<hipStream_t>(stream)),
+                     "dk_swiglu_fwd launch");
+}
+
+int dk_swiglu_bwd(const uint16_t* grad, const uint16_t* gate, const uint16_t* up, uint16_t* dgate,
+                  uint16_t* dup, int64_t n, void* stream) {
+    g_error.clear();
+    if (n < 0 || (n > 0 && (grad == nullptr || gate == nullptr || up == nullptr || dgate == nullptr ||
+                            dup == nullptr)))
+        return fail("dk_swiglu_bwd: bad arguments");
+    if (!aligned(grad, 16) || !aligned(gate, 16) || !aligned(up, 16) || !aligned(dgate, 16) ||
+        !aligned(dup, 16))
+        return fail("dk_swiglu_bwd: pointers must be 16-byte aligned");
+    return check_hip(launch_swiglu_bwd(reinterpret_cast<const _Float16*>(grad),
+                                       reinterpret_cast<const _Float16*>(gate),
+                                       reinterpret_cast<const _Float16*>(up),
+                                       reinterpret_cast<_Float16*>(dgate), reinterpret_cast<_Float16*>(dup),
+                                       n, static_cast<hipStream_t>(stream)),
+                     "dk_swiglu_bwd launch");
+}
+
+}  // extern "C"

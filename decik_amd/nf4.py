@@ -1,0 +1,241 @@
+"""NF4 weights of bitsandbytes' Linear4bit on MI355X: dequantization and the fused linear.
+
+Same module API as the reference (solution/nf4.py): `supported`, `dequantize_nf4`, `NF4Linear`,
+`patch`, `BYTES_PER_PROGRAM`, `NUM_WARPS`. What changes is underneath:
+
+- `dequantize_nf4` runs the HIP kernel `nf4_dequant_kernel` (bit-identical fp16 weights:
+  code[nibble] * scale in fp32, double-quant scale code2[q] * absmax2 + offset with two
+  roundings, round to nearest even), as skc_nf4_dequant_kernel did (solution/nf4.py:27-48).
+- `NF4Linear` no longer materialises the fp16 weight: forward is one fused dequant x fp16 GEMM
+  launch (Y = X.W^T + b), backward one fused launch for dX = dY.W. The reference dequantized
+  the whole weight and called cuBLAS in both directions (solution/nf4.py:93-104).
+- Shapes the fused kernels do not take (k not a multiple of 32, blocksize not a multiple of 32,
+  weight rows not a multiple of 8, unaligned tensors) take the reference's own algorithm on the
+  GPU: this module's dequantization, then F.linear / matmul.
+No path runs on the CPU: the HIP library must be built (`python -m decik_amd.build`).
+"""
+
+import ctypes
+
+import torch
+
+from . import _lib, warmup
+from ._lib import LinearBwdGroup, LinearFwdGroup, check, lib, ptr, stream_of, weight_desc
+from ._state import on_gpu
+
+# Work shape of the dequantization kernel: packed bytes per work-group (256 threads x 16 bytes)
+# and waves (wavefronts of 64) per work-group.
+BYTES_PER_PROGRAM = 4096
+NUM_WARPS = 4
+
+
+def supported(quant_state, n_in=None):
+    """The reference's gate (solution/nf4.py:51-63): nf4, fp16, 2-D, even size, even blocksize,
+    code present; nested needs state2, offset and uint8 absmax; optional input width check."""
+    qs = quant_state
+    try:
+        ok = (qs is not None and qs.quant_type == "nf4" and qs.dtype == torch.float16
+              and len(qs.shape) == 2 and (qs.shape[0] * qs.shape[1]) % 2 == 0
+              and qs.blocksize % 2 == 0 and qs.code is not None)
+        if ok and qs.nested:
+            ok = qs.state2 is not None and qs.offset is not None and qs.absmax.dtype == torch.uint8
+        if ok and n_in is not None:
+            ok = qs.shape[1] == n_in
+        return bool(ok)
+    except AttributeError:
+        return False
+
+
+def dequantize_nf4(packed, quant_state):
+    """[N, K] fp16 weights of a bitsandbytes nf4 tensor (packed uint8 + QuantState)."""
+    warmup.wait()
+    qs = quant_state
+    n_out, n_in = (int(s) for s in qs.shape)
+    out = torch.empty((n_out, n_in), dtype=torch.float16, device=packed.device)
+    w, keep = weight_desc(packed, qs, packed.device)
+    check(lib().dk_nf4_dequant(ctypes.byref(w), ptr(out), stream_of(packed.device)))
+    del keep
+    return out
+
+
+def dequantize_nf4_many(pairs):
+    """Dequantize several (packed, quant_state) weights in as few launches as possible."""
+    if not pairs:
+        return []
+    dev = pairs[0][0].device
+    outs, descs, keep = [], [], []
+    for packed, qs in pairs:
+        n_out, n_in = (int(s) for s in qs.shape)
+        outs.append(torch.empty((n_out, n_in), dtype=torch.float16, device=dev))
+        w, k = weight_desc(packed, qs, dev)
+        descs.append(w)
+        keep += k
+    arr = (_lib.NF4Weight * len(descs))(*descs)
+    out_ptrs = (ctypes.c_void_p * len(outs))(*[o.data_ptr() for o in outs])
+    check(lib().dk_nf4_dequant_batched(arr, out_ptrs, len(descs), stream_of(dev)))
+    return outs
+
+
+def _aligned(t, n=16):
+    return t is None or t.data_ptr() % n == 0
+
+
+def fused_ok(quant_state, k=None):
+    """Whether the fused GEMM kernels take this weight (else: dequantize + F.linear)."""
+    qs = quant_state
+    n, kk = (int(s) for s in qs.shape)
+    return (kk % 32 == 0 and int(qs.blocksize) % 32 == 0 and n % 8 == 0
+            and (k is None or k == kk))
+
+
+def _rows(x):
+    return x.reshape(-1, x.shape[-1])
+
+
+def linear_forward(x16, items, lora_rank=0):
+    """Fused forward for weights that share x16 [M, K] (fp16, contiguous rows).
+
+    items: list of dicts with keys packed, qs, and optional bias (fp16 [N]), lora_u
+    (fp16 [M, r]), lora_b (fp16 [N, r]), lora_scale, out (fp16 [M, N] to write into).
+    Returns the list of outputs [M, N_i]."""
+    assert 1 <= len(items) <= _lib.MAX_GROUPS
+    dev = x16.device
+    x2 = _rows(x16)
+    m, k = x2.shape
+    groups = (LinearFwdGroup * len(items))()
+    keep, outs, ns = [x2], [], []
+    for g, it in enumerate(items):
+        qs = it["qs"]
+        n = int(qs.shape[0])
+        out = it.get("out")
+        if out is None:
+            out = torch.empty((m, n), dtype=torch.float16, device=dev)
+        w, kp = weight_desc(it["packed"], qs, dev)
+        keep += kp
+        groups[g].w = w
+        bias = it.get("bias")
+        groups[g].bias = None if bias is None else bias.data_ptr()
+        u = it.get("lora_u")
+        groups[g].lora_u = None if u is None else u.data_ptr()
+        b = it.get("lora_b")
+        groups[g].lora_b = None if b is None else b.data_ptr()
+        groups[g].lora_scale = float(it.get("lora_scale", 0.0))
+        groups[g].y = out.data_ptr()
+        groups[g].ldy = out.stride(0)
+        keep += [bias, u, b, out]
+        outs.append(out)
+        ns.append(n)
+    ns_arr = (ctypes.c_int64 * len(ns))(*ns)
+    need = lib().dk_nf4_linear_fwd_workspace(m, k, ns_arr, len(ns))
+    ws, ws_bytes = _lib.WORKSPACE.get(need, dev)
+    check(lib().dk_nf4_linear_fwd(ptr(x2), m, k, x2.stride(0), groups, len(items), int(lora_rank),
+                                  ptr(ws), ws_bytes, stream_of(dev)))
+    return outs
+
+
+def linear_backward(items, m, k, dx=None, dx_fp32=False, lora_rank=0):
+    """Fused input gradient dX [m, k] = sum_i dY_i . W_i (+ GU_i . A_i), one fp32 accumulation.
+
+    items: list of dicts with keys packed, qs, dy (fp16 [m, N_i]) and optional lora_gu
+    (fp16 [m, r]), lora_a (fp16 [r, k])."""
+    assert 1 <= len(items) <= _lib.MAX_GROUPS
+    dev = items[0]["dy"].device
+    if dx is None:
+        dx = torch.empty((m, k), dtype=torch.float32 if dx_fp32 else torch.float16, device=dev)
+    groups = (LinearBwdGroup * len(items))()
+    keep, ns = [dx], []
+    for g, it in enumerate(items):
+        qs = it["qs"]
+        w, kp = weight_desc(it["packed"], qs, dev)
+        keep += kp
+        dy = _rows(it["dy"])
+        groups[g].w = w
+        groups[g].dy = dy.data_ptr()
+        groups[g].lddy = dy.stride(0)
+        gu, a = it.get("lora_gu"), it.get("lora_a")
+        groups[g].lora_gu = None if gu is None else gu.data_ptr()
+        groups[g].lora_a = None if a is None else a.data_ptr()
+        keep += [dy, gu, a]
+        ns.append(int(qs.shape[0]))
+    ns_arr = (ctypes.c_int64 * len(ns))(*ns)
+    need = lib().dk_nf4_linear_bwd_workspace(m, k, ns_arr, len(ns))
+    ws, ws_bytes = _lib.WORKSPACE.get(need, dev)
+    check(lib().dk_nf4_linear_bwd(groups, len(items), m, k, ptr(dx), dx.stride(0),
+                                  1 if dx.dtype == torch.float32 else 0, int(lora_rank), ptr(ws),
+                                  ws_bytes, stream_of(dev)))
+    return dx
+
+
+def _fusable(x16, packed, qs, bias16):
+    k = x16.shape[-1]
+    return (fused_ok(qs, k) and x16.is_contiguous() and _aligned(x16) and _aligned(packed)
+            and (bias16 is None or bias16.is_contiguous()))
+
+
+class NF4Linear(torch.autograd.Function):
+    """F.linear(x, dequant(W), bias) with fp16 x; the input gradient is dY . dequant(W), as
+    bitsandbytes' MatMul4Bit (the weight itself is frozen). Both directions are one fused launch."""
+
+    @staticmethod
+    def forward(ctx, x16, packed, bias16, quant_state):
+        ctx.packed, ctx.quant_state = packed, quant_state
+        ctx.x_shape = x16.shape
+        warmup.wait()
+        if _fusable(x16, packed, quant_state, bias16) and x16.numel() > 0:
+            (y,) = linear_forward(x16.contiguous(), [dict(packed=packed, qs=quant_state,
+                                                          bias=bias16)])
+            return y.reshape(*x16.shape[:-1], y.shape[-1])
+        weight = dequantize_nf4(packed, quant_state)
+        return torch.nn.functional.linear(x16, weight, bias16)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        grad_x = None
+        if ctx.needs_input_grad[0]:
+            g16 = grad_out.to(torch.float16).contiguous()
+            qs = ctx.quant_state
+            k = ctx.x_shape[-1]
+            if fused_ok(qs, k) and _aligned(g16) and g16.numel() > 0:
+                m = g16.numel() // g16.shape[-1]
+                grad_x = linear_backward([dict(packed=ctx.packed, qs=qs, dy=g16)], m, k)
+                grad_x = grad_x.reshape(ctx.x_shape)
+            else:
+                weight = dequantize_nf4(ctx.packed, qs)
+                grad_x = torch.matmul(g16, weight)
+        return grad_x, None, None, None
+
+
+def patch():
+    """Send bitsandbytes' Linear4bit.forward through NF4Linear (solution/nf4.py:107-138): same
+    gate, same fallback to the original for anything else."""
+    import bitsandbytes as bnb
+
+    cls = bnb.nn.Linear4bit
+    if getattr(cls.forward, "_skc", False):
+        return
+    original = cls.forward
+    try:
+        from bitsandbytes.nn.modules import fix_4bit_weight_quant_state_from_module as fix_state
+    except ImportError:  # pragma: no cover - older bitsandbytes
+        fix_state = None
+
+    def forward(self, x):
+        weight = getattr(self, "weight", None)
+        if fix_state is not None and weight is not None and getattr(weight, "quant_state", None) is None:
+            fix_state(self)
+        qs = getattr(weight, "quant_state", None)
+        bias = self.bias
+        if not (isinstance(x, torch.Tensor) and on_gpu(x) and x.numel() > 0
+                and weight is not None and on_gpu(weight) and weight.dtype == torch.uint8
+                and not weight.requires_grad
+                and getattr(self, "compute_dtype", None) == torch.float16
+                and (bias is None or not bias.requires_grad)
+                and supported(qs, x.shape[-1])):
+            return original(self, x)
+        inp_dtype = x.dtype
+        bias16 = None if bias is None else bias.to(torch.float16)
+        out = NF4Linear.apply(x.to(torch.float16), weight.data, bias16, qs)
+        return out.to(inp_dtype)
+
+    forward._skc = True
+    cls.forward = forward

@@ -1,0 +1,143 @@
+/*
+ * decik_nf4 — C ABI of the MI355X (gfx950) NF4 quantized-linear path.
+ *
+ * Every pointer is a device pointer (memory owned by the caller, e.g. PyTorch), except the
+ * descriptor arrays themselves, which live in host memory and are copied into the kernel
+ * arguments. fp16 tensors are passed as uint16_t (IEEE binary16 bit patterns). `stream` is a
+ * hipStream_t (NULL = the default stream). Every entry point returns 0 on success and a
+ * non-zero code on error; dk_last_error() then describes the error (per calling thread).
+ * The library never allocates device memory: split-K workspaces are passed in.
+ *
+ * Reference interfaces replaced (tokha-t/decik, Python + Triton):
+ *   dk_nf4_dequant / dk_nf4_dequant_batched  <- skc_nf4_dequant_kernel + dequantize_nf4
+ *                                               (solution/nf4.py:27-48, 66-85)
+ *   dk_nf4_linear_fwd                         <- NF4Linear.forward = dequantize_nf4 + F.linear
+ *                                               (solution/nf4.py:93-96; solution/mlp.py:28-39),
+ *                                               with peft's LoRA term added in the epilogue
+ *                                               (solution/attn.py:225-228, 344-346)
+ *   dk_nf4_linear_bwd                         <- NF4Linear.backward = dequantize_nf4 + matmul
+ *                                               (solution/nf4.py:99-104); the summed input
+ *                                               gradients of RecomputedMLP (solution/mlp.py:106-109)
+ *                                               and of the LoRA branch (solution/attn.py:257)
+ *   dk_lora_down / dk_lora_bwd                <- the rank-r products of LoRAPairFromNorm
+ *                                               (solution/attn.py:225-227, 251-257)
+ *   dk_swiglu_fwd / dk_swiglu_bwd             <- example_swiglu_fwd/bwd_kernel
+ *                                               (solution/swiglu.py:15-37)
+ */
+#ifndef DECIK_NF4_H
+#define DECIK_NF4_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DK_MAX_GROUPS 4
+
+/* A bitsandbytes nf4 weight: Params4bit bytes + QuantState fields read by the reference
+ * (solution/nf4.py:54-58, 70-79). Weight shape [n, k] row-major; flat element index
+ * i = row * k + col; block = i / blocksize; group = block / blocksize2. */
+typedef struct dk_nf4_weight {
+    const uint8_t* packed;  /* [n*k/2] bytes, element 2j in the high nibble of byte j   */
+    const void* absmax;     /* nested: uint8 codes [n_blocks]; plain: fp32 [n_blocks]   */
+    const float* absmax2;   /* nested: fp32 [ceil(n_blocks / blocksize2)]; else NULL   */
+    const float* code2;     /* nested: fp32 [256] (state2.code); else NULL              */
+    const float* offset;    /* nested: fp32 scalar (QuantState.offset); else NULL       */
+    const float* code;      /* fp32 [16] NF4 code book (QuantState.code)                */
+    int64_t n, k;           /* weight shape                                             */
+    int32_t blocksize;      /* QuantState.blocksize (even, >= 2)                        */
+    int32_t blocksize2;     /* state2.blocksize (nested only)                           */
+    int32_t nested;         /* QuantState.nested                                        */
+    int32_t reserved;
+} dk_nf4_weight;
+
+/* One weight of a forward launch. Y[r, c] = sum_j X[r, j] W[c, j] + bias[c]
+ *                                        + lora_scale * sum_t U[r, t] B[c, t]
+ * (U = X.A^T from dk_lora_down, fp16 [m, rank]; B fp16 [n, rank]). */
+typedef struct dk_linear_fwd_group {
+    dk_nf4_weight w;
+    const uint16_t* bias;    /* fp16 [n] or NULL                          */
+    const uint16_t* lora_u;  /* fp16 [m, rank] or NULL (no LoRA term)      */
+    const uint16_t* lora_b;  /* fp16 [n, rank]                            */
+    float lora_scale;
+    int32_t reserved;
+    uint16_t* y;             /* fp16 output, row stride ldy (elements)    */
+    int64_t ldy;
+} dk_linear_fwd_group;
+
+/* One weight of a backward launch. Its contribution to dX[r, j] is
+ *   sum_c dY[r, c] W[c, j] + sum_t GU[r, t] A[t, j]
+ * (GU = lora_scale * dY.B from dk_lora_bwd, fp16 [m, rank]; A fp16 [rank, k]). */
+typedef struct dk_linear_bwd_group {
+    dk_nf4_weight w;
+    const uint16_t* dy;      /* fp16 [m, n], row stride lddy              */
+    int64_t lddy;
+    const uint16_t* lora_gu; /* fp16 [m, rank] or NULL                    */
+    const uint16_t* lora_a;  /* fp16 [rank, k]                            */
+} dk_linear_bwd_group;
+
+/* Standalone dequantization: out = fp16 [n, k], bit-identical to the reference kernel
+ * (code[nibble] * scale in fp32, nested scale = code2[q] * absmax2 + offset with two
+ * roundings, round to nearest even). */
+int dk_nf4_dequant(const dk_nf4_weight* w, uint16_t* out, void* stream);
+
+/* The same for `count` weights in one launch (out[i] receives weight i). */
+int dk_nf4_dequant_batched(const dk_nf4_weight* ws, uint16_t* const* outs, int count,
+                           void* stream);
+
+/* Bytes of workspace dk_nf4_linear_fwd needs for these shapes (0 if none). A workspace must
+ * be zero-filled once when allocated; the library leaves it zeroed after every call. Calls
+ * that run concurrently (different streams) need different workspaces. */
+int64_t dk_nf4_linear_fwd_workspace(int64_t m, int64_t k, const int64_t* ns, int ngroups);
+
+/* Fused dequant x fp16 GEMM, forward, for up to DK_MAX_GROUPS weights that share X
+ * (fp16 [m, k], row stride ldx). fp32 accumulation, one fp16 rounding per output. */
+int dk_nf4_linear_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
+                      const dk_linear_fwd_group* groups, int ngroups, int lora_rank,
+                      void* workspace, int64_t workspace_bytes, void* stream);
+
+int64_t dk_nf4_linear_bwd_workspace(int64_t m, int64_t k, const int64_t* ns, int ngroups);
+
+/* Fused dequant x fp16 GEMM, input gradient: dX = sum over groups of dY_g.W_g (+ GU_g.A_g),
+ * accumulated in fp32 across all groups and rounded once. dx is fp16 (dx_fp32 = 0) or fp32
+ * (dx_fp32 = 1), row stride lddx. */
+int dk_nf4_linear_bwd(const dk_linear_bwd_group* groups, int ngroups, int64_t m, int64_t k,
+                      void* dx, int64_t lddx, int dx_fp32, int lora_rank, void* workspace,
+                      int64_t workspace_bytes, void* stream);
+
+/* U = fp16(X . A^T): X fp16 [m, k] (row stride ldx), A fp16 [rank, k], U fp16 [m, rank]. */
+int dk_lora_down(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const uint16_t* a,
+                 int rank, uint16_t* u, void* stream);
+
+/* LoRA weight and input-branch gradients for out = scale * (U . B^T), U = X . A^T:
+ *   GU = fp16(scale * dY . B)  [m, rank]
+ *   dB = scale * dY^T . U      fp32 [n, rank]
+ *   dA = GU^T . X              fp32 [rank, k]
+ * dY fp16 [m, n] (row stride lddy), U fp16 [m, rank], X fp16 [m, k] (row stride ldx),
+ * B fp16 [n, rank]. The input gradient GU . A is added by dk_nf4_linear_bwd. */
+int dk_lora_bwd(const uint16_t* dy, int64_t lddy, const uint16_t* u, const uint16_t* x,
+                int64_t ldx, const uint16_t* b, int64_t m, int64_t n, int64_t k, int rank,
+                float scale, uint16_t* gu, float* da, float* db, void* stream);
+
+/* out = fp16(silu(gate) * up), computed in fp32 (n elements). */
+int dk_swiglu_fwd(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n,
+                  void* stream);
+
+/* dgate = fp16(G up s (1 + gate (1 - s))), dup = fp16(G gate s), s = sigmoid(gate).
+ * dgate/dup may alias gate/up (every element is read before it is written). */
+int dk_swiglu_bwd(const uint16_t* grad, const uint16_t* gate, const uint16_t* up,
+                  uint16_t* dgate, uint16_t* dup, int64_t n, void* stream);
+
+/* Description of the last error on the calling thread ("" if none). */
+const char* dk_last_error(void);
+
+/* Library version (major * 10000 + minor * 100 + patch). */
+int dk_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DECIK_NF4_H */

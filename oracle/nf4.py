@@ -1,0 +1,298 @@
+"""CPU oracle: NF4 dequantization, the bitsandbytes NF4 quantizer, and fp32 references.
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py): imported by tests/, smoke() and bench.py's
+cpu_baseline leg; never by the product path.
+
+What each function restates, and what pins it (the tests live in tests/test_oracle.py):
+
+- `dequant_nf4` -> C `oracle_nf4_dequant`, restating skc_nf4_dequant_kernel
+  (solution/nf4.py:27-48) and its launch wrapper (solution/nf4.py:66-85). Pinned by:
+  the fp32->fp16 conversion against numpy's independent conversion over every fp32 exponent
+  and a spread of mantissas; closed forms (nibble 7 -> +0, nibbles 0/15 -> -/+scale exactly,
+  plain absmax 1 -> fp16(code)); brute force over all 256 byte values checked against exact
+  rational arithmetic with explicit two-step rounding; inputs where an FMA would change the
+  scale; blocks and double-quant groups that straddle rows; high nibble first.
+- `quantize_nf4` -> bitsandbytes 0.50.2 `functional.quantize_4bit(..., quant_type="nf4",
+  compress_statistics=True)`, `quantize_blockwise` and `create_dynamic_map(signed=True)`
+  (third party; pinned in the reference at README.md:210-211, called at solution/nf4.py:108-115
+  and solution/test_solution.py:18). bitsandbytes is neither vendored nor installed, so the
+  quantizer is PARITY UNPINNED against it; tests check its invariants instead (nearest code,
+  reconstruction bound, layout). Dequant parity does not depend on it: the packed bytes and
+  statistics are inputs.
+- `linear_ref`, `lora_*_ref`, `swiglu_*_ref`, `mlp_ref`: float64 accumulation of the exact fp16
+  operands, rounded where the reference rounds (solution/nf4.py:93-104, solution/mlp.py:62-110,
+  solution/swiglu.py:15-37, solution/attn.py:206-273). Pinned by closed forms in the tests
+  (identity and permutation weights, rank-one inputs, sigmoid identities).
+"""
+
+import ctypes
+import os
+import subprocess
+from dataclasses import dataclass
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "_build", "liboracle_nf4.so")
+_lib = None
+
+# bitsandbytes' NF4 code book (functional.get_4bit_type("nf4")), the NormalFloat4 values of the
+# QLoRA paper (arXiv:2305.14314, appendix E), stored as fp32.
+NF4_CODE = np.array([
+    -1.0, -0.6961928009986877, -0.5250730514526367, -0.39491748809814453,
+    -0.28444138169288635, -0.18477343022823334, -0.09105003625154495, 0.0,
+    0.07958029955625534, 0.16093020141124725, 0.24611230194568634, 0.33791524171829224,
+    0.44070982933044434, 0.5626170039176941, 0.7229568362236023, 1.0], dtype=np.float32)
+
+
+def build():
+    """Compile the C oracle (oracle/Makefile) into oracle/_build/."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        i64, i32, vp, f32 = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_float
+        L.oracle_nf4_dequant.argtypes = [vp, vp, vp, vp, vp, f32, vp, vp, i64, i32, i64, i64, i32]
+        L.oracle_nf4_dequant.restype = None
+        L.oracle_f32_to_f16_array.argtypes = [vp, vp, i64]
+        L.oracle_f16_to_f32_array.argtypes = [vp, vp, i64]
+        L.oracle_num_threads.restype = i32
+        _lib = L
+    return _lib
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def f32_to_f16_bits(x):
+    """The oracle's own fp32 -> fp16 RNE conversion (uint16 bit patterns)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().oracle_f32_to_f16_array(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def f16_bits_to_f32(h):
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, dtype=np.float32)
+    lib().oracle_f16_to_f32_array(_ptr(h), _ptr(out), h.size)
+    return out
+
+
+@dataclass
+class QuantNF4:
+    """The tensors of a bitsandbytes nf4 Params4bit + QuantState (solution/nf4.py:54-58,70-79)."""
+    packed: np.ndarray          # uint8 [N*K/2], two weights per byte, high nibble first
+    absmax: np.ndarray          # nested: uint8 codes [n_blocks]; plain: fp32 [n_blocks]
+    absmax2: np.ndarray         # nested: fp32 [ceil(n_blocks / blocksize2)]; plain: empty
+    code2: np.ndarray           # nested: fp32 [256] (signed dynamic map); plain: empty
+    offset: np.float32          # nested: fp32 mean of the block absmax; plain: 0
+    code: np.ndarray            # fp32 [16] NF4 code book
+    shape: tuple                # (N, K)
+    blocksize: int = 64
+    blocksize2: int = 256
+    nested: bool = True
+
+
+def dequant_nf4(q: QuantNF4, nthreads=1):
+    """fp16 [N, K] weights, bit-exact restatement of solution/nf4.py:27-48,66-85."""
+    n_out, n_in = q.shape
+    n_bytes = n_out * n_in // 2
+    out = np.empty(2 * n_bytes, dtype=np.uint16)
+    packed = np.ascontiguousarray(q.packed, dtype=np.uint8)
+    code = np.ascontiguousarray(q.code, dtype=np.float32)
+    if q.nested:
+        a8 = np.ascontiguousarray(q.absmax, dtype=np.uint8)
+        a2 = np.ascontiguousarray(q.absmax2, dtype=np.float32)
+        c2 = np.ascontiguousarray(q.code2, dtype=np.float32)
+        lib().oracle_nf4_dequant(_ptr(packed), _ptr(a8), None, _ptr(a2), _ptr(c2),
+                                 float(q.offset), _ptr(code), _ptr(out), n_bytes, 1,
+                                 q.blocksize, q.blocksize2, nthreads)
+    else:
+        af = np.ascontiguousarray(q.absmax, dtype=np.float32)
+        lib().oracle_nf4_dequant(_ptr(packed), None, _ptr(af), None, None, 0.0, _ptr(code),
+                                 _ptr(out), n_bytes, 0, q.blocksize, 256, nthreads)
+    return out.view(np.float16).reshape(n_out, n_in)
+
+
+def linspace_f32(start, end, steps):
+    """torch.linspace for float32 as its CPU kernel computes it (which bitsandbytes calls):
+    step = (end - start) / (steps - 1) in fp32; the first half counts up from start, the second
+    half down from end."""
+    start, end = np.float32(start), np.float32(end)
+    step = np.float32((end - start) / np.float32(steps - 1))
+    out = np.empty(steps, np.float32)
+    half = steps // 2
+    for i in range(steps):
+        out[i] = start + step * np.float32(i) if i < half else end - step * np.float32(steps - i - 1)
+    return out
+
+
+def dynamic_map_signed(max_exponent_bits=7, total_bits=8):
+    """bitsandbytes functional.create_dynamic_map(signed=True): 256 sorted fp32 values.
+
+    For exponent i (0..6) the 2**i midpoints of linspace(0.1, 1, 2**i + 1) scaled by 10**(i-6),
+    with both signs, plus 0 and 1.0."""
+    data = []
+    non_sign_bits = total_bits - 1
+    for i in range(max_exponent_bits):
+        fraction_items = 2 ** (i + non_sign_bits - max_exponent_bits) + 1
+        boundaries = linspace_f32(0.1, 1, fraction_items)
+        means = ((boundaries[:-1] + boundaries[1:]) / np.float32(2.0)).astype(np.float32)
+        scale = np.float32(10 ** (-(max_exponent_bits - 1) + i))
+        data += (scale * means).astype(np.float32).tolist()
+        data += (-scale * means).astype(np.float32).tolist()
+    data.append(0.0)
+    data.append(1.0)
+    assert len(data) == 2 ** total_bits
+    data.sort()
+    return np.array(data, dtype=np.float32)
+
+
+def _blockwise_absmax(a, blocksize):
+    n = a.size
+    n_blocks = -(-n // blocksize)
+    padded = np.zeros(n_blocks * blocksize, dtype=np.float32)
+    padded[:n] = a
+    blocks = padded.reshape(n_blocks, blocksize)
+    absmax = np.abs(blocks).max(axis=1).astype(np.float32)
+    inv = np.zeros_like(absmax)
+    nz = absmax > 0
+    inv[nz] = np.float32(1.0) / absmax[nz]
+    normed = (blocks * inv[:, None]).astype(np.float32)
+    return absmax, normed
+
+
+def quantize_nf4(w16, blocksize=64, nested=True, blocksize2=256):
+    """Restatement of bitsandbytes quantize_4bit(quant_type="nf4") (PARITY UNPINNED vs bnb).
+
+    Block absmax over `blocksize` flat elements, x * (1/absmax), NF4 index = number of
+    midpoints between adjacent code values that x exceeds (the CUDA decision tree), two indices
+    per byte with the even element in the high nibble. Double quant: offset = mean(absmax),
+    absmax - offset quantized blockwise (blocksize2) to the nearest signed dynamic-map code."""
+    w = np.asarray(w16)
+    assert w.ndim == 2 and w.size % 2 == 0
+    a = w.astype(np.float32).reshape(-1)
+    absmax, normed = _blockwise_absmax(a, blocksize)
+    thresholds = ((NF4_CODE[:-1].astype(np.float64) + NF4_CODE[1:].astype(np.float64)) / 2.0)
+    thresholds = thresholds.astype(np.float32)
+    idx = np.searchsorted(thresholds, normed.reshape(-1), side="left").astype(np.uint8)[:a.size]
+    packed = ((idx[0::2] << 4) | idx[1::2]).astype(np.uint8)
+    if not nested:
+        return QuantNF4(packed, absmax, np.zeros(0, np.float32), np.zeros(0, np.float32),
+                        np.float32(0), NF4_CODE.copy(), tuple(w.shape), blocksize, blocksize2,
+                        False)
+    offset = np.float32(absmax.astype(np.float64).mean())
+    centred = (absmax - offset).astype(np.float32)
+    code2 = dynamic_map_signed()
+    absmax2, normed2 = _blockwise_absmax(centred, blocksize2)
+    flat2 = normed2.reshape(-1)[:centred.size]
+    # nearest code value; code2 is sorted, so compare the two neighbours of the insertion point
+    hi = np.clip(np.searchsorted(code2, flat2, side="left"), 1, 255)
+    lo = hi - 1
+    pick_hi = np.abs(code2[hi] - flat2) < np.abs(flat2 - code2[lo])
+    q8 = np.where(pick_hi, hi, lo).astype(np.uint8)
+    return QuantNF4(packed, q8, absmax2, code2, offset, NF4_CODE.copy(), tuple(w.shape),
+                    blocksize, blocksize2, True)
+
+
+def block_scales(q: QuantNF4):
+    """The fp32 per-block scales dequant uses (solution/nf4.py:37-43), for the checks."""
+    if not q.nested:
+        return np.asarray(q.absmax, dtype=np.float32)
+    blocks = np.arange(q.absmax.size)
+    s = (q.code2[q.absmax.astype(np.int64)] * q.absmax2[blocks // q.blocksize2]).astype(np.float32)
+    return (s + np.float32(q.offset)).astype(np.float32)
+
+
+# ----------------------------------------------------------------------------------------------
+# fp32-accumulated references (float64 sums of exact fp16 operands)
+
+def _f64(a):
+    return np.asarray(a).astype(np.float64)
+
+
+def linear_ref(x16, w16, bias16=None):
+    """Y = X . W^T (+ b) accumulated exactly, as fp32 (solution/nf4.py:94-96)."""
+    y = _f64(x16) @ _f64(w16).T
+    if bias16 is not None:
+        y = y + _f64(bias16)[None, :]
+    return y.astype(np.float32)
+
+
+def linear_dx_ref(dy16, w16):
+    """dX = dY . W accumulated exactly, as fp32 (solution/nf4.py:101-103)."""
+    return (_f64(dy16) @ _f64(w16)).astype(np.float32)
+
+
+def lora_fwd_ref(x16, a16, b16, scaling):
+    """peft's lora_B(lora_A(x)) * scaling under fp16 autocast (solution/attn.py:225-228,344-346):
+    u = fp16(x . A^T) [M, r]; out = fp16(u . B^T) * scaling. Returns (u16, out as fp32)."""
+    u16 = (_f64(x16) @ _f64(a16).T).astype(np.float32).astype(np.float16)
+    out = (_f64(u16) @ _f64(b16).T) * float(scaling)
+    return u16, out.astype(np.float32)
+
+
+def lora_bwd_ref(dy16, x16, u16, a16, b16, scaling):
+    """The products autograd forms for out = (u . B^T) * s, u = x . A^T (solution/attn.py:251-257):
+    g = dY*s; dB = g^T u; gu = g . B; dA = gu^T x; dX_lora = gu . A. fp32 results; gu rounded
+    to fp16 as the reference's fp16 matmul leaves it."""
+    g = _f64(dy16) * float(scaling)
+    db = g.T @ _f64(u16)
+    gu16 = (g @ _f64(b16)).astype(np.float32).astype(np.float16)
+    da = _f64(gu16).T @ _f64(x16)
+    dx = _f64(gu16) @ _f64(a16)
+    return gu16, da.astype(np.float32), db.astype(np.float32), dx.astype(np.float32)
+
+
+def _sigmoid64(x):
+    return 1.0 / (1.0 + np.exp(-x))
+
+
+def swiglu_fwd_ref(gate16, up16):
+    """fp16(silu(g) * u) computed in fp32 (solution/swiglu.py:15-23)."""
+    g = _f64(gate16)
+    return (g * _sigmoid64(g) * _f64(up16)).astype(np.float32)
+
+
+def swiglu_bwd_ref(grad16, gate16, up16):
+    """dup = G g s, dgate = G u s (1 + g (1 - s)), s = sigmoid(g) (solution/swiglu.py:25-37)."""
+    G, g, u = _f64(grad16), _f64(gate16), _f64(up16)
+    s = _sigmoid64(g)
+    dup = G * g * s
+    dgate = G * u * s * (1.0 + g * (1.0 - s))
+    return dgate.astype(np.float32), dup.astype(np.float32)
+
+
+def mlp_ref(x16, wg16, wu16, wd16, dy16):
+    """Qwen2 MLP forward and input gradient as RecomputedMLP computes it (solution/mlp.py:62-110):
+    gate, up, h, out rounded to fp16 where the fp16 matmuls round; dX = fp32(dgate.Wg) +
+    fp32(dup.Wu). Returns dict of fp32 arrays (gate, up, h, out, gh, dgate, dup, dx)."""
+    gate = linear_ref(x16, wg16).astype(np.float16)
+    up = linear_ref(x16, wu16).astype(np.float16)
+    h = swiglu_fwd_ref(gate, up).astype(np.float16)
+    out = linear_ref(h, wd16)
+    gh = linear_dx_ref(dy16, wd16).astype(np.float16)
+    dgate, dup = swiglu_bwd_ref(gh, gate, up)
+    dgate16, dup16 = dgate.astype(np.float16), dup.astype(np.float16)
+    dx = (_f64(dgate16) @ _f64(wg16) + _f64(dup16) @ _f64(wu16)).astype(np.float32)
+    return dict(gate=gate.astype(np.float32), up=up.astype(np.float32),
+                h=h.astype(np.float32), out=out, gh=gh.astype(np.float32),
+                dgate=dgate, dup=dup, dx=dx)
+
+
+def tolerance(y, ref):
+    """(max|y-ref| / max|ref|, sum|y-ref| / sum|ref|): the two numbers the parity bar bounds
+    (<= 1e-2 and <= 1e-3); the first is the reference's own `rel` (dev/test_cpu_bnb.py:66)."""
+    y = _f64(y)
+    ref = _f64(ref)
+    err = np.abs(y - ref)
+    denom_max = max(np.abs(ref).max(), 1e-30)
+    denom_sum = max(np.abs(ref).sum(), 1e-30)
+    return float(err.max() / denom_max), float(err.sum() / denom_sum)

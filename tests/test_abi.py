@@ -1,0 +1,85 @@
+"""The C ABI (include/decik_nf4.h) without a GPU: the built library exports every declared
+entry point, the ctypes mirrors have the C layout, and argument errors come back as codes with
+a message (validation runs before any GPU call)."""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "decik_nf4.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(dk_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_path():
+    names = declared()
+    for n in ["dk_nf4_dequant", "dk_nf4_dequant_batched", "dk_nf4_linear_fwd", "dk_nf4_linear_bwd",
+              "dk_nf4_linear_fwd_workspace", "dk_nf4_linear_bwd_workspace", "dk_lora_down",
+              "dk_lora_bwd", "dk_swiglu_fwd", "dk_swiglu_bwd", "dk_last_error", "dk_version"]:
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    from decik_amd import _lib
+
+    L = _lib.lib()
+    for n in declared():
+        assert hasattr(L, n), n
+    assert set(declared()) == set(_lib.EXPORTS)
+
+
+def test_struct_layout_matches_c(tmp_path):
+    """sizeof/offsetof from the C compiler vs the ctypes mirrors."""
+    from decik_amd import _lib
+
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "decik_nf4.h"\n'
+                   "int main(void){printf(\"%zu %zu %zu %zu %zu %zu %zu %zu\\n\","
+                   "sizeof(dk_nf4_weight), offsetof(dk_nf4_weight, n), offsetof(dk_nf4_weight, nested),"
+                   "sizeof(dk_linear_fwd_group), offsetof(dk_linear_fwd_group, lora_scale),"
+                   "offsetof(dk_linear_fwd_group, y), sizeof(dk_linear_bwd_group),"
+                   "offsetof(dk_linear_bwd_group, lora_a));return 0;}\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.dirname(HEADER), "-o", str(exe), str(src)], check=True)
+    got = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True,
+                                          check=True).stdout.split()]
+    W, F, B = _lib.NF4Weight, _lib.LinearFwdGroup, _lib.LinearBwdGroup
+    want = [ctypes.sizeof(W), W.n.offset, W.nested.offset, ctypes.sizeof(F), F.lora_scale.offset,
+            F.y.offset, ctypes.sizeof(B), B.lora_a.offset]
+    assert got == want
+
+
+def test_argument_errors_are_reported():
+    from decik_amd import _lib
+
+    L = _lib.lib()
+    g = (_lib.LinearFwdGroup * 1)()
+    # k not a multiple of 32: rejected before anything touches the GPU
+    rc = L.dk_nf4_linear_fwd(ctypes.c_void_p(16), 8, 40, 40, g, 1, 0, None, 0, None)
+    assert rc != 0 and b"multiple of 32" in L.dk_last_error()
+    rc = L.dk_nf4_linear_fwd(ctypes.c_void_p(16), 8, 64, 64, g, 5, 0, None, 0, None)
+    assert rc != 0 and b"1..4 groups" in L.dk_last_error()
+    rc = L.dk_lora_down(ctypes.c_void_p(16), 8, 64, 64, ctypes.c_void_p(16), 8, ctypes.c_void_p(16), None)
+    assert rc != 0 and b"rank" in L.dk_last_error()
+    w = _lib.NF4Weight()
+    rc = L.dk_nf4_dequant(ctypes.byref(w), None, None)
+    assert rc != 0 and b"must be set" in L.dk_last_error()
+    with pytest.raises(_lib.DecikError):
+        _lib.check(1)
+
+
+def test_workspace_sizes():
+    from decik_amd import _lib
+
+    L = _lib.lib()
+    ns = (ctypes.c_int64 * 1)(1536)
+    # split-K plans need counters + partial tiles; plans without a split need nothing
+    assert L.dk_nf4_linear_bwd_workspace(830, 8960, ns, 1) >= 0
+    assert L.dk_nf4_linear_fwd_workspace(0, 1536, ns, 1) == 0
