@@ -1,0 +1,313 @@
+"""Benchmark of the NF4 quantized-linear path on one MI355X.
+
+Workload (one "step"): the Qwen2.5-1.5B MLP block forward + backward on NF4 weights at 830 packed
+tokens -- gate/up [8960, 1536] and down [1536, 8960] (fp16 N(0, 0.02), NF4 blocksize 64 with
+double quant), X [830, 1536] ~ N(0, 1), dY ~ N(0, 1e-2), SwiGLU between the projections, dX
+through the dequantized weights. Per step: 4 fused dequant-GEMM launches (gate+up forward,
+down forward, down backward, gate+up backward) = 6 GEMMs of 2*830*8960*1536 flops, and two
+SwiGLU launches. gate/up are kept from the forward (no recompute). Weights rotate over several
+layers' worth of seeded weights (seed = 7 * layer + projection).
+
+Also measured: the standalone NF4 dequantization of all seven Qwen2.5-1.5B projections (q, k, v,
+o, gate, up, down) over 8 layers per iteration (942 MB of algorithmic traffic, more than the
+256 MB Infinity Cache), in GB/s against the HBM peak.
+
+Prints one JSON line. `value` = whole-step dequant-GEMM throughput in TFLOP/s (inputs resident in
+HBM). `roofline` describes the kernel symbol with the largest share of the step time (launch
+durations from HIP events on the launch stream). `cpu_baseline` times the CPU restatement of the
+reference algorithm (dequantize the whole weight, then an fp32 GEMM) on this host.
+"""
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "NF4 dequant GB/s + dequant-GEMM fwd/bwd TFLOP/s, Qwen2.5-1.5B shapes, M=830"
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2500.0
+M, HIDDEN, INTER = 830, 1536, 8960
+QWEN15_SHAPES = [("q", 1536, 1536), ("k", 256, 1536), ("v", 256, 1536), ("o", 1536, 1536),
+                 ("gate", 8960, 1536), ("up", 8960, 1536), ("down", 1536, 8960)]
+
+
+def dequant_bytes(n, k):
+    """Algorithmic bytes of one dequantization: 0.5 B packed + 1/64 B absmax code + 2 B fp16 out
+    per weight, 4 B per 16384 weights of absmax2, 1092 B of tables and offset."""
+    w = n * k
+    return w * 0.5 + w / 64 + 2 * w + 4 * -(-w // 16384) + 1092
+
+
+def gemm_flops(n, k, m=M):
+    return 2.0 * m * n * k
+
+
+def seeded_fp16(shape, seed, std, device):
+    import torch
+
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    return (torch.randn(shape, generator=g) * std).to(torch.float16).to(device)
+
+
+def make_layers(n_layers, names, device, base_seed=0):
+    from decik_amd.quant import quantize_nf4
+
+    shapes = {s[0]: (s[1], s[2]) for s in QWEN15_SHAPES}
+    order = [s[0] for s in QWEN15_SHAPES]
+    layers = []
+    for layer in range(n_layers):
+        d = {}
+        for name in names:
+            w = seeded_fp16(shapes[name], base_seed + 7 * layer + order.index(name), 0.02, device)
+            d[name] = quantize_nf4(w, blocksize=64, compress_statistics=True)
+            del w
+        layers.append(d)
+    return layers
+
+
+def bench_mlp(steps, warmup, device, n_sets=4):
+    import torch
+
+    from decik_amd import nf4
+    from decik_amd.swiglu import swiglu_bwd, swiglu_fwd
+
+    layers = make_layers(n_sets, ["gate", "up", "down"], device)
+    x = seeded_fp16((M, HIDDEN), 1001, 1.0, device)
+    dy = seeded_fp16((M, HIDDEN), 1002, 1e-2, device)
+    launches = ["fwd_gate_up", "swiglu_fwd", "fwd_down", "bwd_down", "swiglu_bwd", "bwd_gate_up"]
+    symbol = {"fwd_gate_up": "nf4_fwd_kernel", "fwd_down": "nf4_fwd_kernel",
+              "bwd_down": "nf4_bwd_kernel", "bwd_gate_up": "nf4_bwd_kernel",
+              "swiglu_fwd": "swiglu_fwd_kernel", "swiglu_bwd": "swiglu_bwd_kernel"}
+    flops = {"fwd_gate_up": 2 * gemm_flops(INTER, HIDDEN), "fwd_down": gemm_flops(HIDDEN, INTER),
+             "bwd_down": gemm_flops(INTER, HIDDEN), "bwd_gate_up": 2 * gemm_flops(INTER, HIDDEN),
+             "swiglu_fwd": 0.0, "swiglu_bwd": 0.0}
+
+    def step(i, ev=None):
+        L = layers[i % n_sets]
+        g, u = L["gate"], L["up"]
+        dn = L["down"]
+        rec = (lambda j: ev[j].record()) if ev is not None else (lambda j: None)
+        rec(0)
+        gate, up = nf4.linear_forward(x, [dict(packed=g[0], qs=g[1]), dict(packed=u[0], qs=u[1])])
+        rec(1)
+        h = swiglu_fwd(gate, up)
+        rec(2)
+        (out,) = nf4.linear_forward(h, [dict(packed=dn[0], qs=dn[1])])
+        rec(3)
+        gh = nf4.linear_backward([dict(packed=dn[0], qs=dn[1], dy=dy)], M, INTER)
+        rec(4)
+        dgate, dup = swiglu_bwd(gh, gate, up, out=(gate, up))
+        rec(5)
+        dx = nf4.linear_backward([dict(packed=g[0], qs=g[1], dy=dgate),
+                                  dict(packed=u[0], qs=u[1], dy=dup)], M, HIDDEN)
+        rec(6)
+        return out, dx
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    # whole-step timing: K steps between two synchronisations
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for i in range(steps):
+        step(i)
+    t1.record()
+    torch.cuda.synchronize()
+    ms_step = t0.elapsed_time(t1) / steps
+    # per-launch timing: events between the launches, on the launch stream
+    per = {k: [] for k in launches}
+    for i in range(steps):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(7)]
+        step(i, ev)
+        torch.cuda.synchronize()
+        for j, k in enumerate(launches):
+            per[k].append(ev[j].elapsed_time(ev[j + 1]))
+    launch_ms = {k: statistics.median(v) for k, v in per.items()}
+    step_flops = sum(flops.values())
+    return dict(ms_step=ms_step, launch_ms=launch_ms, flops=flops, symbol=symbol,
+                step_flops=step_flops)
+
+
+def bench_dequant(iters, warmup, device, n_layers=8):
+    import torch
+
+    from decik_amd import nf4
+
+    names = [s[0] for s in QWEN15_SHAPES]
+    layers = make_layers(n_layers, names, device, base_seed=10_000)
+    pairs = [L[n] for L in layers for n in names]
+    outs = nf4.dequantize_nf4_many(pairs)  # allocate the outputs once; reused below
+    import ctypes
+
+    from decik_amd import _lib
+
+    descs, keep = [], []
+    for (packed, qs) in pairs:
+        w, kp = _lib.weight_desc(packed, qs, device)
+        descs.append(w)
+        keep += kp
+    arr = (_lib.NF4Weight * len(descs))(*descs)
+    optr = (ctypes.c_void_p * len(outs))(*[o.data_ptr() for o in outs])
+    L = _lib.lib()
+
+    def run():
+        _lib.check(L.dk_nf4_dequant_batched(arr, optr, len(descs), _lib.stream_of(device)))
+
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(iters):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        run()
+        b.record()
+        torch.cuda.synchronize()
+        times.append(a.elapsed_time(b))
+    ms = statistics.median(times)
+    total_bytes = n_layers * sum(dequant_bytes(n, k) for _, n, k in QWEN15_SHAPES)
+    launches = -(-len(descs) // 8)
+    return dict(ms=ms, bytes=total_bytes, gbs=total_bytes / ms / 1e6, launches=launches)
+
+
+def cpu_baseline(sample_steps=3):
+    """The reference algorithm on this host: dequantize each whole weight to fp16 (the oracle's
+    C restatement of the reference kernel, OpenMP on every core we may use), then fp32 GEMMs
+    (torch CPU) for the same MLP step: gate, up, SwiGLU, down forward; down, gate, up backward.
+    Sample: `sample_steps` full steps after one warm-up step; median."""
+    import numpy as np
+    import torch
+
+    from oracle import nf4 as O
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    rng = np.random.default_rng(0)
+    ws = {}
+    for name, n, k in [("gate", INTER, HIDDEN), ("up", INTER, HIDDEN), ("down", HIDDEN, INTER)]:
+        w = (rng.standard_normal((n, k)) * 0.02).astype(np.float16)
+        ws[name] = O.quantize_nf4(w)
+    x = torch.from_numpy((rng.standard_normal((M, HIDDEN))).astype(np.float16)).float()
+    dy = torch.from_numpy((rng.standard_normal((M, HIDDEN)) * 1e-2).astype(np.float16)).float()
+
+    def step():
+        w16 = {k: torch.from_numpy(O.dequant_nf4(q, nthreads=cores)) for k, q in ws.items()}
+        wf = {k: v.float() for k, v in w16.items()}
+        gate = x @ wf["gate"].T
+        up = x @ wf["up"].T
+        h = gate * torch.sigmoid(gate) * up
+        _ = h @ wf["down"].T
+        gh = dy @ wf["down"]
+        s = torch.sigmoid(gate)
+        dgate = gh * up * s * (1 + gate * (1 - s))
+        dup = gh * gate * s
+        return dgate @ wf["gate"] + dup @ wf["up"]
+
+    step()
+    times = []
+    for _ in range(sample_steps):
+        t = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t)
+    sec = statistics.median(times)
+    flops = 6 * gemm_flops(INTER, HIDDEN)
+    return dict(value=round(flops / sec / 1e12, 4), unit="TFLOP/s", cores=cores, kind="port",
+                sample=f"{sample_steps} full MLP fwd+bwd steps (M=830, 3 NF4 weights dequantized by "
+                       f"the C oracle with {cores} OpenMP threads + torch fp32 CPU GEMMs), median "
+                       f"{sec * 1e3:.0f} ms/step")
+
+
+def load_traffic():
+    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 --pmc summary
+    (profiles/traffic.json), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--skip-dequant", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, "
+              f"WORLD_SIZE={world}); the NF4 path needs no collectives and is not run on several GPUs.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from decik_amd import _lib
+
+    _lib.lib()  # fails loudly if the HIP library was not built
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+
+    mlp = bench_mlp(args.steps, args.warmup, device)
+    deq = None if args.skip_dequant else bench_dequant(max(args.steps, 10), args.warmup, device)
+
+    # dominant kernel symbol: largest total time per step
+    by_sym = {}
+    for k, ms in mlp["launch_ms"].items():
+        s = mlp["symbol"][k]
+        d = by_sym.setdefault(s, dict(ms=0.0, flops=0.0, launches=0))
+        d["ms"] += ms
+        d["flops"] += mlp["flops"][k]
+        d["launches"] += 1
+    dom = max(by_sym, key=lambda s: by_sym[s]["ms"])
+    d = by_sym[dom]
+    achieved = d["flops"] / (d["ms"] * 1e-3) / 1e12
+    traffic = load_traffic()
+    roofline = dict(kernel=dom, bound="mfma", achieved=round(achieved, 2), peak=FP16_PEAK_TFLOPS,
+                    unit="TFLOP/s", frac=round(achieved / FP16_PEAK_TFLOPS, 4),
+                    flops_per_launch=d["flops"] / d["launches"],
+                    avg_launch_ms=round(d["ms"] / d["launches"], 5),
+                    traffic=None if traffic is None else traffic.get(dom))
+    value = mlp["step_flops"] / (mlp["ms_step"] * 1e-3) / 1e12
+    line = dict(
+        metric=METRIC, value=round(value, 2), unit="TFLOP/s", n_gpus=1, steps=args.steps,
+        warmup=args.warmup, ms_per_step=round(mlp["ms_step"], 4), higher_is_better=True,
+        scaling="weak", vs_baseline=None, dtype="fp16", data="synthetic",
+        config=dict(workload="Qwen2.5-1.5B MLP block fwd+bwd on NF4 weights: gate/up [8960,1536], "
+                             "down [1536,8960], blocksize 64, double quant; X [830,1536]; SwiGLU; "
+                             "dX through W; gate/up kept from the forward",
+                    m=M, hidden=HIDDEN, intermediate=INTER, weight_sets=4),
+        roofline=roofline,
+        kernels={k: dict(ms=round(v, 4),
+                         tflops=round(mlp["flops"][k] / (v * 1e-3) / 1e12, 1) if mlp["flops"][k] else None)
+                 for k, v in mlp["launch_ms"].items()},
+    )
+    if deq is not None:
+        line["dequant"] = dict(value=round(deq["gbs"], 1), unit="GB/s", ms=round(deq["ms"], 4),
+                               bytes=deq["bytes"], launches=deq["launches"],
+                               workload="all 7 Qwen2.5-1.5B projections x 8 layers per iteration",
+                               roofline=dict(bound="hbm", achieved=round(deq["gbs"], 1),
+                                             peak=HBM_PEAK_GBS, unit="GB/s",
+                                             frac=round(deq["gbs"] / HBM_PEAK_GBS, 4)))
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline()
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -30,13 +30,14 @@ bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p
 
 int to_dev(const dk_nf4_weight* w, NF4Dev* d, const char* who) {
     if (w == nullptr) return fail(std::string(who) + ": null weight descriptor");
-    if (w->packed == nullptr || w->absmax == nullptr || w->code == nullptr)
+    const bool empty = w->n * w->k == 0;
+    if (!empty && (w->packed == nullptr || w->absmax == nullptr || w->code == nullptr))
         return fail(std::string(who) + ": packed, absmax and code must be set");
     if (w->n < 0 || w->k < 0 || ((w->n * w->k) & 1))
         return fail(std::string(who) + ": n*k must be even and non-negative");
     if (w->blocksize < 2 || (w->blocksize & 1))
         return fail(std::string(who) + ": blocksize must be even and >= 2");
-    if (w->nested) {
+    if (w->nested && !empty) {
         if (w->absmax2 == nullptr || w->code2 == nullptr || w->offset == nullptr || w->blocksize2 < 1)
             return fail(std::string(who) + ": nested weights need absmax2, code2, offset, blocksize2");
     }
@@ -114,6 +115,24 @@ int choose_splits(int64_t tiles, int steps, double fix) {
     return best;
 }
 
+// Workspace layout, the same for every plan: kCounterBytes of tile counters (only ever
+// incremented and reset to zero by the kernels, so they stay zero between calls), then the
+// fp32 partial tiles. A plan-dependent counter region would overlap another plan's partials.
+constexpr int64_t kCounterBytes = 64 * 1024;
+constexpr int kMaxSplitTiles = (int)(kCounterBytes / 4);
+
+int64_t workspace_bytes(const GemmPlan& p) {
+    if (p.splits <= 1) return 0;
+    return kCounterBytes + p.partial_floats * 4;
+}
+
+void no_split(GemmPlan& p) {
+    p.splits = 1;
+    p.steps_per_split = p.steps;
+    p.counters = 0;
+    p.partial_floats = 0;
+}
+
 GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
     GemmPlan p{};
     p.mt = choose_mt(m);
@@ -126,6 +145,7 @@ GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
     p.steps_per_split = p.steps > 0 ? (p.steps + p.splits - 1) / p.splits : 0;
     p.counters = p.splits > 1 ? (int)tiles : 0;
     p.partial_floats = p.splits > 1 ? tiles * p.splits * (int64_t)(16 * p.mt) * kFwdBN : 0;
+    if (tiles > kMaxSplitTiles) no_split(p);
     return p;
 }
 
@@ -141,14 +161,11 @@ GemmPlan plan_bwd(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
     p.steps_per_split = p.steps > 0 ? (p.steps + p.splits - 1) / p.splits : 0;
     p.counters = p.splits > 1 ? (int)tiles : 0;
     p.partial_floats = p.splits > 1 ? tiles * p.splits * (int64_t)(16 * p.mt) * kBwdBN : 0;
+    if (tiles > kMaxSplitTiles) no_split(p);
     return p;
 }
 
-int64_t workspace_bytes(const GemmPlan& p) {
-    if (p.splits <= 1) return 0;
-    const int64_t counter_bytes = ((int64_t)p.counters * 4 + 255) & ~int64_t(255);
-    return counter_bytes + p.partial_floats * 4;
-}
+
 
 }  // namespace
 }  // namespace dk
@@ -267,9 +284,8 @@ int dk_nf4_linear_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
     a.ksteps_per_split = p.steps_per_split;
     a.nested = nested;
     if (need > 0) {
-        const int64_t counter_bytes = ((int64_t)p.counters * 4 + 255) & ~int64_t(255);
         a.counters = static_cast<int32_t*>(workspace);
-        a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + counter_bytes);
+        a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
     }
     const int64_t wgs = (int64_t)p.m_tiles * p.n_tiles * p.splits;
     if (wgs > INT32_MAX / 2) return fail("dk_nf4_linear_fwd: problem too large");
@@ -336,9 +352,8 @@ int dk_nf4_linear_bwd(const dk_linear_bwd_group* groups, int ngroups, int64_t m,
     a.dx_fp32 = dx_fp32 ? 1 : 0;
     a.nested = nested;
     if (need > 0) {
-        const int64_t counter_bytes = ((int64_t)p.counters * 4 + 255) & ~int64_t(255);
         a.counters = static_cast<int32_t*>(workspace);
-        a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + counter_bytes);
+        a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
     }
     const int64_t wgs = (int64_t)p.m_tiles * p.n_tiles * p.splits;
     if (wgs > INT32_MAX / 2) return fail("dk_nf4_linear_bwd: problem too large");

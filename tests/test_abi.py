@@ -69,6 +69,7 @@ def test_argument_errors_are_reported():
     rc = L.dk_lora_down(ctypes.c_void_p(16), 8, 64, 64, ctypes.c_void_p(16), 8, ctypes.c_void_p(16), None)
     assert rc != 0 and b"rank" in L.dk_last_error()
     w = _lib.NF4Weight()
+    w.n, w.k, w.blocksize = 8, 64, 64
     rc = L.dk_nf4_dequant(ctypes.byref(w), None, None)
     assert rc != 0 and b"must be set" in L.dk_last_error()
     with pytest.raises(_lib.DecikError):
