@@ -54,6 +54,26 @@ int to_dev(const dk_nf4_weight* w, NF4Dev* d, const char* who) {
     d->blocksize2 = w->nested ? w->blocksize2 : 256;
     d->bs_shift = log2_exact(w->blocksize);
     d->bs2_shift = log2_exact(d->blocksize2);
+    const int64_t n_el = w->n * w->k;
+    const int64_t n_blocks = (n_el + w->blocksize - 1) / w->blocksize;
+    const int64_t packed = n_el / 2;
+    const int64_t amax = w->nested ? n_blocks : 4 * n_blocks;
+    const int64_t amax2 = w->nested ? 4 * ((n_blocks + d->blocksize2 - 1) / d->blocksize2) : 0;
+    auto clamp32 = [](int64_t v) { return (uint32_t)(v < INT32_MAX ? v : INT32_MAX); };
+    d->packed_bytes = clamp32(packed);
+    d->absmax_bytes = clamp32(amax);
+    d->absmax2_bytes = clamp32(amax2);
+    return 0;
+}
+
+// The fused GEMMs index with 32-bit byte offsets and shift-only block arithmetic.
+int gemm_weight_ok(const dk_nf4_weight& w, const char* who) {
+    if (w.n * w.k / 2 >= INT32_MAX) return fail(std::string(who) + ": weight larger than 2^31 bytes");
+    if (w.blocksize % 32 != 0 || log2_exact(w.blocksize) < 0)
+        return fail(std::string(who) + ": blocksize must be a power of two >= 32");
+    if (w.nested && log2_exact(w.blocksize2) < 0)
+        return fail(std::string(who) + ": blocksize2 must be a power of two");
+    if (w.n > INT32_MAX / 2) return fail(std::string(who) + ": too many weight rows");
     return 0;
 }
 
@@ -75,14 +95,15 @@ int pad8(int g) { return (g + 7) & ~7; }
 
 // ---- planning -----------------------------------------------------------------------------
 
-int choose_mt(int64_t m) {
-    // rows per tile = 16 * mt. Cost = tiles * (rows + 64): padded rows plus a per-tile share of
-    // the weight unpacking, which every m-tile repeats.
-    static const int cand[] = {1, 2, 4, 8, 13};
-    int best = 1;
+// Token rows per tile: the candidates are the compiled kernel variants (rows = unit * c).
+// Cost = tiles * (rows + 64): padded rows plus a per-tile share of the weight unpacking, which
+// every tile of rows repeats.
+int choose_rows(int64_t m, int unit, const int* cand, int ncand) {
+    int best = cand[0];
     int64_t best_cost = INT64_MAX;
-    for (int mt : cand) {
-        const int64_t rows = 16 * mt;
+    for (int ci = 0; ci < ncand; ++ci) {
+        const int mt = cand[ci];
+        const int64_t rows = (int64_t)unit * mt;
         const int64_t tiles = (m + rows - 1) / rows;
         const int64_t cost = tiles * (rows + 64);
         if (cost < best_cost) {
@@ -134,9 +155,10 @@ void no_split(GemmPlan& p) {
 }
 
 GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
+    static const int cand[] = {1, 2, 4, 7};
     GemmPlan p{};
-    p.mt = choose_mt(m);
-    p.m_tiles = (int)((m + 16 * p.mt - 1) / (16 * p.mt));
+    p.mt = choose_rows(m, 32, cand, 4);
+    p.m_tiles = (int)((m + 32 * p.mt - 1) / (32 * p.mt));
     p.n_tiles = 0;
     for (int g = 0; g < ngroups; ++g) p.n_tiles += (int)((ns[g] + kFwdBN - 1) / kFwdBN);
     p.steps = (int)((k + kFwdBK - 1) / kFwdBK);
@@ -144,14 +166,15 @@ GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
     p.splits = p.steps > 0 ? choose_splits(tiles, p.steps, 1.0) : 1;
     p.steps_per_split = p.steps > 0 ? (p.steps + p.splits - 1) / p.splits : 0;
     p.counters = p.splits > 1 ? (int)tiles : 0;
-    p.partial_floats = p.splits > 1 ? tiles * p.splits * (int64_t)(16 * p.mt) * kFwdBN : 0;
-    if (tiles > kMaxSplitTiles) no_split(p);
+    p.partial_floats = p.splits > 1 ? tiles * p.splits * (int64_t)(32 * p.mt) * kFwdBN : 0;
+    if (tiles > kMaxSplitTiles || p.partial_floats * 4 >= INT32_MAX) no_split(p);
     return p;
 }
 
 GemmPlan plan_bwd(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
+    static const int cand[] = {1, 2, 4, 8, 13};
     GemmPlan p{};
-    p.mt = choose_mt(m);
+    p.mt = choose_rows(m, 16, cand, 5);
     p.m_tiles = (int)((m + 16 * p.mt - 1) / (16 * p.mt));
     p.n_tiles = (int)((k + kBwdBN - 1) / kBwdBN);
     p.steps = 0;
@@ -161,7 +184,7 @@ GemmPlan plan_bwd(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
     p.steps_per_split = p.steps > 0 ? (p.steps + p.splits - 1) / p.splits : 0;
     p.counters = p.splits > 1 ? (int)tiles : 0;
     p.partial_floats = p.splits > 1 ? tiles * p.splits * (int64_t)(16 * p.mt) * kBwdBN : 0;
-    if (tiles > kMaxSplitTiles) no_split(p);
+    if (tiles > kMaxSplitTiles || p.partial_floats * 4 >= INT32_MAX) no_split(p);
     return p;
 }
 
@@ -245,7 +268,7 @@ int dk_nf4_linear_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
         const dk_linear_fwd_group& G = groups[g];
         if (to_dev(&G.w, &a.g[g].w, "dk_nf4_linear_fwd")) return 1;
         if (G.w.k != k) return fail("dk_nf4_linear_fwd: weight k differs from x");
-        if (G.w.blocksize % 32 != 0) return fail("dk_nf4_linear_fwd: blocksize must be a multiple of 32");
+        if (gemm_weight_ok(G.w, "dk_nf4_linear_fwd")) return 1;
         if (!aligned(G.w.packed, 16)) return fail("dk_nf4_linear_fwd: packed weights must be 16-byte aligned");
         if (nested >= 0 && nested != G.w.nested)
             return fail("dk_nf4_linear_fwd: all groups must be nested or all plain");
@@ -271,8 +294,10 @@ int dk_nf4_linear_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
     const int64_t need = workspace_bytes(p);
     if (need > 0 && (workspace == nullptr || workspace_bytes_ < need || !aligned(workspace, 256)))
         return fail("dk_nf4_linear_fwd: workspace too small (need " + std::to_string(need) + " bytes)");
+    if ((m - 1) * ldx + k >= INT32_MAX / 2) return fail("dk_nf4_linear_fwd: x too large");
     a.x = reinterpret_cast<const _Float16*>(x);
     a.ldx = ldx;
+    a.x_bytes = (uint32_t)(((m - 1) * ldx + k) * 2);
     a.m = (int)m;
     a.k = (int)k;
     a.ngroups = ngroups;
@@ -286,6 +311,7 @@ int dk_nf4_linear_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
     if (need > 0) {
         a.counters = static_cast<int32_t*>(workspace);
         a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
+        a.partial_bytes = (uint32_t)(p.partial_floats * 4);
     }
     const int64_t wgs = (int64_t)p.m_tiles * p.n_tiles * p.splits;
     if (wgs > INT32_MAX / 2) return fail("dk_nf4_linear_fwd: problem too large");
@@ -314,7 +340,8 @@ int dk_nf4_linear_bwd(const dk_linear_bwd_group* groups, int ngroups, int64_t m,
         const dk_linear_bwd_group& G = groups[g];
         if (to_dev(&G.w, &a.g[g].w, "dk_nf4_linear_bwd")) return 1;
         if (G.w.k != k) return fail("dk_nf4_linear_bwd: weight k differs from dx");
-        if (G.w.blocksize % 32 != 0) return fail("dk_nf4_linear_bwd: blocksize must be a multiple of 32");
+        if (gemm_weight_ok(G.w, "dk_nf4_linear_bwd")) return 1;
+        if ((m - 1) * G.lddy + G.w.n >= INT32_MAX / 2) return fail("dk_nf4_linear_bwd: dy too large");
         if (!aligned(G.w.packed, 16)) return fail("dk_nf4_linear_bwd: packed weights must be 16-byte aligned");
         if ((G.w.n % 8) != 0) return fail("dk_nf4_linear_bwd: weight rows must be a multiple of 8");
         if (nested >= 0 && nested != G.w.nested)
@@ -326,6 +353,7 @@ int dk_nf4_linear_bwd(const dk_linear_bwd_group* groups, int ngroups, int64_t m,
             return fail("dk_nf4_linear_bwd: LoRA needs lora_rank > 0, lora_a and 8-byte aligned gu");
         a.g[g].dy = reinterpret_cast<const _Float16*>(G.dy);
         a.g[g].lddy = G.lddy;
+        a.g[g].dy_bytes = m > 0 ? (uint32_t)(((m - 1) * G.lddy + G.w.n) * 2) : 0;
         a.g[g].lora_gu = reinterpret_cast<const _Float16*>(G.lora_gu);
         a.g[g].lora_a = reinterpret_cast<const _Float16*>(G.lora_a);
         a.g[g].step_begin = step;
@@ -354,6 +382,7 @@ int dk_nf4_linear_bwd(const dk_linear_bwd_group* groups, int ngroups, int64_t m,
     if (need > 0) {
         a.counters = static_cast<int32_t*>(workspace);
         a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
+        a.partial_bytes = (uint32_t)(p.partial_floats * 4);
     }
     const int64_t wgs = (int64_t)p.m_tiles * p.n_tiles * p.splits;
     if (wgs > INT32_MAX / 2) return fail("dk_nf4_linear_bwd: problem too large");

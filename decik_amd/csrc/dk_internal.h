@@ -20,13 +20,13 @@ struct DequantArgs {
 __global__ void nf4_dequant_kernel(const DequantArgs a);
 
 // ------------------------------------------------------------------------------------------
-// Fused dequant x GEMM. One work-group = 4 waves. Forward tile: BM = 16*MT rows of X by
-// BN = 256 weight rows (64 per wave); main-loop step 128 along k. Backward tile: BM rows of dY
-// by 256 columns of dX (64 per wave); main-loop step 64 along the contraction (weight rows).
+// Fused dequant x GEMM. One work-group = 4 waves. Forward tile: 32*MB rows of X by 256 weight
+// rows (64 per wave); main-loop step 64 along k. Backward tile: 16*MT rows of dY by 256 columns
+// of dX (64 per wave); main-loop step 64 along the contraction (weight rows).
 
 constexpr int kGemmThreads = 256;
 constexpr int kFwdBN = 256;
-constexpr int kFwdBK = 128;
+constexpr int kFwdBK = 64;
 constexpr int kBwdBN = 256;
 constexpr int kBwdBC = 64;
 constexpr int kMaxGroups = DK_MAX_GROUPS;
@@ -45,11 +45,13 @@ struct FwdGroupDev {
 struct FwdArgs {
     const _Float16* x;
     int64_t ldx;
+    uint32_t x_bytes;
     int32_t m, k;
     int32_t ngroups, lora_rank;
     int32_t m_tiles, n_tiles, splits, ksteps, ksteps_per_split;
     int32_t nested;
     float* partials;
+    uint32_t partial_bytes;
     int32_t* counters;
     FwdGroupDev g[kMaxGroups];
 };
@@ -58,6 +60,7 @@ struct BwdGroupDev {
     NF4Dev w;
     const _Float16* dy;
     int64_t lddy;
+    uint32_t dy_bytes;
     const _Float16* lora_gu;
     const _Float16* lora_a;
     int32_t step_begin;  // first contraction step of this group
@@ -73,6 +76,7 @@ struct BwdArgs {
     int32_t dx_fp32;
     int32_t nested;
     float* partials;
+    uint32_t partial_bytes;
     int32_t* counters;
     BwdGroupDev g[kMaxGroups];
 };
@@ -89,7 +93,7 @@ struct GemmPlan {
     int counters;            // tile counters
 };
 
-hipError_t launch_fwd(const FwdArgs& a, int mt, int grid, hipStream_t s);
+hipError_t launch_fwd(const FwdArgs& a, int mb, int grid, hipStream_t s);
 hipError_t launch_bwd(const BwdArgs& a, int mt, int grid, hipStream_t s);
 
 // LoRA and SwiGLU helpers.

@@ -1,0 +1,120 @@
+// Helpers shared by the fused dequant-GEMM kernels (forward and input gradient).
+#pragma once
+
+#include "dk_internal.h"
+
+namespace dk {
+
+__device__ __forceinline__ int xcd_logical_id() {
+    // The dispatcher deals work-groups to the 8 XCDs round-robin. Renumber them so that logical
+    // ids that are consecutive run on one XCD (and share its L2). gridDim.x is a multiple of 8.
+    const int nwg = gridDim.x, bid = blockIdx.x;
+    return (bid & 7) * (nwg >> 3) + (bid >> 3);
+}
+
+__device__ __forceinline__ uint32_t perm_lo(uint32_t lo_src, uint32_t hi_src) {
+    // low 16 bits of lo_src, then low 16 bits of hi_src
+    return __builtin_amdgcn_perm(hi_src, lo_src, 0x05040100u);
+}
+
+__device__ __forceinline__ uint32_t perm_hi(uint32_t lo_src, uint32_t hi_src) {
+    // high 16 bits of lo_src, then high 16 bits of hi_src
+    return __builtin_amdgcn_perm(hi_src, lo_src, 0x07060302u);
+}
+
+__device__ __forceinline__ float4_t chunk4(const float16_t& v, int q) {
+    switch (q) {
+        case 0: return __builtin_shufflevector(v, v, 0, 1, 2, 3);
+        case 1: return __builtin_shufflevector(v, v, 4, 5, 6, 7);
+        case 2: return __builtin_shufflevector(v, v, 8, 9, 10, 11);
+        default: return __builtin_shufflevector(v, v, 12, 13, 14, 15);
+    }
+}
+
+__device__ __forceinline__ float16_t join4(float4_t a, float4_t b, float4_t c, float4_t d) {
+    typedef float float8_t __attribute__((ext_vector_type(8)));
+    const float8_t ab = __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+    const float8_t cd = __builtin_shufflevector(c, d, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_shufflevector(ab, cd, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
+}
+
+template <typename V>
+struct AccChunks;
+template <>
+struct AccChunks<float4_t> {
+    static constexpr int n = 1;
+    static __device__ __forceinline__ float4_t get(const float4_t& v, int) { return v; }
+    static __device__ __forceinline__ void set(float4_t& v, int, float4_t c) { v = c; }
+};
+template <>
+struct AccChunks<float16_t> {
+    static constexpr int n = 4;
+    static __device__ __forceinline__ float4_t get(const float16_t& v, int q) { return chunk4(v, q); }
+    static __device__ __forceinline__ void set(float16_t& v, int q, float4_t c) {
+        const float16_t w = join4(c, c, c, c);
+        switch (q) {
+            case 0: v = __builtin_shufflevector(v, w, 16, 17, 18, 19, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15); break;
+            case 1: v = __builtin_shufflevector(v, w, 0, 1, 2, 3, 20, 21, 22, 23, 8, 9, 10, 11, 12, 13, 14, 15); break;
+            case 2: v = __builtin_shufflevector(v, w, 0, 1, 2, 3, 4, 5, 6, 7, 24, 25, 26, 27, 12, 13, 14, 15); break;
+            default: v = __builtin_shufflevector(v, w, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 28, 29, 30, 31); break;
+        }
+    }
+};
+
+// Split-K: every work-group of a tile writes its fp32 partial accumulators (chunk-major, so each
+// store instruction is contiguous across the wave), then bumps the tile's counter. The last one
+// to arrive adds the partials in split order (deterministic), resets the counter for the next
+// launch and returns true; the others return false. Works in place on the accumulators.
+//
+// Cross-XCD visibility without cache-wide maintenance: the partials are written with
+// device-scope stores (sc1: written through the XCD's L2) and read back with device-scope loads
+// (sc1: not served from a possibly stale L2 line); the counter atomic is issued only after the
+// stores have completed (vmcnt(0)). A __threadfence() here would write back and invalidate the
+// whole L2 of the XCD for every work-group.
+constexpr int kCPolDevice = 16;  // cache policy SC1: device scope (gfx940+ encoding)
+
+template <typename V, int NA>
+__device__ __forceinline__ bool splitk_finish(V (&acc)[NA], float* partials, int32_t* counters,
+                                              int tile, int splits, int split, int* flag,
+                                              uint32_t partial_bytes) {
+    using C = AccChunks<V>;
+    const int tid = threadIdx.x;
+    constexpr uint32_t per = (uint32_t)NA * C::n * kGemmThreads * 16;  // bytes per partial
+    const rsrc_t prs = make_rsrc(partials, partial_bytes);
+    const uint32_t base = (uint32_t)tile * (uint32_t)splits * per;
+    const uint32_t mine = base + (uint32_t)split * per;
+#pragma unroll
+    for (int a = 0; a < NA; ++a)
+#pragma unroll
+        for (int q = 0; q < C::n; ++q)
+            __builtin_amdgcn_raw_buffer_store_b128(
+                __builtin_bit_cast(u32x4_t, C::get(acc[a], q)), prs,
+                (int)(mine + ((uint32_t)(a * C::n + q) * kGemmThreads + tid) * 16), 0, kCPolDevice);
+    wait_vmcnt<0>();  // this thread's partial stores have completed
+    __syncthreads();
+    if (tid == 0)
+        *flag = (__hip_atomic_fetch_add(counters + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 splits - 1);
+    __syncthreads();
+    if (!*flag) return false;
+    // sum in split order (the same order on every run, whichever work-group finishes last)
+#pragma unroll
+    for (int a = 0; a < NA; ++a) {
+#pragma unroll
+        for (int q = 0; q < C::n; ++q) {
+            const uint32_t off = ((uint32_t)(a * C::n + q) * kGemmThreads + tid) * 16;
+            float4_t sum = {0.f, 0.f, 0.f, 0.f};
+            for (int s = 0; s < splits; ++s)
+                sum += s == split ? C::get(acc[a], q)
+                                  : __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                     prs, (int)(base + (uint32_t)s * per + off),
+                                                                     0, kCPolDevice));
+            C::set(acc[a], q, sum);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (tid == 0) __hip_atomic_store(counters + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+}
+
+}  // namespace dk

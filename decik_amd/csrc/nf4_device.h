@@ -18,6 +18,7 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
@@ -35,7 +36,67 @@ struct NF4Dev {
     int64_t n, k;
     int32_t blocksize, blocksize2;
     int32_t bs_shift, bs2_shift;  // log2 of the block sizes, -1 if not a power of two
+    uint32_t packed_bytes, absmax_bytes, absmax2_bytes;  // buffer sizes (fused GEMM: < 2^31)
 };
+
+// Raw buffer loads (gfx9 resource word 3 = 0x00020000): an offset at or past the buffer's size
+// reads 0, so edge tiles need no branches around their loads -- invalid lanes load at kOOB.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t kOOB = 0x80000000u;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4_t bload128(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ u32x2_t bload64(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ uint32_t bload8(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b8(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ uint32_t bload16(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+}
+// 16 bytes per lane straight into LDS: lane l's data lands at lds_wave_base + 16 * l (the base
+// must be the same for the whole wave). Past-the-end offsets write zeros.
+__device__ __forceinline__ void bload128_lds(rsrc_t r, void* lds_wave_base, uint32_t off) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        r, (__attribute__((address_space(3))) void*)lds_wave_base, 16, (int)off, 0, 0, 0);
+}
+
+// 1 or 4 bytes per lane straight into LDS; each lane's value occupies a dword slot, at
+// lds_wave_base + 4 * l, whatever the load size.
+__device__ __forceinline__ void bload8_lds(rsrc_t r, void* lds_wave_base, uint32_t off) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        r, (__attribute__((address_space(3))) void*)lds_wave_base, 1, (int)off, 0, 0, 0);
+}
+__device__ __forceinline__ void bload32_lds(rsrc_t r, void* lds_wave_base, uint32_t off) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        r, (__attribute__((address_space(3))) void*)lds_wave_base, 4, (int)off, 0, 0, 0);
+}
+
+// Wait until at most n vector-memory operations are outstanding (global loads and the
+// buffer -> LDS loads above). Written as inline asm with a memory clobber so the compiler keeps
+// memory operations on their side of it.
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(n >= 0 && n < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory");
+}
+
+// Work-group barrier for LDS hand-offs: this wave's LDS writes complete, then s_barrier. Unlike
+// __syncthreads() it carries no release fence, which would wait for every outstanding global ->
+// LDS load (vmcnt(0)) and so serialize the prefetch; loads the next phase reads are covered by
+// an explicit wait_vmcnt before the barrier.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+__device__ __forceinline__ float bloadf(rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
 
 __device__ __forceinline__ int64_t block_of(const NF4Dev& w, int64_t flat) {
     return w.bs_shift >= 0 ? (flat >> w.bs_shift) : flat / w.blocksize;
@@ -90,6 +151,20 @@ __device__ __forceinline__ float4_t mfma16x16x32(half8_t a, half8_t b, float4_t 
 
 __device__ __forceinline__ float4_t mfma16x16x16(half4_t a, half4_t b, float4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float16_t mfma32x32x16(half8_t a, half8_t b, float16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// v_mfma_f32_32x32x16_f16 (gfx950), with g = l / 32:
+//   A operand: lane l holds A[l % 32][8 g + e], e = 0..7
+//   B operand: lane l holds B[8 g + e][l % 32]
+//   C/D:       lane l holds D[8 (r / 4) + 4 g + (r % 4)][l % 32], r = 0..15
+// With A row i taken from weight row arow_to_n(i) (a permutation of 0..31), lane l's 16
+// accumulators are the 16 consecutive weight rows 16 g + r.
+__device__ __forceinline__ int arow_to_n(int i) {
+    return 16 * ((i >> 2) & 1) + 4 * (i >> 3) + (i & 3);
 }
 
 // The wave's lane-group layout of v_mfma_f32_16x16x32_f16 (CDNA3/4):
