@@ -1,4 +1,6 @@
 // C ABI (include/decik_nf4.h): argument checks, launch planning and launches.
+#include <cstdio>
+#include <cstdlib>
 #include <mutex>
 #include <string>
 
@@ -95,45 +97,63 @@ int pad8(int g) { return (g + 7) & ~7; }
 
 // ---- planning -----------------------------------------------------------------------------
 
-// Token rows per tile: the candidates are the compiled kernel variants (rows = unit * c).
-// Cost = tiles * (rows + 64): padded rows plus a per-tile share of the weight unpacking, which
-// every tile of rows repeats.
-int choose_rows(int64_t m, int unit, const int* cand, int ncand) {
-    int best = cand[0];
-    int64_t best_cost = INT64_MAX;
-    for (int ci = 0; ci < ncand; ++ci) {
-        const int mt = cand[ci];
-        const int64_t rows = (int64_t)unit * mt;
-        const int64_t tiles = (m + rows - 1) / rows;
-        const int64_t cost = tiles * (rows + 64);
-        if (cost < best_cost) {
-            best_cost = cost;
-            best = mt;
-        }
+// Launch planning. A plan picks the kernel variant (token rows per tile) and the number of
+// contraction splits by an estimate of the launch time:
+//   rounds(tiles * splits, resident work-groups) * steps per split * step time(variant)
+//   + split-K traffic (every split writes an fp32 tile, the last one reads them back)
+//   + the last arriver's serial read of the other splits' tiles.
+// Resident work-groups per CU and the step times are per-variant constants measured on MI355X
+// (Qwen2.5-shaped launches at M = 830, all CUs busy).
+struct VariantCost {
+    int rows_blocks;   // kernel template argument
+    int per_cu;        // resident work-groups per CU
+    double step_us;    // time of one 64-wide contraction step of one work-group
+};
+
+struct PlanCost {
+    int unit;            // token rows per row block
+    int bn;              // output columns per tile
+    const VariantCost* v;
+    int nv;
+};
+
+constexpr double kHbmBytesPerUs = 4.0e6;    // sustained HBM traffic, bytes per microsecond
+constexpr double kSerialBytesPerUs = 1.0e5;  // one work-group's read of other splits' tiles
+
+double plan_time(const PlanCost& pc, const VariantCost& v, int64_t m, int64_t col_tiles, int steps,
+                 int splits) {
+    const int64_t rows = (int64_t)pc.unit * v.rows_blocks;
+    const int64_t tiles = ((m + rows - 1) / rows) * col_tiles;
+    const int64_t slots = (int64_t)num_cus() * v.per_cu;
+    const int per = (steps + splits - 1) / splits;
+    const double rounds = (double)((tiles * splits + slots - 1) / slots);
+    double t = rounds * per * v.step_us;
+    if (splits > 1) {
+        const double tile_bytes = (double)rows * pc.bn * 4.0;
+        t += (double)tiles * splits * tile_bytes * 1.5 / kHbmBytesPerUs;
+        t += (splits - 1) * tile_bytes / kSerialBytesPerUs;
     }
-    return best;
+    return t;
 }
 
-// Split the contraction so that tiles * splits work-groups cover the CUs evenly. Model: a
-// work-group step costs 1; the last work-group of a split tile reads the other partial tiles
-// at `fix` step-costs each.
-int choose_splits(int64_t tiles, int steps, double fix) {
-    const int cus = num_cus();
-    int best = 1;
-    double best_cost = 1e300;
-    const int max_s = steps < 64 ? steps : 64;
-    for (int s = 1; s <= max_s; ++s) {
-        const int per = (steps + s - 1) / s;
-        const int used = (steps + per - 1) / per;  // splits that actually get work
-        if (used != s) continue;
-        const double rounds = (double)((tiles * s + cus - 1) / cus);
-        const double cost = rounds * per + (s > 1 ? fix * s : 0.0);
-        if (cost < best_cost - 1e-9) {
-            best_cost = cost;
-            best = s;
+void choose_plan(const PlanCost& pc, int64_t m, int64_t col_tiles, int steps, int* mt, int* splits) {
+    double best = 1e300;
+    *mt = pc.v[0].rows_blocks;
+    *splits = 1;
+    for (int i = 0; i < pc.nv; ++i) {
+        const VariantCost& v = pc.v[i];
+        const int max_s = steps < 32 ? steps : 32;
+        for (int s = 1; s <= (max_s > 0 ? max_s : 1); ++s) {
+            const int per = steps > 0 ? (steps + s - 1) / s : 0;
+            if (steps > 0 && (steps + per - 1) / per != s) continue;  // s splits must all get work
+            const double t = plan_time(pc, v, m, col_tiles, steps, s);
+            if (t < best * 0.999) {
+                best = t;
+                *mt = v.rows_blocks;
+                *splits = s;
+            }
         }
     }
-    return best;
 }
 
 // Workspace layout, the same for every plan: kCounterBytes of tile counters (only ever
@@ -154,37 +174,61 @@ void no_split(GemmPlan& p) {
     p.partial_floats = 0;
 }
 
+// Tuning hook: DECIK_FWD_PLAN / DECIK_BWD_PLAN = "rows_blocks,splits" forces a plan (both must
+// be valid for the shape: a compiled row-block count and 1 <= splits <= steps). Unset in normal
+// use; read on every call so a sweep can change it between calls.
+bool plan_override(const char* var, const int* cand, int ncand, int steps, int* mt, int* splits) {
+    const char* v = std::getenv(var);
+    if (v == nullptr || *v == 0) return false;
+    int a = 0, b = 0;
+    if (std::sscanf(v, "%d,%d", &a, &b) != 2) return false;
+    bool ok = false;
+    for (int i = 0; i < ncand; ++i) ok |= cand[i] == a;
+    if (!ok || b < 1 || b > (steps > 0 ? steps : 1)) return false;
+    *mt = a;
+    *splits = b;
+    return true;
+}
+
+void finish_plan(GemmPlan& p, int unit, int bn) {
+    p.steps_per_split = p.steps > 0 ? (p.steps + p.splits - 1) / p.splits : 0;
+    if (p.steps > 0) p.splits = (p.steps + p.steps_per_split - 1) / p.steps_per_split;
+    const int64_t tiles = (int64_t)p.m_tiles * p.n_tiles;
+    p.counters = p.splits > 1 ? (int)tiles : 0;
+    p.partial_floats = p.splits > 1 ? tiles * p.splits * (int64_t)(unit * p.mt) * bn : 0;
+    if (tiles > kMaxSplitTiles || p.partial_floats * 4 >= INT32_MAX) no_split(p);
+}
+
+constexpr VariantCost kFwdVariants[] = {{1, 3, 0.55}, {2, 2, 0.85}, {4, 2, 1.30}, {8, 1, 1.60}};
+constexpr VariantCost kBwdVariants[] = {{1, 2, 1.00}, {2, 2, 1.10}, {4, 1, 1.20}, {8, 1, 1.90}, {13, 1, 2.70}};
+
 GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
-    static const int cand[] = {1, 2, 4, 7};
+    static const int cand[] = {1, 2, 4, 8};
     GemmPlan p{};
-    p.mt = choose_rows(m, 32, cand, 4);
-    p.m_tiles = (int)((m + 32 * p.mt - 1) / (32 * p.mt));
+    p.steps = (int)((k + kFwdBK - 1) / kFwdBK);
     p.n_tiles = 0;
     for (int g = 0; g < ngroups; ++g) p.n_tiles += (int)((ns[g] + kFwdBN - 1) / kFwdBN);
-    p.steps = (int)((k + kFwdBK - 1) / kFwdBK);
-    const int64_t tiles = (int64_t)p.m_tiles * p.n_tiles;
-    p.splits = p.steps > 0 ? choose_splits(tiles, p.steps, 1.0) : 1;
-    p.steps_per_split = p.steps > 0 ? (p.steps + p.splits - 1) / p.splits : 0;
-    p.counters = p.splits > 1 ? (int)tiles : 0;
-    p.partial_floats = p.splits > 1 ? tiles * p.splits * (int64_t)(32 * p.mt) * kFwdBN : 0;
-    if (tiles > kMaxSplitTiles || p.partial_floats * 4 >= INT32_MAX) no_split(p);
+    if (!plan_override("DECIK_FWD_PLAN", cand, 4, p.steps, &p.mt, &p.splits)) {
+        const PlanCost pc{32, kFwdBN, kFwdVariants, 4};
+        choose_plan(pc, m, p.n_tiles, p.steps, &p.mt, &p.splits);
+    }
+    p.m_tiles = (int)((m + 32 * p.mt - 1) / (32 * p.mt));
+    finish_plan(p, 32, kFwdBN);
     return p;
 }
 
 GemmPlan plan_bwd(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
     static const int cand[] = {1, 2, 4, 8, 13};
     GemmPlan p{};
-    p.mt = choose_rows(m, 16, cand, 5);
-    p.m_tiles = (int)((m + 16 * p.mt - 1) / (16 * p.mt));
-    p.n_tiles = (int)((k + kBwdBN - 1) / kBwdBN);
     p.steps = 0;
     for (int g = 0; g < ngroups; ++g) p.steps += (int)((ns[g] + kBwdBC - 1) / kBwdBC);
-    const int64_t tiles = (int64_t)p.m_tiles * p.n_tiles;
-    p.splits = p.steps > 0 ? choose_splits(tiles, p.steps, 2.0) : 1;
-    p.steps_per_split = p.steps > 0 ? (p.steps + p.splits - 1) / p.splits : 0;
-    p.counters = p.splits > 1 ? (int)tiles : 0;
-    p.partial_floats = p.splits > 1 ? tiles * p.splits * (int64_t)(16 * p.mt) * kBwdBN : 0;
-    if (tiles > kMaxSplitTiles || p.partial_floats * 4 >= INT32_MAX) no_split(p);
+    p.n_tiles = (int)((k + kBwdBN - 1) / kBwdBN);
+    if (!plan_override("DECIK_BWD_PLAN", cand, 5, p.steps, &p.mt, &p.splits)) {
+        const PlanCost pc{16, kBwdBN, kBwdVariants, 5};
+        choose_plan(pc, m, p.n_tiles, p.steps, &p.mt, &p.splits);
+    }
+    p.m_tiles = (int)((m + 16 * p.mt - 1) / (16 * p.mt));
+    finish_plan(p, 16, kBwdBN);
     return p;
 }
 
@@ -273,12 +317,18 @@ int dk_nf4_linear_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
         if (nested >= 0 && nested != G.w.nested)
             return fail("dk_nf4_linear_fwd: all groups must be nested or all plain");
         nested = G.w.nested;
+        // one statistics slot per row block and step needs 64-wide steps inside one block
+        if (G.w.blocksize < 64 || k % 64 != 0) a.wide_stats = 1;
         if (G.y == nullptr || !aligned(G.y, 16) || G.ldy < G.w.n || (G.ldy % 8) != 0)
             return fail("dk_nf4_linear_fwd: y must be 16-byte aligned with ldy >= n, ldy % 8 == 0");
         if (G.lora_u != nullptr && (lora_rank == 0 || G.lora_b == nullptr))
             return fail("dk_nf4_linear_fwd: LoRA needs lora_rank > 0 and lora_b");
-        if (G.lora_u != nullptr && (!aligned(G.lora_u, 8) || !aligned(G.lora_b, 8)))
-            return fail("dk_nf4_linear_fwd: LoRA operands must be 8-byte aligned");
+        if (G.lora_u != nullptr && (!aligned(G.lora_u, 16) || !aligned(G.lora_b, 16)))
+            return fail("dk_nf4_linear_fwd: LoRA operands must be 16-byte aligned");
+        if (G.lora_u != nullptr && (m * lora_rank * 2 >= INT32_MAX || G.w.n * lora_rank * 2 >= INT32_MAX))
+            return fail("dk_nf4_linear_fwd: LoRA operands larger than 2^31 bytes");
+        if (G.bias != nullptr && !aligned(G.bias, 16))
+            return fail("dk_nf4_linear_fwd: bias must be 16-byte aligned");
         a.g[g].bias = reinterpret_cast<const _Float16*>(G.bias);
         a.g[g].lora_u = reinterpret_cast<const _Float16*>(G.lora_u);
         a.g[g].lora_b = reinterpret_cast<const _Float16*>(G.lora_b);

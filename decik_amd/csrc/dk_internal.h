@@ -50,6 +50,7 @@ struct FwdArgs {
     int32_t ngroups, lora_rank;
     int32_t m_tiles, n_tiles, splits, ksteps, ksteps_per_split;
     int32_t nested;
+    int32_t wide_stats;  // some group has blocksize 32: two statistics slots per lane
     float* partials;
     uint32_t partial_bytes;
     int32_t* counters;

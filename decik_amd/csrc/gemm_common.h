@@ -12,6 +12,15 @@ __device__ __forceinline__ int xcd_logical_id() {
     return (bid & 7) * (nwg >> 3) + (bid >> 3);
 }
 
+// Pin a wave-uniform 32-bit value in an SGPR: the empty asm hides where the value came from, so
+// the compiler can neither re-load it from memory later nor move it to a VGPR.
+template <typename T>
+__device__ __forceinline__ T sgpr(T v) {
+    static_assert(sizeof(T) == 4, "32-bit values only");
+    asm volatile("" : "+s"(v));
+    return v;
+}
+
 __device__ __forceinline__ uint32_t perm_lo(uint32_t lo_src, uint32_t hi_src) {
     // low 16 bits of lo_src, then low 16 bits of hi_src
     return __builtin_amdgcn_perm(hi_src, lo_src, 0x05040100u);

@@ -172,7 +172,7 @@ def linear_backward(items, m, k, dx=None, dx_fp32=False, lora_rank=0):
 def _fusable(x16, packed, qs, bias16):
     k = x16.shape[-1]
     return (fused_ok(qs, k) and x16.is_contiguous() and _aligned(x16) and _aligned(packed)
-            and (bias16 is None or bias16.is_contiguous()))
+            and (bias16 is None or (bias16.is_contiguous() and _aligned(bias16))))
 
 
 class NF4Linear(torch.autograd.Function):

@@ -58,9 +58,9 @@ typedef struct dk_nf4_weight {
  * (U = X.A^T from dk_lora_down, fp16 [m, rank]; B fp16 [n, rank]). */
 typedef struct dk_linear_fwd_group {
     dk_nf4_weight w;
-    const uint16_t* bias;    /* fp16 [n] or NULL                          */
+    const uint16_t* bias;    /* fp16 [n] or NULL (16-byte aligned)         */
     const uint16_t* lora_u;  /* fp16 [m, rank] or NULL (no LoRA term)      */
-    const uint16_t* lora_b;  /* fp16 [n, rank]                            */
+    const uint16_t* lora_b;  /* fp16 [n, rank]; U and B 16-byte aligned    */
     float lora_scale;
     int32_t reserved;
     uint16_t* y;             /* fp16 output, row stride ldy (elements)    */

@@ -63,19 +63,27 @@ def test_backward_fp32_output(device):
     assert torch.equal(dx32.to(torch.float16), dx16)
 
 
-def test_grouped_forward_equals_separate(device):
-    """q, k, v sharing X in one launch = three launches (and the oracle)."""
+@pytest.mark.parametrize("plan", ["2,1", "4,1", "1,3"])
+def test_grouped_forward_equals_separate(plan, device, monkeypatch):
+    """q, k, v sharing X in one launch = three launches with the same plan (bit for bit: the
+    same tile shape and contraction splits give the same fp32 summation order), and each output
+    meets the bar against the oracle with the planner's own choice."""
     from decik_amd.nf4 import linear_forward
 
     x = randn16((830, 1536), seed=1, device=device)
     ws = [make_weight(s, seed=20 + i, device=device) for i, s in
           enumerate([(1536, 1536), (256, 1536), (256, 1536)])]
     bs = [randn16((s[2].shape[0],), seed=30 + i, device=device, std=0.1) for i, s in enumerate(ws)]
-    outs = linear_forward(x, [dict(packed=p, qs=q, bias=b) for (p, q, _), b in zip(ws, bs)])
-    for (p, q, w16), b, o in zip(ws, bs, outs):
+    items = [dict(packed=p, qs=q, bias=b) for (p, q, _), b in zip(ws, bs)]
+    planned = linear_forward(x, items)
+    monkeypatch.setenv("DECIK_FWD_PLAN", plan)
+    outs = linear_forward(x, items)
+    for (p, q, w16), b, o, o2 in zip(ws, bs, outs, planned):
         (single,) = linear_forward(x, [dict(packed=p, qs=q, bias=b)])
         assert torch.equal(o, single)
-        assert_close(o, O.linear_ref(x.cpu().numpy(), w16, b.cpu().numpy()), what="grouped")
+        ref = O.linear_ref(x.cpu().numpy(), w16, b.cpu().numpy())
+        assert_close(o, ref, what="grouped")
+        assert_close(o2, ref, what="grouped, planned")
 
 
 def test_grouped_backward_sums(device):
