@@ -261,11 +261,13 @@ int dk_nf4_dequant_batched(const dk_nf4_weight* ws, uint16_t* const* outs, int c
             a.out[i] = outs[base + i];
             a.nbytes[i] = w->n * w->k / 2;
             a.wg_begin[i] = wg;
-            const int64_t chunks = (a.nbytes[i] + 15) / 16;
-            const int64_t g = (chunks + kDequantThreads - 1) / kDequantThreads;
+            const int64_t span = (int64_t)kDequantThreads * 4 * kDequantUnits;
+            const int64_t g = (a.nbytes[i] + span - 1) / span;
             if (wg + g > INT32_MAX / 2) return fail("dk_nf4_dequant: tensor too large");
             wg += (int)g;
-            a.fast[i] = (w->blocksize % 32 == 0) && aligned(w->packed, 16) && aligned(outs[base + i], 16);
+            a.fast[i] = (w->blocksize % 32 == 0) && log2_exact(w->blocksize) >= 0 &&
+                        (!w->nested || log2_exact(w->blocksize2) >= 0) && aligned(w->packed, 16) &&
+                        aligned(outs[base + i], 16);
             a.count = i + 1;
         }
         a.wg_begin[a.count] = wg;

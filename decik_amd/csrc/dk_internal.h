@@ -7,6 +7,7 @@ namespace dk {
 
 constexpr int kDequantThreads = 256;
 constexpr int kMaxDequantBatch = 8;
+constexpr int kDequantUnits = 8;  // packed dwords per thread
 
 struct DequantArgs {
     NF4Dev w[kMaxDequantBatch];

@@ -1,68 +1,105 @@
 // Standalone NF4 dequantization (HBM-bound): packed uint8 + double-quant statistics -> fp16.
 //
-// Replaces skc_nf4_dequant_kernel (solution/nf4.py:27-48). Each thread owns 16 packed bytes
-// (32 weights; with blocksize % 32 == 0 they share one scale), loads them with one 16-byte
-// load, and writes 64 bytes of fp16 with four 16-byte stores. The 16-entry code book lives in
-// LDS. Several weights can share one launch (dk_nf4_dequant_batched): the grid is the
-// concatenation of each weight's work-groups.
-#include "dk_internal.h"
+// Replaces skc_nf4_dequant_kernel (solution/nf4.py:27-48). A work-group covers
+// kDequantUnits x 256 units of one packed dword (8 weights; with a power-of-two blocksize >= 32
+// a unit lies in one block, so it has one scale). Each thread issues all of its loads first,
+// then unpacks and writes 16 bytes of fp16 per unit with a non-temporal store; consecutive
+// lanes own consecutive units, so every load and store instruction is contiguous per wave. The code book and the code2 table sit in LDS. Loads are buffer
+// loads relative to the work-group's first byte, so offsets stay 32-bit for any tensor size
+// and past-the-end reads give zeros. Several weights can share one launch
+// (dk_nf4_dequant_batched): the grid is the concatenation of each weight's work-groups.
+#include "gemm_common.h"
 
 namespace dk {
 
 __global__ __launch_bounds__(kDequantThreads) void nf4_dequant_kernel(const DequantArgs a) {
     __shared__ float lut[16];
+    __shared__ float c2[256];
     const int tid = threadIdx.x;
     const int bid = blockIdx.x;
-    // pick this work-group's weight (uniform, scalar selects)
-    int wi = 0;
+    int wi = 0;  // this work-group's weight
 #pragma unroll
     for (int j = 1; j < kMaxDequantBatch; ++j)
         if (j < a.count && bid >= a.wg_begin[j]) wi = j;
-    NF4Dev w = a.w[0];
-    uint16_t* out = a.out[0];
-    int64_t nbytes = a.nbytes[0];
-    int wg0 = a.wg_begin[0];
-#pragma unroll
-    for (int j = 1; j < kMaxDequantBatch; ++j)
-        if (j == wi) {
-            w = a.w[j];
-            out = a.out[j];
-            nbytes = a.nbytes[j];
-            wg0 = a.wg_begin[j];
-        }
+    wi = __builtin_amdgcn_readfirstlane(wi);
+    const NF4Dev& w = a.w[wi];
+    const bool nested = w.absmax8 != nullptr;
     if (tid < 16) lut[tid] = w.code[tid];
+    if (nested) c2[tid] = w.code2[tid];
+    const float offset = nested ? *w.offset : 0.0f;
+    const int64_t nbytes = a.nbytes[wi];
+    uint16_t* const out = a.out[wi];
+    constexpr int64_t kSpan = (int64_t)kDequantThreads * 4 * kDequantUnits;  // bytes per work-group
+    const int64_t base = (int64_t)(bid - a.wg_begin[wi]) * kSpan;
     __syncthreads();
 
-    const bool nested = w.absmax8 != nullptr;
-    const float offset = nested ? *w.offset : 0.0f;
-    const int64_t b0 = ((int64_t)(bid - wg0) * kDequantThreads + tid) * 16;
-    if (b0 >= nbytes) return;
-
-    if (a.fast[wi] && b0 + 16 <= nbytes) {
-        const u32x4_t p = __builtin_nontemporal_load((const u32x4_t*)(w.packed + b0));
-        const int64_t blk = block_of(w, 2 * b0);
-        const float s = nested ? block_scale<true>(w, blk, w.code2, offset)
-                               : block_scale<false>(w, blk, w.code2, offset);
-        uint32_t o[16];
-        dequant16(p, s, lut, o);
-        u32x4_t* dst = (u32x4_t*)(out + 2 * b0);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            u32x4_t v = {o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]};
-            __builtin_nontemporal_store(v, dst + q);
-        }
-    } else {
-        // generic path: any even blocksize, unaligned pointers, the tail of the tensor
-        const int64_t end = b0 + 16 < nbytes ? b0 + 16 : nbytes;
-        for (int64_t i = b0; i < end; ++i) {
+    if (!a.fast[wi]) {
+        // generic path: any even blocksize, unaligned pointers
+        const int64_t end = base + kSpan < nbytes ? base + kSpan : nbytes;
+        for (int64_t i = base + tid; i < end; i += kDequantThreads) {
             const int64_t blk = block_of(w, 2 * i);
-            const float s = nested ? block_scale<true>(w, blk, w.code2, offset)
-                                   : block_scale<false>(w, blk, w.code2, offset);
+            const float s = nested ? block_scale<true>(w, blk, c2, offset) : block_scale<false>(w, blk, c2, offset);
             const uint32_t b = w.packed[i];
             const uint32_t v = pack_half2(lut[b >> 4] * s, lut[b & 15u] * s);
             out[2 * i] = (uint16_t)(v & 0xFFFFu);
             out[2 * i + 1] = (uint16_t)(v >> 16);
         }
+        return;
+    }
+
+    // fast path: units of one packed dword (8 weights, one scale) per lane; each load instruction
+    // reads 256 contiguous bytes per wave and each store writes 1 KB contiguous per wave
+    const int64_t left = nbytes - base;  // > 0
+    const uint32_t span = (uint32_t)(left < kSpan ? left : kSpan);
+    const rsrc_t prs = make_rsrc(w.packed + base, span);
+    const uint32_t bs_shift = sgpr((uint32_t)w.bs_shift);
+    const int64_t blk0 = (2 * base) >> bs_shift;  // first block of the work-group
+    const int64_t nblk = (2 * nbytes + w.blocksize - 1) >> bs_shift;
+    const int64_t blk_left = nblk - blk0;
+    const uint32_t blk_span = (uint32_t)(blk_left < (int64_t)INT32_MAX ? blk_left : INT32_MAX);
+    const rsrc_t ars = nested ? make_rsrc(w.absmax8 + blk0, blk_span) : make_rsrc(w.absmaxf + blk0, blk_span * 4u);
+    const uint32_t bs2_shift = sgpr((uint32_t)w.bs2_shift);
+    const int64_t grp0 = nested ? (blk0 >> bs2_shift) : 0;
+    const rsrc_t a2rs = make_rsrc(nested ? w.absmax2 + grp0 : w.absmax2,
+                                  nested ? w.absmax2_bytes - (uint32_t)grp0 * 4u : 0u);
+
+    uint32_t p[kDequantUnits], q[kDequantUnits];
+    float a2[kDequantUnits];
+#pragma unroll
+    for (int u = 0; u < kDequantUnits; ++u) {
+        const uint32_t off = (uint32_t)(u * kDequantThreads + tid) * 4u;  // within the span
+        const bool ok = off + 4u <= span;
+        p[u] = __builtin_amdgcn_raw_buffer_load_b32(prs, (int)(ok ? off : kOOB), 0, 0);
+        const uint32_t rb = (uint32_t)(((2 * (base + off)) >> bs_shift) - blk0);  // block - blk0
+        if (nested) {
+            q[u] = bload8(ars, ok ? rb : kOOB);
+            const uint32_t rg = (uint32_t)(((blk0 + rb) >> bs2_shift) - grp0);
+            a2[u] = bloadf(a2rs, ok ? rg * 4u : kOOB);
+        } else {
+            q[u] = 0;
+            a2[u] = bloadf(ars, ok ? rb * 4u : kOOB);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < kDequantUnits; ++u) {
+        const uint32_t off = (uint32_t)(u * kDequantThreads + tid) * 4u;
+        if (off >= span) break;
+        if (off + 4u > span) {
+            // the tensor's last, partial unit
+            for (int64_t i = base + off; i < nbytes; ++i) {
+                const int64_t blk = block_of(w, 2 * i);
+                const float s = nested ? block_scale<true>(w, blk, c2, offset) : block_scale<false>(w, blk, c2, offset);
+                const uint32_t b = w.packed[i];
+                const uint32_t v = pack_half2(lut[b >> 4] * s, lut[b & 15u] * s);
+                out[2 * i] = (uint16_t)(v & 0xFFFFu);
+                out[2 * i + 1] = (uint16_t)(v >> 16);
+            }
+            break;
+        }
+        const float s = nested ? c2[q[u]] * a2[u] + offset : a2[u];
+        uint32_t o[4];
+        dequant4(p[u], s, lut, o);
+        __builtin_nontemporal_store(u32x4_t{o[0], o[1], o[2], o[3]}, (u32x4_t*)(out + 2 * (base + off)));
     }
 }
 
