@@ -87,25 +87,17 @@ def bench_mlp(steps, warmup, device, n_sets=4):
              "bwd_down": gemm_flops(INTER, HIDDEN), "bwd_gate_up": 2 * gemm_flops(INTER, HIDDEN),
              "swiglu_fwd": 0.0, "swiglu_bwd": 0.0}
 
-    def step(i, ev=None):
+    def step(i):
         L = layers[i % n_sets]
         g, u = L["gate"], L["up"]
         dn = L["down"]
-        rec = (lambda j: ev[j].record()) if ev is not None else (lambda j: None)
-        rec(0)
         gate, up = nf4.linear_forward(x, [dict(packed=g[0], qs=g[1]), dict(packed=u[0], qs=u[1])])
-        rec(1)
         h = swiglu_fwd(gate, up)
-        rec(2)
         (out,) = nf4.linear_forward(h, [dict(packed=dn[0], qs=dn[1])])
-        rec(3)
         gh = nf4.linear_backward([dict(packed=dn[0], qs=dn[1], dy=dy)], M, INTER)
-        rec(4)
         dgate, dup = swiglu_bwd(gh, gate, up, out=(gate, up))
-        rec(5)
         dx = nf4.linear_backward([dict(packed=g[0], qs=g[1], dy=dgate),
                                   dict(packed=u[0], qs=u[1], dy=dup)], M, HIDDEN)
-        rec(6)
         return out, dx
 
     for i in range(warmup):
@@ -120,15 +112,46 @@ def bench_mlp(steps, warmup, device, n_sets=4):
     t1.record()
     torch.cuda.synchronize()
     ms_step = t0.elapsed_time(t1) / steps
-    # per-launch timing: events between the launches, on the launch stream
-    per = {k: [] for k in launches}
-    for i in range(steps):
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(7)]
-        step(i, ev)
+    # Per-launch timing: each launch kind back to back (same inputs as one step, weight sets
+    # rotating), HIP events on the launch stream around the loop. Unlike events between the
+    # launches of one step, this excludes host-side gaps, so the average matches the kernel's
+    # duration in a rocprofv3 kernel trace of this same program.
+    gate0, up0 = nf4.linear_forward(x, [dict(packed=layers[0]["gate"][0], qs=layers[0]["gate"][1]),
+                                        dict(packed=layers[0]["up"][0], qs=layers[0]["up"][1])])
+    h0 = swiglu_fwd(gate0, up0)
+    gh0 = nf4.linear_backward([dict(packed=layers[0]["down"][0], qs=layers[0]["down"][1], dy=dy)], M, INTER)
+    dg0, du0 = swiglu_bwd(gh0, gate0, up0)
+
+    def one(kind, i):
+        L = layers[i % n_sets]
+        g, u, dn = L["gate"], L["up"], L["down"]
+        if kind == "fwd_gate_up":
+            nf4.linear_forward(x, [dict(packed=g[0], qs=g[1]), dict(packed=u[0], qs=u[1])])
+        elif kind == "swiglu_fwd":
+            swiglu_fwd(gate0, up0)
+        elif kind == "fwd_down":
+            nf4.linear_forward(h0, [dict(packed=dn[0], qs=dn[1])])
+        elif kind == "bwd_down":
+            nf4.linear_backward([dict(packed=dn[0], qs=dn[1], dy=dy)], M, INTER)
+        elif kind == "swiglu_bwd":
+            swiglu_bwd(gh0, gate0, up0)
+        else:
+            nf4.linear_backward([dict(packed=g[0], qs=g[1], dy=dg0), dict(packed=u[0], qs=u[1], dy=du0)],
+                                M, HIDDEN)
+
+    per = {}
+    for kind in launches:
+        for i in range(2):
+            one(kind, i)
         torch.cuda.synchronize()
-        for j, k in enumerate(launches):
-            per[k].append(ev[j].elapsed_time(ev[j + 1]))
-    launch_ms = {k: statistics.median(v) for k, v in per.items()}
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(steps):
+            one(kind, i)
+        b.record()
+        torch.cuda.synchronize()
+        per[kind] = a.elapsed_time(b) / steps
+    launch_ms = per
     step_flops = sum(flops.values())
     return dict(ms_step=ms_step, launch_ms=launch_ms, flops=flops, symbol=symbol,
                 step_flops=step_flops)
@@ -242,6 +265,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-dequant", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also convert 128 Mi fp32 values to fp16 three times: one elementwise "
+                         "kernel of known traffic (512 MiB read, 256 MiB written), to scale "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -302,6 +329,13 @@ def main():
                                roofline=dict(bound="hbm", achieved=round(deq["gbs"], 1),
                                              peak=HBM_PEAK_GBS, unit="GB/s",
                                              frac=round(deq["gbs"] / HBM_PEAK_GBS, 4)))
+    if args.copy_probe:
+        src = torch.ones(128 << 20, dtype=torch.float32, device=device)
+        dst = torch.empty(128 << 20, dtype=torch.float16, device=device)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
     else:

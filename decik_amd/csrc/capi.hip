@@ -99,15 +99,15 @@ int pad8(int g) { return (g + 7) & ~7; }
 
 // Launch planning. A plan picks the kernel variant (token rows per tile) and the number of
 // contraction splits by an estimate of the launch time:
-//   rounds(tiles * splits, resident work-groups) * steps per split * step time(variant)
-//   + split-K traffic (every split writes an fp32 tile, the last one reads them back)
-//   + the last arriver's serial read of the other splits' tiles.
+//   full rounds of resident work-groups x steps per split x step time (all slots busy)
+//   + a last, partial round, whose work-groups run faster on less loaded CUs
+//   + the split-K cost, proportional to the fp32 partial tiles written and read back.
 // Resident work-groups per CU and the step times are per-variant constants measured on MI355X
-// (Qwen2.5-shaped launches at M = 830, all CUs busy).
+// (Qwen2.5-1.5B MLP launches at M = 830).
 struct VariantCost {
     int rows_blocks;   // kernel template argument
     int per_cu;        // resident work-groups per CU
-    double step_us;    // time of one 64-wide contraction step of one work-group
+    double step_us;    // one 64-wide contraction step of one work-group, every slot busy
 };
 
 struct PlanCost {
@@ -117,8 +117,8 @@ struct PlanCost {
     int nv;
 };
 
-constexpr double kHbmBytesPerUs = 4.0e6;    // sustained HBM traffic, bytes per microsecond
-constexpr double kSerialBytesPerUs = 1.0e5;  // one work-group's read of other splits' tiles
+constexpr double kPartialUsPerMB = 0.85;  // split-K: write, last-arriver read and sum, per MB
+constexpr double kLightLoad = 0.65;       // step time with few work-groups per CU, relative
 
 double plan_time(const PlanCost& pc, const VariantCost& v, int64_t m, int64_t col_tiles, int steps,
                  int splits) {
@@ -126,13 +126,14 @@ double plan_time(const PlanCost& pc, const VariantCost& v, int64_t m, int64_t co
     const int64_t tiles = ((m + rows - 1) / rows) * col_tiles;
     const int64_t slots = (int64_t)num_cus() * v.per_cu;
     const int per = (steps + splits - 1) / splits;
-    const double rounds = (double)((tiles * splits + slots - 1) / slots);
-    double t = rounds * per * v.step_us;
-    if (splits > 1) {
-        const double tile_bytes = (double)rows * pc.bn * 4.0;
-        t += (double)tiles * splits * tile_bytes * 1.5 / kHbmBytesPerUs;
-        t += (splits - 1) * tile_bytes / kSerialBytesPerUs;
+    const int64_t wgs = tiles * splits;
+    const int64_t full = wgs / slots, rem = wgs - full * slots;
+    double t = (double)full * per * v.step_us;
+    if (rem > 0) {
+        const double load = (double)rem / (double)slots;
+        t += per * v.step_us * (load > kLightLoad ? load : kLightLoad);
     }
+    if (splits > 1) t += (double)wgs * rows * pc.bn * 4.0 * 1e-6 * kPartialUsPerMB;
     return t;
 }
 
@@ -199,8 +200,8 @@ void finish_plan(GemmPlan& p, int unit, int bn) {
     if (tiles > kMaxSplitTiles || p.partial_floats * 4 >= INT32_MAX) no_split(p);
 }
 
-constexpr VariantCost kFwdVariants[] = {{1, 3, 0.55}, {2, 2, 0.85}, {4, 2, 1.30}, {8, 1, 1.60}};
-constexpr VariantCost kBwdVariants[] = {{1, 2, 1.00}, {2, 2, 1.10}, {4, 1, 1.20}, {8, 1, 1.90}, {13, 1, 2.70}};
+constexpr VariantCost kFwdVariants[] = {{1, 3, 2.35}, {2, 2, 2.23}, {4, 2, 3.10}, {8, 1, 2.94}};
+constexpr VariantCost kBwdVariants[] = {{1, 1, 1.31}, {2, 1, 1.59}, {4, 1, 2.60}, {8, 1, 4.08}, {13, 1, 7.50}};
 
 GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
     static const int cand[] = {1, 2, 4, 8};
