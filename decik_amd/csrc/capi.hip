@@ -108,6 +108,7 @@ struct VariantCost {
     int rows_blocks;   // kernel template argument
     int per_cu;        // resident work-groups per CU
     double step_us;    // one 64-wide contraction step of one work-group, every slot busy
+    double lone;       // step time relative to step_us with few work-groups per CU
 };
 
 struct PlanCost {
@@ -117,8 +118,8 @@ struct PlanCost {
     int nv;
 };
 
-constexpr double kPartialUsPerMB = 0.85;  // split-K: write, last-arriver read and sum, per MB
-constexpr double kLightLoad = 0.65;       // step time with few work-groups per CU, relative
+constexpr double kPartialUsPerMB = 0.35;  // split-K: partial slabs written, then read and summed
+constexpr double kReduceLaunchUs = 4.0;   // split-K: the reduction launch
 
 double plan_time(const PlanCost& pc, const VariantCost& v, int64_t m, int64_t col_tiles, int steps,
                  int splits) {
@@ -131,9 +132,9 @@ double plan_time(const PlanCost& pc, const VariantCost& v, int64_t m, int64_t co
     double t = (double)full * per * v.step_us;
     if (rem > 0) {
         const double load = (double)rem / (double)slots;
-        t += per * v.step_us * (load > kLightLoad ? load : kLightLoad);
+        t += per * v.step_us * (load > v.lone ? load : v.lone);
     }
-    if (splits > 1) t += (double)wgs * rows * pc.bn * 4.0 * 1e-6 * kPartialUsPerMB;
+    if (splits > 1) t += (double)splits * m * col_tiles * pc.bn * 4.0 * 1e-6 * kPartialUsPerMB + kReduceLaunchUs;
     return t;
 }
 
@@ -157,21 +158,13 @@ void choose_plan(const PlanCost& pc, int64_t m, int64_t col_tiles, int steps, in
     }
 }
 
-// Workspace layout, the same for every plan: kCounterBytes of tile counters (only ever
-// incremented and reset to zero by the kernels, so they stay zero between calls), then the
-// fp32 partial tiles. A plan-dependent counter region would overlap another plan's partials.
-constexpr int64_t kCounterBytes = 64 * 1024;
-constexpr int kMaxSplitTiles = (int)(kCounterBytes / 4);
-
-int64_t workspace_bytes(const GemmPlan& p) {
-    if (p.splits <= 1) return 0;
-    return kCounterBytes + p.partial_floats * 4;
-}
+// Split-K workspace: the fp32 partial slabs (splits x m x ncols), nothing else. Contents need not
+// be initialised and are dead after the call.
+int64_t workspace_bytes(const GemmPlan& p) { return p.splits > 1 ? p.partial_floats * 4 : 0; }
 
 void no_split(GemmPlan& p) {
     p.splits = 1;
     p.steps_per_split = p.steps;
-    p.counters = 0;
     p.partial_floats = 0;
 }
 
@@ -191,17 +184,16 @@ bool plan_override(const char* var, const int* cand, int ncand, int steps, int* 
     return true;
 }
 
-void finish_plan(GemmPlan& p, int unit, int bn) {
+void finish_plan(GemmPlan& p, int64_t m, int64_t ncols) {
     p.steps_per_split = p.steps > 0 ? (p.steps + p.splits - 1) / p.splits : 0;
     if (p.steps > 0) p.splits = (p.steps + p.steps_per_split - 1) / p.steps_per_split;
-    const int64_t tiles = (int64_t)p.m_tiles * p.n_tiles;
-    p.counters = p.splits > 1 ? (int)tiles : 0;
-    p.partial_floats = p.splits > 1 ? tiles * p.splits * (int64_t)(unit * p.mt) * bn : 0;
-    if (tiles > kMaxSplitTiles || p.partial_floats * 4 >= INT32_MAX) no_split(p);
+    p.partial_floats = p.splits > 1 ? (int64_t)p.splits * m * ncols : 0;
+    if (p.partial_floats * 4 >= (int64_t(1) << 34)) no_split(p);  // 16 GiB: never worth it
 }
 
-constexpr VariantCost kFwdVariants[] = {{1, 3, 2.35}, {2, 2, 2.23}, {4, 2, 3.10}, {8, 1, 2.94}};
-constexpr VariantCost kBwdVariants[] = {{1, 1, 1.31}, {2, 1, 1.59}, {4, 1, 2.60}, {8, 1, 4.08}, {13, 1, 7.50}};
+constexpr VariantCost kFwdVariants[] = {
+    {1, 3, 2.35, 0.65}, {2, 2, 2.23, 0.65}, {4, 2, 3.10, 0.65}, {8, 1, 2.94, 0.85}};
+constexpr VariantCost kBwdVariants[] = {{2, 1, 3.70, 1.0}, {4, 1, 4.10, 1.0}};
 
 GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
     static const int cand[] = {1, 2, 4, 8};
@@ -214,22 +206,24 @@ GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
         choose_plan(pc, m, p.n_tiles, p.steps, &p.mt, &p.splits);
     }
     p.m_tiles = (int)((m + 32 * p.mt - 1) / (32 * p.mt));
-    finish_plan(p, 32, kFwdBN);
+    int64_t ncols = 0;
+    for (int g = 0; g < ngroups; ++g) ncols += ns[g];
+    finish_plan(p, m, ncols);
     return p;
 }
 
 GemmPlan plan_bwd(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
-    static const int cand[] = {1, 2, 4, 8, 13};
+    static const int cand[] = {2, 4};
     GemmPlan p{};
     p.steps = 0;
     for (int g = 0; g < ngroups; ++g) p.steps += (int)((ns[g] + kBwdBC - 1) / kBwdBC);
     p.n_tiles = (int)((k + kBwdBN - 1) / kBwdBN);
-    if (!plan_override("DECIK_BWD_PLAN", cand, 5, p.steps, &p.mt, &p.splits)) {
-        const PlanCost pc{16, kBwdBN, kBwdVariants, 5};
+    if (!plan_override("DECIK_BWD_PLAN", cand, 2, p.steps, &p.mt, &p.splits)) {
+        const PlanCost pc{32, kBwdBN, kBwdVariants, 2};
         choose_plan(pc, m, p.n_tiles, p.steps, &p.mt, &p.splits);
     }
-    p.m_tiles = (int)((m + 16 * p.mt - 1) / (16 * p.mt));
-    finish_plan(p, 16, kBwdBN);
+    p.m_tiles = (int)((m + 32 * p.mt - 1) / (32 * p.mt));
+    finish_plan(p, m, k);
     return p;
 }
 
@@ -311,6 +305,7 @@ int dk_nf4_linear_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
     int64_t ns[kMaxGroups];
     int nested = -1;
     int tile = 0;
+    int64_t ncols = 0;
     for (int g = 0; g < ngroups; ++g) {
         const dk_linear_fwd_group& G = groups[g];
         if (to_dev(&G.w, &a.g[g].w, "dk_nf4_linear_fwd")) return 1;
@@ -339,7 +334,9 @@ int dk_nf4_linear_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
         a.g[g].y = reinterpret_cast<_Float16*>(G.y);
         a.g[g].ldy = G.ldy;
         a.g[g].tile_begin = tile;
+        a.g[g].col_begin = (int32_t)ncols;
         tile += (int)((G.w.n + kFwdBN - 1) / kFwdBN);
+        ncols += G.w.n;
         ns[g] = G.w.n;
     }
     if (m == 0 || tile == 0) return 0;
@@ -361,15 +358,24 @@ int dk_nf4_linear_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
     a.ksteps = p.steps;
     a.ksteps_per_split = p.steps_per_split;
     a.nested = nested;
-    if (need > 0) {
-        a.counters = static_cast<int32_t*>(workspace);
-        a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
-        a.partial_bytes = (uint32_t)(p.partial_floats * 4);
-    }
+    a.ncols = (int32_t)ncols;
+    if (need > 0) a.partials = static_cast<float*>(workspace);
     const int64_t wgs = (int64_t)p.m_tiles * p.n_tiles * p.splits;
-    if (wgs > INT32_MAX / 2) return fail("dk_nf4_linear_fwd: problem too large");
-    return check_hip(launch_fwd(a, p.mt, pad8((int)wgs), static_cast<hipStream_t>(stream)),
-                     "dk_nf4_linear_fwd launch");
+    if (wgs > INT32_MAX / 2 || ncols > INT32_MAX / 2) return fail("dk_nf4_linear_fwd: problem too large");
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    if (check_hip(launch_fwd(a, p.mt, pad8((int)wgs), st), "dk_nf4_linear_fwd launch")) return 1;
+    if (p.splits <= 1) return 0;
+    ReduceArgs r{};
+    r.partials = a.partials;
+    r.slab = m * ncols;
+    r.splits = p.splits;
+    r.m = (int)m;
+    r.ncols = (int)ncols;
+    r.nout = ngroups;
+    r.out_fp32 = 0;
+    for (int g = 0; g < ngroups; ++g)
+        r.o[g] = ReduceOut{groups[g].y, groups[g].ldy, a.g[g].bias, a.g[g].col_begin, (int32_t)ns[g]};
+    return check_hip(launch_splitk_reduce(r, st), "dk_nf4_linear_fwd split-K reduction");
 }
 
 int dk_nf4_linear_bwd(const dk_linear_bwd_group* groups, int ngroups, int64_t m, int64_t k, void* dx,
@@ -402,10 +408,12 @@ int dk_nf4_linear_bwd(const dk_linear_bwd_group* groups, int ngroups, int64_t m,
         nested = G.w.nested;
         if (G.dy == nullptr || !aligned(G.dy, 16) || G.lddy < G.w.n || (G.lddy % 8) != 0)
             return fail("dk_nf4_linear_bwd: dy must be 16-byte aligned with lddy >= n, lddy % 8 == 0");
-        if (G.lora_gu != nullptr && (lora_rank == 0 || G.lora_a == nullptr || !aligned(G.lora_gu, 8)))
-            return fail("dk_nf4_linear_bwd: LoRA needs lora_rank > 0, lora_a and 8-byte aligned gu");
+        if (G.lora_gu != nullptr && (lora_rank == 0 || G.lora_a == nullptr || !aligned(G.lora_gu, 16)))
+            return fail("dk_nf4_linear_bwd: LoRA needs lora_rank > 0, lora_a and 16-byte aligned gu");
+        if (G.lora_gu != nullptr && (m * lora_rank * 2 >= INT32_MAX || k * lora_rank * 2 >= INT32_MAX))
+            return fail("dk_nf4_linear_bwd: LoRA operands larger than 2^31 bytes");
         a.g[g].dy = reinterpret_cast<const _Float16*>(G.dy);
-        a.g[g].lddy = G.lddy;
+        a.g[g].lddy = (int32_t)G.lddy;
         a.g[g].dy_bytes = m > 0 ? (uint32_t)(((m - 1) * G.lddy + G.w.n) * 2) : 0;
         a.g[g].lora_gu = reinterpret_cast<const _Float16*>(G.lora_gu);
         a.g[g].lora_a = reinterpret_cast<const _Float16*>(G.lora_a);
@@ -432,15 +440,22 @@ int dk_nf4_linear_bwd(const dk_linear_bwd_group* groups, int ngroups, int64_t m,
     a.csteps_per_split = p.steps_per_split;
     a.dx_fp32 = dx_fp32 ? 1 : 0;
     a.nested = nested;
-    if (need > 0) {
-        a.counters = static_cast<int32_t*>(workspace);
-        a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
-        a.partial_bytes = (uint32_t)(p.partial_floats * 4);
-    }
+    if (need > 0) a.partials = static_cast<float*>(workspace);
     const int64_t wgs = (int64_t)p.m_tiles * p.n_tiles * p.splits;
     if (wgs > INT32_MAX / 2) return fail("dk_nf4_linear_bwd: problem too large");
-    return check_hip(launch_bwd(a, p.mt, pad8((int)wgs), static_cast<hipStream_t>(stream)),
-                     "dk_nf4_linear_bwd launch");
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    if (check_hip(launch_bwd(a, p.mt, pad8((int)wgs), st), "dk_nf4_linear_bwd launch")) return 1;
+    if (p.splits <= 1) return 0;
+    ReduceArgs r{};
+    r.partials = a.partials;
+    r.slab = m * k;
+    r.splits = p.splits;
+    r.m = (int)m;
+    r.ncols = (int)k;
+    r.nout = 1;
+    r.out_fp32 = dx_fp32 ? 1 : 0;
+    r.o[0] = ReduceOut{dx, lddx, nullptr, 0, (int32_t)k};
+    return check_hip(launch_splitk_reduce(r, st), "dk_nf4_linear_bwd split-K reduction");
 }
 
 int dk_lora_down(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const uint16_t* a, int rank,

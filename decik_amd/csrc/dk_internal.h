@@ -21,14 +21,20 @@ struct DequantArgs {
 __global__ void nf4_dequant_kernel(const DequantArgs a);
 
 // ------------------------------------------------------------------------------------------
-// Fused dequant x GEMM. One work-group = 4 waves. Forward tile: 32*MB rows of X by 256 weight
-// rows (64 per wave); main-loop step 64 along k. Backward tile: 16*MT rows of dY by 256 columns
-// of dX (64 per wave); main-loop step 64 along the contraction (weight rows).
+// Fused dequant x GEMM. Forward: work-group = 4 waves, tile = 32*MB token rows by 256 weight
+// rows (64 per wave), main-loop step 64 along k. Backward: work-group = 8 waves, tile = 32*MB
+// token rows by 512 columns of dX (64 per wave), main-loop step 64 along the contraction
+// (weight rows).
+//
+// Split-K: with splits > 1 each work-group writes its fp32 partial sums (row-major, one slab of
+// m x ncols floats per split) and splitk_reduce_kernel adds the slabs in split order (the same
+// order on every run) and applies the epilogue.
 
 constexpr int kGemmThreads = 256;
 constexpr int kFwdBN = 256;
 constexpr int kFwdBK = 64;
-constexpr int kBwdBN = 256;
+constexpr int kBwdThreads = 512;
+constexpr int kBwdBN = 512;
 constexpr int kBwdBC = 64;
 constexpr int kMaxGroups = DK_MAX_GROUPS;
 
@@ -41,6 +47,7 @@ struct FwdGroupDev {
     int64_t ldy;
     float lora_scale;
     int32_t tile_begin;  // first n-tile of this group in the launch's n-tile space
+    int32_t col_begin;   // first column of this group in the partial slabs
 };
 
 struct FwdArgs {
@@ -51,17 +58,16 @@ struct FwdArgs {
     int32_t ngroups, lora_rank;
     int32_t m_tiles, n_tiles, splits, ksteps, ksteps_per_split;
     int32_t nested;
-    int32_t wide_stats;  // some group has blocksize 32: two statistics slots per lane
-    float* partials;
-    uint32_t partial_bytes;
-    int32_t* counters;
+    int32_t wide_stats;  // some group has blocksize 32 or k % 64 != 0: two statistics slots per lane
+    int32_t ncols;       // columns of a partial slab (sum of the groups' n)
+    float* partials;     // splits x m x ncols fp32 (splits > 1)
     FwdGroupDev g[kMaxGroups];
 };
 
 struct BwdGroupDev {
     NF4Dev w;
     const _Float16* dy;
-    int64_t lddy;
+    int32_t lddy;
     uint32_t dy_bytes;
     const _Float16* lora_gu;
     const _Float16* lora_a;
@@ -77,26 +83,40 @@ struct BwdArgs {
     int32_t m_tiles, k_tiles, splits, csteps, csteps_per_split;
     int32_t dx_fp32;
     int32_t nested;
-    float* partials;
-    uint32_t partial_bytes;
-    int32_t* counters;
+    float* partials;  // splits x m x k fp32 (splits > 1)
     BwdGroupDev g[kMaxGroups];
+};
+
+// Split-K epilogue: out_g[r, c - col_begin_g] = round(sum_s partial[s, r, c] + bias_g[...]).
+struct ReduceOut {
+    void* out;
+    int64_t ld;
+    const _Float16* bias;
+    int32_t col_begin, ncols;
+};
+
+struct ReduceArgs {
+    const float* partials;
+    int64_t slab;  // floats per split slab (m * ncols)
+    int32_t splits, m, ncols, nout;
+    int32_t out_fp32;
+    ReduceOut o[kMaxGroups];
 };
 
 // Launch plans (tile size, split-K factor) chosen by the host.
 struct GemmPlan {
-    int mt;        // 16-row blocks per tile (tile rows = 16 * mt)
+    int mt;        // 32-row token blocks per tile
     int m_tiles;
-    int n_tiles;   // output column tiles (fwd: weight rows / 256; bwd: k / 256)
+    int n_tiles;   // output column tiles (fwd: weight rows / 256; bwd: k / 512)
     int steps;     // main-loop steps over the whole contraction
     int splits;
     int steps_per_split;
-    int64_t partial_floats;  // fp32 partial-tile storage
-    int counters;            // tile counters
+    int64_t partial_floats;  // fp32 partial slabs (splits > 1)
 };
 
 hipError_t launch_fwd(const FwdArgs& a, int mb, int grid, hipStream_t s);
 hipError_t launch_bwd(const BwdArgs& a, int mt, int grid, hipStream_t s);
+hipError_t launch_splitk_reduce(const ReduceArgs& a, hipStream_t s);
 
 // LoRA and SwiGLU helpers.
 hipError_t launch_lora_down(const _Float16* x, int64_t m, int64_t k, int64_t ldx, const _Float16* a,

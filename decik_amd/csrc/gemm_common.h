@@ -70,60 +70,4 @@ struct AccChunks<float16_t> {
     }
 };
 
-// Split-K: every work-group of a tile writes its fp32 partial accumulators (chunk-major, so each
-// store instruction is contiguous across the wave), then bumps the tile's counter. The last one
-// to arrive adds the partials in split order (deterministic), resets the counter for the next
-// launch and returns true; the others return false. Works in place on the accumulators.
-//
-// Cross-XCD visibility without cache-wide maintenance: the partials are written with
-// device-scope stores (sc1: written through the XCD's L2) and read back with device-scope loads
-// (sc1: not served from a possibly stale L2 line); the counter atomic is issued only after the
-// stores have completed (vmcnt(0)). A __threadfence() here would write back and invalidate the
-// whole L2 of the XCD for every work-group.
-constexpr int kCPolDevice = 16;  // cache policy SC1: device scope (gfx940+ encoding)
-
-template <typename V, int NA>
-__device__ __forceinline__ bool splitk_finish(V (&acc)[NA], float* partials, int32_t* counters,
-                                              int tile, int splits, int split, int* flag,
-                                              uint32_t partial_bytes) {
-    using C = AccChunks<V>;
-    const int tid = threadIdx.x;
-    constexpr uint32_t per = (uint32_t)NA * C::n * kGemmThreads * 16;  // bytes per partial
-    const rsrc_t prs = make_rsrc(partials, partial_bytes);
-    const uint32_t base = (uint32_t)tile * (uint32_t)splits * per;
-    const uint32_t mine = base + (uint32_t)split * per;
-#pragma unroll
-    for (int a = 0; a < NA; ++a)
-#pragma unroll
-        for (int q = 0; q < C::n; ++q)
-            __builtin_amdgcn_raw_buffer_store_b128(
-                __builtin_bit_cast(u32x4_t, C::get(acc[a], q)), prs,
-                (int)(mine + ((uint32_t)(a * C::n + q) * kGemmThreads + tid) * 16), 0, kCPolDevice);
-    wait_vmcnt<0>();  // this thread's partial stores have completed
-    __syncthreads();
-    if (tid == 0)
-        *flag = (__hip_atomic_fetch_add(counters + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                 splits - 1);
-    __syncthreads();
-    if (!*flag) return false;
-    // sum in split order (the same order on every run, whichever work-group finishes last)
-#pragma unroll
-    for (int a = 0; a < NA; ++a) {
-#pragma unroll
-        for (int q = 0; q < C::n; ++q) {
-            const uint32_t off = ((uint32_t)(a * C::n + q) * kGemmThreads + tid) * 16;
-            float4_t sum = {0.f, 0.f, 0.f, 0.f};
-            for (int s = 0; s < splits; ++s)
-                sum += s == split ? C::get(acc[a], q)
-                                  : __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                                     prs, (int)(base + (uint32_t)s * per + off),
-                                                                     0, kCPolDevice));
-            C::set(acc[a], q, sum);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    if (tid == 0) __hip_atomic_store(counters + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return true;
-}
-
 }  // namespace dk

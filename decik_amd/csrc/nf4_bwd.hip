@@ -3,32 +3,57 @@
 //
 //     dX[m, k] = sum_g sum_n dY_g[m, n] W_g[n, k]  (+ sum_g GU_g[m, t] A_g[t, k] for LoRA)
 //
-// The contraction runs over weight rows, so the weight must be read transposed: each step the
-// work-group unpacks a 64 x 256 weight tile into LDS (row-major fp16), and every wave reads 8
-// rows x 4 columns per lane (ds_read_b64) and transposes them into MFMA operands with
-// v_perm_b32 (output columns interleaved by 4, so each lane ends with 16 consecutive outputs of
-// one row). dY (BM x 64 fp16) is staged in LDS, double-buffered. Split-K over the contraction
-// with a deterministic last-arriver reduction (gemm_common.h).
+// MFMA v_mfma_f32_32x32x16_f16, fp32 accumulation. The contraction runs over weight rows n, so
+// A = W^T (32 output columns x 16 weight rows) and B = dY^T (16 weight rows x 32 tokens), and
+// D = (dY.W)^T. Work-group = 8 waves (two per SIMD); tile = 32*MB tokens x 512 output columns,
+// 64 columns per wave; main-loop step = 64 weight rows.
+//
+// A operands straight from the packed bytes: lane l (l32 = l % 32, g = l / 32) serves A row
+// l32 of two MFMA column blocks cb = 0, 1, mapped to output column 2 beta + cb of the wave's
+// 64, beta = arow_to_n(l32) -- the high and low nibble of packed byte beta of a row. Its eight
+// contraction slots of slice j are the eight weight rows 32 g + 8 j + e (the permutation
+// freedom of the MFMA sum; dY's B operand uses the same order). With this column order each
+// lane ends with 32 consecutive output columns of one token row.
+//
+// Each wave stages its own packed bytes in LDS transposed to dword-columns ([byte/4][row], a
+// dword = 4 bytes of one row), so a lane reads its eight rows with two 16-byte loads. Row scales
+// (one per row and 32-column half: blocks are 32-aligned in the flat index) are computed one
+// step ahead, one row per lane, and published in a per-wave LDS table. dY tiles (32*MB x 64
+// fp16) are shared by the work-group. All global loads go straight into LDS rings
+// (buffer_load ... lds) issued up to three steps ahead; each step ends with one wait and one
+// barrier. Split-K: fp32 partial slabs reduced by splitk_reduce_kernel.
 #include "gemm_common.h"
 
 namespace dk {
 
-template <int MT, bool NESTED>
-__global__ __launch_bounds__(kGemmThreads, 1) void nf4_bwd_kernel(const BwdArgs a) {
-    constexpr int BM = 16 * MT;
-    constexpr int DBUF = BM * 128;   // bytes of one dY buffer (BM rows x 64 fp16)
-    constexpr int WBUF = 64 * 512;   // bytes of one weight buffer (64 rows x 256 fp16)
-    constexpr int DCH = BM * 8;      // 16-byte chunks per dY tile
-    constexpr int DPT = (DCH + kGemmThreads - 1) / kGemmThreads;
+constexpr int kBwdTableBytes = (16 + 256) * 4;            // per group: code book + code2
+constexpr int kBwdHeader = kMaxGroups * kBwdTableBytes;    // 4352
+constexpr int kBwdPkStride = 72;                           // dwords per dword-column (64 rows + pad)
+constexpr int kBwdPkBytes = 8 * kBwdPkStride * 4;          // 2304: packed, 8 dword-columns
+constexpr int kBwdStatBytes = 1024;                        // codes / absmax: 2 x 256, absmax2: 2 x 256
+constexpr int kBwdWSlot = kBwdPkBytes + kBwdStatBytes;     // 3328
+constexpr int kBwdScaleBytes = 2 * 2 * 64 * 4;             // [parity][half][row] fp32
+
+__host__ __device__ constexpr size_t bwd_smem_bytes(int mb) {
+    return kBwdHeader + 3 * (size_t)(32 * mb * 128) + 8 * (3 * (size_t)kBwdWSlot + kBwdScaleBytes);
+}
+
+template <int MB, bool NESTED>
+__global__ __launch_bounds__(kBwdThreads, 1) void nf4_bwd_kernel(const BwdArgs a) {
+    static_assert(MB % 2 == 0, "the dY tile loader assumes an even MB");
+    constexpr int BM = 32 * MB;
+    constexpr int DBUF = BM * 128;                   // bytes of one dY ring buffer
+    constexpr int DPT = MB / 2;                      // 16-byte dY loads per thread and step
+    constexpr int NL = DPT + 8 + (NESTED ? 4 : 2);   // loads per thread and step
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    uint8_t* ds = smem;
-    uint8_t* wt = smem + 2 * DBUF;
-    float* lut = (float*)(wt + 2 * WBUF);    // [kMaxGroups][16]
-    float* c2 = lut + 16 * kMaxGroups;        // [kMaxGroups][256]
-    int* flag = (int*)(c2 + 256 * kMaxGroups);
+    uint8_t* dring = smem + kBwdHeader;
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int l16 = lane & 15, lg = lane >> 4;
+    const int l32 = lane & 31, g = lane >> 5;
+    const int beta = arow_to_n(l32);      // this lane's packed byte within the wave's 32
+    const int half = beta >> 4;           // ... and its 32-column half (scale)
+    const int bsh = 8 * (beta & 3);       // ... bit offset inside its dword-column
+    const int xsw = (l32 >> 1) & 7;       // LDS swizzle of this lane's dY rows
 
     const int L = xcd_logical_id();
     if (L >= a.m_tiles * a.k_tiles * a.splits) return;
@@ -36,239 +61,251 @@ __global__ __launch_bounds__(kGemmThreads, 1) void nf4_bwd_kernel(const BwdArgs 
     const int rest = L / a.m_tiles;
     const int k_tile = rest % a.k_tiles;
     const int split = rest / a.k_tiles;
-    const int M = a.m, K = a.k;
+    const int M = sgpr(a.m), K = sgpr(a.k);
     const int m0 = m_tile * BM;
-    const int k0 = k_tile * kBwdBN;         // work-group's first output column
-    const int kw0 = k0 + 64 * wave;         // wave's first output column
+    const int kw0 = k_tile * kBwdBN + 64 * wave;  // wave's first output column
     const int cs0 = split * a.csteps_per_split;
     const int cs1 = min(a.csteps, cs0 + a.csteps_per_split);
 
-    // each group's code books (groups may come from different QuantStates)
-#pragma unroll
-    for (int g = 0; g < kMaxGroups; ++g) {
-        if (g >= a.ngroups) break;
-        if (tid < 16) lut[16 * g + tid] = a.g[g].w.code[tid];
-        if constexpr (NESTED) c2[256 * g + tid] = a.g[g].w.code2[tid];
+    // every group's code book and code2 table
+    for (int gg = 0; gg < a.ngroups; ++gg) {
+        float* t = (float*)(smem + gg * kBwdTableBytes);
+        if (tid < 16) t[tid] = a.g[gg].w.code[tid];
+        if (NESTED && tid < 256) t[16 + tid] = a.g[gg].w.code2[tid];
     }
 
-    u32x4_t dr[DPT];
-    u32x4_t wraw[2];
-    uint32_t wq[2];
-    float wa[2];
-    bool wok[2];
-    float woff = 0.0f;
-    int wgi = 0;  // group of the step held in the load registers
-
-    auto load_step = [&](int s) {
-        BwdGroupDev G = a.g[0];
+    uint8_t* wring = dring + 3 * DBUF + wave * (3 * kBwdWSlot);
+    float* scales = (float*)(dring + 3 * DBUF + 8 * 3 * kBwdWSlot + wave * kBwdScaleBytes);
+    auto ring = [&](int t) __attribute__((always_inline)) { return (t - cs0) % 3; };
+    auto group_of_step = [&](int t) __attribute__((always_inline)) {
         int gi = 0;
 #pragma unroll
         for (int i = 1; i < kMaxGroups; ++i)
-            if (i < a.ngroups && s >= a.g[i].step_begin) {
-                G = a.g[i];
-                gi = i;
-            }
-        wgi = gi;
-        const int n0 = (s - G.step_begin) * kBwdBC;
+            if (i < a.ngroups && t >= a.g[i].step_begin) gi = i;
+        return __builtin_amdgcn_readfirstlane(gi);
+    };
+
+    // Loads of step t: the shared dY tile (cooperative), then this wave's packed bytes
+    // (transposed to dword-columns) and its rows' statistics for both 32-column halves.
+    auto load_step = [&](int t) __attribute__((always_inline)) {
+        const int gi = group_of_step(t);
+        const BwdGroupDev& G = a.g[gi];
+        const int n0 = (t - G.step_begin) * kBwdBC;
         const int N = (int)G.w.n;
         const rsrc_t drs = make_rsrc(G.dy, G.dy_bytes);
+        uint8_t* db = dring + ring(t) * DBUF;
 #pragma unroll
-        for (int i = 0; i < DPT; ++i) {
-            const int q = tid + kGemmThreads * i;
-            const int row = q >> 3, c = q & 7;
+        for (int h = 0; h < DPT; ++h) {
+            const int q = tid + kBwdThreads * h;
+            const int row = q >> 3, pc = q & 7;
+            const int c = pc ^ ((row >> 1) & 7);
             const int gm = m0 + row, gn = n0 + 8 * c;
-            const uint32_t off = (q < DCH && gm < M && gn < N) ? (uint32_t)(gm * (int)G.lddy + gn) * 2u : kOOB;
-            dr[i] = bload128(drs, off);
+            bload128_lds(drs, db + (kBwdThreads * h + 64 * wave) * 16,
+                         off_if(gm < M && gn < N, (uint32_t)(gm * G.lddy + gn) * 2u));
         }
+        uint8_t* slot = wring + ring(t) * kBwdWSlot;
         const rsrc_t wrs = make_rsrc(G.w.packed, G.w.packed_bytes);
+        const int row = n0 + lane;  // weight row this lane fetches for
+        const bool rok = row < N;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+            const bool ok = rok && kw0 + 8 * d < K;
+            bload32_lds(wrs, slot + d * kBwdPkStride * 4,
+                        off_if(ok, ((uint32_t)row * (uint32_t)K + (uint32_t)(kw0 + 8 * d)) >> 1));
+        }
         const rsrc_t ars = make_rsrc(NESTED ? (const void*)G.w.absmax8 : (const void*)G.w.absmaxf,
                                      G.w.absmax_bytes);
         const rsrc_t a2rs = make_rsrc(G.w.absmax2, G.w.absmax2_bytes);
+        const uint32_t bs_shift = (uint32_t)G.w.bs_shift, bs2_shift = (uint32_t)G.w.bs2_shift;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int q = tid + kGemmThreads * i;
-            const int row = q >> 3, c = q & 7;
-            const int n = n0 + row, kk = k0 + 32 * c;
-            wok[i] = n < N && kk < K;
-            const uint32_t flat = (uint32_t)n * (uint32_t)K + (uint32_t)kk;
-            const uint32_t blk = flat >> G.w.bs_shift;
-            wraw[i] = bload128(wrs, wok[i] ? flat >> 1 : kOOB);
+        for (int hh = 0; hh < 2; ++hh) {
+            const bool ok = rok && kw0 + 32 * hh < K;
+            const uint32_t blk = ((uint32_t)row * (uint32_t)K + (uint32_t)(kw0 + 32 * hh)) >> bs_shift;
             if constexpr (NESTED) {
-                wq[i] = bload8(ars, wok[i] ? blk : kOOB);
-                wa[i] = bloadf(a2rs, wok[i] ? (blk >> G.w.bs2_shift) * 4u : kOOB);
+                bload8_lds(ars, slot + kBwdPkBytes + 256 * hh, off_if(ok, blk));
+                bload32_lds(a2rs, slot + kBwdPkBytes + 512 + 256 * hh, off_if(ok, (blk >> bs2_shift) * 4u));
             } else {
-                wq[i] = 0;
-                wa[i] = bloadf(ars, wok[i] ? blk * 4u : kOOB);
+                bload32_lds(ars, slot + kBwdPkBytes + 256 * hh, off_if(ok, blk * 4u));
             }
         }
-        woff = NESTED ? *G.w.offset : 0.0f;
     };
-    auto store_step = [&](int buf) {
+    // Row scales of step t (this lane's row, both halves) into the per-wave table. The
+    // statistics were fetched by this same wave, so its own wait suffices (no barrier).
+    auto make_scales = [&](int t) __attribute__((always_inline)) {
+        const int gi = group_of_step(t);
+        const BwdGroupDev& G = a.g[gi];
+        const int row = (t - G.step_begin) * kBwdBC + lane;
+        const uint8_t* slot = wring + ring(t) * kBwdWSlot;
+        const float* c2 = (const float*)(smem + gi * kBwdTableBytes) + 16;
+        const float offset = NESTED ? *G.w.offset : 0.0f;
+        float* dst = scales + ((t - cs0) & 1) * 128;
 #pragma unroll
-        for (int i = 0; i < DPT; ++i) {
-            const int q = tid + kGemmThreads * i;
-            if (q < DCH) {
-                const int row = q >> 3, c = q & 7;
-                *(u32x4_t*)(ds + buf * DBUF + row * 128 + ((c ^ ((row >> 1) & 7)) << 4)) = dr[i];
+        for (int hh = 0; hh < 2; ++hh) {
+            const bool ok = row < (int)G.w.n && kw0 + 32 * hh < K;
+            float sc;
+            if constexpr (NESTED) {
+                const uint32_t q = slot[kBwdPkBytes + 256 * hh + 4 * lane];
+                const float a2 = *(const float*)(slot + kBwdPkBytes + 512 + 256 * hh + 4 * lane);
+                sc = c2[q] * a2 + offset;
+            } else {
+                sc = *(const float*)(slot + kBwdPkBytes + 256 * hh + 4 * lane);
             }
-        }
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int q = tid + kGemmThreads * i;
-            const int row = q >> 3, c = q & 7;
-            float s;
-            if constexpr (NESTED) s = wok[i] ? c2[256 * wgi + wq[i]] * wa[i] + woff : 0.0f;
-            else s = wa[i];
-            uint32_t o[16];
-            dequant16(wraw[i], s, lut + 16 * wgi, o);
-            const int sw = ((row >> 4) & 1) << 3;
-#pragma unroll
-            for (int p = 0; p < 4; ++p)
-                *(u32x4_t*)(wt + buf * WBUF + row * 512 + (((4 * c + p) ^ sw) << 4)) =
-                    u32x4_t{o[4 * p], o[4 * p + 1], o[4 * p + 2], o[4 * p + 3]};
+            dst[64 * hh + lane] = ok ? sc : 0.0f;
         }
     };
 
-    float4_t acc_flat[MT * 4];
-    float4_t (&acc)[MT][4] = *reinterpret_cast<float4_t(*)[MT][4]>(&acc_flat);
+    float16_t acc[MB * 2];  // [token block i][column block cb] at i * 2 + cb
 #pragma unroll
-    for (int t = 0; t < MT * 4; ++t) acc_flat[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < MB * 2; ++t) acc[t] = float16_t{};
 
-    if (cs0 < cs1) load_step(cs0);
-    __syncthreads();  // code books
-    if (cs0 < cs1) store_step(0);
-    __syncthreads();
-
-    for (int s = cs0; s < cs1; ++s) {
-        const int buf = (s - cs0) & 1;
-        const bool more = s + 1 < cs1;
-        if (more) load_step(s + 1);
-        const uint8_t* wb = wt + buf * WBUF;
-        const uint8_t* db = ds + buf * DBUF;
+    // LoRA input-gradient terms GU_g . A_g first (split 0 only; trip count 0 without LoRA).
+    {
+        const int R = split == 0 ? sgpr(a.lora_rank) : 0;
+        for (int gg = 0; gg < a.ngroups; ++gg) {
+            const BwdGroupDev& G = a.g[gg];
+            if (G.lora_gu == nullptr || R == 0) continue;
+            const rsrc_t ars = make_rsrc(G.lora_a, (uint32_t)R * (uint32_t)K * 2u);
+            const rsrc_t grs = make_rsrc(G.lora_gu, (uint32_t)M * (uint32_t)R * 2u);
+            for (int t0 = 0; t0 < R; t0 += 16) {
+                half8_t al[2];
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-            // 8 weight rows x 4 columns per lane -> A operands of 4 interleaved column blocks
-            u32x2_t h[8];
-            const int sw = (lg & 1) << 3;
-            const int chunk = 8 * wave + (l16 >> 1);
+                for (int e = 0; e < 8; ++e) {
+                    const int tr = t0 + 8 * g + e;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int row = 16 * lg + 8 * jj + e;
-                h[e] = *(const u32x2_t*)(wb + row * 512 + ((chunk ^ sw) << 4) + ((l16 & 1) << 3));
-            }
-            half8_t aop[4];
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                uint32_t d[4];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const uint32_t lo = h[2 * q][b >> 1], hi = h[2 * q + 1][b >> 1];
-                    d[q] = (b & 1) ? perm_hi(lo, hi) : perm_lo(lo, hi);
-                }
-                aop[b] = __builtin_bit_cast(half8_t, u32x4_t{d[0], d[1], d[2], d[3]});
-            }
-#pragma unroll
-            for (int i = 0; i < MT; ++i) {
-                const int row = 16 * i + l16;
-                const half8_t bo =
-                    *(const half8_t*)(db + row * 128 + (((2 * lg + jj) ^ ((l16 >> 1) & 7)) << 4));
-#pragma unroll
-                for (int b = 0; b < 4; ++b) acc[i][b] = mfma16x16x32(aop[b], bo, acc[i][b]);
-            }
-        }
-        if (more) store_step(buf ^ 1);
-        __syncthreads();
-    }
-
-    if (a.splits > 1) {
-        const int tile = k_tile * a.m_tiles + m_tile;
-        if (!splitk_finish(acc_flat, a.partials, a.counters, tile, a.splits, split, flag, a.partial_bytes)) return;
-    }
-
-    // ---- epilogue: LoRA input-gradient terms GU_g . A_g, rounding, stores
-    if (a.lora_rank > 0) {
-        const int R = a.lora_rank;
-#pragma unroll
-        for (int g = 0; g < kMaxGroups; ++g) {
-            if (g >= a.ngroups) break;
-            const BwdGroupDev& G = a.g[g];
-            if (G.lora_gu == nullptr) continue;
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                const int kc = kw0 + 4 * l16 + b;
-                for (int t0 = 0; t0 < R; t0 += 16) {
-                    half4_t av;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        av[e] = kc < K ? G.lora_a[(int64_t)(t0 + 4 * lg + e) * K + kc] : (_Float16)0;
-#pragma unroll
-                    for (int i = 0; i < MT; ++i) {
-                        const int m = m0 + 16 * i + l16;
-                        const half4_t gv = m < M ? *(const half4_t*)(G.lora_gu + (int64_t)m * R + t0 + 4 * lg)
-                                                 : half4_t{0, 0, 0, 0};
-                        acc[i][b] = mfma16x16x16(av, gv, acc[i][b]);
+                    for (int cb = 0; cb < 2; ++cb) {
+                        const int col = kw0 + 2 * beta + cb;
+                        al[cb][e] = __builtin_bit_cast(
+                            _Float16, (uint16_t)bload16(ars, off_if(col < K, (uint32_t)(tr * K + col) * 2u)));
                     }
                 }
+#pragma unroll
+                for (int i = 0; i < MB; ++i) {
+                    const int m = m0 + 32 * i + l32;
+                    const half8_t gu = __builtin_bit_cast(
+                        half8_t, bload128(grs, off_if(m < M, (uint32_t)(m * R + t0 + 8 * g) * 2u)));
+#pragma unroll
+                    for (int cb = 0; cb < 2; ++cb) acc[i * 2 + cb] = mfma32x32x16(al[cb], gu, acc[i * 2 + cb]);
+                }
             }
         }
     }
-    const int kb = kw0 + 16 * lg;  // this lane's 16 consecutive output columns: t = 4 r + b
+
+    // Prologue: up to three steps in flight; wait for the first.
+    if (cs0 < cs1) load_step(cs0);
+    if (cs0 + 1 < cs1) load_step(cs0 + 1);
+    if (cs0 + 2 < cs1) load_step(cs0 + 2);
+    if (cs0 + 2 < cs1)
+        wait_vmcnt<2 * NL>();
+    else if (cs0 + 1 < cs1)
+        wait_vmcnt<NL>();
+    else
+        wait_vmcnt<0>();
+    lds_barrier();  // dY(cs0) from every wave, code tables
+    if (cs0 < cs1) make_scales(cs0);
+
+    for (int t = cs0; t < cs1; ++t) {
+        const int gi = group_of_step(t);
+        const float* lut = (const float*)(smem + gi * kBwdTableBytes);
+        const uint8_t* db = dring + ring(t) * DBUF;
+        const uint32_t* pk = (const uint32_t*)(wring + ring(t) * kBwdWSlot) + (beta >> 2) * kBwdPkStride;
+        const float* sc = scales + ((t - cs0) & 1) * 128 + 64 * half;
 #pragma unroll
-    for (int i = 0; i < MT; ++i) {
-        const int m = m0 + 16 * i + l16;
-        if (m >= M) continue;
-        float v[16];
+        for (int j = 0; j < 4; ++j) {
+            const int r0 = 32 * g + 8 * j;  // this lane's eight weight rows r0 .. r0 + 7
+            const u32x4_t d0 = *(const u32x4_t*)(pk + r0), d1 = *(const u32x4_t*)(pk + r0 + 4);
+            const float4_t s0 = *(const float4_t*)(sc + r0), s1 = *(const float4_t*)(sc + r0 + 4);
+            half8_t xf[MB];
 #pragma unroll
-        for (int t = 0; t < 16; ++t) v[t] = acc[i][t & 3][t >> 2];
+            for (int i = 0; i < MB; ++i)
+                xf[i] = *(const half8_t*)(db + (32 * i + l32) * 128 + (((4 * g + j) ^ xsw) << 4));
+            uint32_t hi[4], lo[4];
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                const uint32_t b0 = ((e < 4 ? d0[e] : d1[e - 4]) >> bsh) & 0xFFu;
+                const uint32_t b1 = ((e + 1 < 4 ? d0[e + 1] : d1[e - 3]) >> bsh) & 0xFFu;
+                const float sa = e < 4 ? s0[e] : s1[e - 4], sb = e + 1 < 4 ? s0[e + 1] : s1[e - 3];
+                hi[e >> 1] = pack_half2(lut[b0 >> 4] * sa, lut[b1 >> 4] * sb);
+                lo[e >> 1] = pack_half2(lut[b0 & 15u] * sa, lut[b1 & 15u] * sb);
+            }
+            const half8_t w0 = __builtin_bit_cast(half8_t, u32x4_t{hi[0], hi[1], hi[2], hi[3]});
+            const half8_t w1 = __builtin_bit_cast(half8_t, u32x4_t{lo[0], lo[1], lo[2], lo[3]});
+#pragma unroll
+            for (int i = 0; i < MB; ++i) {
+                acc[i * 2 + 0] = mfma32x32x16(w0, xf[i], acc[i * 2 + 0]);
+                acc[i * 2 + 1] = mfma32x32x16(w1, xf[i], acc[i * 2 + 1]);
+            }
+            __builtin_amdgcn_sched_barrier(0);  // one slice at a time (register bound)
+        }
+        // Step t+1's loads have landed (only step t+2's may be in flight): its row scales can be
+        // made now; after the barrier every wave is done with step t's slots: refill them.
+        if (t + 2 < cs1)
+            wait_vmcnt<NL>();
+        else
+            wait_vmcnt<0>();
+        if (t + 1 < cs1) make_scales(t + 1);
+        lds_barrier();
+        if (t + 3 < cs1) load_step(t + 3);
+    }
+
+    // ---- epilogue: lane (l32, g) holds columns kw0 + 32 g + c, c = 2 r + cb, of token rows
+    // m0 + 32 i + l32 (acc[i * 2 + cb][r]).
+    const int kc = kw0 + 32 * g;
+    if (a.splits > 1) {
+        float* slab = a.partials + (int64_t)split * M * K;
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+            const int m = m0 + 32 * i + l32;
+            if (m >= M) continue;
+            float* dst = slab + (int64_t)m * K + kc;
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                if (kc + 4 * q < K)  // k % 32 == 0: this lane's 32 columns are all in or all out
+                    *(float4_t*)(dst + 4 * q) = float4_t{acc[i * 2][2 * q], acc[i * 2 + 1][2 * q],
+                                                         acc[i * 2][2 * q + 1], acc[i * 2 + 1][2 * q + 1]};
+        }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+        const int m = m0 + 32 * i + l32;
+        if (m >= M || kc >= K) continue;
         if (a.dx_fp32) {
-            float* row = (float*)a.dx + (int64_t)m * a.lddx + kb;
-            if (kb + 16 <= K) {
+            float* dst = (float*)a.dx + (int64_t)m * a.lddx + kc;
 #pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    *(float4_t*)(row + 4 * q) = float4_t{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
-            } else {
-                for (int t = 0; t < 16 && kb + t < K; ++t) row[t] = v[t];
-            }
+            for (int q = 0; q < 8; ++q)
+                *(float4_t*)(dst + 4 * q) = float4_t{acc[i * 2][2 * q], acc[i * 2 + 1][2 * q],
+                                                     acc[i * 2][2 * q + 1], acc[i * 2 + 1][2 * q + 1]};
         } else {
-            _Float16* row = (_Float16*)a.dx + (int64_t)m * a.lddx + kb;
-            uint32_t o[8];
+            _Float16* dst = (_Float16*)a.dx + (int64_t)m * a.lddx + kc;
 #pragma unroll
-            for (int t = 0; t < 8; ++t) o[t] = pack_half2(v[2 * t], v[2 * t + 1]);
-            if (kb + 16 <= K) {
-                *(u32x4_t*)(row) = u32x4_t{o[0], o[1], o[2], o[3]};
-                *(u32x4_t*)(row + 8) = u32x4_t{o[4], o[5], o[6], o[7]};
-            } else {
-                for (int t = 0; t < 16 && kb + t < K; ++t) row[t] = (_Float16)v[t];
-            }
+            for (int q = 0; q < 4; ++q)
+                *(u32x4_t*)(dst + 8 * q) = u32x4_t{
+                    pack_half2(acc[i * 2][4 * q], acc[i * 2 + 1][4 * q]),
+                    pack_half2(acc[i * 2][4 * q + 1], acc[i * 2 + 1][4 * q + 1]),
+                    pack_half2(acc[i * 2][4 * q + 2], acc[i * 2 + 1][4 * q + 2]),
+                    pack_half2(acc[i * 2][4 * q + 3], acc[i * 2 + 1][4 * q + 3])};
         }
     }
 }
 
-// ------------------------------------------------------------------------------------------
-// launch
-
-template <int MT>
-static size_t bwd_smem() { return 2 * (16 * MT) * 128 + 2 * 64 * 512 + (16 + 256) * 4 * kMaxGroups + 16; }
-
-template <int MT, bool NESTED>
+template <int MB, bool NESTED>
 static hipError_t launch_bwd_t(const BwdArgs& a, int grid, hipStream_t s) {
     static bool attr = false;
-    const size_t sm = bwd_smem<MT>();
+    const size_t sm = bwd_smem_bytes(MB);
     if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void*)nf4_bwd_kernel<MT, NESTED>,
+        hipError_t e = hipFuncSetAttribute((const void*)nf4_bwd_kernel<MB, NESTED>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
         if (e != hipSuccess) return e;
         attr = true;
     }
-    hipLaunchKernelGGL((nf4_bwd_kernel<MT, NESTED>), dim3(grid), dim3(kGemmThreads), sm, s, a);
+    hipLaunchKernelGGL((nf4_bwd_kernel<MB, NESTED>), dim3(grid), dim3(kBwdThreads), sm, s, a);
     return hipGetLastError();
 }
 
-
-hipError_t launch_bwd(const BwdArgs& a, int mt, int grid, hipStream_t s) {
+hipError_t launch_bwd(const BwdArgs& a, int mb, int grid, hipStream_t s) {
 #define X(T) \
-    if (mt == T) return a.nested ? launch_bwd_t<T, true>(a, grid, s) : launch_bwd_t<T, false>(a, grid, s);
-    X(1) X(2) X(4) X(8) X(13)
+    if (mb == T) return a.nested ? launch_bwd_t<T, true>(a, grid, s) : launch_bwd_t<T, false>(a, grid, s);
+    X(2) X(4)
 #undef X
     return hipErrorInvalidValue;
 }

@@ -44,6 +44,12 @@ struct NF4Dev {
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 constexpr uint32_t kOOB = 0x80000000u;
 
+// Buffer offset that reads zeros unless `ok`: sets bit 31 (every buffer here is < 2^31 bytes).
+// Written as arithmetic so the compiler keeps one load instead of branching around two.
+__device__ __forceinline__ uint32_t off_if(bool ok, uint32_t off) {
+    return off | ((uint32_t)!ok << 31);
+}
+
 __device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
 }

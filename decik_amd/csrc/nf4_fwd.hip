@@ -28,7 +28,7 @@
 
 namespace dk {
 
-constexpr int kFwdSmemHeader = 2048;  // code book, code2 table, split-K flag; X ring follows
+constexpr int kFwdSmemHeader = 2048;  // code book and code2 table; X ring follows
 
 // Per-wave ring slot of one step: 2 x 1 KB packed bytes, then block statistics in dword slots
 // (codes or fp32 absmax, then absmax2). Narrow layout (every blocksize >= 64 and k % 64 == 0,
@@ -49,7 +49,6 @@ __global__ __launch_bounds__(kGemmThreads, MB <= 4 ? 2 : 1) void nf4_fwd_kernel(
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     float* lut = (float*)smem;  // at LDS address 0: the lookup address is nibble * 4
     float* c2 = lut + 16;
-    int* flag = (int*)(c2 + 256);
     uint8_t* xs = smem + kFwdSmemHeader;
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -109,7 +108,7 @@ __global__ __launch_bounds__(kGemmThreads, MB <= 4 ? 2 : 1) void nf4_fwd_kernel(
             const int c = pc ^ ((row >> 1) & 7);  // the logical k chunk stored at this position
             const int gm = m0 + row, gk = k0 + 8 * c;
             bload128_lds(xrs, xd + (kGemmThreads * h + 64 * wave) * 16,
-                         (gm < M && gk < K) ? (uint32_t)(gm * ldx + gk) * 2u : kOOB);
+                         off_if(gm < M && gk < K, (uint32_t)(gm * ldx + gk) * 2u));
         }
         const int krun = k0 + 32 * g;
         uint8_t* slot = wslot(t);
@@ -118,7 +117,7 @@ __global__ __launch_bounds__(kGemmThreads, MB <= 4 ? 2 : 1) void nf4_fwd_kernel(
             const int row = wrow0 + 32 * b;
             const bool ok = row < N && krun < K;
             bload128_lds(wrs, slot + b * 1024,
-                         ok ? ((uint32_t)row * (uint32_t)K + (uint32_t)krun) >> 1 : kOOB);
+                         off_if(ok, ((uint32_t)row * (uint32_t)K + (uint32_t)krun) >> 1));
         }
         if (!wide) {
             // lane (l32, g) fetches row block g's statistics (one block spans the 64-wide step)
@@ -126,10 +125,10 @@ __global__ __launch_bounds__(kGemmThreads, MB <= 4 ? 2 : 1) void nf4_fwd_kernel(
             const bool ok = row < N && k0 < K;
             const uint32_t blk = ((uint32_t)row * (uint32_t)K + (uint32_t)k0) >> bs_shift;
             if constexpr (NESTED) {
-                bload8_lds(ars, slot + 2048, ok ? blk : kOOB);
-                bload32_lds(a2rs, slot + 2304, ok ? (blk >> bs2_shift) * 4u : kOOB);
+                bload8_lds(ars, slot + 2048, off_if(ok, blk));
+                bload32_lds(a2rs, slot + 2304, off_if(ok, (blk >> bs2_shift) * 4u));
             } else {
-                bload32_lds(ars, slot + 2048, ok ? blk * 4u : kOOB);
+                bload32_lds(ars, slot + 2048, off_if(ok, blk * 4u));
             }
         } else {
 #pragma unroll
@@ -138,10 +137,10 @@ __global__ __launch_bounds__(kGemmThreads, MB <= 4 ? 2 : 1) void nf4_fwd_kernel(
                 const bool ok = row < N && krun < K;
                 const uint32_t blk = ((uint32_t)row * (uint32_t)K + (uint32_t)krun) >> bs_shift;
                 if constexpr (NESTED) {
-                    bload8_lds(ars, slot + 2048 + 256 * b, ok ? blk : kOOB);
-                    bload32_lds(a2rs, slot + 2560 + 256 * b, ok ? (blk >> bs2_shift) * 4u : kOOB);
+                    bload8_lds(ars, slot + 2048 + 256 * b, off_if(ok, blk));
+                    bload32_lds(a2rs, slot + 2560 + 256 * b, off_if(ok, (blk >> bs2_shift) * 4u));
                 } else {
-                    bload32_lds(ars, slot + 2048 + 256 * b, ok ? blk * 4u : kOOB);
+                    bload32_lds(ars, slot + 2048 + 256 * b, off_if(ok, blk * 4u));
                 }
             }
         }
@@ -188,14 +187,14 @@ __global__ __launch_bounds__(kGemmThreads, MB <= 4 ? 2 : 1) void nf4_fwd_kernel(
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
                 const int row = wrow0 + 32 * b;
-                bl[b] = __builtin_bit_cast(half8_t, bload128(brs, row < N ? (uint32_t)(row * R + t0 + 8 * g) * 2u : kOOB));
+                bl[b] = __builtin_bit_cast(half8_t, bload128(brs, off_if(row < N, (uint32_t)(row * R + t0 + 8 * g) * 2u)));
 #pragma unroll
                 for (int e = 0; e < 8; ++e) bl[b][e] = (_Float16)((float)bl[b][e] * ls);
             }
 #pragma unroll
             for (int i = 0; i < MB; ++i) {
                 const int m = m0 + 32 * i + l32;
-                const half8_t uu = __builtin_bit_cast(half8_t, bload128(urs, m < M ? (uint32_t)(m * R + t0 + 8 * g) * 2u : kOOB));
+                const half8_t uu = __builtin_bit_cast(half8_t, bload128(urs, off_if(m < M, (uint32_t)(m * R + t0 + 8 * g) * 2u)));
 #pragma unroll
                 for (int b = 0; b < 2; ++b) acc[i * 2 + b] = mfma32x32x16(bl[b], uu, acc[i * 2 + b]);
             }
@@ -246,9 +245,9 @@ __global__ __launch_bounds__(kGemmThreads, MB <= 4 ? 2 : 1) void nf4_fwd_kernel(
         if (t + 3 < ks1) load_step(t + 3);
     }
 
-    // ---- epilogue: bias, one fp16 rounding, stores. Both paths end in their own copy of the
-    // stores, so the accumulators never meet at a control-flow merge (which makes the register
-    // allocator copy all of them).
+    // ---- epilogue: bias, one fp16 rounding, stores (or, with split-K, the fp32 partial slab).
+    // Both paths end in their own stores, so the accumulators never meet at a control-flow merge
+    // (which makes the register allocator copy all of them).
     auto store = [&]() __attribute__((always_inline)) {
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
@@ -283,8 +282,22 @@ __global__ __launch_bounds__(kGemmThreads, MB <= 4 ? 2 : 1) void nf4_fwd_kernel(
         }
     };
     if (a.splits > 1) {
-        const int tile = n_tile * a.m_tiles + m_tile;
-        if (splitk_finish(acc, a.partials, a.counters, tile, a.splits, split, flag, a.partial_bytes)) store();
+        // fp32 partial sums into this split's slab (bias and rounding happen in the reduction)
+        float* slab = a.partials + (int64_t)split * a.m * a.ncols;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const int nb = nw0 + 32 * b + 16 * g;
+#pragma unroll
+            for (int i = 0; i < MB; ++i) {
+                const int m = m0 + 32 * i + l32;
+                if (m >= M) continue;
+                float* dst = slab + (int64_t)m * a.ncols + G.col_begin + nb;
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (nb + 4 * q < N)  // n % 8 == 0: whole 16-byte chunks
+                        *(float4_t*)(dst + 4 * q) = AccChunks<float16_t>::get(acc[i * 2 + b], q);
+            }
+        }
         return;
     }
     store();

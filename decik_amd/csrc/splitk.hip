@@ -1,0 +1,54 @@
+// Split-K epilogue of the fused GEMMs: sums the per-split fp32 partial slabs in split order
+// (deterministic: the same additions in the same order on every run, whatever order the
+// work-groups of the GEMM ran in), adds the bias, rounds once and stores fp16 (or fp32).
+// One work-group per output row; each thread takes 8 consecutive columns at a time, so every
+// load and store instruction is contiguous across the wave.
+#include "dk_internal.h"
+
+namespace dk {
+
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const ReduceArgs a) {
+    const int row = blockIdx.x;
+    const int chunks = a.ncols >> 3;
+    const float* base = a.partials + (int64_t)row * a.ncols;
+    for (int c = threadIdx.x; c < chunks; c += 256) {
+        const int col = c << 3;
+        float4_t v0 = {0.f, 0.f, 0.f, 0.f}, v1 = v0;
+        for (int s = 0; s < a.splits; ++s) {
+            const float4_t* p = (const float4_t*)(base + s * a.slab + col);
+            v0 += __builtin_nontemporal_load(p);
+            v1 += __builtin_nontemporal_load(p + 1);
+        }
+        int g = 0;
+#pragma unroll
+        for (int i = 1; i < kMaxGroups; ++i)
+            if (i < a.nout && col >= a.o[i].col_begin) g = i;
+        const ReduceOut& o = a.o[g];
+        const int oc = col - o.col_begin;
+        if (o.bias != nullptr) {
+            const half8_t b = *(const half8_t*)(o.bias + oc);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v0[e] += (float)b[e];
+                v1[e] += (float)b[e + 4];
+            }
+        }
+        if (a.out_fp32) {
+            float* dst = (float*)o.out + (int64_t)row * o.ld + oc;
+            *(float4_t*)dst = v0;
+            *(float4_t*)(dst + 4) = v1;
+        } else {
+            _Float16* dst = (_Float16*)o.out + (int64_t)row * o.ld + oc;
+            *(u32x4_t*)dst = u32x4_t{pack_half2(v0[0], v0[1]), pack_half2(v0[2], v0[3]),
+                                     pack_half2(v1[0], v1[1]), pack_half2(v1[2], v1[3])};
+        }
+    }
+}
+
+hipError_t launch_splitk_reduce(const ReduceArgs& a, hipStream_t s) {
+    if (a.m <= 0 || a.ncols <= 0) return hipSuccess;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(a.m), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace dk
