@@ -412,6 +412,7 @@ int dk_nf4_linear_bwd(const dk_linear_bwd_group* groups, int ngroups, int64_t m,
             return fail("dk_nf4_linear_bwd: LoRA needs lora_rank > 0, lora_a and 16-byte aligned gu");
         if (G.lora_gu != nullptr && (m * lora_rank * 2 >= INT32_MAX || k * lora_rank * 2 >= INT32_MAX))
             return fail("dk_nf4_linear_bwd: LoRA operands larger than 2^31 bytes");
+        if (G.w.blocksize < 64 || k % 64 != 0) a.wide_stats = 1;
         a.g[g].dy = reinterpret_cast<const _Float16*>(G.dy);
         a.g[g].lddy = (int32_t)G.lddy;
         a.g[g].dy_bytes = m > 0 ? (uint32_t)(((m - 1) * G.lddy + G.w.n) * 2) : 0;

@@ -83,6 +83,7 @@ struct BwdArgs {
     int32_t m_tiles, k_tiles, splits, csteps, csteps_per_split;
     int32_t dx_fp32;
     int32_t nested;
+    int32_t wide_stats;  // some group has blocksize 32 or k % 64 != 0: one scale per 32 columns
     float* partials;  // splits x m x k fp32 (splits > 1)
     BwdGroupDev g[kMaxGroups];
 };

@@ -15,8 +15,10 @@
 // freedom of the MFMA sum; dY's B operand uses the same order). With this column order each
 // lane ends with 32 consecutive output columns of one token row.
 //
-// Each wave stages its own packed bytes in LDS transposed to dword-columns ([byte/4][row], a
-// dword = 4 bytes of one row), so a lane reads its eight rows with two 16-byte loads. Row scales
+// Each wave stages its own packed bytes in LDS as 8-row groups of 4-row quads per dword-column
+// (a dword = 4 bytes of one row): the global loads stay contiguous along rows (8 rows x 32
+// bytes per instruction) and a lane reads its eight rows of one dword-column with two 16-byte
+// loads. Row scales
 // (one per row and 32-column half: blocks are 32-aligned in the flat index) are computed one
 // step ahead, one row per lane, and published in a per-wave LDS table. dY tiles (32*MB x 64
 // fp16) are shared by the work-group. All global loads go straight into LDS rings
@@ -28,8 +30,8 @@ namespace dk {
 
 constexpr int kBwdTableBytes = (16 + 256) * 4;            // per group: code book + code2
 constexpr int kBwdHeader = kMaxGroups * kBwdTableBytes;    // 4352
-constexpr int kBwdPkStride = 72;                           // dwords per dword-column (64 rows + pad)
-constexpr int kBwdPkBytes = 8 * kBwdPkStride * 4;          // 2304: packed, 8 dword-columns
+constexpr int kBwdPkStride = 72;                           // dwords per 8-row group (64 + pad)
+constexpr int kBwdPkBytes = 8 * kBwdPkStride * 4;          // 2304: packed bytes of 64 rows
 constexpr int kBwdStatBytes = 1024;                        // codes / absmax: 2 x 256, absmax2: 2 x 256
 constexpr int kBwdWSlot = kBwdPkBytes + kBwdStatBytes;     // 3328
 constexpr int kBwdScaleBytes = 2 * 2 * 64 * 4;             // [parity][half][row] fp32
@@ -44,7 +46,8 @@ __global__ __launch_bounds__(kBwdThreads, 1) void nf4_bwd_kernel(const BwdArgs a
     constexpr int BM = 32 * MB;
     constexpr int DBUF = BM * 128;                   // bytes of one dY ring buffer
     constexpr int DPT = MB / 2;                      // 16-byte dY loads per thread and step
-    constexpr int NL = DPT + 8 + (NESTED ? 4 : 2);   // loads per thread and step
+    constexpr int NL = DPT + 8 + (NESTED ? 2 : 1);   // loads per thread and step (narrow; the
+                                                     // wide layout has more: waits stay safe)
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     uint8_t* dring = smem + kBwdHeader;
 
@@ -54,6 +57,9 @@ __global__ __launch_bounds__(kBwdThreads, 1) void nf4_bwd_kernel(const BwdArgs a
     const int half = beta >> 4;           // ... and its 32-column half (scale)
     const int bsh = 8 * (beta & 3);       // ... bit offset inside its dword-column
     const int xsw = (l32 >> 1) & 7;       // LDS swizzle of this lane's dY rows
+    // Narrow statistics (every blocksize >= 64 and k % 64 == 0): a row's 64 wave columns lie in
+    // one block, one scale per row. Wide: one scale per row and 32-column half.
+    const bool wide = a.wide_stats != 0;
 
     const int L = xcd_logical_id();
     if (L >= a.m_tiles * a.k_tiles * a.splits) return;
@@ -105,20 +111,26 @@ __global__ __launch_bounds__(kBwdThreads, 1) void nf4_bwd_kernel(const BwdArgs a
         }
         uint8_t* slot = wring + ring(t) * kBwdWSlot;
         const rsrc_t wrs = make_rsrc(G.w.packed, G.w.packed_bytes);
-        const int row = n0 + lane;  // weight row this lane fetches for
-        const bool rok = row < N;
+        {
+            // instruction d fetches rows 8 d .. 8 d + 7, all 8 dwords (32 contiguous bytes) of
+            // each; lane -> (row quad, dword-column, row) lands at dword 72 d + 32 rq + 4 cg + rho
+            const int rq = lane >> 5, cg = (lane >> 2) & 7, rho = lane & 3;
+            const bool cok = kw0 + 8 * cg < K;
+            const uint32_t cbyte = (uint32_t)((kw0 + 8 * cg) >> 1);
 #pragma unroll
-        for (int d = 0; d < 8; ++d) {
-            const bool ok = rok && kw0 + 8 * d < K;
-            bload32_lds(wrs, slot + d * kBwdPkStride * 4,
-                        off_if(ok, ((uint32_t)row * (uint32_t)K + (uint32_t)(kw0 + 8 * d)) >> 1));
+            for (int d = 0; d < 8; ++d) {
+                const int r = n0 + 8 * d + 4 * rq + rho;
+                bload32_lds(wrs, slot + d * kBwdPkStride * 4,
+                            off_if(cok && r < N, (uint32_t)r * (uint32_t)(K >> 1) + cbyte));
+            }
         }
+        const int row = n0 + lane;  // weight row this lane fetches statistics for
+        const bool rok = row < N;
         const rsrc_t ars = make_rsrc(NESTED ? (const void*)G.w.absmax8 : (const void*)G.w.absmaxf,
                                      G.w.absmax_bytes);
         const rsrc_t a2rs = make_rsrc(G.w.absmax2, G.w.absmax2_bytes);
         const uint32_t bs_shift = (uint32_t)G.w.bs_shift, bs2_shift = (uint32_t)G.w.bs2_shift;
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
+        for (int hh = 0; hh < (wide ? 2 : 1); ++hh) {
             const bool ok = rok && kw0 + 32 * hh < K;
             const uint32_t blk = ((uint32_t)row * (uint32_t)K + (uint32_t)(kw0 + 32 * hh)) >> bs_shift;
             if constexpr (NESTED) {
@@ -139,8 +151,7 @@ __global__ __launch_bounds__(kBwdThreads, 1) void nf4_bwd_kernel(const BwdArgs a
         const float* c2 = (const float*)(smem + gi * kBwdTableBytes) + 16;
         const float offset = NESTED ? *G.w.offset : 0.0f;
         float* dst = scales + ((t - cs0) & 1) * 128;
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
+        for (int hh = 0; hh < (wide ? 2 : 1); ++hh) {
             const bool ok = row < (int)G.w.n && kw0 + 32 * hh < K;
             float sc;
             if constexpr (NESTED) {
@@ -207,12 +218,14 @@ __global__ __launch_bounds__(kBwdThreads, 1) void nf4_bwd_kernel(const BwdArgs a
         const int gi = group_of_step(t);
         const float* lut = (const float*)(smem + gi * kBwdTableBytes);
         const uint8_t* db = dring + ring(t) * DBUF;
-        const uint32_t* pk = (const uint32_t*)(wring + ring(t) * kBwdWSlot) + (beta >> 2) * kBwdPkStride;
-        const float* sc = scales + ((t - cs0) & 1) * 128 + 64 * half;
+        const uint32_t* pk = (const uint32_t*)(wring + ring(t) * kBwdWSlot) + 4 * (beta >> 2);
+        const float* sc = scales + ((t - cs0) & 1) * 128 + (wide ? 64 * half : 0);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int r0 = 32 * g + 8 * j;  // this lane's eight weight rows r0 .. r0 + 7
-            const u32x4_t d0 = *(const u32x4_t*)(pk + r0), d1 = *(const u32x4_t*)(pk + r0 + 4);
+            const int dg = 4 * g + j;       // ... the 8-row group r0 / 8
+            const u32x4_t d0 = *(const u32x4_t*)(pk + kBwdPkStride * dg);
+            const u32x4_t d1 = *(const u32x4_t*)(pk + kBwdPkStride * dg + 32);
             const float4_t s0 = *(const float4_t*)(sc + r0), s1 = *(const float4_t*)(sc + r0 + 4);
             half8_t xf[MB];
 #pragma unroll
