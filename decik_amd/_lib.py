@@ -7,6 +7,7 @@ is no fallback: every entry point raises if the library is missing or returns an
 import ctypes
 import os
 import threading
+import weakref
 
 import torch
 
@@ -40,6 +41,7 @@ class LinearBwdGroup(ctypes.Structure):
 EXPORTS = {
     "dk_nf4_dequant": ([ctypes.POINTER(NF4Weight), c_vp, c_vp], c_i32),
     "dk_nf4_dequant_batched": ([ctypes.POINTER(NF4Weight), ctypes.POINTER(c_vp), c_i32, c_vp], c_i32),
+    "dk_nf4_block_scales": ([ctypes.POINTER(NF4Weight), c_vp, c_vp], c_i32),
     "dk_nf4_linear_fwd_workspace": ([c_i64, c_i64, ctypes.POINTER(c_i64), c_i32], c_i64),
     "dk_nf4_linear_fwd": ([c_vp, c_i64, c_i64, c_i64, ctypes.POINTER(LinearFwdGroup), c_i32, c_i32,
                            c_vp, c_i64, c_vp], c_i32),
@@ -90,8 +92,10 @@ def ptr(t):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
-def weight_desc(packed, qs, device):
-    """NF4Weight of a packed uint8 tensor and its QuantState (fields of solution/nf4.py:70-79)."""
+def weight_desc(packed, qs, device, scales=None):
+    """NF4Weight of a packed uint8 tensor and its QuantState (fields of solution/nf4.py:70-79).
+    With `scales` (fp32 block scales from dk_nf4_block_scales), a nested weight is described as
+    plain with those scales: the same dequantized bits, a shorter path in the fused GEMMs."""
     n, k = (int(s) for s in qs.shape)
     code = qs.code if qs.code.device == device else qs.code.to(device)
     w = NF4Weight()
@@ -101,7 +105,12 @@ def weight_desc(packed, qs, device):
     w.blocksize = int(qs.blocksize)
     w.nested = 1 if qs.nested else 0
     keep = [packed, code]
-    if qs.nested:
+    if scales is not None:
+        w.nested = 0
+        w.absmax = scales.data_ptr()
+        w.blocksize2 = 256
+        keep.append(scales)
+    elif qs.nested:
         w.absmax = qs.absmax.data_ptr()
         w.absmax2 = qs.state2.absmax.data_ptr()
         w.code2 = qs.state2.code.data_ptr()
@@ -118,8 +127,52 @@ def weight_desc(packed, qs, device):
     return w, keep
 
 
+def _version_key(qs):
+    """What the block scales of a nested QuantState depend on: storage and in-place version of
+    each statistics tensor, the offset and the block sizes."""
+    def tk(t):
+        return (t.data_ptr(), t._version) if torch.is_tensor(t) else (float(t),)
+    return (tk(qs.absmax), tk(qs.state2.absmax), tk(qs.state2.code), tk(qs.offset),
+            int(qs.blocksize), int(qs.state2.blocksize), tuple(int(s) for s in qs.shape))
+
+
+class ScaleCache:
+    """fp32 block scales of nested weights (dk_nf4_block_scales), computed once per QuantState
+    and reused while its statistics tensors are unchanged (a frozen QLoRA base weight). An
+    in-place change of any statistics tensor bumps its version and forces a recomputation; the
+    entry goes away with the QuantState."""
+
+    def __init__(self):
+        self._d = {}
+        self._lock = threading.Lock()
+
+    def get(self, packed, qs, device):
+        key, ver = id(qs), _version_key(qs)
+        with self._lock:
+            ent = self._d.get(key)
+        if ent is not None and ent[0] == ver and ent[2]() is qs:
+            return ent[1]
+        n, k = (int(s) for s in qs.shape)
+        nblocks = (n * k + int(qs.blocksize) - 1) // int(qs.blocksize)
+        scales = torch.empty(max(nblocks, 1), dtype=torch.float32, device=device)
+        w, keep = weight_desc(packed, qs, device)
+        check(lib().dk_nf4_block_scales(ctypes.byref(w), scales.data_ptr(), stream_of(device)))
+        del keep
+
+        def drop(_ref, key=key):
+            with self._lock:
+                self._d.pop(key, None)
+
+        with self._lock:
+            self._d[key] = (ver, scales, weakref.ref(qs, drop))
+        return scales
+
+
+SCALES = ScaleCache()
+
+
 class Workspace:
-    """Zero-filled split-K workspaces, one per (device, stream); the kernels leave them zeroed."""
+    """Split-K workspaces (fp32 partial slabs), one per (device, stream), grown on demand."""
 
     def __init__(self):
         self._bufs = {}
@@ -133,7 +186,7 @@ class Workspace:
             buf = self._bufs.get(key)
             if buf is None or buf.numel() < nbytes:
                 size = max(nbytes, 0 if buf is None else 2 * buf.numel())
-                buf = torch.zeros(size, dtype=torch.uint8, device=device)
+                buf = torch.empty(size, dtype=torch.uint8, device=device)
                 self._bufs[key] = buf
         return buf, buf.numel()
 

@@ -118,7 +118,7 @@ struct PlanCost {
     int nv;
 };
 
-constexpr double kPartialUsPerMB = 0.35;  // split-K: partial slabs written, then read and summed
+constexpr double kPartialUsPerMB = 0.45;  // split-K: partial slabs written, then read and summed
 constexpr double kReduceLaunchUs = 4.0;   // split-K: the reduction launch
 
 double plan_time(const PlanCost& pc, const VariantCost& v, int64_t m, int64_t col_tiles, int steps,
@@ -193,7 +193,7 @@ void finish_plan(GemmPlan& p, int64_t m, int64_t ncols) {
 
 constexpr VariantCost kFwdVariants[] = {
     {1, 3, 2.35, 0.65}, {2, 2, 2.23, 0.65}, {4, 2, 3.10, 0.65}, {8, 1, 2.94, 0.85}};
-constexpr VariantCost kBwdVariants[] = {{2, 1, 3.70, 1.0}, {4, 1, 4.10, 1.0}};
+constexpr VariantCost kBwdVariants[] = {{2, 1, 2.60, 1.0}, {4, 1, 3.40, 1.0}};
 
 GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
     static const int cand[] = {1, 2, 4, 8};
@@ -276,6 +276,17 @@ int dk_nf4_dequant_batched(const dk_nf4_weight* ws, uint16_t* const* outs, int c
 
 int dk_nf4_dequant(const dk_nf4_weight* w, uint16_t* out, void* stream) {
     return dk_nf4_dequant_batched(w, &out, 1, stream);
+}
+
+int dk_nf4_block_scales(const dk_nf4_weight* w, float* scales, void* stream) {
+    g_error.clear();
+    NF4Dev d{};
+    if (to_dev(w, &d, "dk_nf4_block_scales")) return 1;
+    const int64_t nblocks = (w->n * w->k + w->blocksize - 1) / w->blocksize;
+    if (nblocks > 0 && scales == nullptr) return fail("dk_nf4_block_scales: null output");
+    if (nblocks / 256 >= INT32_MAX) return fail("dk_nf4_block_scales: tensor too large");
+    return check_hip(launch_block_scales(d, nblocks, scales, static_cast<hipStream_t>(stream)),
+                     "dk_nf4_block_scales launch");
 }
 
 int64_t dk_nf4_linear_fwd_workspace(int64_t m, int64_t k, const int64_t* ns, int ngroups) {

@@ -19,6 +19,7 @@ struct DequantArgs {
 };
 
 __global__ void nf4_dequant_kernel(const DequantArgs a);
+hipError_t launch_block_scales(const NF4Dev& w, int64_t nblocks, float* out, hipStream_t s);
 
 // ------------------------------------------------------------------------------------------
 // Fused dequant x GEMM. Forward: work-group = 4 waves, tile = 32*MB token rows by 256 weight

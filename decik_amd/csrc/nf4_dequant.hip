@@ -103,4 +103,26 @@ __global__ __launch_bounds__(kDequantThreads) void nf4_dequant_kernel(const Dequ
     }
 }
 
+// fp32 scale of every block (solution/nf4.py:37-43): nested
+// fp32(fp32(code2[q] * absmax2[block / blocksize2]) + offset), plain absmax itself. The same two
+// roundings as the dequantization, so a plain-statistics dequantization with these scales gives
+// bit-identical weights.
+__global__ __launch_bounds__(256) void nf4_block_scales_kernel(const NF4Dev w, int64_t nblocks, float* out) {
+    __shared__ float c2[256];
+    const bool nested = w.absmax8 != nullptr;
+    if (nested) c2[threadIdx.x] = w.code2[threadIdx.x];
+    __syncthreads();
+    const float offset = nested ? *w.offset : 0.0f;
+    const int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (b >= nblocks) return;
+    out[b] = nested ? block_scale<true>(w, b, c2, offset) : block_scale<false>(w, b, c2, offset);
+}
+
+hipError_t launch_block_scales(const NF4Dev& w, int64_t nblocks, float* out, hipStream_t s) {
+    if (nblocks <= 0) return hipSuccess;
+    const int64_t grid = (nblocks + 255) / 256;
+    hipLaunchKernelGGL(nf4_block_scales_kernel, dim3((unsigned)grid), dim3(256), 0, s, w, nblocks, out);
+    return hipGetLastError();
+}
+
 }  // namespace dk

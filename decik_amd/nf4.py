@@ -95,6 +95,11 @@ def _rows(x):
     return x.reshape(-1, x.shape[-1])
 
 
+def _scales(packed, qs, device):
+    """Cached fp32 block scales of a nested weight for the fused GEMMs (None for plain ones)."""
+    return _lib.SCALES.get(packed, qs, device) if qs.nested else None
+
+
 def linear_forward(x16, items, lora_rank=0):
     """Fused forward for weights that share x16 [M, K] (fp16, contiguous rows).
 
@@ -113,7 +118,7 @@ def linear_forward(x16, items, lora_rank=0):
         out = it.get("out")
         if out is None:
             out = torch.empty((m, n), dtype=torch.float16, device=dev)
-        w, kp = weight_desc(it["packed"], qs, dev)
+        w, kp = weight_desc(it["packed"], qs, dev, _scales(it["packed"], qs, dev))
         keep += kp
         groups[g].w = w
         bias = it.get("bias")
@@ -149,7 +154,7 @@ def linear_backward(items, m, k, dx=None, dx_fp32=False, lora_rank=0):
     keep, ns = [dx], []
     for g, it in enumerate(items):
         qs = it["qs"]
-        w, kp = weight_desc(it["packed"], qs, dev)
+        w, kp = weight_desc(it["packed"], qs, dev, _scales(it["packed"], qs, dev))
         keep += kp
         dy = _rows(it["dy"])
         groups[g].w = w

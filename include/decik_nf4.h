@@ -11,6 +11,8 @@
  * Reference interfaces replaced (tokha-t/decik, Python + Triton):
  *   dk_nf4_dequant / dk_nf4_dequant_batched  <- skc_nf4_dequant_kernel + dequantize_nf4
  *                                               (solution/nf4.py:27-48, 66-85)
+ *   dk_nf4_block_scales                       <- the scale step of skc_nf4_dequant_kernel
+ *                                               (solution/nf4.py:37-43)
  *   dk_nf4_linear_fwd                         <- NF4Linear.forward = dequantize_nf4 + F.linear
  *                                               (solution/nf4.py:93-96; solution/mlp.py:28-39),
  *                                               with peft's LoRA term added in the epilogue
@@ -86,6 +88,13 @@ int dk_nf4_dequant(const dk_nf4_weight* w, uint16_t* out, void* stream);
 /* The same for `count` weights in one launch (out[i] receives weight i). */
 int dk_nf4_dequant_batched(const dk_nf4_weight* ws, uint16_t* const* outs, int count,
                            void* stream);
+
+/* fp32 scale of every block, scales[ceil(n*k / blocksize)]: the scale computation of
+ * skc_nf4_dequant_kernel (solution/nf4.py:37-43) on its own, with the same two roundings. A
+ * weight described as plain (nested = 0) with absmax = these scales dequantizes to the same
+ * bits; the fused GEMMs run faster on it (one fp32 load per block instead of the code2 /
+ * absmax2 chain), so a caller may compute it once per frozen weight and reuse it. */
+int dk_nf4_block_scales(const dk_nf4_weight* w, float* scales, void* stream);
 
 /* Bytes of workspace dk_nf4_linear_fwd needs for these shapes (0 if none). A workspace must
  * be zero-filled once when allocated; the library leaves it zeroed after every call. Calls

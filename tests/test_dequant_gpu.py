@@ -114,3 +114,24 @@ def test_oracle_state_roundtrip(device):
     packed, qs, _ = make_weight((16, 128), seed=1, device=device)
     q = oracle_state(packed, qs)
     assert q.packed.size == 16 * 128 // 2 and q.absmax.size == 16 * 128 // 64
+
+
+@pytest.mark.parametrize("shape,blocksize", [((1536, 1536), 64), ((256, 2560), 128), ((96, 128), 32),
+                                             ((300, 264), 64)])
+def test_block_scales_bit_exact(shape, blocksize, device):
+    """dk_nf4_block_scales = the scale step of the reference kernel (solution/nf4.py:37-43), and a
+    plain description with those scales dequantizes to the same bits as the nested weight."""
+    import ctypes
+
+    from decik_amd import _lib
+
+    packed, qs, w16 = make_weight(shape, seed=sum(shape) + blocksize, device=device,
+                                  blocksize=blocksize)
+    scales = _lib.SCALES.get(packed, qs, device)
+    ref = O.block_scales(oracle_state(packed, qs))
+    got = scales[: ref.size].cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), ref.astype(np.float32).view(np.uint32))
+    w, keep = _lib.weight_desc(packed, qs, device, scales)
+    out = torch.empty(shape, dtype=torch.float16, device=device)
+    _lib.check(_lib.lib().dk_nf4_dequant(ctypes.byref(w), out.data_ptr(), _lib.stream_of(device)))
+    assert np.array_equal(_bits(out), w16.view(np.uint16).reshape(-1))

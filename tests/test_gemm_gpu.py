@@ -164,3 +164,23 @@ def test_unsupported_k_takes_reference_algorithm(device):
     assert_close(y, O.linear_ref(x.detach().cpu().numpy(), w16), what="odd k")
     ref_dx = O.linear_dx_ref(np.ones((10, 64), np.float16), w16)
     assert_close(x.grad, ref_dx, what="odd k dx")
+
+
+def test_scale_cache_follows_in_place_updates(device):
+    """The fused GEMMs reuse cached block scales of a nested weight; changing a statistics
+    tensor in place (its version counter moves) makes the next call recompute them."""
+    from decik_amd import _lib
+    from decik_amd.nf4 import linear_forward
+    from helpers import oracle_state
+
+    packed, qs, w16 = make_weight((512, 1024), seed=91, device=device)
+    x = randn16((64, 1024), seed=92, device=device)
+    (y1,) = linear_forward(x, [dict(packed=packed, qs=qs)])
+    s1 = _lib.SCALES.get(packed, qs, device)
+    assert _lib.SCALES.get(packed, qs, device) is s1  # a hit
+    qs.state2.absmax.mul_(2.0)
+    (y2,) = linear_forward(x, [dict(packed=packed, qs=qs)])
+    s2 = _lib.SCALES.get(packed, qs, device)
+    assert s2 is not s1 and not torch.equal(y1, y2)
+    w16b = O.dequant_nf4(oracle_state(packed, qs), nthreads=0)
+    assert_close(y2, O.linear_ref(x.cpu().numpy(), w16b), what="after in-place update")
