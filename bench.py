@@ -70,7 +70,23 @@ def make_layers(n_layers, names, device, base_seed=0):
     return layers
 
 
-def bench_mlp(steps, warmup, device, n_sets=4):
+def split_launch(kind):
+    """Whether this launch kind takes the split-K path (then the call is the GEMM kernel plus
+    splitk_reduce_kernel): the library asks for a workspace only then."""
+    import ctypes
+
+    from decik_amd import _lib
+
+    L = _lib.lib()
+    shapes = {"fwd_gate_up": ("fwd", HIDDEN, [INTER, INTER]), "fwd_down": ("fwd", INTER, [HIDDEN]),
+              "bwd_down": ("bwd", INTER, [HIDDEN]), "bwd_gate_up": ("bwd", HIDDEN, [INTER, INTER])}
+    d, k, ns = shapes[kind]
+    arr = (ctypes.c_int64 * len(ns))(*ns)
+    fn = L.dk_nf4_linear_fwd_workspace if d == "fwd" else L.dk_nf4_linear_bwd_workspace
+    return fn(M, k, arr, len(ns)) > 0
+
+
+def bench_mlp(steps, warmup, device, n_sets=4, only=None):
     import torch
 
     from decik_amd import nf4
@@ -80,6 +96,8 @@ def bench_mlp(steps, warmup, device, n_sets=4):
     x = seeded_fp16((M, HIDDEN), 1001, 1.0, device)
     dy = seeded_fp16((M, HIDDEN), 1002, 1e-2, device)
     launches = ["fwd_gate_up", "swiglu_fwd", "fwd_down", "bwd_down", "swiglu_bwd", "bwd_gate_up"]
+    if only is not None:
+        launches = [only]
     symbol = {"fwd_gate_up": "nf4_fwd_kernel", "fwd_down": "nf4_fwd_kernel",
               "bwd_down": "nf4_bwd_kernel", "bwd_gate_up": "nf4_bwd_kernel",
               "swiglu_fwd": "swiglu_fwd_kernel", "swiglu_bwd": "swiglu_bwd_kernel"}
@@ -100,18 +118,20 @@ def bench_mlp(steps, warmup, device, n_sets=4):
                                   dict(packed=u[0], qs=u[1], dy=dup)], M, HIDDEN)
         return out, dx
 
-    for i in range(warmup):
-        step(i)
-    torch.cuda.synchronize()
-    # whole-step timing: K steps between two synchronisations
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    t0.record()
-    for i in range(steps):
-        step(i)
-    t1.record()
-    torch.cuda.synchronize()
-    ms_step = t0.elapsed_time(t1) / steps
+    ms_step = None
+    if only is None:
+        for i in range(warmup):
+            step(i)
+        torch.cuda.synchronize()
+        # whole-step timing: K steps between two synchronisations
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for i in range(steps):
+            step(i)
+        t1.record()
+        torch.cuda.synchronize()
+        ms_step = t0.elapsed_time(t1) / steps
     # Per-launch timing: each launch kind back to back (same inputs as one step, weight sets
     # rotating), HIP events on the launch stream around the loop. Unlike events between the
     # launches of one step, this excludes host-side gaps, so the average matches the kernel's
@@ -247,14 +267,16 @@ def cpu_baseline(sample_steps=3):
                        f"{sec * 1e3:.0f} ms/step")
 
 
-def load_traffic():
-    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 --pmc summary
-    (profiles/traffic.json), or None."""
+def load_traffic(kind):
+    """HBM bytes per call of launch `kind`, from the committed rocprofv3 --pmc FETCH_SIZE /
+    WRITE_SIZE summary (profiles/traffic.json, made with `bench.py --only <kind>`), or None if
+    that summary covers another launch."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:
-            return json.load(f)
-    except (OSError, ValueError):
+            t = json.load(f)
+        return t["bytes_per_call"] if t["launch"] == kind else None
+    except (OSError, ValueError, KeyError, TypeError):
         return None
 
 
@@ -265,6 +287,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-dequant", action="store_true")
+    ap.add_argument("--only", default=None,
+                    choices=["fwd_gate_up", "fwd_down", "bwd_down", "bwd_gate_up"],
+                    help="time only this launch kind (for counter runs); prints its roofline only")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also convert 128 Mi fp32 values to fp16 three times: one elementwise "
                          "kernel of known traffic (512 MiB read, 256 MiB written), to scale "
@@ -288,26 +313,32 @@ def main():
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
 
-    mlp = bench_mlp(args.steps, args.warmup, device)
-    deq = None if args.skip_dequant else bench_dequant(max(args.steps, 10), args.warmup, device)
+    mlp = bench_mlp(args.steps, args.warmup, device, only=args.only)
+    if args.copy_probe:
+        src = torch.ones(128 << 20, dtype=torch.float32, device=device)
+        dst = torch.empty(128 << 20, dtype=torch.float16, device=device)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+    deq = None if (args.skip_dequant or args.only) else bench_dequant(max(args.steps, 10), args.warmup, device)
 
-    # dominant kernel symbol: largest total time per step
-    by_sym = {}
-    for k, ms in mlp["launch_ms"].items():
-        s = mlp["symbol"][k]
-        d = by_sym.setdefault(s, dict(ms=0.0, flops=0.0, launches=0))
-        d["ms"] += ms
-        d["flops"] += mlp["flops"][k]
-        d["launches"] += 1
-    dom = max(by_sym, key=lambda s: by_sym[s]["ms"])
-    d = by_sym[dom]
-    achieved = d["flops"] / (d["ms"] * 1e-3) / 1e12
-    traffic = load_traffic()
-    roofline = dict(kernel=dom, bound="mfma", achieved=round(achieved, 2), peak=FP16_PEAK_TFLOPS,
-                    unit="TFLOP/s", frac=round(achieved / FP16_PEAK_TFLOPS, 4),
-                    flops_per_launch=d["flops"] / d["launches"],
-                    avg_launch_ms=round(d["ms"] / d["launches"], 5),
-                    traffic=None if traffic is None else traffic.get(dom))
+    # Dominant launch: the fused GEMM call with the largest time. Its kernels: the GEMM kernel,
+    # plus splitk_reduce_kernel when the call takes the split-K path. `achieved` = the call's
+    # algorithmic flops / its average duration (HIP events on the launch stream around
+    # back-to-back calls); rocprofv3 lists the same call as the sum of its kernels' durations.
+    gemm = [k for k in mlp["launch_ms"] if mlp["flops"][k]]
+    dom = max(gemm, key=lambda k: mlp["launch_ms"][k])
+    ms = mlp["launch_ms"][dom]
+    achieved = mlp["flops"][dom] / (ms * 1e-3) / 1e12
+    kern = mlp["symbol"][dom] + (" + splitk_reduce_kernel" if split_launch(dom) else "")
+    roofline = dict(kernel=kern, launch=dom, bound="mfma", achieved=round(achieved, 2),
+                    peak=FP16_PEAK_TFLOPS, unit="TFLOP/s", frac=round(achieved / FP16_PEAK_TFLOPS, 4),
+                    flops_per_launch=mlp["flops"][dom], avg_launch_ms=round(ms, 5),
+                    traffic=load_traffic(dom))
+    if args.only is not None:
+        print(json.dumps(dict(only=args.only, roofline=roofline)))
+        return
     value = mlp["step_flops"] / (mlp["ms_step"] * 1e-3) / 1e12
     line = dict(
         metric=METRIC, value=round(value, 2), unit="TFLOP/s", n_gpus=1, steps=args.steps,
@@ -329,13 +360,6 @@ def main():
                                roofline=dict(bound="hbm", achieved=round(deq["gbs"], 1),
                                              peak=HBM_PEAK_GBS, unit="GB/s",
                                              frac=round(deq["gbs"] / HBM_PEAK_GBS, 4)))
-    if args.copy_probe:
-        src = torch.ones(128 << 20, dtype=torch.float32, device=device)
-        dst = torch.empty(128 << 20, dtype=torch.float16, device=device)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
     else:
