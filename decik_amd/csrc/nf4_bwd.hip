@@ -28,8 +28,8 @@
 
 namespace dk {
 
-constexpr int kBwdTableBytes = (16 + 256) * 4;            // per group: code book + code2
-constexpr int kBwdHeader = kMaxGroups * kBwdTableBytes;    // 4352
+constexpr int kBwdTableBytes = 256 * 4;                   // per group: code2 table
+constexpr int kBwdHeader = kMaxGroups * kBwdTableBytes;    // 4096 (code books: static LDS)
 constexpr int kBwdPkStride = 72;                           // dwords per 8-row group (64 + pad)
 constexpr int kBwdPkBytes = 8 * kBwdPkStride * 4;          // 2304: packed bytes of 64 rows
 constexpr int kBwdStatBytes = 1024;                        // codes / absmax: 2 x 256, absmax2: 2 x 256
@@ -55,7 +55,6 @@ __global__ __launch_bounds__(kBwdThreads, 1) void nf4_bwd_kernel(const BwdArgs a
     const int l32 = lane & 31, g = lane >> 5;
     const int beta = arow_to_n(l32);      // this lane's packed byte within the wave's 32
     const int half = beta >> 4;           // ... and its 32-column half (scale)
-    const int bsh = 8 * (beta & 3);       // ... bit offset inside its dword-column
     const int xsw = (l32 >> 1) & 7;       // LDS swizzle of this lane's dY rows
     // Narrow statistics (every blocksize >= 64 and k % 64 == 0): a row's 64 wave columns lie in
     // one block, one scale per row. Wide: one scale per row and 32-column half.
@@ -73,12 +72,14 @@ __global__ __launch_bounds__(kBwdThreads, 1) void nf4_bwd_kernel(const BwdArgs a
     const int cs0 = split * a.csteps_per_split;
     const int cs1 = min(a.csteps, cs0 + a.csteps_per_split);
 
-    // every group's code book and code2 table
+    // every group's code book (static LDS, group g at byte 64 g) and code2 table
+    __shared__ float luts[16 * kMaxGroups];
     for (int gg = 0; gg < a.ngroups; ++gg) {
-        float* t = (float*)(smem + gg * kBwdTableBytes);
-        if (tid < 16) t[tid] = a.g[gg].w.code[tid];
-        if (NESTED && tid < 256) t[16 + tid] = a.g[gg].w.code2[tid];
+        if (tid < 16) luts[16 * gg + tid] = a.g[gg].w.code[tid];
+        if (NESTED && tid < 256) ((float*)(smem + gg * kBwdTableBytes))[tid] = a.g[gg].w.code2[tid];
     }
+    // v_perm selector that gathers byte (beta & 3) of two dwords into the low two bytes
+    const uint32_t bsel = (uint32_t)(beta & 3) | ((uint32_t)((beta & 3) + 4) << 8) | 0x0C0C0000u;
 
     uint8_t* wring = dring + 3 * DBUF + wave * (3 * kBwdWSlot);
     float* scales = (float*)(dring + 3 * DBUF + 8 * 3 * kBwdWSlot + wave * kBwdScaleBytes);
@@ -148,7 +149,7 @@ __global__ __launch_bounds__(kBwdThreads, 1) void nf4_bwd_kernel(const BwdArgs a
         const BwdGroupDev& G = a.g[gi];
         const int row = (t - G.step_begin) * kBwdBC + lane;
         const uint8_t* slot = wring + ring(t) * kBwdWSlot;
-        const float* c2 = (const float*)(smem + gi * kBwdTableBytes) + 16;
+        const float* c2 = (const float*)(smem + gi * kBwdTableBytes);
         const float offset = NESTED ? *G.w.offset : 0.0f;
         float* dst = scales + ((t - cs0) & 1) * 128;
         for (int hh = 0; hh < (wide ? 2 : 1); ++hh) {
@@ -216,7 +217,7 @@ __global__ __launch_bounds__(kBwdThreads, 1) void nf4_bwd_kernel(const BwdArgs a
 
     for (int t = cs0; t < cs1; ++t) {
         const int gi = group_of_step(t);
-        const float* lut = (const float*)(smem + gi * kBwdTableBytes);
+        const uint32_t gbase4 = (uint32_t)(64 * gi) * 0x01010101u;  // code book gi in every byte
         const uint8_t* db = dring + ring(t) * DBUF;
         const uint32_t* pk = (const uint32_t*)(wring + ring(t) * kBwdWSlot) + 4 * (beta >> 2);
         const float* sc = scales + ((t - cs0) & 1) * 128 + (wide ? 64 * half : 0);
@@ -231,14 +232,21 @@ __global__ __launch_bounds__(kBwdThreads, 1) void nf4_bwd_kernel(const BwdArgs a
 #pragma unroll
             for (int i = 0; i < MB; ++i)
                 xf[i] = *(const half8_t*)(db + (32 * i + l32) * 128 + (((4 * g + j) ^ xsw) << 4));
+            // this lane's byte of rows r0 .. r0 + 3 and r0 + 4 .. r0 + 7, gathered into two dwords
+            const uint32_t rb0 = __builtin_amdgcn_perm(d0[1], d0[0], bsel) |
+                                 (__builtin_amdgcn_perm(d0[3], d0[2], bsel) << 16);
+            const uint32_t rb1 = __builtin_amdgcn_perm(d1[1], d1[0], bsel) |
+                                 (__builtin_amdgcn_perm(d1[3], d1[2], bsel) << 16);
+            uint32_t ah0, al0, ah1, al1;
+            nib_addrs(rb0, gbase4, ah0, al0);
+            nib_addrs(rb1, gbase4, ah1, al1);
             uint32_t hi[4], lo[4];
 #pragma unroll
-            for (int e = 0; e < 8; e += 2) {
-                const uint32_t b0 = ((e < 4 ? d0[e] : d1[e - 4]) >> bsh) & 0xFFu;
-                const uint32_t b1 = ((e + 1 < 4 ? d0[e + 1] : d1[e - 3]) >> bsh) & 0xFFu;
-                const float sa = e < 4 ? s0[e] : s1[e - 4], sb = e + 1 < 4 ? s0[e + 1] : s1[e - 3];
-                hi[e >> 1] = pack_half2(lut[b0 >> 4] * sa, lut[b1 >> 4] * sb);
-                lo[e >> 1] = pack_half2(lut[b0 & 15u] * sa, lut[b1 & 15u] * sb);
+            for (int q = 0; q < 2; ++q) {
+                hi[q] = pack_half2(lut_at(luts, ah0, 2 * q) * s0[2 * q], lut_at(luts, ah0, 2 * q + 1) * s0[2 * q + 1]);
+                lo[q] = pack_half2(lut_at(luts, al0, 2 * q) * s0[2 * q], lut_at(luts, al0, 2 * q + 1) * s0[2 * q + 1]);
+                hi[q + 2] = pack_half2(lut_at(luts, ah1, 2 * q) * s1[2 * q], lut_at(luts, ah1, 2 * q + 1) * s1[2 * q + 1]);
+                lo[q + 2] = pack_half2(lut_at(luts, al1, 2 * q) * s1[2 * q], lut_at(luts, al1, 2 * q + 1) * s1[2 * q + 1]);
             }
             const half8_t w0 = __builtin_bit_cast(half8_t, u32x4_t{hi[0], hi[1], hi[2], hi[3]});
             const half8_t w1 = __builtin_bit_cast(half8_t, u32x4_t{lo[0], lo[1], lo[2], lo[3]});

@@ -132,6 +132,32 @@ __device__ __forceinline__ float block_scale(const NF4Dev& w, int64_t block, con
     }
 }
 
+// Code-book lookups with cheap addresses. The kernels keep their 16-entry code books in a static
+// __shared__ array, whose LDS address is a compile-time constant that folds into the ds_read
+// offset; code book g occupies bytes 64 g .. 64 g + 63, so every lookup address fits in a byte.
+// nib_addrs turns a packed dword into two words of such byte addresses (4 * nibble + 64 g):
+// `hi` for the high nibbles of its 4 bytes, `lo` for the low ones; each lookup then costs one
+// v_bfe_u32. The empty asm keeps the compiler from folding the masks back into per-lookup
+// shift-and pairs.
+__device__ __forceinline__ void nib_addrs(uint32_t w, uint32_t gbase4, uint32_t& hi, uint32_t& lo) {
+    hi = ((w >> 2) & 0x3C3C3C3Cu) | gbase4;
+    lo = ((w << 2) & 0x3C3C3C3Cu) | gbase4;
+    asm("" : "+v"(hi), "+v"(lo));
+}
+
+__device__ __forceinline__ float lut_at(const float* lut, uint32_t addrs, int byte) {
+    return *(const float*)((const char*)lut + __builtin_amdgcn_ubfe(addrs, 8 * byte, 8));
+}
+
+// Dequantize 4 packed bytes (8 weights, one scale) with a static-LDS code book (see nib_addrs):
+// dword j = fp16 pair (high nibble of byte j, low nibble of byte j).
+__device__ __forceinline__ void dequant4s(uint32_t word, float s, const float* lut, uint32_t* o) {
+    uint32_t hi, lo;
+    nib_addrs(word, 0u, hi, lo);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = pack_half2(lut_at(lut, hi, j) * s, lut_at(lut, lo, j) * s);
+}
+
 // Dequantize 4 packed bytes (8 weights, one scale) into 4 dwords of fp16 pairs: dword d holds
 // byte d's high-nibble weight in its low half and low-nibble weight in its high half, which is
 // the element order of the unpacked row. `lut` is the 16-entry code book (LDS).

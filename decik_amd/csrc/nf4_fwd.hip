@@ -28,7 +28,7 @@
 
 namespace dk {
 
-constexpr int kFwdSmemHeader = 2048;  // code book and code2 table; X ring follows
+constexpr int kFwdSmemHeader = 1024;  // code2 table; X ring follows (the code book is static LDS)
 
 // Per-wave ring slot of one step: 2 x 1 KB packed bytes, then block statistics in dword slots
 // (codes or fp32 absmax, then absmax2). Narrow layout (every blocksize >= 64 and k % 64 == 0,
@@ -47,8 +47,8 @@ __global__ __launch_bounds__(kGemmThreads, MB <= 4 ? 2 : 1) void nf4_fwd_kernel(
     constexpr int XBUF = BM * 128;             // bytes of one X ring buffer
     constexpr int NL = MB + (NESTED ? 4 : 3);  // loads per step and thread (narrow layout)
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    float* lut = (float*)smem;  // at LDS address 0: the lookup address is nibble * 4
-    float* c2 = lut + 16;
+    __shared__ float lut[16];  // code book (static: its address folds into the lookups)
+    float* c2 = (float*)smem;
     uint8_t* xs = smem + kFwdSmemHeader;
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -166,7 +166,7 @@ __global__ __launch_bounds__(kGemmThreads, MB <= 4 ? 2 : 1) void nf4_fwd_kernel(
     };
     auto unpack8 = [&](uint32_t word, float s) __attribute__((always_inline)) -> half8_t {
         uint32_t o[4];
-        dequant4(word, s, lut, o);
+        dequant4s(word, s, lut, o);
         return __builtin_bit_cast(half8_t, u32x4_t{o[0], o[1], o[2], o[3]});
     };
 
