@@ -105,25 +105,22 @@ int pad8(int g) { return (g + 7) & ~7; }
 // Resident work-groups per CU and the step times are per-variant constants measured on MI355X
 // (Qwen2.5-1.5B MLP launches at M = 830).
 struct VariantCost {
-    int rows_blocks;   // kernel template argument
+    int rows_blocks;   // kernel template argument: token rows per tile / 32
+    int waves;         // work-group waves (backward: 64 output columns each)
+    int bn;            // output columns per tile
     int per_cu;        // resident work-groups per CU
     double step_us;    // one 64-wide contraction step of one work-group, every slot busy
     double lone;       // step time relative to step_us with few work-groups per CU
 };
 
-struct PlanCost {
-    int unit;            // token rows per row block
-    int bn;              // output columns per tile
-    const VariantCost* v;
-    int nv;
-};
-
 constexpr double kPartialUsPerMB = 0.45;  // split-K: partial slabs written, then read and summed
 constexpr double kReduceLaunchUs = 4.0;   // split-K: the reduction launch
+constexpr int kRowUnit = 32;              // token rows per row block
 
-double plan_time(const PlanCost& pc, const VariantCost& v, int64_t m, int64_t col_tiles, int steps,
+// col_tiles: output column tiles of the launch for this variant's tile width.
+double plan_time(const VariantCost& v, int64_t m, int64_t col_tiles, int64_t ncols, int steps,
                  int splits) {
-    const int64_t rows = (int64_t)pc.unit * v.rows_blocks;
+    const int64_t rows = (int64_t)kRowUnit * v.rows_blocks;
     const int64_t tiles = ((m + rows - 1) / rows) * col_tiles;
     const int64_t slots = (int64_t)num_cus() * v.per_cu;
     const int per = (steps + splits - 1) / splits;
@@ -134,28 +131,32 @@ double plan_time(const PlanCost& pc, const VariantCost& v, int64_t m, int64_t co
         const double load = (double)rem / (double)slots;
         t += per * v.step_us * (load > v.lone ? load : v.lone);
     }
-    if (splits > 1) t += (double)splits * m * col_tiles * pc.bn * 4.0 * 1e-6 * kPartialUsPerMB + kReduceLaunchUs;
+    if (splits > 1) t += (double)splits * m * ncols * 4.0 * 1e-6 * kPartialUsPerMB + kReduceLaunchUs;
     return t;
 }
 
-void choose_plan(const PlanCost& pc, int64_t m, int64_t col_tiles, int steps, int* mt, int* splits) {
+// Best (variant, splits) for a launch; col_tiles_of(v) gives the column tiles for variant v.
+template <typename ColTiles>
+const VariantCost* choose_plan(const VariantCost* vs, int nv, int64_t m, int64_t ncols, int steps,
+                               ColTiles col_tiles_of, int* splits) {
     double best = 1e300;
-    *mt = pc.v[0].rows_blocks;
+    const VariantCost* pick = &vs[0];
     *splits = 1;
-    for (int i = 0; i < pc.nv; ++i) {
-        const VariantCost& v = pc.v[i];
+    for (int i = 0; i < nv; ++i) {
+        const VariantCost& v = vs[i];
         const int max_s = steps < 32 ? steps : 32;
         for (int s = 1; s <= (max_s > 0 ? max_s : 1); ++s) {
             const int per = steps > 0 ? (steps + s - 1) / s : 0;
             if (steps > 0 && (steps + per - 1) / per != s) continue;  // s splits must all get work
-            const double t = plan_time(pc, v, m, col_tiles, steps, s);
+            const double t = plan_time(v, m, col_tiles_of(v), ncols, steps, s);
             if (t < best * 0.999) {
                 best = t;
-                *mt = v.rows_blocks;
+                pick = &v;
                 *splits = s;
             }
         }
     }
+    return pick;
 }
 
 // Split-K workspace: the fp32 partial slabs (splits x m x ncols), nothing else. Contents need not
@@ -168,20 +169,21 @@ void no_split(GemmPlan& p) {
     p.partial_floats = 0;
 }
 
-// Tuning hook: DECIK_FWD_PLAN / DECIK_BWD_PLAN = "rows_blocks,splits" forces a plan (both must
-// be valid for the shape: a compiled row-block count and 1 <= splits <= steps). Unset in normal
-// use; read on every call so a sweep can change it between calls.
-bool plan_override(const char* var, const int* cand, int ncand, int steps, int* mt, int* splits) {
+// Tuning hook: DECIK_FWD_PLAN / DECIK_BWD_PLAN = "rows_blocks,splits[,waves]" forces a plan
+// (a compiled variant and 1 <= splits <= steps; waves defaults to the variant list's first match).
+// Unset in normal use; read on every call so a sweep can change it between calls.
+const VariantCost* plan_override(const char* var, const VariantCost* vs, int nv, int steps, int* splits) {
     const char* v = std::getenv(var);
-    if (v == nullptr || *v == 0) return false;
-    int a = 0, b = 0;
-    if (std::sscanf(v, "%d,%d", &a, &b) != 2) return false;
-    bool ok = false;
-    for (int i = 0; i < ncand; ++i) ok |= cand[i] == a;
-    if (!ok || b < 1 || b > (steps > 0 ? steps : 1)) return false;
-    *mt = a;
-    *splits = b;
-    return true;
+    if (v == nullptr || *v == 0) return nullptr;
+    int a = 0, b = 0, w = 0;
+    const int got = std::sscanf(v, "%d,%d,%d", &a, &b, &w);
+    if (got < 2 || b < 1 || b > (steps > 0 ? steps : 1)) return nullptr;
+    for (int i = 0; i < nv; ++i)
+        if (vs[i].rows_blocks == a && (got < 3 || vs[i].waves == w)) {
+            *splits = b;
+            return &vs[i];
+        }
+    return nullptr;
 }
 
 void finish_plan(GemmPlan& p, int64_t m, int64_t ncols) {
@@ -191,38 +193,48 @@ void finish_plan(GemmPlan& p, int64_t m, int64_t ncols) {
     if (p.partial_floats * 4 >= (int64_t(1) << 34)) no_split(p);  // 16 GiB: never worth it
 }
 
-constexpr VariantCost kFwdVariants[] = {
-    {1, 3, 2.35, 0.65}, {2, 2, 2.23, 0.65}, {4, 2, 3.10, 0.65}, {8, 1, 2.94, 0.85}};
-constexpr VariantCost kBwdVariants[] = {{2, 1, 2.60, 1.0}, {4, 1, 3.40, 1.0}};
+constexpr VariantCost kFwdVariants[] = {{1, 4, kFwdBN, 3, 2.35, 0.65},
+                                       {2, 4, kFwdBN, 2, 2.23, 0.65},
+                                       {4, 4, kFwdBN, 2, 3.10, 0.65},
+                                       {8, 4, kFwdBN, 1, 2.94, 0.85}};
+constexpr VariantCost kBwdVariants[] = {{2, 4, 256, 2, 3.20, 0.90},
+                                       {2, 8, 512, 1, 2.60, 1.0},
+                                       {4, 8, 512, 1, 3.40, 1.0}};
 
 GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
-    static const int cand[] = {1, 2, 4, 8};
     GemmPlan p{};
     p.steps = (int)((k + kFwdBK - 1) / kFwdBK);
     p.n_tiles = 0;
-    for (int g = 0; g < ngroups; ++g) p.n_tiles += (int)((ns[g] + kFwdBN - 1) / kFwdBN);
-    if (!plan_override("DECIK_FWD_PLAN", cand, 4, p.steps, &p.mt, &p.splits)) {
-        const PlanCost pc{32, kFwdBN, kFwdVariants, 4};
-        choose_plan(pc, m, p.n_tiles, p.steps, &p.mt, &p.splits);
-    }
-    p.m_tiles = (int)((m + 32 * p.mt - 1) / (32 * p.mt));
     int64_t ncols = 0;
-    for (int g = 0; g < ngroups; ++g) ncols += ns[g];
+    for (int g = 0; g < ngroups; ++g) {
+        p.n_tiles += (int)((ns[g] + kFwdBN - 1) / kFwdBN);
+        ncols += ns[g];
+    }
+    const VariantCost* v = plan_override("DECIK_FWD_PLAN", kFwdVariants, 4, p.steps, &p.splits);
+    if (v == nullptr) {
+        const int64_t nt = p.n_tiles;
+        v = choose_plan(kFwdVariants, 4, m, ncols, p.steps, [nt](const VariantCost&) { return nt; },
+                        &p.splits);
+    }
+    p.mt = v->rows_blocks;
+    p.waves = v->waves;
+    p.m_tiles = (int)((m + kRowUnit * p.mt - 1) / (kRowUnit * p.mt));
     finish_plan(p, m, ncols);
     return p;
 }
 
 GemmPlan plan_bwd(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
-    static const int cand[] = {2, 4};
     GemmPlan p{};
     p.steps = 0;
     for (int g = 0; g < ngroups; ++g) p.steps += (int)((ns[g] + kBwdBC - 1) / kBwdBC);
-    p.n_tiles = (int)((k + kBwdBN - 1) / kBwdBN);
-    if (!plan_override("DECIK_BWD_PLAN", cand, 2, p.steps, &p.mt, &p.splits)) {
-        const PlanCost pc{32, kBwdBN, kBwdVariants, 2};
-        choose_plan(pc, m, p.n_tiles, p.steps, &p.mt, &p.splits);
-    }
-    p.m_tiles = (int)((m + 32 * p.mt - 1) / (32 * p.mt));
+    const VariantCost* v = plan_override("DECIK_BWD_PLAN", kBwdVariants, 3, p.steps, &p.splits);
+    if (v == nullptr)
+        v = choose_plan(kBwdVariants, 3, m, k, p.steps,
+                        [k](const VariantCost& c) { return (k + c.bn - 1) / c.bn; }, &p.splits);
+    p.mt = v->rows_blocks;
+    p.waves = v->waves;
+    p.n_tiles = (int)((k + v->bn - 1) / v->bn);
+    p.m_tiles = (int)((m + kRowUnit * p.mt - 1) / (kRowUnit * p.mt));
     finish_plan(p, m, k);
     return p;
 }
@@ -456,7 +468,7 @@ int dk_nf4_linear_bwd(const dk_linear_bwd_group* groups, int ngroups, int64_t m,
     const int64_t wgs = (int64_t)p.m_tiles * p.n_tiles * p.splits;
     if (wgs > INT32_MAX / 2) return fail("dk_nf4_linear_bwd: problem too large");
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    if (check_hip(launch_bwd(a, p.mt, pad8((int)wgs), st), "dk_nf4_linear_bwd launch")) return 1;
+    if (check_hip(launch_bwd(a, p.mt, p.waves, pad8((int)wgs), st), "dk_nf4_linear_bwd launch")) return 1;
     if (p.splits <= 1) return 0;
     ReduceArgs r{};
     r.partials = a.partials;

@@ -23,8 +23,8 @@ hipError_t launch_block_scales(const NF4Dev& w, int64_t nblocks, float* out, hip
 
 // ------------------------------------------------------------------------------------------
 // Fused dequant x GEMM. Forward: work-group = 4 waves, tile = 32*MB token rows by 256 weight
-// rows (64 per wave), main-loop step 64 along k. Backward: work-group = 8 waves, tile = 32*MB
-// token rows by 512 columns of dX (64 per wave), main-loop step 64 along the contraction
+// rows (64 per wave), main-loop step 64 along k. Backward: work-group = 4 or 8 waves, tile =
+// 32*MB token rows by 64 columns of dX per wave, main-loop step 64 along the contraction
 // (weight rows).
 //
 // Split-K: with splits > 1 each work-group writes its fp32 partial sums (row-major, one slab of
@@ -34,8 +34,6 @@ hipError_t launch_block_scales(const NF4Dev& w, int64_t nblocks, float* out, hip
 constexpr int kGemmThreads = 256;
 constexpr int kFwdBN = 256;
 constexpr int kFwdBK = 64;
-constexpr int kBwdThreads = 512;
-constexpr int kBwdBN = 512;
 constexpr int kBwdBC = 64;
 constexpr int kMaxGroups = DK_MAX_GROUPS;
 
@@ -108,6 +106,7 @@ struct ReduceArgs {
 // Launch plans (tile size, split-K factor) chosen by the host.
 struct GemmPlan {
     int mt;        // 32-row token blocks per tile
+    int waves;     // backward: waves per work-group (64 output columns each)
     int m_tiles;
     int n_tiles;   // output column tiles (fwd: weight rows / 256; bwd: k / 512)
     int steps;     // main-loop steps over the whole contraction
@@ -117,7 +116,7 @@ struct GemmPlan {
 };
 
 hipError_t launch_fwd(const FwdArgs& a, int mb, int grid, hipStream_t s);
-hipError_t launch_bwd(const BwdArgs& a, int mt, int grid, hipStream_t s);
+hipError_t launch_bwd(const BwdArgs& a, int mb, int waves, int grid, hipStream_t s);
 hipError_t launch_splitk_reduce(const ReduceArgs& a, hipStream_t s);
 
 // LoRA and SwiGLU helpers.

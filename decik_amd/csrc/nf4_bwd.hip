@@ -36,16 +36,20 @@ constexpr int kBwdStatBytes = 1024;                        // codes / absmax: 2 
 constexpr int kBwdWSlot = kBwdPkBytes + kBwdStatBytes;     // 3328
 constexpr int kBwdScaleBytes = 2 * 2 * 64 * 4;             // [parity][half][row] fp32
 
-__host__ __device__ constexpr size_t bwd_smem_bytes(int mb) {
-    return kBwdHeader + 3 * (size_t)(32 * mb * 128) + 8 * (3 * (size_t)kBwdWSlot + kBwdScaleBytes);
+__host__ __device__ constexpr size_t bwd_smem_bytes(int mb, int waves) {
+    return kBwdHeader + 3 * (size_t)(32 * mb * 128) + waves * (3 * (size_t)kBwdWSlot + kBwdScaleBytes);
 }
 
-template <int MB, bool NESTED>
-__global__ __launch_bounds__(kBwdThreads, 1) void nf4_bwd_kernel(const BwdArgs a) {
-    static_assert(MB % 2 == 0, "the dY tile loader assumes an even MB");
+// WAVES = 8: one work-group per CU, 512 output columns; WAVES = 4: two per CU, 256 columns (more
+// work-groups for launches with few output tiles).
+template <int MB, int WAVES, bool NESTED>
+__global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void nf4_bwd_kernel(const BwdArgs a) {
+    constexpr int NT = 64 * WAVES;                   // threads
+    constexpr int BN = 64 * WAVES;                   // output columns per tile
     constexpr int BM = 32 * MB;
     constexpr int DBUF = BM * 128;                   // bytes of one dY ring buffer
-    constexpr int DPT = MB / 2;                      // 16-byte dY loads per thread and step
+    constexpr int DPT = BM * 8 / NT;                 // 16-byte dY loads per thread and step
+    static_assert(DPT * NT == BM * 8, "dY tile loader: whole loads per thread");
     constexpr int NL = DPT + 8 + (NESTED ? 2 : 1);   // loads per thread and step (narrow; the
                                                      // wide layout has more: waits stay safe)
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -68,7 +72,7 @@ __global__ __launch_bounds__(kBwdThreads, 1) void nf4_bwd_kernel(const BwdArgs a
     const int split = rest / a.k_tiles;
     const int M = sgpr(a.m), K = sgpr(a.k);
     const int m0 = m_tile * BM;
-    const int kw0 = k_tile * kBwdBN + 64 * wave;  // wave's first output column
+    const int kw0 = k_tile * BN + 64 * wave;  // wave's first output column
     const int cs0 = split * a.csteps_per_split;
     const int cs1 = min(a.csteps, cs0 + a.csteps_per_split);
 
@@ -82,7 +86,7 @@ __global__ __launch_bounds__(kBwdThreads, 1) void nf4_bwd_kernel(const BwdArgs a
     const uint32_t bsel = (uint32_t)(beta & 3) | ((uint32_t)((beta & 3) + 4) << 8) | 0x0C0C0000u;
 
     uint8_t* wring = dring + 3 * DBUF + wave * (3 * kBwdWSlot);
-    float* scales = (float*)(dring + 3 * DBUF + 8 * 3 * kBwdWSlot + wave * kBwdScaleBytes);
+    float* scales = (float*)(dring + 3 * DBUF + WAVES * 3 * kBwdWSlot + wave * kBwdScaleBytes);
     auto ring = [&](int t) __attribute__((always_inline)) { return (t - cs0) % 3; };
     auto group_of_step = [&](int t) __attribute__((always_inline)) {
         int gi = 0;
@@ -103,11 +107,11 @@ __global__ __launch_bounds__(kBwdThreads, 1) void nf4_bwd_kernel(const BwdArgs a
         uint8_t* db = dring + ring(t) * DBUF;
 #pragma unroll
         for (int h = 0; h < DPT; ++h) {
-            const int q = tid + kBwdThreads * h;
+            const int q = tid + NT * h;
             const int row = q >> 3, pc = q & 7;
             const int c = pc ^ ((row >> 1) & 7);
             const int gm = m0 + row, gn = n0 + 8 * c;
-            bload128_lds(drs, db + (kBwdThreads * h + 64 * wave) * 16,
+            bload128_lds(drs, db + (NT * h + 64 * wave) * 16,
                          off_if(gm < M && gn < N, (uint32_t)(gm * G.lddy + gn) * 2u));
         }
         uint8_t* slot = wring + ring(t) * kBwdWSlot;
@@ -309,24 +313,26 @@ __global__ __launch_bounds__(kBwdThreads, 1) void nf4_bwd_kernel(const BwdArgs a
     }
 }
 
-template <int MB, bool NESTED>
+template <int MB, int WAVES, bool NESTED>
 static hipError_t launch_bwd_t(const BwdArgs& a, int grid, hipStream_t s) {
     static bool attr = false;
-    const size_t sm = bwd_smem_bytes(MB);
+    const size_t sm = bwd_smem_bytes(MB, WAVES);
     if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void*)nf4_bwd_kernel<MB, NESTED>,
+        hipError_t e = hipFuncSetAttribute((const void*)nf4_bwd_kernel<MB, WAVES, NESTED>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
         if (e != hipSuccess) return e;
         attr = true;
     }
-    hipLaunchKernelGGL((nf4_bwd_kernel<MB, NESTED>), dim3(grid), dim3(kBwdThreads), sm, s, a);
+    hipLaunchKernelGGL((nf4_bwd_kernel<MB, WAVES, NESTED>), dim3(grid), dim3(64 * WAVES), sm, s, a);
     return hipGetLastError();
 }
 
-hipError_t launch_bwd(const BwdArgs& a, int mb, int grid, hipStream_t s) {
-#define X(T) \
-    if (mb == T) return a.nested ? launch_bwd_t<T, true>(a, grid, s) : launch_bwd_t<T, false>(a, grid, s);
-    X(2) X(4)
+// variant: (token row blocks, waves) -- see kBwdVariants in capi.hip
+hipError_t launch_bwd(const BwdArgs& a, int mb, int waves, int grid, hipStream_t s) {
+#define X(T, W)                                                                                  \
+    if (mb == T && waves == W)                                                                   \
+        return a.nested ? launch_bwd_t<T, W, true>(a, grid, s) : launch_bwd_t<T, W, false>(a, grid, s);
+    X(2, 4) X(2, 8) X(4, 8)
 #undef X
     return hipErrorInvalidValue;
 }
