@@ -97,7 +97,9 @@ __global__ __launch_bounds__(kGemmThreads, MB <= 4 ? 2 : 1) void nf4_fwd_kernel(
     auto wslot = [&](int t) -> uint8_t* { return wring + ring(t) * wslot_bytes; };
 
     // Loads of step t: the X tile, then this wave's packed weights and statistics.
-    auto load_step = [&](int t) __attribute__((always_inline)) {
+    // `live` false: every load reads zeros (a step past the split's end keeps the ring's load
+    // count uniform without a branch).
+    auto load_step = [&](int t, bool live) __attribute__((always_inline)) {
         const int k0 = t * kFwdBK;
         uint8_t* xd = xbuf(t);
 #pragma unroll
@@ -108,21 +110,21 @@ __global__ __launch_bounds__(kGemmThreads, MB <= 4 ? 2 : 1) void nf4_fwd_kernel(
             const int c = pc ^ ((row >> 1) & 7);  // the logical k chunk stored at this position
             const int gm = m0 + row, gk = k0 + 8 * c;
             bload128_lds(xrs, xd + (kGemmThreads * h + 64 * wave) * 16,
-                         off_if(gm < M && gk < K, (uint32_t)(gm * ldx + gk) * 2u));
+                         off_if(live && gm < M && gk < K, (uint32_t)(gm * ldx + gk) * 2u));
         }
         const int krun = k0 + 32 * g;
         uint8_t* slot = wslot(t);
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             const int row = wrow0 + 32 * b;
-            const bool ok = row < N && krun < K;
+            const bool ok = live && row < N && krun < K;
             bload128_lds(wrs, slot + b * 1024,
                          off_if(ok, ((uint32_t)row * (uint32_t)K + (uint32_t)krun) >> 1));
         }
         if (!wide) {
             // lane (l32, g) fetches row block g's statistics (one block spans the 64-wide step)
             const int row = wrow0 + 32 * g;
-            const bool ok = row < N && k0 < K;
+            const bool ok = live && row < N && k0 < K;
             const uint32_t blk = ((uint32_t)row * (uint32_t)K + (uint32_t)k0) >> bs_shift;
             if constexpr (NESTED) {
                 bload8_lds(ars, slot + 2048, off_if(ok, blk));
@@ -134,7 +136,7 @@ __global__ __launch_bounds__(kGemmThreads, MB <= 4 ? 2 : 1) void nf4_fwd_kernel(
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
                 const int row = wrow0 + 32 * b;
-                const bool ok = row < N && krun < K;
+                const bool ok = live && row < N && krun < K;
                 const uint32_t blk = ((uint32_t)row * (uint32_t)K + (uint32_t)krun) >> bs_shift;
                 if constexpr (NESTED) {
                     bload8_lds(ars, slot + 2048 + 256 * b, off_if(ok, blk));
@@ -201,49 +203,123 @@ __global__ __launch_bounds__(kGemmThreads, MB <= 4 ? 2 : 1) void nf4_fwd_kernel(
         }
     }
 
-    // Prologue: up to three steps in flight; wait for the first.
-    load_step(ks0);
-    if (ks0 + 1 < ks1) load_step(ks0 + 1);
-    if (ks0 + 2 < ks1) load_step(ks0 + 2);
-    if (ks0 + 2 < ks1)
-        wait_vmcnt<2 * NL>();
-    else if (ks0 + 1 < ks1)
-        wait_vmcnt<NL>();
-    else
-        wait_vmcnt<0>();
+    // Prologue: three steps in flight; wait for the first.
+    load_step(ks0, true);
+    load_step(ks0 + 1, ks0 + 1 < ks1);
+    load_step(ks0 + 2, ks0 + 2 < ks1);
+    wait_vmcnt<2 * NL>();
     lds_barrier();
 
-    for (int t = ks0; t < ks1; ++t) {
-        const uint8_t* xb = xbuf(t);
+    // Software pipeline over 16-wide k slices: while the 2*MB MFMAs of slice j run, the wave
+    // prepares slice j + 1 in stages placed between them (sched_barrier keeps each stage next to
+    // its MFMA): A = code-book addresses and X fragment reads, B = code-book reads (one per
+    // weight), C = scale and fp16 packing. The LDS latency of A and B then hides under the matrix
+    // core. Slice 3 holds the step boundary: after its first MFMA the wave fetches step t+1's
+    // packed weights and scales from its own ring slot (its own loads, no barrier needed), and
+    // the barrier before step t+1's X fragments sits between later MFMAs.
+    u32x4_t p0, p1;  // packed weights of the current step (rows of block 0 and 1)
+    float s0, s1;
+    half8_t xf[MB], w0, w1;
+    auto fetch_step = [&](int t) __attribute__((always_inline)) {
         const uint8_t* ws = wslot(t);
-        const u32x4_t p0 = *(const u32x4_t*)(ws + 16 * lane);
-        const u32x4_t p1 = *(const u32x4_t*)(ws + 1024 + 16 * lane);
-        const float s0 = scale_of(ws, t, 0), s1 = scale_of(ws, t, 1);
-        // The four 16-wide k slices: read the X fragments, unpack the weights, run the MFMAs.
-        // The second wave on the SIMD covers this wave's LDS latency.
+        p0 = *(const u32x4_t*)(ws + 16 * lane);
+        p1 = *(const u32x4_t*)(ws + 1024 + 16 * lane);
+        s0 = scale_of(ws, t, 0);
+        s1 = scale_of(ws, t, 1);
+    };
+    fetch_step(ks0);
+#pragma unroll
+    for (int i = 0; i < MB; ++i) xf[i] = xfrag(xbuf(ks0), i, 0);
+    w0 = unpack8(p0[0], s0);
+    w1 = unpack8(p1[0], s1);
+
+    constexpr int nm = 2 * MB;  // MFMAs per slice
+    // stage positions: the MFMA index after which a stage is issued
+    constexpr int qB0 = nm >= 8 ? 1 : 0;
+    constexpr int qB1 = nm >= 8 ? 2 : (nm >= 4 ? 1 : 0);
+    constexpr int qC0 = nm >= 8 ? nm / 2 + 1 : (nm >= 4 ? 2 : 1);
+    constexpr int qC1 = qC0 + (nm >= 4 ? 1 : 0);
+    // ... in slice 3: F = own-slot fetch, then A, B; the barrier, step t+3's loads and X reads
+    constexpr int qA3 = nm >= 4 ? 1 : 0;
+    constexpr int qB13 = nm >= 8 ? 2 : qA3;
+    constexpr int qBar = nm >= 8 ? 3 : (nm >= 4 ? 2 : 0);
+
+    uint32_t h0, l0, h1, l1;  // code-book byte addresses of the next slice (see nib_addrs)
+    float v0[8], v1[8];       // its code-book values
+    half8_t xn[MB], wn0, wn1;
+    auto stage_A = [&](int jn) __attribute__((always_inline)) {
+        nib_addrs(p0[jn], 0u, h0, l0);
+        nib_addrs(p1[jn], 0u, h1, l1);
+    };
+    auto stage_X = [&](const uint8_t* xb, int jn) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < MB; ++i) xn[i] = xfrag(xb, i, jn);
+    };
+    auto stage_B = [&](float* v, uint32_t h, uint32_t l) __attribute__((always_inline)) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[2 * e] = lut_at(lut, h, e);
+            v[2 * e + 1] = lut_at(lut, l, e);
+        }
+    };
+    auto stage_C = [&](const float* v, float sc) __attribute__((always_inline)) -> half8_t {
+        u32x4_t o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = pack_half2(v[2 * e] * sc, v[2 * e + 1] * sc);
+        return __builtin_bit_cast(half8_t, o);
+    };
+    auto mfma_q = [&](int q) __attribute__((always_inline)) {
+        const int i = q >> 1;
+        if (q & 1)
+            acc[i * 2 + 1] = mfma32x32x16(w1, xf[i], acc[i * 2 + 1]);
+        else
+            acc[i * 2 + 0] = mfma32x32x16(w0, xf[i], acc[i * 2 + 0]);
+    };
+
+    for (int t = ks0; t < ks1; ++t) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            half8_t xf[MB];
 #pragma unroll
-            for (int i = 0; i < MB; ++i) xf[i] = xfrag(xb, i, j);
-            const half8_t w0 = unpack8(p0[j], s0), w1 = unpack8(p1[j], s1);
-#pragma unroll
-            for (int i = 0; i < MB; ++i) {
-                acc[i * 2 + 0] = mfma32x32x16(w0, xf[i], acc[i * 2 + 0]);
-                acc[i * 2 + 1] = mfma32x32x16(w1, xf[i], acc[i * 2 + 1]);
+            for (int q = 0; q < nm; ++q) {
+                mfma_q(q);
+                if (j < 3) {
+                    if (q == 0) {
+                        stage_A(j + 1);
+                        stage_X(xbuf(t), j + 1);
+                    }
+                    if (q == qB0) stage_B(v0, h0, l0);
+                    if (q == qB1) stage_B(v1, h1, l1);
+                } else {
+                    if (q == 0) {
+                        // step t+1's loads have landed (only step t+2's may be in flight)
+                        wait_vmcnt<NL>();
+                        fetch_step(t + 1);
+                    }
+                    if (q == qA3) {
+                        stage_A(0);
+                        stage_B(v0, h0, l0);
+                    }
+                    if (q == qB13) stage_B(v1, h1, l1);
+                    if (q == qBar) {
+                        // every wave is past step t's slots: refill them with step t+3 (zeros
+                        // past the split's end). Past the last step the reads above and below
+                        // see stale slots and their values go unused.
+                        lds_barrier();
+                        load_step(t + 3, t + 3 < ks1);
+                        stage_X(xbuf(t + 1), 0);
+                    }
+                }
+                if (q == qC0) wn0 = stage_C(v0, s0);
+                if (q == qC1) wn1 = stage_C(v1, s1);
+                __builtin_amdgcn_sched_barrier(0);
             }
-            // keep each slice's reads and unpacking next to its MFMAs (bounds the live registers)
-            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < MB; ++i) xf[i] = xn[i];
+            w0 = wn0;
+            w1 = wn1;
         }
-        // Step t+1's loads have landed (only step t+2's may still be in flight) and, after the
-        // barrier, every wave is done with step t's slots: refill them with step t+3.
-        if (t + 2 < ks1)
-            wait_vmcnt<NL>();
-        else
-            wait_vmcnt<0>();
-        lds_barrier();
-        if (t + 3 < ks1) load_step(t + 3);
     }
+    wait_vmcnt<0>();
 
     // ---- epilogue: bias, one fp16 rounding, stores (or, with split-K, the fp32 partial slab).
     // Both paths end in their own stores, so the accumulators never meet at a control-flow merge
