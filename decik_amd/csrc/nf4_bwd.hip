@@ -98,7 +98,9 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void nf4_bwd_kernel(const Bw
 
     // Loads of step t: the shared dY tile (cooperative), then this wave's packed bytes
     // (transposed to dword-columns) and its rows' statistics for both 32-column halves.
-    auto load_step = [&](int t) __attribute__((always_inline)) {
+    // `live` false: every load reads zeros (steps past the split's end keep the ring's load
+    // count uniform without a branch).
+    auto load_step = [&](int t, bool live) __attribute__((always_inline)) {
         const int gi = group_of_step(t);
         const BwdGroupDev& G = a.g[gi];
         const int n0 = (t - G.step_begin) * kBwdBC;
@@ -112,7 +114,7 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void nf4_bwd_kernel(const Bw
             const int c = pc ^ ((row >> 1) & 7);
             const int gm = m0 + row, gn = n0 + 8 * c;
             bload128_lds(drs, db + (NT * h + 64 * wave) * 16,
-                         off_if(gm < M && gn < N, (uint32_t)(gm * G.lddy + gn) * 2u));
+                         off_if(live && gm < M && gn < N, (uint32_t)(gm * G.lddy + gn) * 2u));
         }
         uint8_t* slot = wring + ring(t) * kBwdWSlot;
         const rsrc_t wrs = make_rsrc(G.w.packed, G.w.packed_bytes);
@@ -120,7 +122,7 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void nf4_bwd_kernel(const Bw
             // instruction d fetches rows 8 d .. 8 d + 7, all 8 dwords (32 contiguous bytes) of
             // each; lane -> (row quad, dword-column, row) lands at dword 72 d + 32 rq + 4 cg + rho
             const int rq = lane >> 5, cg = (lane >> 2) & 7, rho = lane & 3;
-            const bool cok = kw0 + 8 * cg < K;
+            const bool cok = live && kw0 + 8 * cg < K;
             const uint32_t cbyte = (uint32_t)((kw0 + 8 * cg) >> 1);
 #pragma unroll
             for (int d = 0; d < 8; ++d) {
@@ -130,7 +132,7 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void nf4_bwd_kernel(const Bw
             }
         }
         const int row = n0 + lane;  // weight row this lane fetches statistics for
-        const bool rok = row < N;
+        const bool rok = live && row < N;
         const rsrc_t ars = make_rsrc(NESTED ? (const void*)G.w.absmax8 : (const void*)G.w.absmaxf,
                                      G.w.absmax_bytes);
         const rsrc_t a2rs = make_rsrc(G.w.absmax2, G.w.absmax2_bytes);
@@ -206,71 +208,135 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void nf4_bwd_kernel(const Bw
         }
     }
 
-    // Prologue: up to three steps in flight; wait for the first.
-    if (cs0 < cs1) load_step(cs0);
-    if (cs0 + 1 < cs1) load_step(cs0 + 1);
-    if (cs0 + 2 < cs1) load_step(cs0 + 2);
-    if (cs0 + 2 < cs1)
-        wait_vmcnt<2 * NL>();
-    else if (cs0 + 1 < cs1)
-        wait_vmcnt<NL>();
-    else
-        wait_vmcnt<0>();
+    // Prologue: three steps in flight; wait for the first.
+    load_step(cs0, cs0 < cs1);
+    load_step(cs0 + 1, cs0 + 1 < cs1);
+    load_step(cs0 + 2, cs0 + 2 < cs1);
+    wait_vmcnt<2 * NL>();
     lds_barrier();  // dY(cs0) from every wave, code tables
-    if (cs0 < cs1) make_scales(cs0);
+    make_scales(cs0);
+
+    // Software pipeline over 16-row slices, as in the forward kernel: while the 2*MB MFMAs of
+    // slice j run, the wave prepares slice j + 1 in stages placed between them (sched_barrier
+    // keeps each stage next to its MFMA): A = reads of its packed dwords, row scales and dY
+    // fragments; B = byte gather, code-book addresses and code-book reads; C = scaling and fp16
+    // packing. Step t+1's row scales are made during slice 2 (its statistics are this wave's own
+    // loads); the barrier before step t+1's dY fragments sits between slice 3's MFMAs.
+    constexpr int nm = 2 * MB;  // MFMAs per slice
+    constexpr int qB = nm >= 8 ? 1 : (nm >= 4 ? 1 : 0);
+    constexpr int qC0 = nm >= 8 ? nm / 2 + 1 : (nm >= 4 ? 2 : 1);
+    constexpr int qC1 = qC0 + (nm >= 4 ? 1 : 0);
+    constexpr int qBar = nm >= 8 ? 2 : (nm >= 4 ? qC0 : 0);
+
+    half8_t xf[MB], w0, w1;      // operands of the current slice
+    half8_t xn[MB], wn0, wn1;    // ... of the next slice
+    u32x4_t d0, d1;              // next slice: packed dwords of rows r0 .. r0 + 3, r0 + 4 .. r0 + 7
+    float4_t s0, s1;             // ... and their row scales
+    float vh[8], vl[8];          // ... code-book values of the high and low nibbles
+    auto pk_of = [&](int t) __attribute__((always_inline)) {
+        return (const uint32_t*)(wring + ring(t) * kBwdWSlot) + 4 * (beta >> 2);
+    };
+    auto sc_of = [&](int t) __attribute__((always_inline)) {
+        return scales + ((t - cs0) & 1) * 128 + (wide ? 64 * half : 0);
+    };
+    auto stage_A = [&](int t, int j) __attribute__((always_inline)) {
+        const uint32_t* pk = pk_of(t);
+        const float* sc = sc_of(t);
+        const int r0 = 32 * g + 8 * j, dg = 4 * g + j;
+        d0 = *(const u32x4_t*)(pk + kBwdPkStride * dg);
+        d1 = *(const u32x4_t*)(pk + kBwdPkStride * dg + 32);
+        s0 = *(const float4_t*)(sc + r0);
+        s1 = *(const float4_t*)(sc + r0 + 4);
+    };
+    auto stage_X = [&](int t, int j) __attribute__((always_inline)) {
+        const uint8_t* db = dring + ring(t) * DBUF;
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+            xn[i] = *(const half8_t*)(db + (32 * i + l32) * 128 + (((4 * g + j) ^ xsw) << 4));
+    };
+    auto stage_B = [&](int t) __attribute__((always_inline)) {
+        const uint32_t gbase4 = (uint32_t)(64 * group_of_step(t)) * 0x01010101u;
+        // this lane's byte of rows r0 .. r0 + 3 and r0 + 4 .. r0 + 7, gathered into two dwords
+        const uint32_t rb0 = __builtin_amdgcn_perm(d0[1], d0[0], bsel) | (__builtin_amdgcn_perm(d0[3], d0[2], bsel) << 16);
+        const uint32_t rb1 = __builtin_amdgcn_perm(d1[1], d1[0], bsel) | (__builtin_amdgcn_perm(d1[3], d1[2], bsel) << 16);
+        uint32_t ah0, al0, ah1, al1;
+        nib_addrs(rb0, gbase4, ah0, al0);
+        nib_addrs(rb1, gbase4, ah1, al1);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            vh[e] = lut_at(luts, ah0, e);
+            vl[e] = lut_at(luts, al0, e);
+            vh[e + 4] = lut_at(luts, ah1, e);
+            vl[e + 4] = lut_at(luts, al1, e);
+        }
+    };
+    auto stage_C = [&](const float* v) __attribute__((always_inline)) -> half8_t {
+        u32x4_t o;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            o[q] = pack_half2(v[2 * q] * s0[2 * q], v[2 * q + 1] * s0[2 * q + 1]);
+            o[q + 2] = pack_half2(v[2 * q + 4] * s1[2 * q], v[2 * q + 5] * s1[2 * q + 1]);
+        }
+        return __builtin_bit_cast(half8_t, o);
+    };
+    auto mfma_q = [&](int q) __attribute__((always_inline)) {
+        const int i = q >> 1;
+        if (q & 1)
+            acc[i * 2 + 1] = mfma32x32x16(w1, xf[i], acc[i * 2 + 1]);
+        else
+            acc[i * 2 + 0] = mfma32x32x16(w0, xf[i], acc[i * 2 + 0]);
+    };
+
+    // slice 0 of the first step
+    stage_A(cs0, 0);
+    stage_X(cs0, 0);
+    stage_B(cs0);
+    w0 = stage_C(vh);
+    w1 = stage_C(vl);
+#pragma unroll
+    for (int i = 0; i < MB; ++i) xf[i] = xn[i];
 
     for (int t = cs0; t < cs1; ++t) {
-        const int gi = group_of_step(t);
-        const uint32_t gbase4 = (uint32_t)(64 * gi) * 0x01010101u;  // code book gi in every byte
-        const uint8_t* db = dring + ring(t) * DBUF;
-        const uint32_t* pk = (const uint32_t*)(wring + ring(t) * kBwdWSlot) + 4 * (beta >> 2);
-        const float* sc = scales + ((t - cs0) & 1) * 128 + (wide ? 64 * half : 0);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int r0 = 32 * g + 8 * j;  // this lane's eight weight rows r0 .. r0 + 7
-            const int dg = 4 * g + j;       // ... the 8-row group r0 / 8
-            const u32x4_t d0 = *(const u32x4_t*)(pk + kBwdPkStride * dg);
-            const u32x4_t d1 = *(const u32x4_t*)(pk + kBwdPkStride * dg + 32);
-            const float4_t s0 = *(const float4_t*)(sc + r0), s1 = *(const float4_t*)(sc + r0 + 4);
-            half8_t xf[MB];
 #pragma unroll
-            for (int i = 0; i < MB; ++i)
-                xf[i] = *(const half8_t*)(db + (32 * i + l32) * 128 + (((4 * g + j) ^ xsw) << 4));
-            // this lane's byte of rows r0 .. r0 + 3 and r0 + 4 .. r0 + 7, gathered into two dwords
-            const uint32_t rb0 = __builtin_amdgcn_perm(d0[1], d0[0], bsel) |
-                                 (__builtin_amdgcn_perm(d0[3], d0[2], bsel) << 16);
-            const uint32_t rb1 = __builtin_amdgcn_perm(d1[1], d1[0], bsel) |
-                                 (__builtin_amdgcn_perm(d1[3], d1[2], bsel) << 16);
-            uint32_t ah0, al0, ah1, al1;
-            nib_addrs(rb0, gbase4, ah0, al0);
-            nib_addrs(rb1, gbase4, ah1, al1);
-            uint32_t hi[4], lo[4];
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                hi[q] = pack_half2(lut_at(luts, ah0, 2 * q) * s0[2 * q], lut_at(luts, ah0, 2 * q + 1) * s0[2 * q + 1]);
-                lo[q] = pack_half2(lut_at(luts, al0, 2 * q) * s0[2 * q], lut_at(luts, al0, 2 * q + 1) * s0[2 * q + 1]);
-                hi[q + 2] = pack_half2(lut_at(luts, ah1, 2 * q) * s1[2 * q], lut_at(luts, ah1, 2 * q + 1) * s1[2 * q + 1]);
-                lo[q + 2] = pack_half2(lut_at(luts, al1, 2 * q) * s1[2 * q], lut_at(luts, al1, 2 * q + 1) * s1[2 * q + 1]);
+            for (int q = 0; q < nm; ++q) {
+                mfma_q(q);
+                if (j < 3) {
+                    if (q == 0) {
+                        if (j == 2) {
+                            // step t+1's loads have landed (only step t+2's may be in flight):
+                            // its row scales from its statistics (this wave's own loads)
+                            wait_vmcnt<NL>();
+                            make_scales(t + 1);
+                        }
+                        stage_A(t, j + 1);
+                        stage_X(t, j + 1);
+                    }
+                    if (q == qB) stage_B(t);
+                } else {
+                    if (q == 0) stage_A(t + 1, 0);
+                    if (q == qB) stage_B(t + 1);
+                    if (q == qBar) {
+                        // every wave is past step t's slots: refill them with step t+3 (zeros
+                        // past the split's end). Past the last step the reads of this slice see
+                        // stale slots and their values go unused.
+                        lds_barrier();
+                        load_step(t + 3, t + 3 < cs1);
+                        stage_X(t + 1, 0);
+                    }
+                }
+                if (q == qC0) wn0 = stage_C(vh);
+                if (q == qC1) wn1 = stage_C(vl);
+                __builtin_amdgcn_sched_barrier(0);
             }
-            const half8_t w0 = __builtin_bit_cast(half8_t, u32x4_t{hi[0], hi[1], hi[2], hi[3]});
-            const half8_t w1 = __builtin_bit_cast(half8_t, u32x4_t{lo[0], lo[1], lo[2], lo[3]});
 #pragma unroll
-            for (int i = 0; i < MB; ++i) {
-                acc[i * 2 + 0] = mfma32x32x16(w0, xf[i], acc[i * 2 + 0]);
-                acc[i * 2 + 1] = mfma32x32x16(w1, xf[i], acc[i * 2 + 1]);
-            }
-            __builtin_amdgcn_sched_barrier(0);  // one slice at a time (register bound)
+            for (int i = 0; i < MB; ++i) xf[i] = xn[i];
+            w0 = wn0;
+            w1 = wn1;
         }
-        // Step t+1's loads have landed (only step t+2's may be in flight): its row scales can be
-        // made now; after the barrier every wave is done with step t's slots: refill them.
-        if (t + 2 < cs1)
-            wait_vmcnt<NL>();
-        else
-            wait_vmcnt<0>();
-        if (t + 1 < cs1) make_scales(t + 1);
-        lds_barrier();
-        if (t + 3 < cs1) load_step(t + 3);
     }
+    wait_vmcnt<0>();
 
     // ---- epilogue: lane (l32, g) holds columns kw0 + 32 g + c, c = 2 r + cb, of token rows
     // m0 + 32 i + l32 (acc[i * 2 + cb][r]).

@@ -11,13 +11,28 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const ReduceArgs a) 
     const int row = blockIdx.x;
     const int chunks = a.ncols >> 3;
     const float* base = a.partials + (int64_t)row * a.ncols;
+    constexpr int kBatch = 8;  // splits whose loads are in flight together
     for (int c = threadIdx.x; c < chunks; c += 256) {
         const int col = c << 3;
         float4_t v0 = {0.f, 0.f, 0.f, 0.f}, v1 = v0;
-        for (int s = 0; s < a.splits; ++s) {
-            const float4_t* p = (const float4_t*)(base + s * a.slab + col);
-            v0 += __builtin_nontemporal_load(p);
-            v1 += __builtin_nontemporal_load(p + 1);
+        for (int s0 = 0; s0 < a.splits; s0 += kBatch) {
+            float4_t l0[kBatch], l1[kBatch];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                if (s0 + u < a.splits) {
+                    const float4_t* p = (const float4_t*)(base + (int64_t)(s0 + u) * a.slab + col);
+                    l0[u] = __builtin_nontemporal_load(p);
+                    l1[u] = __builtin_nontemporal_load(p + 1);
+                }
+            }
+            // the additions stay in split order
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                if (s0 + u < a.splits) {
+                    v0 += l0[u];
+                    v1 += l1[u];
+                }
+            }
         }
         int g = 0;
 #pragma unroll
