@@ -3,9 +3,10 @@
 Workload (one "step"): the Qwen2.5-1.5B MLP block forward + backward on NF4 weights at 830 packed
 tokens -- gate/up [8960, 1536] and down [1536, 8960] (fp16 N(0, 0.02), NF4 blocksize 64 with
 double quant), X [830, 1536] ~ N(0, 1), dY ~ N(0, 1e-2), SwiGLU between the projections, dX
-through the dequantized weights. Per step: 4 fused dequant-GEMM launches (gate+up forward,
-down forward, down backward, gate+up backward) = 6 GEMMs of 2*830*8960*1536 flops, and two
-SwiGLU launches. gate/up are kept from the forward (no recompute). Weights rotate over several
+through the dequantized weights. Per step: 4 fused dequant-GEMM launches = 6 GEMMs of
+2*830*8960*1536 flops: gate+up forward with SwiGLU in its epilogue, down forward, down backward
+with the SwiGLU backward in its epilogue, gate+up backward. gate/up are kept from the forward (no
+recompute). Weights rotate over several
 layers' worth of seeded weights (seed = 7 * layer + projection).
 
 Also measured: the standalone NF4 dequantization of all seven Qwen2.5-1.5B projections (q, k, v,
@@ -77,6 +78,8 @@ def split_launch(kind):
 
     from decik_amd import _lib
 
+    if kind in ("fwd_gate_up", "bwd_down"):
+        return False  # the SwiGLU-fused launches never split
     L = _lib.lib()
     shapes = {"fwd_gate_up": ("fwd", HIDDEN, [INTER, INTER]), "fwd_down": ("fwd", INTER, [HIDDEN]),
               "bwd_down": ("bwd", INTER, [HIDDEN]), "bwd_gate_up": ("bwd", HIDDEN, [INTER, INTER])}
@@ -90,30 +93,26 @@ def bench_mlp(steps, warmup, device, n_sets=4, only=None):
     import torch
 
     from decik_amd import nf4
-    from decik_amd.swiglu import swiglu_bwd, swiglu_fwd
 
     layers = make_layers(n_sets, ["gate", "up", "down"], device)
     x = seeded_fp16((M, HIDDEN), 1001, 1.0, device)
     dy = seeded_fp16((M, HIDDEN), 1002, 1e-2, device)
-    launches = ["fwd_gate_up", "swiglu_fwd", "fwd_down", "bwd_down", "swiglu_bwd", "bwd_gate_up"]
+    launches = ["fwd_gate_up", "fwd_down", "bwd_down", "bwd_gate_up"]
     if only is not None:
         launches = [only]
     symbol = {"fwd_gate_up": "nf4_fwd_kernel", "fwd_down": "nf4_fwd_kernel",
-              "bwd_down": "nf4_bwd_kernel", "bwd_gate_up": "nf4_bwd_kernel",
-              "swiglu_fwd": "swiglu_fwd_kernel", "swiglu_bwd": "swiglu_bwd_kernel"}
+              "bwd_down": "nf4_bwd_kernel", "bwd_gate_up": "nf4_bwd_kernel"}
     flops = {"fwd_gate_up": 2 * gemm_flops(INTER, HIDDEN), "fwd_down": gemm_flops(HIDDEN, INTER),
-             "bwd_down": gemm_flops(INTER, HIDDEN), "bwd_gate_up": 2 * gemm_flops(INTER, HIDDEN),
-             "swiglu_fwd": 0.0, "swiglu_bwd": 0.0}
+             "bwd_down": gemm_flops(INTER, HIDDEN), "bwd_gate_up": 2 * gemm_flops(INTER, HIDDEN)}
 
     def step(i):
         L = layers[i % n_sets]
         g, u = L["gate"], L["up"]
         dn = L["down"]
-        gate, up = nf4.linear_forward(x, [dict(packed=g[0], qs=g[1]), dict(packed=u[0], qs=u[1])])
-        h = swiglu_fwd(gate, up)
+        gate, up, h = nf4.glu_forward(x, dict(packed=g[0], qs=g[1]), dict(packed=u[0], qs=u[1]))
         (out,) = nf4.linear_forward(h, [dict(packed=dn[0], qs=dn[1])])
-        gh = nf4.linear_backward([dict(packed=dn[0], qs=dn[1], dy=dy)], M, INTER)
-        dgate, dup = swiglu_bwd(gh, gate, up, out=(gate, up))
+        dgate, dup = nf4.linear_backward_swiglu(dict(packed=dn[0], qs=dn[1], dy=dy), gate, up,
+                                                out=(gate, up))
         dx = nf4.linear_backward([dict(packed=g[0], qs=g[1], dy=dgate),
                                   dict(packed=u[0], qs=u[1], dy=dup)], M, HIDDEN)
         return out, dx
@@ -136,25 +135,20 @@ def bench_mlp(steps, warmup, device, n_sets=4, only=None):
     # rotating), HIP events on the launch stream around the loop. Unlike events between the
     # launches of one step, this excludes host-side gaps, so the average matches the kernel's
     # duration in a rocprofv3 kernel trace of this same program.
-    gate0, up0 = nf4.linear_forward(x, [dict(packed=layers[0]["gate"][0], qs=layers[0]["gate"][1]),
-                                        dict(packed=layers[0]["up"][0], qs=layers[0]["up"][1])])
-    h0 = swiglu_fwd(gate0, up0)
-    gh0 = nf4.linear_backward([dict(packed=layers[0]["down"][0], qs=layers[0]["down"][1], dy=dy)], M, INTER)
-    dg0, du0 = swiglu_bwd(gh0, gate0, up0)
+    gate0, up0, h0 = nf4.glu_forward(x, dict(packed=layers[0]["gate"][0], qs=layers[0]["gate"][1]),
+                                     dict(packed=layers[0]["up"][0], qs=layers[0]["up"][1]))
+    dg0, du0 = nf4.linear_backward_swiglu(dict(packed=layers[0]["down"][0], qs=layers[0]["down"][1], dy=dy),
+                                          gate0, up0)
 
     def one(kind, i):
         L = layers[i % n_sets]
         g, u, dn = L["gate"], L["up"], L["down"]
         if kind == "fwd_gate_up":
-            nf4.linear_forward(x, [dict(packed=g[0], qs=g[1]), dict(packed=u[0], qs=u[1])])
-        elif kind == "swiglu_fwd":
-            swiglu_fwd(gate0, up0)
+            nf4.glu_forward(x, dict(packed=g[0], qs=g[1]), dict(packed=u[0], qs=u[1]))
         elif kind == "fwd_down":
             nf4.linear_forward(h0, [dict(packed=dn[0], qs=dn[1])])
         elif kind == "bwd_down":
-            nf4.linear_backward([dict(packed=dn[0], qs=dn[1], dy=dy)], M, INTER)
-        elif kind == "swiglu_bwd":
-            swiglu_bwd(gh0, gate0, up0)
+            nf4.linear_backward_swiglu(dict(packed=dn[0], qs=dn[1], dy=dy), gate0, up0)
         else:
             nf4.linear_backward([dict(packed=g[0], qs=g[1], dy=dg0), dict(packed=u[0], qs=u[1], dy=du0)],
                                 M, HIDDEN)

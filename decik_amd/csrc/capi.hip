@@ -138,13 +138,13 @@ double plan_time(const VariantCost& v, int64_t m, int64_t col_tiles, int64_t nco
 // Best (variant, splits) for a launch; col_tiles_of(v) gives the column tiles for variant v.
 template <typename ColTiles>
 const VariantCost* choose_plan(const VariantCost* vs, int nv, int64_t m, int64_t ncols, int steps,
-                               ColTiles col_tiles_of, int* splits) {
+                               ColTiles col_tiles_of, int* splits, int max_splits = 32) {
     double best = 1e300;
     const VariantCost* pick = &vs[0];
     *splits = 1;
     for (int i = 0; i < nv; ++i) {
         const VariantCost& v = vs[i];
-        const int max_s = steps < 32 ? steps : 32;
+        const int max_s = steps < max_splits ? steps : max_splits;
         for (int s = 1; s <= (max_s > 0 ? max_s : 1); ++s) {
             const int per = steps > 0 ? (steps + s - 1) / s : 0;
             if (steps > 0 && (steps + per - 1) / per != s) continue;  // s splits must all get work
@@ -201,20 +201,29 @@ constexpr VariantCost kBwdVariants[] = {{2, 4, 256, 2, 3.20, 0.90},
                                        {2, 8, 512, 1, 2.60, 1.0},
                                        {4, 8, 512, 1, 3.40, 1.0}};
 
-GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
+// glu: two weights of ns[0] rows, a tile takes 128 rows of each; never split (the epilogue
+// needs the finished sums).
+GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool glu,
+                  bool no_split = false) {
     GemmPlan p{};
     p.steps = (int)((k + kFwdBK - 1) / kFwdBK);
     p.n_tiles = 0;
     int64_t ncols = 0;
-    for (int g = 0; g < ngroups; ++g) {
-        p.n_tiles += (int)((ns[g] + kFwdBN - 1) / kFwdBN);
-        ncols += ns[g];
+    if (glu) {
+        p.n_tiles = (int)((ns[0] + kFwdBN / 2 - 1) / (kFwdBN / 2));
+        ncols = 2 * ns[0];
+    } else {
+        for (int g = 0; g < ngroups; ++g) {
+            p.n_tiles += (int)((ns[g] + kFwdBN - 1) / kFwdBN);
+            ncols += ns[g];
+        }
     }
     const VariantCost* v = plan_override("DECIK_FWD_PLAN", kFwdVariants, 4, p.steps, &p.splits);
+    if (v != nullptr && (glu || no_split)) p.splits = 1;
     if (v == nullptr) {
         const int64_t nt = p.n_tiles;
         v = choose_plan(kFwdVariants, 4, m, ncols, p.steps, [nt](const VariantCost&) { return nt; },
-                        &p.splits);
+                        &p.splits, (glu || no_split) ? 1 : 32);
     }
     p.mt = v->rows_blocks;
     p.waves = v->waves;
@@ -223,14 +232,16 @@ GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
     return p;
 }
 
-GemmPlan plan_bwd(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
+GemmPlan plan_bwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool no_split = false) {
     GemmPlan p{};
     p.steps = 0;
     for (int g = 0; g < ngroups; ++g) p.steps += (int)((ns[g] + kBwdBC - 1) / kBwdBC);
     const VariantCost* v = plan_override("DECIK_BWD_PLAN", kBwdVariants, 3, p.steps, &p.splits);
+    if (v != nullptr && no_split) p.splits = 1;
     if (v == nullptr)
         v = choose_plan(kBwdVariants, 3, m, k, p.steps,
-                        [k](const VariantCost& c) { return (k + c.bn - 1) / c.bn; }, &p.splits);
+                        [k](const VariantCost& c) { return (k + c.bn - 1) / c.bn; }, &p.splits,
+                        no_split ? 1 : 32);
     p.mt = v->rows_blocks;
     p.waves = v->waves;
     p.n_tiles = (int)((k + v->bn - 1) / v->bn);
@@ -303,7 +314,7 @@ int dk_nf4_block_scales(const dk_nf4_weight* w, float* scales, void* stream) {
 
 int64_t dk_nf4_linear_fwd_workspace(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
     if (ngroups < 1 || ngroups > kMaxGroups || ns == nullptr || m <= 0 || k <= 0) return 0;
-    return workspace_bytes(plan_fwd(m, k, ns, ngroups));
+    return workspace_bytes(plan_fwd(m, k, ns, ngroups, false));
 }
 
 int64_t dk_nf4_linear_bwd_workspace(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
@@ -311,19 +322,25 @@ int64_t dk_nf4_linear_bwd_workspace(int64_t m, int64_t k, const int64_t* ns, int
     return workspace_bytes(plan_bwd(m, k, ns, ngroups));
 }
 
-int dk_nf4_linear_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
-                      const dk_linear_fwd_group* groups, int ngroups, int lora_rank, void* workspace,
-                      int64_t workspace_bytes_, void* stream) {
-    g_error.clear();
+}  // extern "C"
+
+// The forward launch behind dk_nf4_linear_fwd and dk_nf4_glu_fwd. h != NULL: GLU mode (two groups
+// of one shape, plain narrow statistics; gate/up outputs optional). no_split: a single pass
+// (no workspace).
+static int linear_fwd_impl(const std::string& name, const uint16_t* x, int64_t m, int64_t k,
+                           int64_t ldx, const dk_linear_fwd_group* groups, int ngroups, int lora_rank,
+                           void* workspace, int64_t workspace_bytes_, void* stream, uint16_t* h,
+                           int64_t ldh, bool no_split) {
+    const bool glu = h != nullptr;
     if (ngroups < 1 || ngroups > kMaxGroups || groups == nullptr)
-        return fail("dk_nf4_linear_fwd: need 1..4 groups");
+        return fail(name + ": need 1..4 groups");
     if (m < 0 || k <= 0 || (k % 32) != 0)
-        return fail("dk_nf4_linear_fwd: k must be a positive multiple of 32");
-    if (m > INT32_MAX / 2 || k > INT32_MAX / 2) return fail("dk_nf4_linear_fwd: m or k too large");
+        return fail(name + ": k must be a positive multiple of 32");
+    if (m > INT32_MAX / 2 || k > INT32_MAX / 2) return fail(name + ": m or k too large");
     if (x == nullptr || !aligned(x, 16) || ldx < k || (ldx % 8) != 0)
-        return fail("dk_nf4_linear_fwd: x must be 16-byte aligned with ldx >= k, ldx % 8 == 0");
+        return fail(name + ": x must be 16-byte aligned with ldx >= k, ldx % 8 == 0");
     if (lora_rank != 0 && lora_rank != 16 && lora_rank != 32)
-        return fail("dk_nf4_linear_fwd: lora_rank must be 0, 16 or 32");
+        return fail(name + ": lora_rank must be 0, 16 or 32");
     FwdArgs a{};
     int64_t ns[kMaxGroups];
     int nested = -1;
@@ -331,25 +348,25 @@ int dk_nf4_linear_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
     int64_t ncols = 0;
     for (int g = 0; g < ngroups; ++g) {
         const dk_linear_fwd_group& G = groups[g];
-        if (to_dev(&G.w, &a.g[g].w, "dk_nf4_linear_fwd")) return 1;
-        if (G.w.k != k) return fail("dk_nf4_linear_fwd: weight k differs from x");
-        if (gemm_weight_ok(G.w, "dk_nf4_linear_fwd")) return 1;
-        if (!aligned(G.w.packed, 16)) return fail("dk_nf4_linear_fwd: packed weights must be 16-byte aligned");
+        if (to_dev(&G.w, &a.g[g].w, name.c_str())) return 1;
+        if (G.w.k != k) return fail(name + ": weight k differs from x");
+        if (gemm_weight_ok(G.w, name.c_str())) return 1;
+        if (!aligned(G.w.packed, 16)) return fail(name + ": packed weights must be 16-byte aligned");
         if (nested >= 0 && nested != G.w.nested)
-            return fail("dk_nf4_linear_fwd: all groups must be nested or all plain");
+            return fail(name + ": all groups must be nested or all plain");
         nested = G.w.nested;
         // one statistics slot per row block and step needs 64-wide steps inside one block
         if (G.w.blocksize < 64 || k % 64 != 0) a.wide_stats = 1;
-        if (G.y == nullptr || !aligned(G.y, 16) || G.ldy < G.w.n || (G.ldy % 8) != 0)
-            return fail("dk_nf4_linear_fwd: y must be 16-byte aligned with ldy >= n, ldy % 8 == 0");
+        if ((G.y == nullptr && !glu) || (G.y != nullptr && (!aligned(G.y, 16) || G.ldy < G.w.n || (G.ldy % 8) != 0)))
+            return fail(name + ": y must be 16-byte aligned with ldy >= n, ldy % 8 == 0");
         if (G.lora_u != nullptr && (lora_rank == 0 || G.lora_b == nullptr))
-            return fail("dk_nf4_linear_fwd: LoRA needs lora_rank > 0 and lora_b");
+            return fail(name + ": LoRA needs lora_rank > 0 and lora_b");
         if (G.lora_u != nullptr && (!aligned(G.lora_u, 16) || !aligned(G.lora_b, 16)))
-            return fail("dk_nf4_linear_fwd: LoRA operands must be 16-byte aligned");
+            return fail(name + ": LoRA operands must be 16-byte aligned");
         if (G.lora_u != nullptr && (m * lora_rank * 2 >= INT32_MAX || G.w.n * lora_rank * 2 >= INT32_MAX))
-            return fail("dk_nf4_linear_fwd: LoRA operands larger than 2^31 bytes");
+            return fail(name + ": LoRA operands larger than 2^31 bytes");
         if (G.bias != nullptr && !aligned(G.bias, 16))
-            return fail("dk_nf4_linear_fwd: bias must be 16-byte aligned");
+            return fail(name + ": bias must be 16-byte aligned");
         a.g[g].bias = reinterpret_cast<const _Float16*>(G.bias);
         a.g[g].lora_u = reinterpret_cast<const _Float16*>(G.lora_u);
         a.g[g].lora_b = reinterpret_cast<const _Float16*>(G.lora_b);
@@ -362,12 +379,15 @@ int dk_nf4_linear_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
         ncols += G.w.n;
         ns[g] = G.w.n;
     }
+    if (glu && (ngroups != 2 || ns[0] != ns[1] || nested || a.wide_stats ||
+                groups[0].w.blocksize != groups[1].w.blocksize))
+        return fail(name + ": GLU mode needs two plain weights of one shape, blocksize >= 64, k % 64 == 0");
     if (m == 0 || tile == 0) return 0;
-    const GemmPlan p = plan_fwd(m, k, ns, ngroups);
+    const GemmPlan p = plan_fwd(m, k, ns, ngroups, glu, no_split);
     const int64_t need = workspace_bytes(p);
     if (need > 0 && (workspace == nullptr || workspace_bytes_ < need || !aligned(workspace, 256)))
-        return fail("dk_nf4_linear_fwd: workspace too small (need " + std::to_string(need) + " bytes)");
-    if ((m - 1) * ldx + k >= INT32_MAX / 2) return fail("dk_nf4_linear_fwd: x too large");
+        return fail(name + ": workspace too small (need " + std::to_string(need) + " bytes)");
+    if ((m - 1) * ldx + k >= INT32_MAX / 2) return fail(name + ": x too large");
     a.x = reinterpret_cast<const _Float16*>(x);
     a.ldx = ldx;
     a.x_bytes = (uint32_t)(((m - 1) * ldx + k) * 2);
@@ -382,9 +402,12 @@ int dk_nf4_linear_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
     a.ksteps_per_split = p.steps_per_split;
     a.nested = nested;
     a.ncols = (int32_t)ncols;
+    a.glu = glu ? 1 : 0;
+    a.h = reinterpret_cast<_Float16*>(h);
+    a.ldh = ldh;
     if (need > 0) a.partials = static_cast<float*>(workspace);
     const int64_t wgs = (int64_t)p.m_tiles * p.n_tiles * p.splits;
-    if (wgs > INT32_MAX / 2 || ncols > INT32_MAX / 2) return fail("dk_nf4_linear_fwd: problem too large");
+    if (wgs > INT32_MAX / 2 || ncols > INT32_MAX / 2) return fail(name + ": problem too large");
     const hipStream_t st = static_cast<hipStream_t>(stream);
     if (check_hip(launch_fwd(a, p.mt, pad8((int)wgs), st), "dk_nf4_linear_fwd launch")) return 1;
     if (p.splits <= 1) return 0;
@@ -401,40 +424,94 @@ int dk_nf4_linear_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
     return check_hip(launch_splitk_reduce(r, st), "dk_nf4_linear_fwd split-K reduction");
 }
 
-int dk_nf4_linear_bwd(const dk_linear_bwd_group* groups, int ngroups, int64_t m, int64_t k, void* dx,
-                      int64_t lddx, int dx_fp32, int lora_rank, void* workspace,
+
+extern "C" {
+
+int dk_nf4_linear_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
+                      const dk_linear_fwd_group* groups, int ngroups, int lora_rank, void* workspace,
                       int64_t workspace_bytes_, void* stream) {
     g_error.clear();
+    return linear_fwd_impl("dk_nf4_linear_fwd", x, m, k, ldx, groups, ngroups, lora_rank, workspace,
+                           workspace_bytes_, stream, nullptr, 0, false);
+}
+
+int dk_nf4_glu_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
+                   const dk_linear_fwd_group* groups, int lora_rank, uint16_t* h, int64_t ldh,
+                   void* stream) {
+    g_error.clear();
+    if (groups == nullptr || h == nullptr) return fail("dk_nf4_glu_fwd: groups and h are required");
+    const dk_nf4_weight& wg = groups[0].w;
+    const dk_nf4_weight& wu = groups[1].w;
+    if (wg.n != wu.n || wg.k != wu.k) return fail("dk_nf4_glu_fwd: gate and up shapes differ");
+    const int64_t n = wg.n;
+    if (!aligned(h, 16) || ldh < n || (ldh % 8) != 0)
+        return fail("dk_nf4_glu_fwd: h must be 16-byte aligned with ldh >= n, ldh % 8 == 0");
+    const bool fused = !wg.nested && !wu.nested && wg.blocksize == wu.blocksize && wg.blocksize >= 64 &&
+                       k % 64 == 0;
+    if (fused)
+        return linear_fwd_impl("dk_nf4_glu_fwd", x, m, k, ldx, groups, 2, lora_rank, nullptr, 0, stream,
+                               h, ldh, true);
+    // other statistics: gate and up by the grouped launch (one pass), then the SwiGLU kernel
+    if (groups[0].y == nullptr || groups[1].y == nullptr || groups[0].ldy != n || groups[1].ldy != n ||
+        ldh != n)
+        return fail("dk_nf4_glu_fwd: nested or narrow-block weights need gate and up outputs, all rows contiguous");
+    if (linear_fwd_impl("dk_nf4_glu_fwd", x, m, k, ldx, groups, 2, lora_rank, nullptr, 0, stream, nullptr,
+                        0, true))
+        return 1;
+    return check_hip(launch_swiglu_fwd(reinterpret_cast<const _Float16*>(groups[0].y),
+                                       reinterpret_cast<const _Float16*>(groups[1].y),
+                                       reinterpret_cast<_Float16*>(h), m * n, static_cast<hipStream_t>(stream)),
+                     "dk_nf4_glu_fwd SwiGLU");
+}
+
+}  // extern "C"
+
+// SwiGLU backward fused into the epilogue of an input-gradient launch (dk_nf4_linear_bwd_swiglu).
+struct SwigluBwdOut {
+    const uint16_t* gate;
+    const uint16_t* up;
+    int64_t ldgu;
+    uint16_t* dgate;
+    uint16_t* dup;
+    int64_t ldd;
+};
+
+// The input-gradient launch behind dk_nf4_linear_bwd and dk_nf4_linear_bwd_swiglu (sw != NULL:
+// no dX; the epilogue turns fp16(dY.W) into dgate / dup; never split).
+static int linear_bwd_impl(const std::string& name, const dk_linear_bwd_group* groups, int ngroups,
+                           int64_t m, int64_t k, void* dx, int64_t lddx, int dx_fp32, int lora_rank,
+                           void* workspace, int64_t workspace_bytes_, void* stream,
+                           const SwigluBwdOut* sw) {
     if (ngroups < 1 || ngroups > kMaxGroups || groups == nullptr)
-        return fail("dk_nf4_linear_bwd: need 1..4 groups");
+        return fail(name + ": need 1..4 groups");
     if (m < 0 || k <= 0 || (k % 32) != 0)
-        return fail("dk_nf4_linear_bwd: k must be a positive multiple of 32");
-    if (m > INT32_MAX / 2 || k > INT32_MAX / 2) return fail("dk_nf4_linear_bwd: m or k too large");
-    if (dx == nullptr || !aligned(dx, 16) || lddx < k || (lddx % 8) != 0)
-        return fail("dk_nf4_linear_bwd: dx must be 16-byte aligned with lddx >= k, lddx % 8 == 0");
+        return fail(name + ": k must be a positive multiple of 32");
+    if (m > INT32_MAX / 2 || k > INT32_MAX / 2) return fail(name + ": m or k too large");
+    if (sw == nullptr && (dx == nullptr || !aligned(dx, 16) || lddx < k || (lddx % 8) != 0))
+        return fail(name + ": dx must be 16-byte aligned with lddx >= k, lddx % 8 == 0");
     if (lora_rank != 0 && lora_rank != 16 && lora_rank != 32)
-        return fail("dk_nf4_linear_bwd: lora_rank must be 0, 16 or 32");
+        return fail(name + ": lora_rank must be 0, 16 or 32");
     BwdArgs a{};
     int64_t ns[kMaxGroups];
     int nested = -1;
     int step = 0;
     for (int g = 0; g < ngroups; ++g) {
         const dk_linear_bwd_group& G = groups[g];
-        if (to_dev(&G.w, &a.g[g].w, "dk_nf4_linear_bwd")) return 1;
-        if (G.w.k != k) return fail("dk_nf4_linear_bwd: weight k differs from dx");
-        if (gemm_weight_ok(G.w, "dk_nf4_linear_bwd")) return 1;
-        if ((m - 1) * G.lddy + G.w.n >= INT32_MAX / 2) return fail("dk_nf4_linear_bwd: dy too large");
-        if (!aligned(G.w.packed, 16)) return fail("dk_nf4_linear_bwd: packed weights must be 16-byte aligned");
-        if ((G.w.n % 8) != 0) return fail("dk_nf4_linear_bwd: weight rows must be a multiple of 8");
+        if (to_dev(&G.w, &a.g[g].w, name.c_str())) return 1;
+        if (G.w.k != k) return fail(name + ": weight k differs from dx");
+        if (gemm_weight_ok(G.w, name.c_str())) return 1;
+        if ((m - 1) * G.lddy + G.w.n >= INT32_MAX / 2) return fail(name + ": dy too large");
+        if (!aligned(G.w.packed, 16)) return fail(name + ": packed weights must be 16-byte aligned");
+        if ((G.w.n % 8) != 0) return fail(name + ": weight rows must be a multiple of 8");
         if (nested >= 0 && nested != G.w.nested)
-            return fail("dk_nf4_linear_bwd: all groups must be nested or all plain");
+            return fail(name + ": all groups must be nested or all plain");
         nested = G.w.nested;
         if (G.dy == nullptr || !aligned(G.dy, 16) || G.lddy < G.w.n || (G.lddy % 8) != 0)
-            return fail("dk_nf4_linear_bwd: dy must be 16-byte aligned with lddy >= n, lddy % 8 == 0");
+            return fail(name + ": dy must be 16-byte aligned with lddy >= n, lddy % 8 == 0");
         if (G.lora_gu != nullptr && (lora_rank == 0 || G.lora_a == nullptr || !aligned(G.lora_gu, 16)))
-            return fail("dk_nf4_linear_bwd: LoRA needs lora_rank > 0, lora_a and 16-byte aligned gu");
+            return fail(name + ": LoRA needs lora_rank > 0, lora_a and 16-byte aligned gu");
         if (G.lora_gu != nullptr && (m * lora_rank * 2 >= INT32_MAX || k * lora_rank * 2 >= INT32_MAX))
-            return fail("dk_nf4_linear_bwd: LoRA operands larger than 2^31 bytes");
+            return fail(name + ": LoRA operands larger than 2^31 bytes");
         if (G.w.blocksize < 64 || k % 64 != 0) a.wide_stats = 1;
         a.g[g].dy = reinterpret_cast<const _Float16*>(G.dy);
         a.g[g].lddy = (int32_t)G.lddy;
@@ -447,10 +524,10 @@ int dk_nf4_linear_bwd(const dk_linear_bwd_group* groups, int ngroups, int64_t m,
         ns[g] = G.w.n;
     }
     if (m == 0) return 0;
-    const GemmPlan p = plan_bwd(m, k, ns, ngroups);
+    const GemmPlan p = plan_bwd(m, k, ns, ngroups, sw != nullptr);
     const int64_t need = workspace_bytes(p);
     if (need > 0 && (workspace == nullptr || workspace_bytes_ < need || !aligned(workspace, 256)))
-        return fail("dk_nf4_linear_bwd: workspace too small (need " + std::to_string(need) + " bytes)");
+        return fail(name + ": workspace too small (need " + std::to_string(need) + " bytes)");
     a.dx = dx;
     a.lddx = lddx;
     a.m = (int)m;
@@ -464,9 +541,18 @@ int dk_nf4_linear_bwd(const dk_linear_bwd_group* groups, int ngroups, int64_t m,
     a.csteps_per_split = p.steps_per_split;
     a.dx_fp32 = dx_fp32 ? 1 : 0;
     a.nested = nested;
+    if (sw != nullptr) {
+        a.swiglu = 1;
+        a.gate = reinterpret_cast<const _Float16*>(sw->gate);
+        a.up = reinterpret_cast<const _Float16*>(sw->up);
+        a.ldgu = sw->ldgu;
+        a.dgate = reinterpret_cast<_Float16*>(sw->dgate);
+        a.dup = reinterpret_cast<_Float16*>(sw->dup);
+        a.ldd = sw->ldd;
+    }
     if (need > 0) a.partials = static_cast<float*>(workspace);
     const int64_t wgs = (int64_t)p.m_tiles * p.n_tiles * p.splits;
-    if (wgs > INT32_MAX / 2) return fail("dk_nf4_linear_bwd: problem too large");
+    if (wgs > INT32_MAX / 2) return fail(name + ": problem too large");
     const hipStream_t st = static_cast<hipStream_t>(stream);
     if (check_hip(launch_bwd(a, p.mt, p.waves, pad8((int)wgs), st), "dk_nf4_linear_bwd launch")) return 1;
     if (p.splits <= 1) return 0;
@@ -480,6 +566,30 @@ int dk_nf4_linear_bwd(const dk_linear_bwd_group* groups, int ngroups, int64_t m,
     r.out_fp32 = dx_fp32 ? 1 : 0;
     r.o[0] = ReduceOut{dx, lddx, nullptr, 0, (int32_t)k};
     return check_hip(launch_splitk_reduce(r, st), "dk_nf4_linear_bwd split-K reduction");
+}
+
+extern "C" {
+
+int dk_nf4_linear_bwd(const dk_linear_bwd_group* groups, int ngroups, int64_t m, int64_t k, void* dx,
+                      int64_t lddx, int dx_fp32, int lora_rank, void* workspace,
+                      int64_t workspace_bytes_, void* stream) {
+    g_error.clear();
+    return linear_bwd_impl("dk_nf4_linear_bwd", groups, ngroups, m, k, dx, lddx, dx_fp32, lora_rank,
+                           workspace, workspace_bytes_, stream, nullptr);
+}
+
+int dk_nf4_linear_bwd_swiglu(const dk_linear_bwd_group* group, int64_t m, int64_t k, int lora_rank,
+                             const uint16_t* gate, const uint16_t* up, int64_t ldgu, uint16_t* dgate,
+                             uint16_t* dup, int64_t ldd, void* stream) {
+    g_error.clear();
+    if (gate == nullptr || up == nullptr || dgate == nullptr || dup == nullptr)
+        return fail("dk_nf4_linear_bwd_swiglu: gate, up, dgate and dup are required");
+    if (!aligned(gate, 16) || !aligned(up, 16) || !aligned(dgate, 16) || !aligned(dup, 16) || ldgu < k ||
+        ldd < k || (ldgu % 8) != 0 || (ldd % 8) != 0)
+        return fail("dk_nf4_linear_bwd_swiglu: gate/up/dgate/dup must be 16-byte aligned, row strides >= k and % 8 == 0");
+    const SwigluBwdOut sw{gate, up, ldgu, dgate, dup, ldd};
+    return linear_bwd_impl("dk_nf4_linear_bwd_swiglu", group, 1, m, k, nullptr, 0, 0, lora_rank, nullptr, 0,
+                           stream, &sw);
 }
 
 int dk_lora_down(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const uint16_t* a, int rank,

@@ -60,6 +60,11 @@ struct FwdArgs {
     int32_t wide_stats;  // some group has blocksize 32 or k % 64 != 0: two statistics slots per lane
     int32_t ncols;       // columns of a partial slab (sum of the groups' n)
     float* partials;     // splits x m x ncols fp32 (splits > 1)
+    // GLU mode: groups 0 (gate) and 1 (up) of one shape; a tile takes 128 rows of each and the
+    // epilogue also writes h = fp16(silu(gate) up) (no split-K; plain narrow statistics)
+    int32_t glu;
+    _Float16* h;
+    int64_t ldh;
     FwdGroupDev g[kMaxGroups];
 };
 
@@ -84,6 +89,15 @@ struct BwdArgs {
     int32_t nested;
     int32_t wide_stats;  // some group has blocksize 32 or k % 64 != 0: one scale per 32 columns
     float* partials;  // splits x m x k fp32 (splits > 1)
+    // SwiGLU mode (no split-K): no dX; with G = fp16(dY.W), dgate / dup from G, gate and up
+    // (may alias gate / up)
+    int32_t swiglu;
+    const _Float16* gate;
+    const _Float16* up;
+    int64_t ldgu;
+    _Float16* dgate;
+    _Float16* dup;
+    int64_t ldd;
     BwdGroupDev g[kMaxGroups];
 };
 

@@ -356,27 +356,102 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void nf4_bwd_kernel(const Bw
         }
         return;
     }
+    // Output tiles go through LDS so that every global access instruction covers whole row
+    // segments (a lane's own fragment is 32 columns of one token row; accessed directly, each
+    // instruction would touch 16-byte pieces of 32 rows). Staging area: this wave's own weight ring
+    // (its loads have all landed; LDS operations of one wave complete in order, so no barrier).
+    // A 32-row tile of 64 columns has rows 64 * esize + 16 bytes apart.
+    uint8_t* stage = wring;
+    constexpr int kRow16 = 64 * 2 + 16, kRow32 = 64 * 4 + 16;
+    // 32 rows of 64 columns (kw0 .. kw0 + 63) between LDS tile `t` (fp16) and global memory
+    auto tile_io = [&](bool to_global, int t, _Float16* gp, int64_t ld, int m_first) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < MB; ++i) {
-        const int m = m0 + 32 * i + l32;
-        if (m >= M || kc >= K) continue;
-        if (a.dx_fp32) {
+        for (int q = 0; q < 4; ++q) {
+            const int c = q * 64 + lane, row = c >> 3, cc = c & 7;
+            uint8_t* lp = stage + t * 32 * kRow16 + row * kRow16 + cc * 16;
+            const int m = m_first + row, col = kw0 + 8 * cc;
+            const bool ok = m < M && col < K;  // k % 32 == 0: chunks are wholly in or out
+            if (to_global) {
+                if (ok) *(u32x4_t*)(gp + (int64_t)m * ld + col) = *(const u32x4_t*)lp;
+            } else {
+                *(u32x4_t*)lp = ok ? *(const u32x4_t*)(gp + (int64_t)m * ld + col) : u32x4_t{0u, 0u, 0u, 0u};
+            }
+        }
+    };
+    // this lane's 32 columns (32 g .. 32 g + 31 of the tile) of token row l32, fp16 pairs
+    auto frag_put = [&](int t, const uint32_t* o) __attribute__((always_inline)) {
+        uint8_t* lp = stage + t * 32 * kRow16 + l32 * kRow16 + 64 * g;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) *(u32x4_t*)(lp + 16 * q) = u32x4_t{o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]};
+    };
+    auto frag_get = [&](int t, uint32_t* o) __attribute__((always_inline)) {
+        const uint8_t* lp = stage + t * 32 * kRow16 + l32 * kRow16 + 64 * g;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const u32x4_t v = *(const u32x4_t*)(lp + 16 * q);
+            o[4 * q] = v[0];
+            o[4 * q + 1] = v[1];
+            o[4 * q + 2] = v[2];
+            o[4 * q + 3] = v[3];
+        }
+    };
+    // column kc + 2 p + cb of this lane is acc[i * 2 + cb][p]; fp16 pair j = columns 2 j, 2 j + 1
+    auto pack_row = [&](int i, uint32_t* o) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) o[j] = pack_half2(acc[i * 2][j], acc[i * 2 + 1][j]);
+    };
+    if (a.swiglu) {
+        // G = fp16(dY.W) (the rounding of the matmul output), then dgate / dup of SwiGLU from the
+        // lane's 32 columns of gate and up (the tiles are read before any output is written: the
+        // outputs may alias gate and up)
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+            const int mf = m0 + 32 * i;
+            tile_io(false, 0, const_cast<_Float16*>(a.gate), a.ldgu, mf);
+            tile_io(false, 1, const_cast<_Float16*>(a.up), a.ldgu, mf);
+            uint32_t gw[16], uw[16], Gw[16], dg[16], du[16];
+            frag_get(0, gw);
+            frag_get(1, uw);
+            pack_row(i, Gw);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const half2_t G2 = __builtin_bit_cast(half2_t, Gw[j]);
+                const half2_t g2 = __builtin_bit_cast(half2_t, gw[j]), u2 = __builtin_bit_cast(half2_t, uw[j]);
+                float d0, d1, e0, e1;
+                swiglu_bwd1((float)G2.x, (float)g2.x, (float)u2.x, d0, e0);
+                swiglu_bwd1((float)G2.y, (float)g2.y, (float)u2.y, d1, e1);
+                dg[j] = pack_half2(d0, d1);
+                du[j] = pack_half2(e0, e1);
+            }
+            frag_put(0, dg);
+            frag_put(1, du);
+            tile_io(true, 0, a.dgate, a.ldd, mf);
+            tile_io(true, 1, a.dup, a.ldd, mf);
+        }
+        return;
+    }
+    if (a.dx_fp32) {
+        // fp32: each lane's 32 columns straight from the accumulators (128 bytes per row and lane)
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+            const int m = m0 + 32 * i + l32;
+            if (m >= M || kc >= K) continue;
             float* dst = (float*)a.dx + (int64_t)m * a.lddx + kc;
 #pragma unroll
             for (int q = 0; q < 8; ++q)
                 *(float4_t*)(dst + 4 * q) = float4_t{acc[i * 2][2 * q], acc[i * 2 + 1][2 * q],
                                                      acc[i * 2][2 * q + 1], acc[i * 2 + 1][2 * q + 1]};
-        } else {
-            _Float16* dst = (_Float16*)a.dx + (int64_t)m * a.lddx + kc;
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-                *(u32x4_t*)(dst + 8 * q) = u32x4_t{
-                    pack_half2(acc[i * 2][4 * q], acc[i * 2 + 1][4 * q]),
-                    pack_half2(acc[i * 2][4 * q + 1], acc[i * 2 + 1][4 * q + 1]),
-                    pack_half2(acc[i * 2][4 * q + 2], acc[i * 2 + 1][4 * q + 2]),
-                    pack_half2(acc[i * 2][4 * q + 3], acc[i * 2 + 1][4 * q + 3])};
         }
+        return;
     }
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+        uint32_t o[16];
+        pack_row(i, o);
+        frag_put(0, o);
+        tile_io(true, 0, (_Float16*)a.dx, a.lddx, m0 + 32 * i);
+    }
+    (void)kRow32;
 }
 
 template <int MB, int WAVES, bool NESTED>

@@ -177,6 +177,29 @@ __device__ __forceinline__ void dequant16(u32x4_t p, float s, const float* lut, 
     dequant4(p.w, s, lut, o + 12);
 }
 
+// SwiGLU arithmetic (solution/swiglu.py:15-37), shared by the elementwise kernels and the fused
+// GEMM epilogues so both give the same bits: fp32 from fp16 inputs, one fp16 rounding. The
+// sigmoid uses the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32: about 1 ulp each, far
+// below the fp16 output rounding), three instructions instead of a full-precision expf and
+// division: in a GEMM epilogue nothing hides this arithmetic.
+__device__ __forceinline__ float swiglu_sigmoid(float g) {
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.44269504088896341f));
+}
+
+// fp16 pairs: h = (g sigmoid(g)) u
+__device__ __forceinline__ uint32_t swiglu_fwd2(uint32_t g2, uint32_t u2) {
+    const half2_t g = __builtin_bit_cast(half2_t, g2), u = __builtin_bit_cast(half2_t, u2);
+    const float g0 = (float)g.x, g1 = (float)g.y;
+    return pack_half2(g0 * swiglu_sigmoid(g0) * (float)u.x, g1 * swiglu_sigmoid(g1) * (float)u.y);
+}
+
+// one element: dup = G g s, dgate = G u s (1 + g (1 - s)), s = sigmoid(g)
+__device__ __forceinline__ void swiglu_bwd1(float G, float g, float u, float& dg, float& du) {
+    const float s = swiglu_sigmoid(g);
+    du = G * g * s;
+    dg = G * u * s * (1.0f + g * (1.0f - s));
+}
+
 __device__ __forceinline__ float4_t mfma16x16x32(half8_t a, half8_t b, float4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }

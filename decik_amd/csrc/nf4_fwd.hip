@@ -45,15 +45,18 @@ template <int MB, bool NESTED>
 __global__ __launch_bounds__(kGemmThreads, MB <= 4 ? 2 : 1) void nf4_fwd_kernel(const FwdArgs a) {
     constexpr int BM = 32 * MB;
     constexpr int XBUF = BM * 128;             // bytes of one X ring buffer
-    constexpr int NL = MB + (NESTED ? 4 : 3);  // loads per step and thread (narrow layout)
+    constexpr int NL = MB + 4;  // loads per step and thread (narrow layout)
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    __shared__ float lut[16];  // code book (static: its address folds into the lookups)
+    // code books of row blocks 0 and 1 (the same book unless GLU); static, so their addresses
+    // fold into the lookups
+    __shared__ float lut[32];
     float* c2 = (float*)smem;
     uint8_t* xs = smem + kFwdSmemHeader;
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int l32 = lane & 31, g = lane >> 5;
     const bool wide = a.wide_stats != 0;
+    const bool glu = a.glu != 0;  // (host: plain narrow statistics, two weights of one shape)
     const int wslot_bytes = fwd_wslot_bytes(wide);
 
     const int L = xcd_logical_id();
@@ -67,28 +70,34 @@ __global__ __launch_bounds__(kGemmThreads, MB <= 4 ? 2 : 1) void nf4_fwd_kernel(
 #pragma unroll
     for (int i = 1; i < kMaxGroups; ++i)
         if (i < a.ngroups && n_tile >= a.g[i].tile_begin) gi = i;
-    gi = __builtin_amdgcn_readfirstlane(gi);
-    const FwdGroupDev& G = a.g[gi];
+    gi = __builtin_amdgcn_readfirstlane(glu ? 0 : gi);
+    const FwdGroupDev& G = a.g[gi];                 // row block 0's weight (and block 1's ...
+    const FwdGroupDev& G1 = a.g[glu ? 1 : gi];      // ... unless GLU: block 1 is the up weight)
     const NF4Dev& W = G.w;
+    const NF4Dev& W1 = G1.w;
     // Scalars the main loop uses, pinned in SGPRs: left to itself the compiler re-reads them
     // from the kernel arguments inside the loop, and every such scalar load waits for all
     // outstanding LDS reads (they share the lgkm counter).
     const int M = sgpr(a.m), K = sgpr(a.k), N = sgpr((int)W.n), ldx = sgpr((int)a.ldx);
     const uint32_t bs_shift = sgpr((uint32_t)W.bs_shift), bs2_shift = sgpr((uint32_t)W.bs2_shift);
     const int m0 = m_tile * BM;
-    const int nw0 = (n_tile - G.tile_begin) * kFwdBN + wave * 64;
+    // first weight row of the wave: 64 rows (blocks 0, 1) or, GLU, 32 rows of each weight
+    const int nw0 = glu ? n_tile * (kFwdBN / 2) + wave * 32 : (n_tile - G.tile_begin) * kFwdBN + wave * 64;
     const int ks0 = split * a.ksteps_per_split;
     const int ks1 = min(a.ksteps, ks0 + a.ksteps_per_split);
 
-    if (tid < 16) lut[tid] = W.code[tid];
+    if (tid < 32) lut[tid] = (tid < 16 ? W.code : W1.code)[tid & 15];
     if constexpr (NESTED) c2[tid] = W.code2[tid];
     const float offset = NESTED ? *W.offset : 0.0f;
 
     const rsrc_t xrs = make_rsrc(a.x, a.x_bytes);
     const rsrc_t wrs = make_rsrc(W.packed, W.packed_bytes);
+    const rsrc_t wrs1 = make_rsrc(W1.packed, W1.packed_bytes);
     const rsrc_t ars = make_rsrc(NESTED ? (const void*)W.absmax8 : (const void*)W.absmaxf, W.absmax_bytes);
+    const rsrc_t ars1 = make_rsrc(W1.absmaxf, NESTED ? 0u : W1.absmax_bytes);  // GLU (plain) only
     const rsrc_t a2rs = make_rsrc(W.absmax2, W.absmax2_bytes);
-    const int wrow0 = nw0 + arow_to_n(l32);  // this lane's A row in block 0 (block 1: +32)
+    const int wrow0 = nw0 + arow_to_n(l32);   // this lane's A row in block 0 ...
+    const int wrow1 = glu ? wrow0 : wrow0 + 32;  // ... and in block 1
     const int xsw = (l32 >> 1) & 7;           // LDS swizzle of this lane's X rows
 
     uint8_t* wring = xs + 3 * XBUF + wave * (3 * wslot_bytes);
@@ -116,21 +125,24 @@ __global__ __launch_bounds__(kGemmThreads, MB <= 4 ? 2 : 1) void nf4_fwd_kernel(
         uint8_t* slot = wslot(t);
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
-            const int row = wrow0 + 32 * b;
+            const int row = b ? wrow1 : wrow0;
             const bool ok = live && row < N && krun < K;
-            bload128_lds(wrs, slot + b * 1024,
+            bload128_lds(b ? wrs1 : wrs, slot + b * 1024,
                          off_if(ok, ((uint32_t)row * (uint32_t)K + (uint32_t)krun) >> 1));
         }
         if (!wide) {
-            // lane (l32, g) fetches row block g's statistics (one block spans the 64-wide step)
-            const int row = wrow0 + 32 * g;
+            // lane (l32, g) fetches row block g's statistics (one block spans the 64-wide step);
+            // GLU: lanes g = 0 those of the gate row, lanes g = 1 those of the up row (a second
+            // load, into slot + 2304; all-zero without GLU)
+            const int row = glu ? wrow0 : wrow0 + 32 * g;
             const bool ok = live && row < N && k0 < K;
             const uint32_t blk = ((uint32_t)row * (uint32_t)K + (uint32_t)k0) >> bs_shift;
             if constexpr (NESTED) {
                 bload8_lds(ars, slot + 2048, off_if(ok, blk));
                 bload32_lds(a2rs, slot + 2304, off_if(ok, (blk >> bs2_shift) * 4u));
             } else {
-                bload32_lds(ars, slot + 2048, off_if(ok, blk * 4u));
+                bload32_lds(ars, slot + 2048, off_if(ok && (!glu || g == 0), blk * 4u));
+                bload32_lds(ars1, slot + 2304, off_if(ok && glu && g == 1, blk * 4u));
             }
         } else {
 #pragma unroll
@@ -147,7 +159,7 @@ __global__ __launch_bounds__(kGemmThreads, MB <= 4 ? 2 : 1) void nf4_fwd_kernel(
             }
         }
     };
-    const bool rowok0 = wrow0 < N, rowok1 = wrow0 + 32 < N;
+    const bool rowok0 = wrow0 < N, rowok1 = wrow1 < N;
     // fp32 scale of this lane's row block b at step t (0 outside the weight)
     auto scale_of = [&](const uint8_t* slot, int t, int b) __attribute__((always_inline)) -> float {
         const int si = wide ? lane + 64 * b : l32 + 32 * b;
@@ -159,16 +171,16 @@ __global__ __launch_bounds__(kGemmThreads, MB <= 4 ? 2 : 1) void nf4_fwd_kernel(
             const float a2 = *(const float*)(slot + a2o + 4 * si);
             sc = c2[q] * a2 + offset;
         } else {
-            sc = *(const float*)(slot + 2048 + 4 * si);
+            sc = *(const float*)(slot + 2048 + 4 * si + (b && glu ? 256 : 0));
         }
         return ok ? sc : 0.0f;
     };
     auto xfrag = [&](const uint8_t* xb, int i, int j) __attribute__((always_inline)) -> half8_t {
         return *(const half8_t*)(xb + (32 * i + l32) * 128 + (((4 * g + j) ^ xsw) << 4));
     };
-    auto unpack8 = [&](uint32_t word, float s) __attribute__((always_inline)) -> half8_t {
+    auto unpack8 = [&](uint32_t word, float s, int b) __attribute__((always_inline)) -> half8_t {
         uint32_t o[4];
-        dequant4s(word, s, lut, o);
+        dequant4s(word, s, lut + 16 * b, o);
         return __builtin_bit_cast(half8_t, u32x4_t{o[0], o[1], o[2], o[3]});
     };
 
@@ -180,25 +192,32 @@ __global__ __launch_bounds__(kGemmThreads, MB <= 4 ? 2 : 1) void nf4_fwd_kernel(
     // A = fp16(s * B) and B = U. Loads are branch-free (rows past the end read zeros) and the
     // trip count is 0 without LoRA.
     {
-        const int R = (G.lora_u != nullptr && split == 0) ? sgpr(a.lora_rank) : 0;
-        const float ls = G.lora_scale;
-        const rsrc_t brs = make_rsrc(G.lora_b, (uint32_t)N * (uint32_t)R * 2u);
-        const rsrc_t urs = make_rsrc(G.lora_u, (uint32_t)M * (uint32_t)R * 2u);
+        const bool has = G.lora_u != nullptr || G1.lora_u != nullptr;
+        const int R = (has && split == 0) ? sgpr(a.lora_rank) : 0;
+        // a weight without LoRA gets zero-size buffers: its loads read zeros
+        const rsrc_t brs0 = make_rsrc(G.lora_b, G.lora_u ? (uint32_t)N * (uint32_t)R * 2u : 0u);
+        const rsrc_t urs0 = make_rsrc(G.lora_u, G.lora_u ? (uint32_t)M * (uint32_t)R * 2u : 0u);
+        const rsrc_t brs1 = make_rsrc(G1.lora_b, G1.lora_u ? (uint32_t)N * (uint32_t)R * 2u : 0u);
+        const rsrc_t urs1 = make_rsrc(G1.lora_u, G1.lora_u ? (uint32_t)M * (uint32_t)R * 2u : 0u);
         for (int t0 = 0; t0 < R; t0 += 16) {
             half8_t bl[2];
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
-                const int row = wrow0 + 32 * b;
-                bl[b] = __builtin_bit_cast(half8_t, bload128(brs, off_if(row < N, (uint32_t)(row * R + t0 + 8 * g) * 2u)));
+                const int row = b ? wrow1 : wrow0;
+                const float ls = b ? G1.lora_scale : G.lora_scale;
+                bl[b] = __builtin_bit_cast(half8_t, bload128(b ? brs1 : brs0, off_if(row < N, (uint32_t)(row * R + t0 + 8 * g) * 2u)));
 #pragma unroll
                 for (int e = 0; e < 8; ++e) bl[b][e] = (_Float16)((float)bl[b][e] * ls);
             }
 #pragma unroll
             for (int i = 0; i < MB; ++i) {
                 const int m = m0 + 32 * i + l32;
-                const half8_t uu = __builtin_bit_cast(half8_t, bload128(urs, off_if(m < M, (uint32_t)(m * R + t0 + 8 * g) * 2u)));
+                const uint32_t uo = off_if(m < M, (uint32_t)(m * R + t0 + 8 * g) * 2u);
 #pragma unroll
-                for (int b = 0; b < 2; ++b) acc[i * 2 + b] = mfma32x32x16(bl[b], uu, acc[i * 2 + b]);
+                for (int b = 0; b < 2; ++b) {
+                    const half8_t uu = __builtin_bit_cast(half8_t, bload128(b ? urs1 : urs0, uo));
+                    acc[i * 2 + b] = mfma32x32x16(bl[b], uu, acc[i * 2 + b]);
+                }
             }
         }
     }
@@ -230,8 +249,8 @@ __global__ __launch_bounds__(kGemmThreads, MB <= 4 ? 2 : 1) void nf4_fwd_kernel(
     fetch_step(ks0);
 #pragma unroll
     for (int i = 0; i < MB; ++i) xf[i] = xfrag(xbuf(ks0), i, 0);
-    w0 = unpack8(p0[0], s0);
-    w1 = unpack8(p1[0], s1);
+    w0 = unpack8(p0[0], s0, 0);
+    w1 = unpack8(p1[0], s1, 1);
 
     constexpr int nm = 2 * MB;  // MFMAs per slice
     // stage positions: the MFMA index after which a stage is issued
@@ -255,11 +274,11 @@ __global__ __launch_bounds__(kGemmThreads, MB <= 4 ? 2 : 1) void nf4_fwd_kernel(
 #pragma unroll
         for (int i = 0; i < MB; ++i) xn[i] = xfrag(xb, i, jn);
     };
-    auto stage_B = [&](float* v, uint32_t h, uint32_t l) __attribute__((always_inline)) {
+    auto stage_B = [&](float* v, uint32_t h, uint32_t l, int b) __attribute__((always_inline)) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            v[2 * e] = lut_at(lut, h, e);
-            v[2 * e + 1] = lut_at(lut, l, e);
+            v[2 * e] = lut_at(lut + 16 * b, h, e);
+            v[2 * e + 1] = lut_at(lut + 16 * b, l, e);
         }
     };
     auto stage_C = [&](const float* v, float sc) __attribute__((always_inline)) -> half8_t {
@@ -287,8 +306,8 @@ __global__ __launch_bounds__(kGemmThreads, MB <= 4 ? 2 : 1) void nf4_fwd_kernel(
                         stage_A(j + 1);
                         stage_X(xbuf(t), j + 1);
                     }
-                    if (q == qB0) stage_B(v0, h0, l0);
-                    if (q == qB1) stage_B(v1, h1, l1);
+                    if (q == qB0) stage_B(v0, h0, l0, 0);
+                    if (q == qB1) stage_B(v1, h1, l1, 1);
                 } else {
                     if (q == 0) {
                         // step t+1's loads have landed (only step t+2's may be in flight)
@@ -297,9 +316,9 @@ __global__ __launch_bounds__(kGemmThreads, MB <= 4 ? 2 : 1) void nf4_fwd_kernel(
                     }
                     if (q == qA3) {
                         stage_A(0);
-                        stage_B(v0, h0, l0);
+                        stage_B(v0, h0, l0, 0);
                     }
-                    if (q == qB13) stage_B(v1, h1, l1);
+                    if (q == qB13) stage_B(v1, h1, l1, 1);
                     if (q == qBar) {
                         // every wave is past step t's slots: refill them with step t+3 (zeros
                         // past the split's end). Past the last step the reads above and below
@@ -324,39 +343,87 @@ __global__ __launch_bounds__(kGemmThreads, MB <= 4 ? 2 : 1) void nf4_fwd_kernel(
     // ---- epilogue: bias, one fp16 rounding, stores (or, with split-K, the fp32 partial slab).
     // Both paths end in their own stores, so the accumulators never meet at a control-flow merge
     // (which makes the register allocator copy all of them).
+    // Output tiles go through LDS so that every store instruction writes whole row segments
+    // (a lane's own fragment is 16 columns of one token row; stored directly, each instruction
+    // would scatter 16-byte pieces over 32 rows). The staging area is this wave's own weight ring
+    // (its loads have all landed), so no barrier is needed: LDS operations of one wave complete
+    // in order. A 32-row tile of `cols` columns has rows `cols * 2 + 16` bytes apart (no bank
+    // conflicts on the fragment writes).
+    uint8_t* stage = wring;
+    auto stage_put = [&](int tile, int cols, int col0, const uint32_t* o) __attribute__((always_inline)) {
+        uint8_t* p = stage + tile * 32 * (cols * 2 + 16) + l32 * (cols * 2 + 16) + col0 * 2;
+        *(u32x4_t*)p = u32x4_t{o[0], o[1], o[2], o[3]};
+        *(u32x4_t*)(p + 16) = u32x4_t{o[4], o[5], o[6], o[7]};
+    };
+    // rows m_first .. m_first + 31, columns n_first .. n_first + cols - 1 of out (row stride ld)
+    auto stage_out = [&](int tile, int cols, _Float16* out, int64_t ld, int m_first, int n_first)
+                         __attribute__((always_inline)) {
+        const int cpr = cols / 8;  // 16-byte chunks per row
+#pragma unroll
+        for (int q = 0; q < cols / 16; ++q) {
+            const int c = q * 64 + lane, row = c / cpr, cc = c % cpr;
+            const u32x4_t v = *(const u32x4_t*)(stage + tile * 32 * (cols * 2 + 16) + row * (cols * 2 + 16) + cc * 16);
+            const int m = m_first + row, n = n_first + 8 * cc;
+            if (m < M && n < N)  // n % 8 == 0: a chunk is wholly inside or past the end
+                *(u32x4_t*)(out + (int64_t)m * ld + n) = v;
+        }
+    };
+    auto load_bias16 = [&](const _Float16* bp, int nb, float* bias) __attribute__((always_inline)) {
+        // two 16-byte loads (n % 8 == 0, so each is wholly inside or past the end)
+        const rsrc_t brs = make_rsrc(bp, bp != nullptr ? (uint32_t)N * 2u : 0u);
+        const half8_t b0 = __builtin_bit_cast(half8_t, bload128(brs, (uint32_t)nb * 2u));
+        const half8_t b1 = __builtin_bit_cast(half8_t, bload128(brs, (uint32_t)nb * 2u + 16u));
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            bias[r] = (float)b0[r];
+            bias[r + 8] = (float)b1[r];
+        }
+    };
     auto store = [&]() __attribute__((always_inline)) {
+        // lane: columns nw0 + 32 b + 16 g .. + 15 of token row m0 + 32 i + l32; the wave's 32 x 64
+        // tile per i
+        float bias[2][16];
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            const int nb = nw0 + 32 * b + 16 * g;  // this lane's 16 consecutive output columns
-            // bias: two 16-byte loads (n % 8 == 0, so each is wholly inside or past the end)
-            const rsrc_t brs = make_rsrc(G.bias, G.bias != nullptr ? (uint32_t)N * 2u : 0u);
-            const half8_t b0 = __builtin_bit_cast(half8_t, bload128(brs, (uint32_t)nb * 2u));
-            const half8_t b1 = __builtin_bit_cast(half8_t, bload128(brs, (uint32_t)nb * 2u + 16u));
-            float bias[16];
+        for (int b = 0; b < 2; ++b) load_bias16(G.bias, nw0 + 32 * b + 16 * g, bias[b]);
 #pragma unroll
-            for (int r = 0; r < 8; ++r) {
-                bias[r] = (float)b0[r];
-                bias[r + 8] = (float)b1[r];
-            }
+        for (int i = 0; i < MB; ++i) {
 #pragma unroll
-            for (int i = 0; i < MB; ++i) {
-                const int m = m0 + 32 * i + l32;
-                if (m >= M) continue;
+            for (int b = 0; b < 2; ++b) {
                 uint32_t o[8];
 #pragma unroll
                 for (int r = 0; r < 16; r += 2)
-                    o[r >> 1] = pack_half2(acc[i * 2 + b][r] + bias[r], acc[i * 2 + b][r + 1] + bias[r + 1]);
-                _Float16* yrow = G.y + (int64_t)m * G.ldy + nb;
-                if (nb + 16 <= N) {
-                    *(u32x4_t*)(yrow) = u32x4_t{o[0], o[1], o[2], o[3]};
-                    *(u32x4_t*)(yrow + 8) = u32x4_t{o[4], o[5], o[6], o[7]};
-                } else {
-                    for (int r = 0; r < 16 && nb + r < N; ++r)
-                        yrow[r] = __builtin_bit_cast(_Float16, (uint16_t)((o[r >> 1] >> (16 * (r & 1))) & 0xFFFFu));
-                }
+                    o[r >> 1] = pack_half2(acc[i * 2 + b][r] + bias[b][r], acc[i * 2 + b][r + 1] + bias[b][r + 1]);
+                stage_put(0, 64, 32 * b + 16 * g, o);
             }
+            stage_out(0, 64, G.y, G.ldy, m0 + 32 * i, nw0);
         }
     };
+    if (glu) {
+        // gate = fp16(acc0 + bias0), up = fp16(acc1 + bias1), h = fp16(silu(gate) up): this
+        // lane's 16 consecutive columns nw0 + 16 g .. + 15 of each, token rows m0 + 32 i + l32;
+        // three 32 x 32 tiles per i
+        const int nb = nw0 + 16 * g;
+        float bias[2][16];
+        load_bias16(G.bias, nb, bias[0]);
+        load_bias16(G1.bias, nb, bias[1]);
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+            uint32_t og[8], ou[8], oh[8];
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                og[r >> 1] = pack_half2(acc[i * 2][r] + bias[0][r], acc[i * 2][r + 1] + bias[0][r + 1]);
+                ou[r >> 1] = pack_half2(acc[i * 2 + 1][r] + bias[1][r], acc[i * 2 + 1][r + 1] + bias[1][r + 1]);
+                oh[r >> 1] = swiglu_fwd2(og[r >> 1], ou[r >> 1]);
+            }
+            stage_put(0, 32, 16 * g, og);
+            stage_put(1, 32, 16 * g, ou);
+            stage_put(2, 32, 16 * g, oh);
+            if (G.y != nullptr) stage_out(0, 32, G.y, G.ldy, m0 + 32 * i, nw0);
+            if (G1.y != nullptr) stage_out(1, 32, G1.y, G1.ldy, m0 + 32 * i, nw0);
+            stage_out(2, 32, a.h, a.ldh, m0 + 32 * i, nw0);
+        }
+        return;
+    }
     if (a.splits > 1) {
         // fp32 partial sums into this split's slab (bias and rounding happen in the reduction)
         float* slab = a.partials + (int64_t)split * a.m * a.ncols;

@@ -7,8 +7,6 @@ namespace dk {
 
 constexpr int kEwThreads = 256;
 
-__device__ __forceinline__ float sigmoidf_(float g) { return 1.0f / (1.0f + expf(-g)); }
-
 __global__ __launch_bounds__(kEwThreads) void swiglu_fwd_kernel(const _Float16* __restrict__ g,
                                                                  const _Float16* __restrict__ u,
                                                                  _Float16* __restrict__ o,
@@ -17,17 +15,13 @@ __global__ __launch_bounds__(kEwThreads) void swiglu_fwd_kernel(const _Float16* 
     if (i0 + 8 <= n) {
         const half8_t gv = *(const half8_t*)(g + i0);
         const half8_t uv = *(const half8_t*)(u + i0);
-        half8_t ov;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float gf = (float)gv[e];
-            ov[e] = (_Float16)(gf * sigmoidf_(gf) * (float)uv[e]);
-        }
-        *(half8_t*)(o + i0) = ov;
+        const u32x4_t g4 = __builtin_bit_cast(u32x4_t, gv), u4 = __builtin_bit_cast(u32x4_t, uv);
+        *(u32x4_t*)(o + i0) = u32x4_t{swiglu_fwd2(g4[0], u4[0]), swiglu_fwd2(g4[1], u4[1]),
+                                      swiglu_fwd2(g4[2], u4[2]), swiglu_fwd2(g4[3], u4[3])};
     } else {
         for (int64_t i = i0; i < n; ++i) {
-            const float gf = (float)g[i];
-            o[i] = (_Float16)(gf * sigmoidf_(gf) * (float)u[i]);
+            const uint32_t h = swiglu_fwd2(__builtin_bit_cast(uint16_t, g[i]), __builtin_bit_cast(uint16_t, u[i]));
+            o[i] = __builtin_bit_cast(_Float16, (uint16_t)(h & 0xFFFFu));
         }
     }
 }
@@ -46,19 +40,19 @@ __global__ __launch_bounds__(kEwThreads) void swiglu_bwd_kernel(const _Float16* 
         half8_t dgv, duv;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const float G = (float)Gv[e], gf = (float)gv[e], uf = (float)uv[e];
-            const float s = sigmoidf_(gf);
-            duv[e] = (_Float16)(G * gf * s);
-            dgv[e] = (_Float16)(G * uf * s * (1.0f + gf * (1.0f - s)));
+            float dgf, duf;
+            swiglu_bwd1((float)Gv[e], (float)gv[e], (float)uv[e], dgf, duf);
+            dgv[e] = (_Float16)dgf;
+            duv[e] = (_Float16)duf;
         }
         *(half8_t*)(dg + i0) = dgv;
         *(half8_t*)(du + i0) = duv;
     } else {
         for (int64_t i = i0; i < n; ++i) {
-            const float G = (float)gr[i], gf = (float)g[i], uf = (float)u[i];
-            const float s = sigmoidf_(gf);
-            du[i] = (_Float16)(G * gf * s);
-            dg[i] = (_Float16)(G * uf * s * (1.0f + gf * (1.0f - s)));
+            float dgf, duf;
+            swiglu_bwd1((float)gr[i], (float)g[i], (float)u[i], dgf, duf);
+            du[i] = (_Float16)duf;
+            dg[i] = (_Float16)dgf;
         }
     }
 }

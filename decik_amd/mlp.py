@@ -2,10 +2,11 @@
 
 Mirrors the reference's RecomputedMLP (solution/mlp.py:62-110) and its patch of Qwen2MLP
 (solution/mlp.py:113-162):
-- forward: gate and up share x, so they are ONE fused launch (two weights, one X tile stream);
-  SwiGLU (HIP kernel); down is a second fused launch. Output fp16, as the reference returns.
-- backward: dH = dY . W_down (fused launch); gate and up are recomputed (recompute=True, the
-  reference's default) or kept from the forward; SwiGLU backward in place; then
+- forward: gate and up share x, so they are ONE fused launch (two weights, one X tile stream)
+  whose epilogue also applies SwiGLU; down is a second fused launch. Output fp16, as the
+  reference returns.
+- backward: gate and up are recomputed (recompute=True, the reference's default) or kept from
+  the forward; dH = dY . W_down and the SwiGLU backward are one fused launch; then
   dX = dgate . W_gate + dup . W_up as ONE fused launch that accumulates both products in fp32
   and rounds once (the reference sums two fp16 matmul results in fp32, solution/mlp.py:106-109).
 No fp16 weight is ever materialised.
@@ -15,7 +16,6 @@ import torch
 
 from . import nf4
 from ._state import on_gpu
-from .swiglu import swiglu_bwd, swiglu_fwd
 
 
 def _w(module):
@@ -27,11 +27,11 @@ def _bias16(module):
     return None if b is None else b.to(torch.float16)
 
 
-def mlp_forward(x16, gate, up, down, bias=(None, None, None)):
-    """(out, gate_out, up_out) for (packed, quant_state) pairs gate/up/down; x16 [M, K] fp16."""
-    g, u = nf4.linear_forward(x16, [dict(packed=gate[0], qs=gate[1], bias=bias[0]),
-                                    dict(packed=up[0], qs=up[1], bias=bias[1])])
-    h = swiglu_fwd(g, u)
+def mlp_forward(x16, gate, up, down, bias=(None, None, None), keep_gate_up=True):
+    """(out, gate_out, up_out) for (packed, quant_state) pairs gate/up/down; x16 [M, K] fp16.
+    keep_gate_up=False: gate_out and up_out are not stored (None)."""
+    g, u, h = nf4.glu_forward(x16, dict(packed=gate[0], qs=gate[1], bias=bias[0]),
+                              dict(packed=up[0], qs=up[1], bias=bias[1]), keep_gate_up=keep_gate_up)
     (out,) = nf4.linear_forward(h, [dict(packed=down[0], qs=down[1], bias=bias[2])])
     return out, g, u
 
@@ -39,14 +39,13 @@ def mlp_forward(x16, gate, up, down, bias=(None, None, None)):
 def mlp_backward(grad16, x16, gate, up, down, saved=None, bias=(None, None, None), dx_fp32=False):
     """dX of the MLP; `saved` = (gate_out, up_out) from the forward, else they are recomputed."""
     m, k = x16.shape
-    n_inter = int(gate[1].shape[0])
-    gh = nf4.linear_backward([dict(packed=down[0], qs=down[1], dy=grad16)], m, n_inter)
     if saved is None:
         g, u = nf4.linear_forward(x16, [dict(packed=gate[0], qs=gate[1], bias=bias[0]),
                                         dict(packed=up[0], qs=up[1], bias=bias[1])])
     else:
         g, u = saved
-    dgate, dup = swiglu_bwd(gh, g, u, out=(g, u) if saved is None else None)
+    dgate, dup = nf4.linear_backward_swiglu(dict(packed=down[0], qs=down[1], dy=grad16), g, u,
+                                            out=(g, u) if saved is None else None)
     return nf4.linear_backward([dict(packed=gate[0], qs=gate[1], dy=dgate),
                                 dict(packed=up[0], qs=up[1], dy=dup)], m, k, dx_fp32=dx_fp32)
 
@@ -61,7 +60,7 @@ class FusedMLP(torch.autograd.Function):
         shape = x.shape
         x16 = x.to(torch.float16).reshape(-1, shape[-1]).contiguous()
         gate, up, down = (gate_p, gate_qs), (up_p, up_qs), (down_p, down_qs)
-        out, g, u = mlp_forward(x16, gate, up, down, biases)
+        out, g, u = mlp_forward(x16, gate, up, down, biases, keep_gate_up=not recompute)
         ctx.weights, ctx.biases, ctx.recompute = (gate, up, down), biases, recompute
         ctx.shape, ctx.in_dtype = shape, x.dtype
         if recompute:

@@ -174,6 +174,68 @@ def linear_backward(items, m, k, dx=None, dx_fp32=False, lora_rank=0):
     return dx
 
 
+def _fwd_group(g, it, dev, keep):
+    qs = it["qs"]
+    w, kp = weight_desc(it["packed"], qs, dev, _scales(it["packed"], qs, dev))
+    keep += kp
+    g.w = w
+    bias = it.get("bias")
+    g.bias = None if bias is None else bias.data_ptr()
+    u, b = it.get("lora_u"), it.get("lora_b")
+    g.lora_u = None if u is None else u.data_ptr()
+    g.lora_b = None if b is None else b.data_ptr()
+    g.lora_scale = float(it.get("lora_scale", 0.0))
+    keep += [bias, u, b]
+
+
+def glu_forward(x16, gate, up, keep_gate_up=True, lora_rank=0):
+    """(gate_out, up_out, h) with h = silu(gate_out) * up_out, one launch (dk_nf4_glu_fwd).
+
+    gate / up: dicts as for linear_forward (packed, qs, optional bias, lora_u, lora_b,
+    lora_scale). keep_gate_up=False skips storing gate_out and up_out (returned as None)."""
+    dev = x16.device
+    x2 = _rows(x16)
+    m, k = x2.shape
+    n = int(gate["qs"].shape[0])
+    groups = (LinearFwdGroup * 2)()
+    keep, outs = [x2], []
+    for g, it in enumerate((gate, up)):
+        _fwd_group(groups[g], it, dev, keep)
+        out = torch.empty((m, n), dtype=torch.float16, device=dev) if keep_gate_up else None
+        groups[g].y = None if out is None else out.data_ptr()
+        groups[g].ldy = n
+        outs.append(out)
+    h = torch.empty((m, n), dtype=torch.float16, device=dev)
+    check(lib().dk_nf4_glu_fwd(ptr(x2), m, k, x2.stride(0), groups, int(lora_rank), ptr(h), n,
+                               stream_of(dev)))
+    return outs[0], outs[1], h
+
+
+def linear_backward_swiglu(item, gate, up, out=None, lora_rank=0):
+    """(dgate, dup) of SwiGLU for G = dY . W of one weight (dk_nf4_linear_bwd_swiglu): the MLP's
+    down-projection input gradient and the SwiGLU backward in one launch. item: dict with packed,
+    qs, dy (and optional lora_gu, lora_a); gate, up fp16 [m, k]; out = (dgate, dup) buffers, which
+    may be gate and up themselves."""
+    dev = gate.device
+    m, k = gate.shape
+    dgate, dup = out if out is not None else (torch.empty_like(gate), torch.empty_like(up))
+    assert gate.is_contiguous() and up.is_contiguous() and dgate.is_contiguous() and dup.is_contiguous()
+    groups = (LinearBwdGroup * 1)()
+    qs = item["qs"]
+    w, keep = weight_desc(item["packed"], qs, dev, _scales(item["packed"], qs, dev))
+    dy = _rows(item["dy"])
+    groups[0].w = w
+    groups[0].dy = dy.data_ptr()
+    groups[0].lddy = dy.stride(0)
+    gu, a = item.get("lora_gu"), item.get("lora_a")
+    groups[0].lora_gu = None if gu is None else gu.data_ptr()
+    groups[0].lora_a = None if a is None else a.data_ptr()
+    keep += [dy, gu, a]
+    check(lib().dk_nf4_linear_bwd_swiglu(groups, m, k, int(lora_rank), ptr(gate), ptr(up), k,
+                                         ptr(dgate), ptr(dup), k, stream_of(dev)))
+    return dgate, dup
+
+
 def _fusable(x16, packed, qs, bias16):
     k = x16.shape[-1]
     return (fused_ok(qs, k) and x16.is_contiguous() and _aligned(x16) and _aligned(packed)

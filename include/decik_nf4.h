@@ -21,6 +21,10 @@
  *                                               (solution/nf4.py:99-104); the summed input
  *                                               gradients of RecomputedMLP (solution/mlp.py:106-109)
  *                                               and of the LoRA branch (solution/attn.py:257)
+ *   dk_nf4_glu_fwd                            <- gate and up projections + _swiglu_fwd of the
+ *                                               Qwen2 MLP forward (solution/mlp.py:69-71)
+ *   dk_nf4_linear_bwd_swiglu                  <- matmul(g16, w_down) + _swiglu_bwd of the MLP
+ *                                               backward (solution/mlp.py:95, 104)
  *   dk_lora_down / dk_lora_bwd                <- the rank-r products of LoRAPairFromNorm
  *                                               (solution/attn.py:225-227, 251-257)
  *   dk_swiglu_fwd / dk_swiglu_bwd             <- example_swiglu_fwd/bwd_kernel
@@ -96,9 +100,9 @@ int dk_nf4_dequant_batched(const dk_nf4_weight* ws, uint16_t* const* outs, int c
  * absmax2 chain), so a caller may compute it once per frozen weight and reuse it. */
 int dk_nf4_block_scales(const dk_nf4_weight* w, float* scales, void* stream);
 
-/* Bytes of workspace dk_nf4_linear_fwd needs for these shapes (0 if none). A workspace must
- * be zero-filled once when allocated; the library leaves it zeroed after every call. Calls
- * that run concurrently (different streams) need different workspaces. */
+/* Bytes of workspace dk_nf4_linear_fwd needs for these shapes (0 if none): the fp32 partial
+ * sums of a split contraction. Its contents need not be initialised and are dead after the
+ * call. Calls that run concurrently (different streams) need different workspaces. */
 int64_t dk_nf4_linear_fwd_workspace(int64_t m, int64_t k, const int64_t* ns, int ngroups);
 
 /* Fused dequant x fp16 GEMM, forward, for up to DK_MAX_GROUPS weights that share X
@@ -107,6 +111,17 @@ int dk_nf4_linear_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
                       const dk_linear_fwd_group* groups, int ngroups, int lora_rank,
                       void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Gate and up projections and SwiGLU in one launch: groups[0] = gate, groups[1] = up (one shape
+ * [n, k]; bias and LoRA as in dk_nf4_linear_fwd), h = fp16(silu(gate) * up) [m, n] (row stride
+ * ldh) from the fp16-rounded gate and up -- the same bits as dk_nf4_linear_fwd followed by
+ * dk_swiglu_fwd. groups[i].y may be NULL (not stored) for plain weights with blocksize >= 64 and
+ * k % 64 == 0; other weights run as the grouped launch then the SwiGLU kernel and need both y,
+ * with rows contiguous (ldy = ldh = n). No workspace. */
+int dk_nf4_glu_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
+                   const dk_linear_fwd_group* groups, int lora_rank, uint16_t* h, int64_t ldh,
+                   void* stream);
+
+/* As dk_nf4_linear_fwd_workspace, for dk_nf4_linear_bwd. */
 int64_t dk_nf4_linear_bwd_workspace(int64_t m, int64_t k, const int64_t* ns, int ngroups);
 
 /* Fused dequant x fp16 GEMM, input gradient: dX = sum over groups of dY_g.W_g (+ GU_g.A_g),
@@ -115,6 +130,15 @@ int64_t dk_nf4_linear_bwd_workspace(int64_t m, int64_t k, const int64_t* ns, int
 int dk_nf4_linear_bwd(const dk_linear_bwd_group* groups, int ngroups, int64_t m, int64_t k,
                       void* dx, int64_t lddx, int dx_fp32, int lora_rank, void* workspace,
                       int64_t workspace_bytes, void* stream);
+
+/* Input gradient of one weight (the MLP's down projection, group->w [n, k]) with the SwiGLU
+ * backward in its epilogue: G = fp16(dY . W) [m, k] is never stored; dgate =
+ * fp16(G up s (1 + gate (1 - s))), dup = fp16(G gate s), s = sigmoid(gate) -- the same bits as
+ * dk_nf4_linear_bwd followed by dk_swiglu_bwd. gate, up fp16 [m, k] (row stride ldgu); dgate,
+ * dup fp16 [m, k] (row stride ldd), which may alias gate and up. No workspace. */
+int dk_nf4_linear_bwd_swiglu(const dk_linear_bwd_group* group, int64_t m, int64_t k, int lora_rank,
+                             const uint16_t* gate, const uint16_t* up, int64_t ldgu, uint16_t* dgate,
+                             uint16_t* dup, int64_t ldd, void* stream);
 
 /* U = fp16(X . A^T): X fp16 [m, k] (row stride ldx), A fp16 [rank, k], U fp16 [m, rank]. */
 int dk_lora_down(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const uint16_t* a,
