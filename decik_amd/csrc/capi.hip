@@ -193,10 +193,15 @@ void finish_plan(GemmPlan& p, int64_t m, int64_t ncols) {
     if (p.partial_floats * 4 >= (int64_t(1) << 34)) no_split(p);  // 16 GiB: never worth it
 }
 
+// waves 4: nf4_fwd_kernel (two work-groups per CU for mb <= 4); waves 8: nf4_fwd8_kernel (one
+// work-group of eight waves per CU, 32*mb tokens x 256 weight rows)
 constexpr VariantCost kFwdVariants[] = {{1, 4, kFwdBN, 3, 2.35, 0.65},
                                        {2, 4, kFwdBN, 2, 2.23, 0.65},
                                        {4, 4, kFwdBN, 2, 3.10, 0.65},
-                                       {8, 4, kFwdBN, 1, 2.94, 0.85}};
+                                       {8, 4, kFwdBN, 1, 2.94, 0.85},
+                                       {8, 8, kFwdBN, 1, 2.60, 0.80},
+                                       {9, 8, kFwdBN, 1, 2.95, 0.80}};
+constexpr int kNumFwdVariants = sizeof(kFwdVariants) / sizeof(kFwdVariants[0]);
 constexpr VariantCost kBwdVariants[] = {{2, 4, 256, 2, 3.20, 0.90},
                                        {2, 8, 512, 1, 2.60, 1.0},
                                        {4, 8, 512, 1, 3.40, 1.0}};
@@ -218,11 +223,11 @@ GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool glu
             ncols += ns[g];
         }
     }
-    const VariantCost* v = plan_override("DECIK_FWD_PLAN", kFwdVariants, 4, p.steps, &p.splits);
+    const VariantCost* v = plan_override("DECIK_FWD_PLAN", kFwdVariants, kNumFwdVariants, p.steps, &p.splits);
     if (v != nullptr && (glu || no_split)) p.splits = 1;
     if (v == nullptr) {
         const int64_t nt = p.n_tiles;
-        v = choose_plan(kFwdVariants, 4, m, ncols, p.steps, [nt](const VariantCost&) { return nt; },
+        v = choose_plan(kFwdVariants, kNumFwdVariants, m, ncols, p.steps, [nt](const VariantCost&) { return nt; },
                         &p.splits, (glu || no_split) ? 1 : 32);
     }
     p.mt = v->rows_blocks;
@@ -409,7 +414,8 @@ static int linear_fwd_impl(const std::string& name, const uint16_t* x, int64_t m
     const int64_t wgs = (int64_t)p.m_tiles * p.n_tiles * p.splits;
     if (wgs > INT32_MAX / 2 || ncols > INT32_MAX / 2) return fail(name + ": problem too large");
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    if (check_hip(launch_fwd(a, p.mt, pad8((int)wgs), st), "dk_nf4_linear_fwd launch")) return 1;
+    const hipError_t le = p.waves == 8 ? launch_fwd8(a, p.mt, pad8((int)wgs), st) : launch_fwd(a, p.mt, pad8((int)wgs), st);
+    if (check_hip(le, "dk_nf4_linear_fwd launch")) return 1;
     if (p.splits <= 1) return 0;
     ReduceArgs r{};
     r.partials = a.partials;

@@ -120,7 +120,8 @@ struct ReduceArgs {
 // Launch plans (tile size, split-K factor) chosen by the host.
 struct GemmPlan {
     int mt;        // 32-row token blocks per tile
-    int waves;     // backward: waves per work-group (64 output columns each)
+    int waves;     // waves per work-group (forward: 4 = nf4_fwd_kernel, 8 = nf4_fwd8_kernel;
+                   // backward: 4 or 8, 64 output columns each)
     int m_tiles;
     int n_tiles;   // output column tiles (fwd: weight rows / 256; bwd: k / 512)
     int steps;     // main-loop steps over the whole contraction
@@ -130,6 +131,8 @@ struct GemmPlan {
 };
 
 hipError_t launch_fwd(const FwdArgs& a, int mb, int grid, hipStream_t s);
+// 8-wave forward kernel (32 weight rows x 32*mb tokens per wave), mb = 8 or 9
+hipError_t launch_fwd8(const FwdArgs& a, int mb, int grid, hipStream_t s);
 hipError_t launch_bwd(const BwdArgs& a, int mb, int waves, int grid, hipStream_t s);
 hipError_t launch_splitk_reduce(const ReduceArgs& a, hipStream_t s);
 

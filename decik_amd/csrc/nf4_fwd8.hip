@@ -1,0 +1,369 @@
+// Fused NF4 dequant x fp16 GEMM, forward, for launches with many token rows (the same product as
+// nf4_fwd_kernel: Y = X.W^T + bias + LoRA, solution/nf4.py:93-96, and the GLU mode of
+// dk_nf4_glu_fwd, solution/mlp.py:69-71).
+//
+// Why a second kernel: with 128-token tiles every packed weight is dequantized once per 128
+// tokens, and the dequant (code-book address, code-book read, fp32 multiply, fp16 pack per
+// weight) is ~6 VALU instructions per 32x32x16 MFMA -- more than the SIMD co-issues with the
+// matrix pipe (~4). Here a work-group is 8 waves (two per SIMD, one work-group per CU) on a tile
+// of 32*MB tokens (MB = 8 or 9: 256 or 288 tokens) x 256 weight rows; each wave owns 32 weight
+// rows and all 32*MB tokens, so each dequantized weight feeds MB MFMAs (~3 VALU per MFMA), and
+// the X tile, staged once per step for all eight waves, is read by each wave at one 16-byte
+// fragment per MFMA.
+//
+// Per wave and 64-wide step: one 16-byte packed load per lane (row arow_to_n(l32), k half
+// g = lane / 32) and the row's block statistics, through a per-wave LDS ring three steps deep;
+// the X tile through a shared ring three steps deep (buffer_load ... lds). Slice j (16 of k) =
+// one unpacked dword of 8 weights (A operand) x MB X fragments (B operands). The loop is
+// software-pipelined one slice ahead: between the MFMAs of slice j the wave refills each X
+// fragment register right after its MFMA has read it and unpacks slice j + 1 in three stages
+// (code-book addresses, code-book reads, scaling and fp16 packing). Slice 3 holds the step
+// boundary (own-slot fetch, wait, barrier, refill of the freed ring slots).
+//
+// Epilogue: each token block's 32 x 256 output tile goes through LDS (the X ring, after a
+// barrier) and leaves as whole 512-byte rows; GLU tiles pair the gate wave (0..3) and up wave
+// (4..7) of the same columns there, so the SwiGLU needs no register exchange.
+#include "gemm_common.h"
+
+namespace dk {
+
+constexpr int kF8Waves = 8;
+constexpr int kF8Threads = 64 * kF8Waves;
+constexpr int kF8Header = 1024;  // code2 table
+constexpr int kF8Dummy = 1024;   // target of the X loads of waves past the tile (zeros)
+
+// Per-wave ring slot of one step: 1 KB packed bytes (lane: 16 bytes), then 64 statistics dword
+// slots (codes or fp32 absmax at +1024, absmax2 at +1280). Narrow (every blocksize >= 64,
+// k % 64 == 0): slot l32 holds row arow(l32)'s block (lanes g = 1 load zeros into slots 32..63);
+// wide: slot lane holds the block of the lane's row and k half.
+constexpr int kF8WSlot = 1536;
+
+__host__ __device__ constexpr size_t fwd8_smem_bytes(int mb) {
+    return kF8Header + kF8Dummy + 3 * (size_t)(32 * mb * 128) + kF8Waves * 3 * (size_t)kF8WSlot;
+}
+
+template <int MB, bool NESTED>
+__global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a) {
+    constexpr int BM = 32 * MB;
+    constexpr int XBUF = BM * 128;                               // bytes of one X ring buffer
+    constexpr int XCH = BM * 8;                                  // its 16-byte chunks
+    constexpr int XPT = (XCH + kF8Threads - 1) / kF8Threads;     // X loads per thread and step
+    constexpr int NL = XPT + 1 + (NESTED ? 2 : 1);               // loads per thread and step
+    static_assert(XCH % 64 == 0, "a wave's X load is wholly inside or past the tile");
+    static_assert(2 * 32 * (256 * 4 + 16) <= 3 * XBUF, "epilogue staging fits the X ring");
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ float lut[32];  // code books (gate, up in GLU mode; the same book otherwise)
+    float* c2 = (float*)smem;
+    uint8_t* dummy = smem + kF8Header;
+    uint8_t* xs = dummy + kF8Dummy;
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int l32 = lane & 31, g = lane >> 5;
+    const bool wide = a.wide_stats != 0;
+    const bool glu = a.glu != 0;
+    const int wslot_bytes = kF8WSlot;
+
+    const int L = xcd_logical_id();
+    if (L >= a.m_tiles * a.n_tiles * a.splits) return;
+    const int m_tile = L % a.m_tiles;
+    const int rest = L / a.m_tiles;
+    const int n_tile = rest % a.n_tiles;
+    const int split = rest / a.n_tiles;
+
+    int gi = 0;  // the weight of this tile (normal mode)
+#pragma unroll
+    for (int i = 1; i < kMaxGroups; ++i)
+        if (i < a.ngroups && n_tile >= a.g[i].tile_begin) gi = i;
+    // this wave's weight: GLU waves 0..3 the gate weight, 4..7 the up weight (wave-uniform index)
+    const int wgi = __builtin_amdgcn_readfirstlane(glu ? (wave >> 2) : gi);
+    const FwdGroupDev& G = a.g[wgi];
+    const NF4Dev& W = G.w;
+    const int M = sgpr(a.m), K = sgpr(a.k), N = sgpr((int)W.n), ldx = sgpr((int)a.ldx);
+    const uint32_t bs_shift = sgpr((uint32_t)W.bs_shift), bs2_shift = sgpr((uint32_t)W.bs2_shift);
+    const int m0 = m_tile * BM;
+    // the tile's first weight row and this wave's 32 rows within the tile's columns
+    const int tile_n0 = glu ? n_tile * (kFwdBN / 2) : (n_tile - G.tile_begin) * kFwdBN;
+    const int wcol = glu ? 32 * (wave & 3) : 32 * wave;  // the wave's first column in the tile
+    const int nw0 = tile_n0 + wcol;
+    const int ks0 = split * a.ksteps_per_split;
+    const int ks1 = min(a.ksteps, ks0 + a.ksteps_per_split);
+
+    if (tid < 32) lut[tid] = a.g[glu ? (tid >> 4) : gi].w.code[tid & 15];
+    if constexpr (NESTED) {
+        if (tid < 256) c2[tid] = W.code2[tid];
+    }
+    const float offset = NESTED ? *W.offset : 0.0f;
+    // this wave's code book (bytes 64 * book of the static table), folded into the lookup
+    // addresses (see nib_addrs)
+    const uint32_t book4 = (uint32_t)(glu ? 64 * (wave >> 2) : 0) * 0x01010101u;
+
+    const rsrc_t xrs = make_rsrc(a.x, a.x_bytes);
+    const rsrc_t wrs = make_rsrc(W.packed, W.packed_bytes);
+    const rsrc_t ars = make_rsrc(NESTED ? (const void*)W.absmax8 : (const void*)W.absmaxf, W.absmax_bytes);
+    const rsrc_t a2rs = make_rsrc(W.absmax2, W.absmax2_bytes);
+    const int wrow = nw0 + arow_to_n(l32);  // this lane's A row
+    const bool rowok = wrow < N;
+    const int xsw = (l32 >> 1) & 7;          // LDS swizzle of this lane's X rows
+
+    uint8_t* wring = xs + 3 * XBUF + wave * (3 * wslot_bytes);
+    auto ring = [&](int t) __attribute__((always_inline)) { return (t - ks0) % 3; };
+    auto xbuf = [&](int t) -> uint8_t* { return xs + ring(t) * XBUF; };
+    auto wslot = [&](int t) -> uint8_t* { return wring + ring(t) * wslot_bytes; };
+
+    // Loads of step t (`live` false: zeros, keeping the ring's load count uniform).
+    auto load_step = [&](int t, bool live) __attribute__((always_inline)) {
+        const int k0 = t * kFwdBK;
+        uint8_t* xd = xbuf(t);
+#pragma unroll
+        for (int h = 0; h < XPT; ++h) {
+            // chunk q lands at q * 16 = row * 128 + pc * 16; waves past the tile load zeros
+            // into the dummy area
+            const int q = tid + kF8Threads * h;
+            const int row = q >> 3, pc = q & 7;
+            const int c = pc ^ ((row >> 1) & 7);
+            const int gm = m0 + row, gk = k0 + 8 * c;
+            const int wq0 = kF8Threads * h + 64 * wave;  // the wave's first chunk (uniform)
+            uint8_t* dst = wq0 < XCH ? xd + wq0 * 16 : dummy;
+            bload128_lds(xrs, dst, off_if(live && q < XCH && gm < M && gk < K, (uint32_t)(gm * ldx + gk) * 2u));
+        }
+        const int krun = k0 + 32 * g;
+        uint8_t* slot = wslot(t);
+        bload128_lds(wrs, slot, off_if(live && rowok && krun < K, ((uint32_t)wrow * (uint32_t)K + (uint32_t)krun) >> 1));
+        // statistics: narrow -- lanes g = 0 fetch their row's block at k0 (g = 1 lanes load zeros
+        // into unused slots); wide -- every lane its row's block at its own k half
+        const int kb = wide ? krun : k0;
+        const bool sok = live && rowok && kb < K && (wide || g == 0);
+        const uint32_t blk = ((uint32_t)wrow * (uint32_t)K + (uint32_t)kb) >> bs_shift;
+        if constexpr (NESTED) {
+            bload8_lds(ars, slot + 1024, off_if(sok, blk));
+            bload32_lds(a2rs, slot + 1280, off_if(sok, (blk >> bs2_shift) * 4u));
+        } else {
+            bload32_lds(ars, slot + 1024, off_if(sok, blk * 4u));
+        }
+    };
+    // fp32 scale of this lane's row at step t (0 outside the weight)
+    auto scale_of = [&](const uint8_t* slot, int t) __attribute__((always_inline)) -> float {
+        const int si = wide ? lane : l32;
+        const bool ok = rowok && t * kFwdBK + 32 * g < K;
+        float sc;
+        if constexpr (NESTED) {
+            const uint32_t q = slot[1024 + 4 * si];
+            const float a2 = *(const float*)(slot + 1280 + 4 * si);
+            sc = c2[q] * a2 + offset;
+        } else {
+            sc = *(const float*)(slot + 1024 + 4 * si);
+        }
+        return ok ? sc : 0.0f;
+    };
+    auto xfrag = [&](const uint8_t* xb, int i, int j) __attribute__((always_inline)) -> half8_t {
+        return *(const half8_t*)(xb + (32 * i + l32) * 128 + (((4 * g + j) ^ xsw) << 4));
+    };
+
+    float16_t acc[MB];  // token block i
+#pragma unroll
+    for (int i = 0; i < MB; ++i) acc[i] = float16_t{};
+
+    // LoRA term s * U.B^T first (split 0 only), as in nf4_fwd_kernel, for this wave's weight.
+    {
+        const int R = (G.lora_u != nullptr && split == 0) ? sgpr(a.lora_rank) : 0;
+        const float ls = G.lora_scale;
+        const rsrc_t brs = make_rsrc(G.lora_b, (uint32_t)N * (uint32_t)R * 2u);
+        const rsrc_t urs = make_rsrc(G.lora_u, (uint32_t)M * (uint32_t)R * 2u);
+        for (int t0 = 0; t0 < R; t0 += 16) {
+            half8_t bl = __builtin_bit_cast(half8_t, bload128(brs, off_if(rowok, (uint32_t)(wrow * R + t0 + 8 * g) * 2u)));
+#pragma unroll
+            for (int e = 0; e < 8; ++e) bl[e] = (_Float16)((float)bl[e] * ls);
+#pragma unroll
+            for (int i = 0; i < MB; ++i) {
+                const int m = m0 + 32 * i + l32;
+                const half8_t uu = __builtin_bit_cast(half8_t, bload128(urs, off_if(m < M, (uint32_t)(m * R + t0 + 8 * g) * 2u)));
+                acc[i] = mfma32x32x16(bl, uu, acc[i]);
+            }
+        }
+    }
+
+    // Prologue: three steps in flight; wait for the first.
+    load_step(ks0, true);
+    load_step(ks0 + 1, ks0 + 1 < ks1);
+    load_step(ks0 + 2, ks0 + 2 < ks1);
+    wait_vmcnt<2 * NL>();
+    lds_barrier();
+
+    u32x4_t p;  // packed weights of the current step (slice j: dword j)
+    float s;    // their scale
+    auto fetch_step = [&](int t) __attribute__((always_inline)) {
+        const uint8_t* ws = wslot(t);
+        p = *(const u32x4_t*)(ws + 16 * lane);
+        s = scale_of(ws, t);
+    };
+    half8_t xf[MB], w, wn;
+    uint32_t ah, al;  // code-book byte addresses of the next slice (see nib_addrs)
+    float v[8];       // its code-book values
+    fetch_step(ks0);
+#pragma unroll
+    for (int i = 0; i < MB; ++i) xf[i] = xfrag(xbuf(ks0), i, 0);
+    {
+        nib_addrs(p[0], book4, ah, al);
+        u32x4_t o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = pack_half2(lut_at(lut, ah, e) * s, lut_at(lut, al, e) * s);
+        w = __builtin_bit_cast(half8_t, o);
+    }
+    // stage positions (MFMA index after which a stage runs)
+    constexpr int qA = 0, qB = 1, qC = MB - 3;
+    for (int t = ks0; t < ks1; ++t) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int jn = (j + 1) & 3;
+#pragma unroll
+            for (int q = 0; q < MB; ++q) {
+                acc[q] = mfma32x32x16(w, xf[q], acc[q]);
+                if (j == 3 && q == 0) {
+                    // step t+1's loads have landed (only step t+2's may be in flight): fetch this
+                    // wave's packed bytes and scale; after the barrier no wave reads step t's
+                    // slots again: refill them with step t+3. Past the last step these reads
+                    // see stale slots and their values go unused.
+                    wait_vmcnt<NL>();
+                    fetch_step(t + 1);
+                    lds_barrier();
+                    load_step(t + 3, t + 3 < ks1);
+                }
+                // refill the X fragment the MFMA above has read (slice j + 1)
+                xf[q] = xfrag(j < 3 ? xbuf(t) : xbuf(t + 1), q, jn);
+                if (q == (j < 3 ? qA : qA + 1)) nib_addrs(p[jn], book4, ah, al);
+                if (q == (j < 3 ? qB : qB + 1)) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        v[2 * e] = lut_at(lut, ah, e);
+                        v[2 * e + 1] = lut_at(lut, al, e);
+                    }
+                }
+                if (q == qC) {
+                    u32x4_t o;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) o[e] = pack_half2(v[2 * e] * s, v[2 * e + 1] * s);
+                    wn = __builtin_bit_cast(half8_t, o);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            w = wn;
+        }
+    }
+    wait_vmcnt<0>();
+    lds_barrier();  // every wave is done with the X ring: it becomes the staging area
+
+    // ---- epilogue. Lane (l32, g) holds, for token block i, token row m0 + 32 i + l32 and the 16
+    // consecutive columns nw0 + 16 g + r (acc[i][r]).
+    const int colw = wcol + 16 * g;  // ... as a column of the tile
+    float bias[16];
+    {
+        const rsrc_t brs = make_rsrc(G.bias, G.bias != nullptr ? (uint32_t)N * 2u : 0u);
+        const uint32_t nb = (uint32_t)(nw0 + 16 * g);
+        const half8_t b0 = __builtin_bit_cast(half8_t, bload128(brs, nb * 2u));
+        const half8_t b1 = __builtin_bit_cast(half8_t, bload128(brs, nb * 2u + 16u));
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            bias[r] = (float)b0[r];
+            bias[r + 8] = (float)b1[r];
+        }
+    }
+    if (a.splits > 1) {
+        // fp32 partial sums, staged as 32 x 256 fp32 tiles (rows 1040 bytes apart), into this
+        // split's slab (bias and rounding happen in the reduction)
+        constexpr int RB = 256 * 4 + 16;
+        float* slab = a.partials + (int64_t)split * a.m * a.ncols;
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+            uint8_t* buf = xs + (i & 1) * 32 * RB;
+            uint8_t* lp = buf + l32 * RB + colw * 4;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) *(float4_t*)(lp + 16 * q) = AccChunks<float16_t>::get(acc[i], q);
+            lds_barrier();
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                const int c = tid + kF8Threads * h, row = c >> 6, cc = c & 63;
+                const float4_t val = *(const float4_t*)(buf + row * RB + cc * 16);
+                const int m = m0 + 32 * i + row, n = tile_n0 + 4 * cc;
+                if (m < M && n < N) *(float4_t*)(slab + (int64_t)m * a.ncols + G.col_begin + n) = val;
+            }
+        }
+        return;
+    }
+    if (glu) {
+        // gate (waves 0..3) and up (waves 4..7) tiles of 32 x 128 fp16 side by side in LDS; each
+        // thread then owns one 16-byte chunk of both and writes gate, up and h
+        constexpr int RB = 128 * 2 + 16;
+        const FwdGroupDev& Gg = a.g[0];
+        const FwdGroupDev& Gu = a.g[1];
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+            uint8_t* buf = xs + (i & 1) * 2 * 32 * RB;
+            uint8_t* lp = buf + (wave >> 2) * 32 * RB + l32 * RB + colw * 2;
+            uint32_t o[8];
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) o[r >> 1] = pack_half2(acc[i][r] + bias[r], acc[i][r + 1] + bias[r + 1]);
+            *(u32x4_t*)lp = u32x4_t{o[0], o[1], o[2], o[3]};
+            *(u32x4_t*)(lp + 16) = u32x4_t{o[4], o[5], o[6], o[7]};
+            lds_barrier();
+            const int row = tid >> 4, cc = tid & 15;
+            const u32x4_t gv = *(const u32x4_t*)(buf + row * RB + cc * 16);
+            const u32x4_t uv = *(const u32x4_t*)(buf + 32 * RB + row * RB + cc * 16);
+            const int m = m0 + 32 * i + row, n = tile_n0 + 8 * cc;
+            if (m < M && n < N) {
+                if (Gg.y != nullptr) *(u32x4_t*)(Gg.y + (int64_t)m * Gg.ldy + n) = gv;
+                if (Gu.y != nullptr) *(u32x4_t*)(Gu.y + (int64_t)m * Gu.ldy + n) = uv;
+                *(u32x4_t*)(a.h + (int64_t)m * a.ldh + n) =
+                    u32x4_t{swiglu_fwd2(gv[0], uv[0]), swiglu_fwd2(gv[1], uv[1]), swiglu_fwd2(gv[2], uv[2]),
+                            swiglu_fwd2(gv[3], uv[3])};
+            }
+        }
+        return;
+    }
+    {
+        // 32 x 256 fp16 tiles (rows 528 bytes apart) -> whole 512-byte rows of y
+        constexpr int RB = 256 * 2 + 16;
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+            uint8_t* buf = xs + (i & 1) * 32 * RB;
+            uint8_t* lp = buf + l32 * RB + colw * 2;
+            uint32_t o[8];
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) o[r >> 1] = pack_half2(acc[i][r] + bias[r], acc[i][r + 1] + bias[r + 1]);
+            *(u32x4_t*)lp = u32x4_t{o[0], o[1], o[2], o[3]};
+            *(u32x4_t*)(lp + 16) = u32x4_t{o[4], o[5], o[6], o[7]};
+            lds_barrier();
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int c = tid + kF8Threads * h, row = c >> 5, cc = c & 31;
+                const u32x4_t val = *(const u32x4_t*)(buf + row * RB + cc * 16);
+                const int m = m0 + 32 * i + row, n = tile_n0 + 8 * cc;
+                if (m < M && n < N) *(u32x4_t*)(G.y + (int64_t)m * G.ldy + n) = val;
+            }
+        }
+    }
+}
+
+template <int MB, bool NESTED>
+static hipError_t launch_fwd8_t(const FwdArgs& a, int grid, hipStream_t s) {
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute((const void*)nf4_fwd8_kernel<MB, NESTED>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)fwd8_smem_bytes(MB));
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    hipLaunchKernelGGL((nf4_fwd8_kernel<MB, NESTED>), dim3(grid), dim3(kF8Threads),
+                       fwd8_smem_bytes(MB), s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_fwd8(const FwdArgs& a, int mb, int grid, hipStream_t s) {
+#define X(T) \
+    if (mb == T) return a.nested ? launch_fwd8_t<T, true>(a, grid, s) : launch_fwd8_t<T, false>(a, grid, s);
+    X(8) X(9)
+#undef X
+    return hipErrorInvalidValue;
+}
+
+}  // namespace dk

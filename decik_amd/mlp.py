@@ -40,8 +40,9 @@ def mlp_backward(grad16, x16, gate, up, down, saved=None, bias=(None, None, None
     """dX of the MLP; `saved` = (gate_out, up_out) from the forward, else they are recomputed."""
     m, k = x16.shape
     if saved is None:
-        g, u = nf4.linear_forward(x16, [dict(packed=gate[0], qs=gate[1], bias=bias[0]),
-                                        dict(packed=up[0], qs=up[1], bias=bias[1])])
+        # the forward's own launch again (same kernel and plan, so the same bits); h is unused
+        g, u, _ = nf4.glu_forward(x16, dict(packed=gate[0], qs=gate[1], bias=bias[0]),
+                                  dict(packed=up[0], qs=up[1], bias=bias[1]))
     else:
         g, u = saved
     dgate, dup = nf4.linear_backward_swiglu(dict(packed=down[0], qs=down[1], dy=grad16), g, u,

@@ -36,6 +36,23 @@ def test_forward(m, n, k, bias, device):
     assert_close(y, ref, what=f"fwd {m}x{n}x{k}")
 
 
+@pytest.mark.parametrize("plan", ["9,1,8", "8,2,8"])
+@pytest.mark.parametrize("m,n,k", [(830, 1536, 1536), (830, 8960, 1536), (300, 264, 160), (17, 96, 128),
+                                   (2048, 1536, 1536)])
+def test_forward_eight_wave_kernel(m, n, k, plan, device, monkeypatch):
+    """The 8-wave forward kernel (288- or 256-token tiles, one work-group per CU), with bias, on
+    its own and with a two-way split of the contraction."""
+    from decik_amd.nf4 import linear_forward
+
+    monkeypatch.setenv("DECIK_FWD_PLAN", plan)
+    packed, qs, w16 = make_weight((n, k), seed=n + k + 1, device=device)
+    x = randn16((m, k), seed=m + 2, device=device)
+    b = randn16((n,), seed=6, device=device, std=0.1)
+    (y,) = linear_forward(x, [dict(packed=packed, qs=qs, bias=b)])
+    ref = O.linear_ref(x.cpu().numpy(), w16, b.cpu().numpy())
+    assert_close(y, ref, what=f"fwd8 {plan} {m}x{n}x{k}")
+
+
 @pytest.mark.parametrize("m,n,k", [(830, 1536, 1536), (830, 256, 1536), (830, 8960, 1536),
                                    (830, 1536, 8960), (1, 3584, 3584), (64, 512, 3584),
                                    (17, 96, 128), (300, 264, 160)])
