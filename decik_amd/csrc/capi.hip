@@ -632,6 +632,63 @@ int dk_lora_bwd(const uint16_t* dy, int64_t lddy, const uint16_t* u, const uint1
                      "dk_lora_bwd launch");
 }
 
+int dk_lora_keep_pack(const uint8_t* keep_q, const uint8_t* keep_v, uint8_t* bits_q, uint8_t* bits_v,
+                      int64_t rows, int64_t width, void* stream) {
+    g_error.clear();
+    if (rows < 0 || width < 0 || (width % 8) != 0) return fail("dk_lora_keep_pack: width must be a multiple of 8");
+    if (rows * width == 0) return 0;
+    if (keep_q == nullptr || keep_v == nullptr || bits_q == nullptr || bits_v == nullptr)
+        return fail("dk_lora_keep_pack: null pointer");
+    if (!aligned(keep_q, 8) || !aligned(keep_v, 8)) return fail("dk_lora_keep_pack: masks must be 8-byte aligned");
+    return check_hip(launch_lora_keep_pack(keep_q, keep_v, bits_q, bits_v, rows * width / 8,
+                                           static_cast<hipStream_t>(stream)),
+                     "dk_lora_keep_pack launch");
+}
+
+int dk_lora_dropout_inputs(const void* x, int x_fp32, const uint8_t* bits_q, const uint8_t* bits_v,
+                           const float* scale_q, const float* scale_v, uint16_t* xq, uint16_t* xv,
+                           int64_t rows, int64_t width, void* stream) {
+    g_error.clear();
+    if (rows < 0 || width < 0 || (width % 8) != 0) return fail("dk_lora_dropout_inputs: width must be a multiple of 8");
+    if (rows * width == 0) return 0;
+    if (x == nullptr || bits_q == nullptr || bits_v == nullptr || scale_q == nullptr || scale_v == nullptr ||
+        xq == nullptr || xv == nullptr)
+        return fail("dk_lora_dropout_inputs: null pointer");
+    if (!aligned(x, 16) || !aligned(xq, 16) || !aligned(xv, 16))
+        return fail("dk_lora_dropout_inputs: x, xq and xv must be 16-byte aligned");
+    return check_hip(launch_lora_dropout_inputs(x, x_fp32 != 0, bits_q, bits_v, scale_q, scale_v,
+                                                reinterpret_cast<_Float16*>(xq), reinterpret_cast<_Float16*>(xv),
+                                                rows * width / 8, static_cast<hipStream_t>(stream)),
+                     "dk_lora_dropout_inputs launch");
+}
+
+int dk_lora_input_grad(const uint16_t* gq, const uint16_t* gv, const uint8_t* bits_q, const uint8_t* bits_v,
+                       float scale_q, float scale_v, float* out, int64_t rows, int64_t width, void* stream) {
+    g_error.clear();
+    if (rows < 0 || width < 0 || (width % 8) != 0) return fail("dk_lora_input_grad: width must be a multiple of 8");
+    if (rows * width == 0) return 0;
+    if (gq == nullptr || gv == nullptr || bits_q == nullptr || bits_v == nullptr || out == nullptr)
+        return fail("dk_lora_input_grad: null pointer");
+    if (!aligned(gq, 16) || !aligned(gv, 16) || !aligned(out, 16))
+        return fail("dk_lora_input_grad: gq, gv and out must be 16-byte aligned");
+    return check_hip(launch_lora_input_grad(reinterpret_cast<const _Float16*>(gq), reinterpret_cast<const _Float16*>(gv),
+                                            bits_q, bits_v, scale_q, scale_v, out, rows * width / 8,
+                                            static_cast<hipStream_t>(stream)),
+                     "dk_lora_input_grad launch");
+}
+
+int dk_lora_up(const uint16_t* gu, const uint16_t* a, int rank, uint16_t* out, int64_t m, int64_t k, void* stream) {
+    g_error.clear();
+    if (rank != 16 && rank != 32) return fail("dk_lora_up: rank must be 16 or 32");
+    if (m < 0 || k < 0 || (k % 8) != 0) return fail("dk_lora_up: k must be a multiple of 8");
+    if (m * k == 0) return 0;
+    if (gu == nullptr || a == nullptr || out == nullptr) return fail("dk_lora_up: null pointer");
+    if (!aligned(a, 16) || !aligned(out, 16)) return fail("dk_lora_up: a and out must be 16-byte aligned");
+    return check_hip(launch_lora_up(reinterpret_cast<const _Float16*>(gu), reinterpret_cast<const _Float16*>(a), rank,
+                                    reinterpret_cast<_Float16*>(out), m, k, static_cast<hipStream_t>(stream)),
+                     "dk_lora_up launch");
+}
+
 int dk_swiglu_fwd(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n, void* stream) {
     g_error.clear();
     if (n < 0 || (n > 0 && (gate == nullptr || up == nullptr || out == nullptr)))

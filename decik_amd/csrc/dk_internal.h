@@ -142,6 +142,15 @@ hipError_t launch_lora_down(const _Float16* x, int64_t m, int64_t k, int64_t ldx
 hipError_t launch_lora_bwd(const _Float16* dy, int64_t lddy, const _Float16* u, const _Float16* x,
                            int64_t ldx, const _Float16* b, int64_t m, int64_t n, int64_t k, int rank,
                            float scale, _Float16* gu, float* da, float* db, hipStream_t s);
+hipError_t launch_lora_keep_pack(const uint8_t* kq, const uint8_t* kv, uint8_t* bq, uint8_t* bv,
+                                 int64_t nbytes, hipStream_t s);
+hipError_t launch_lora_dropout_inputs(const void* x, bool x32, const uint8_t* bq, const uint8_t* bv,
+                                      const float* sq, const float* sv, _Float16* xq, _Float16* xv,
+                                      int64_t nbytes, hipStream_t s);
+hipError_t launch_lora_input_grad(const _Float16* gq, const _Float16* gv, const uint8_t* bq, const uint8_t* bv,
+                                  float sq, float sv, float* out, int64_t nbytes, hipStream_t s);
+hipError_t launch_lora_up(const _Float16* gu, const _Float16* a, int rank, _Float16* out, int64_t m, int64_t k,
+                          hipStream_t s);
 hipError_t launch_swiglu_fwd(const _Float16* g, const _Float16* u, _Float16* o, int64_t n,
                              hipStream_t s);
 hipError_t launch_swiglu_bwd(const _Float16* gr, const _Float16* g, const _Float16* u,

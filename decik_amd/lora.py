@@ -7,8 +7,10 @@ peft's branch for a 4-bit layer under fp16 autocast is lora_B(lora_A(dropout(x))
 Here the base projection and the LoRA term are one launch in each direction: the forward GEMM's
 epilogue adds s * U.B^T (an extra rank-r MFMA per output tile) before the single fp16 rounding,
 and the backward GEMM's epilogue adds GU.A to dX. U and GU come from small HIP kernels
-(dk_lora_down, dk_lora_bwd), which also produce dA and dB in fp32. Dropout is not applied
-(p = 0); its masks are a later addition.
+(dk_lora_down, dk_lora_bwd), which also produce dA and dB in fp32. With dropout (p > 0) the
+branch runs beside the projection as LoRAPairFromNorm does (LoRAPair below): packed keep-masks,
+dropped-out fp16 inputs, and the input gradient through the masks (dk_lora_keep_pack,
+dk_lora_dropout_inputs, dk_lora_up, dk_lora_input_grad).
 """
 
 import torch
@@ -41,6 +43,100 @@ def lora_grads(dy16, u16, x16, b16, scaling, want_da=True, want_db=True):
     check(lib().dk_lora_bwd(ptr(dy2), dy2.stride(0), ptr(u16), ptr(x2), x2.stride(0), ptr(b16), m, n, k,
                             r, float(scaling), ptr(gu), ptr(da), ptr(db), stream_of(dev)))
     return gu, da, db
+
+
+def pack_keep(keep_q, keep_v):
+    """Two bool keep-masks [T, W] (W % 8 == 0) -> bit-packed uint8 [T, W / 8] each
+    (pack_keep, solution/attn.py:195-203)."""
+    rows, width = keep_q.shape
+    bq = torch.empty((rows, width // 8), dtype=torch.uint8, device=keep_q.device)
+    bv = torch.empty_like(bq)
+    kq, kv = keep_q.contiguous().view(torch.uint8), keep_v.contiguous().view(torch.uint8)
+    check(lib().dk_lora_keep_pack(ptr(kq), ptr(kv), ptr(bq), ptr(bv), rows, width, stream_of(kq.device)))
+    return bq, bv
+
+
+def lora_inputs(x, bits_q, bits_v, scale_q, scale_v):
+    """fp16(x * dropout values) of the q and v branches, [T, W] each (_lora_inputs,
+    solution/attn.py:183-192). x fp16 or fp32 [.., W]; scale_*: fp32 device scalars (1/(1-p))."""
+    width = x.shape[-1]
+    x2 = x.reshape(-1, width).contiguous()
+    rows = x2.shape[0]
+    xq = torch.empty((rows, width), dtype=torch.float16, device=x.device)
+    xv = torch.empty_like(xq)
+    sq = scale_q.to(torch.float32).reshape(1).contiguous()
+    sv = scale_v.to(torch.float32).reshape(1).contiguous()
+    check(lib().dk_lora_dropout_inputs(ptr(x2), 1 if x2.dtype == torch.float32 else 0, ptr(bits_q),
+                                       ptr(bits_v), ptr(sq), ptr(sv), ptr(xq), ptr(xv), rows, width,
+                                       stream_of(x.device)))
+    return xq, xv
+
+
+def lora_input_grad(gq, gv, bits_q, bits_v, scale_q, scale_v):
+    """Input gradient of both branches through their dropout, fp32 [T, W]: (g * keep) * 1/(1-p)
+    per branch, summed (skc_lora_input_grad_kernel, solution/attn.py:168-180, 259-266)."""
+    rows, width = gq.shape
+    out = torch.empty((rows, width), dtype=torch.float32, device=gq.device)
+    check(lib().dk_lora_input_grad(ptr(gq.contiguous()), ptr(gv.contiguous()), ptr(bits_q), ptr(bits_v),
+                                   float(scale_q), float(scale_v), ptr(out), rows, width,
+                                   stream_of(gq.device)))
+    return out
+
+
+def lora_up(gu16, a16):
+    """A branch's input gradient before dropout: fp16(GU . A) [M, K] (grad_u.mm(a16),
+    solution/attn.py:257)."""
+    m, r = gu16.shape
+    k = a16.shape[1]
+    out = torch.empty((m, k), dtype=torch.float16, device=gu16.device)
+    check(lib().dk_lora_up(ptr(gu16.contiguous()), ptr(a16.contiguous()), r, ptr(out), m, k,
+                           stream_of(gu16.device)))
+    return out
+
+
+class LoRAPair(torch.autograd.Function):
+    """The q and v LoRA branches with dropout, lora_B(lora_A(dropout(x))) * scaling each, as
+    LoRAPairFromNorm computes them on its packed-mask path (solution/attn.py:206-273): the masks
+    are kept packed to bits and backward rebuilds the dropped-out inputs from x. (The reference
+    rebuilds x itself from the RMSNorm input; here x is saved.) x: [.., W] fp16 or fp32;
+    bits_*: packed keep-masks; scale_*: fp32 device scalars 1/(1-p); a_* [r, W], b_* [N, r]
+    adapter weights (used in fp16); returns (out_q, out_v) fp16."""
+
+    @staticmethod
+    def forward(ctx, x, bits_q, scale_q, bits_v, scale_v, a_q, b_q, a_v, b_v, scaling_q, scaling_v,
+                p_q, p_v):
+        inputs = lora_inputs(x, bits_q, bits_v, scale_q, scale_v)
+        outs, us = [], []
+        for x16, a, b, s in zip(inputs, (a_q, a_v), (b_q, b_v), (scaling_q, scaling_v)):
+            a16 = a.to(torch.float16).contiguous()
+            u = lora_down(x16, a16)
+            # fp16(u . B^T) (the rank-r up product), then * scaling in fp16 as torch scales
+            up = lora_up(u, b.to(torch.float16).t().contiguous())
+            outs.append(up * s)
+            us.append(u)
+        ctx.save_for_backward(x, bits_q, scale_q, bits_v, scale_v, us[0], us[1], a_q, b_q, a_v, b_v)
+        ctx.scalings, ctx.ps = (scaling_q, scaling_v), (p_q, p_v)
+        shape = x.shape[:-1]
+        return outs[0].reshape(*shape, -1), outs[1].reshape(*shape, -1)
+
+    @staticmethod
+    def backward(ctx, grad_q, grad_v):
+        x, bits_q, scale_q, bits_v, scale_v, u_q, u_v, a_q, b_q, a_v, b_v = ctx.saved_tensors
+        inputs = lora_inputs(x, bits_q, bits_v, scale_q, scale_v)
+        grads, input_grads = [], []
+        branches = ((grad_q, u_q, a_q, b_q, ctx.scalings[0]), (grad_v, u_v, a_v, b_v, ctx.scalings[1]))
+        for (grad, u, a, b, s), x16 in zip(branches, inputs):
+            if grad is None:
+                grad = torch.zeros(u.shape[:-1] + (b.shape[0],), dtype=torch.float16, device=u.device)
+            g16 = grad.to(torch.float16).reshape(-1, grad.shape[-1]).contiguous()
+            a16 = a.to(torch.float16).contiguous()
+            gu, da, db = lora_grads(g16, u, x16, b.to(torch.float16).contiguous(), s)
+            grads += [da.to(a.dtype), db.to(b.dtype)]
+            input_grads.append(lora_up(gu, a16))
+        grad_x = lora_input_grad(input_grads[0], input_grads[1], bits_q, bits_v,
+                                 1.0 / (1.0 - ctx.ps[0]), 1.0 / (1.0 - ctx.ps[1]))
+        return (grad_x.view(x.shape), None, None, None, None, grads[0], grads[1], grads[2], grads[3],
+                None, None, None, None)
 
 
 class NF4LoRALinear(torch.autograd.Function):

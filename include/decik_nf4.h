@@ -27,6 +27,13 @@
  *                                               backward (solution/mlp.py:95, 104)
  *   dk_lora_down / dk_lora_bwd                <- the rank-r products of LoRAPairFromNorm
  *                                               (solution/attn.py:225-227, 251-257)
+ *   dk_lora_keep_pack                         <- skc_keep_pack_kernel / pack_keep
+ *                                               (solution/attn.py:129-144, 195-203)
+ *   dk_lora_dropout_inputs                    <- skc_lora_inputs_kernel / _lora_inputs
+ *                                               (solution/attn.py:153-165, 183-192)
+ *   dk_lora_input_grad                        <- skc_lora_input_grad_kernel (solution/attn.py:168-180)
+ *   dk_lora_up                                <- grad_u.mm(a16) of LoRAPairFromNorm.backward
+ *                                               (solution/attn.py:257)
  *   dk_swiglu_fwd / dk_swiglu_bwd             <- example_swiglu_fwd/bwd_kernel
  *                                               (solution/swiglu.py:15-37)
  */
@@ -153,6 +160,28 @@ int dk_lora_down(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const uin
 int dk_lora_bwd(const uint16_t* dy, int64_t lddy, const uint16_t* u, const uint16_t* x,
                 int64_t ldx, const uint16_t* b, int64_t m, int64_t n, int64_t k, int rank,
                 float scale, uint16_t* gu, float* da, float* db, void* stream);
+
+/* LoRA dropout (the packed-mask path of LoRAPairFromNorm). Masks are bool bytes (0/1), rows x width
+ * row-major, width % 8 == 0; bits are [rows, width / 8]. */
+
+/* bits_q[r, c / 8] bit (c % 8) = keep_q[r, c], the same for v (keep_* 8-byte aligned). */
+int dk_lora_keep_pack(const uint8_t* keep_q, const uint8_t* keep_v, uint8_t* bits_q, uint8_t* bits_v,
+                      int64_t rows, int64_t width, void* stream);
+
+/* xq = fp16(x * (keep_q * scale_q)), xv = fp16(x * (keep_v * scale_v)) in fp32; x fp16 (x_fp32 = 0)
+ * or fp32 [rows, width]; scale_q, scale_v: device fp32 scalars (the kept value 1 / (1 - p)). */
+int dk_lora_dropout_inputs(const void* x, int x_fp32, const uint8_t* bits_q, const uint8_t* bits_v,
+                           const float* scale_q, const float* scale_v, uint16_t* xq, uint16_t* xv,
+                           int64_t rows, int64_t width, void* stream);
+
+/* out = (fp32(gq) * keep_q) * scale_q + (fp32(gv) * keep_v) * scale_v, fp32 [rows, width]: the input
+ * gradient of both branches through their dropout. */
+int dk_lora_input_grad(const uint16_t* gq, const uint16_t* gv, const uint8_t* bits_q, const uint8_t* bits_v,
+                       float scale_q, float scale_v, float* out, int64_t rows, int64_t width, void* stream);
+
+/* A branch's input gradient before its dropout mask: out = fp16(GU . A) [m, k], GU fp16 [m, rank],
+ * A fp16 [rank, k] (rank 16 or 32, k % 8 == 0). */
+int dk_lora_up(const uint16_t* gu, const uint16_t* a, int rank, uint16_t* out, int64_t m, int64_t k, void* stream);
 
 /* out = fp16(silu(gate) * up), computed in fp32 (n elements). */
 int dk_swiglu_fwd(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n,

@@ -19,6 +19,9 @@ What each function restates, and what pins it (the tests live in tests/test_orac
   quantizer is PARITY UNPINNED against it; tests check its invariants instead (nearest code,
   reconstruction bound, layout). Dequant parity does not depend on it: the packed bytes and
   statistics are inputs.
+- `keep_pack`, `lora_dropout_inputs_ref`, `lora_input_grad_ref`: the LoRA dropout steps of
+  solution/attn.py:129-180, elementwise fp32 in the reference's order (exact). Pinned by
+  numpy.packbits (an independent bit packer) and closed forms (all-keep / no-keep masks, scale 1).
 - `linear_ref`, `lora_*_ref`, `swiglu_*_ref`, `mlp_ref`: float64 accumulation of the exact fp16
   operands, rounded where the reference rounds (solution/nf4.py:93-104, solution/mlp.py:62-110,
   solution/swiglu.py:15-37, solution/attn.py:206-273). Pinned by closed forms in the tests
@@ -249,6 +252,43 @@ def lora_bwd_ref(dy16, x16, u16, a16, b16, scaling):
     da = _f64(gu16).T @ _f64(x16)
     dx = _f64(gu16) @ _f64(a16)
     return gu16, da.astype(np.float32), db.astype(np.float32), dx.astype(np.float32)
+
+
+# LoRA dropout with packed keep-masks (solution/attn.py:129-180): elementwise fp32 arithmetic in the
+# reference's order, so these are exact restatements (numpy float32 ops round like the GPU's).
+
+def keep_pack(keep):
+    """bool [rows, width] -> uint8 [rows, width / 8], bit j of byte c = keep[r, 8 c + j]
+    (skc_keep_pack_kernel, solution/attn.py:129-144)."""
+    k = np.asarray(keep).astype(np.uint8).reshape(keep.shape[0], -1, 8)
+    return np.bitwise_or.reduce(k << np.arange(8, dtype=np.uint8), axis=2).astype(np.uint8)
+
+
+def keep_unpack(bits, width):
+    """Inverse of keep_pack: float32 0/1 [rows, width] (the reference's _keep,
+    solution/attn.py:147-150)."""
+    b = np.asarray(bits).astype(np.uint32)
+    cols = np.arange(width)
+    return ((b[:, cols // 8] >> (cols % 8)) & 1).astype(np.float32)
+
+
+def lora_dropout_inputs_ref(x, bits_q, bits_v, scale_q, scale_v):
+    """fp16(x * (keep * scale)) in fp32 for the q and v branches (skc_lora_inputs_kernel,
+    solution/attn.py:153-165)."""
+    xf = np.asarray(x).astype(np.float32)
+    w = xf.shape[1]
+    mq = keep_unpack(bits_q, w) * np.float32(scale_q)
+    mv = keep_unpack(bits_v, w) * np.float32(scale_v)
+    return (xf * mq).astype(np.float16), (xf * mv).astype(np.float16)
+
+
+def lora_input_grad_ref(gq16, gv16, bits_q, bits_v, scale_q, scale_v):
+    """(fp32(gq) * keep_q) * sq + (fp32(gv) * keep_v) * sv (skc_lora_input_grad_kernel,
+    solution/attn.py:168-180)."""
+    w = np.asarray(gq16).shape[1]
+    tq = (np.asarray(gq16).astype(np.float32) * keep_unpack(bits_q, w)) * np.float32(scale_q)
+    tv = (np.asarray(gv16).astype(np.float32) * keep_unpack(bits_v, w)) * np.float32(scale_v)
+    return (tq + tv).astype(np.float32)
 
 
 def _sigmoid64(x):

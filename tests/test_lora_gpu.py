@@ -97,3 +97,88 @@ def test_qkv_projection_with_lora_on_q_and_v(device):
             assert_close(p["lora_b"].grad, db, what="dB")
         assert_close(o, y_ref, what="qkv Y")
     assert_close(x.grad, dx_ref, what="qkv dX")
+
+
+def _masks(rows, width, p, seed, device):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    kq = torch.rand((rows, width), generator=g) >= p
+    kv = torch.rand((rows, width), generator=g) >= p
+    return kq.to(device), kv.to(device)
+
+
+@pytest.mark.parametrize("xdtype", [torch.float32, torch.float16])
+def test_dropout_steps_bit_exact(xdtype, device):
+    """Mask packing, the dropped-out fp16 inputs and the input gradient through both masks match
+    the oracle bit for bit (elementwise fp32 in the reference's order, solution/attn.py:129-180),
+    on 830 tokens x 1536 with p = 0.05 (the real run's lora_dropout)."""
+    from decik_amd.lora import lora_input_grad, lora_inputs, pack_keep
+
+    rows, width, p = 830, 1536, 0.05
+    kq, kv = _masks(rows, width, p, 11, device)
+    bq, bv = pack_keep(kq, kv)
+    assert np.array_equal(bq.cpu().numpy(), O.keep_pack(kq.cpu().numpy()))
+    assert np.array_equal(bv.cpu().numpy(), O.keep_pack(kv.cpu().numpy()))
+    x = (torch.randn((rows, width), generator=torch.Generator().manual_seed(12)) * 2).to(xdtype).to(device)
+    s = torch.tensor(1.0 / (1.0 - p), dtype=torch.float32, device=device)
+    xq, xv = lora_inputs(x, bq, bv, s, s)
+    rq, rv = O.lora_dropout_inputs_ref(x.cpu().numpy(), bq.cpu().numpy(), bv.cpu().numpy(),
+                                       1.0 / (1.0 - p), 1.0 / (1.0 - p))
+    assert np.array_equal(xq.cpu().numpy().view(np.uint16), rq.view(np.uint16))
+    assert np.array_equal(xv.cpu().numpy().view(np.uint16), rv.view(np.uint16))
+    gq = randn16((rows, width), seed=13, device=device, std=1e-2)
+    gv = randn16((rows, width), seed=14, device=device, std=1e-2)
+    out = lora_input_grad(gq, gv, bq, bv, 1.0 / (1.0 - p), 1.0 / (1.0 - p))
+    ref = O.lora_input_grad_ref(gq.cpu().numpy(), gv.cpu().numpy(), bq.cpu().numpy(), bv.cpu().numpy(),
+                                1.0 / (1.0 - p), 1.0 / (1.0 - p))
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("r", [16, 32])
+def test_lora_up(r, device):
+    from decik_amd.lora import lora_up
+
+    gu = randn16((830, r), seed=15, device=device, std=1e-2)
+    a = randn16((r, 1536), seed=16, device=device, std=0.03)
+    out = lora_up(gu, a)
+    ref = (O._f64(gu.cpu().numpy()) @ O._f64(a.cpu().numpy())).astype(np.float32)
+    assert out.dtype == torch.float16
+    assert_close(out, ref, what=f"lora_up r={r}")
+
+
+def test_lora_pair_with_dropout(device):
+    """LoRAPair (q and v branches with p = 0.05 dropout) against the oracle restatement of
+    LoRAPairFromNorm's packed path (solution/attn.py:206-273): outputs, dA/dB of both branches
+    and the fp32 input gradient through both masks."""
+    from decik_amd.lora import LoRAPair, pack_keep
+
+    rows, width, p, s = 830, 1536, 0.05, 2.0
+    kq, kv = _masks(rows, width, p, 21, device)
+    bq, bv = pack_keep(kq, kv)
+    x = torch.randn((rows, width), generator=torch.Generator().manual_seed(22)).to(device)  # fp32
+    a_q, b_q = adapters(1536, width, 23, device)
+    a_v, b_v = adapters(256, width, 24, device)
+    b_q = (b_q.float() * 30).half()  # larger B so the outputs are not all rounding noise
+    b_v = (b_v.float() * 30).half()
+    ws = [t.float().requires_grad_(True) for t in (a_q, b_q, a_v, b_v)]
+    sc = torch.tensor(1.0 / (1.0 - p), dtype=torch.float32, device=device)
+    xin = x.clone().requires_grad_(True)
+    out_q, out_v = LoRAPair.apply(xin, bq, sc, bv, sc, *ws, s, s, p, p)
+    gq = randn16((rows, 1536), seed=25, device=device, std=1e-2)
+    gv = randn16((rows, 256), seed=26, device=device, std=1e-2)
+    torch.autograd.backward([out_q, out_v], [gq, gv])
+    # oracle
+    xn = x.cpu().numpy()
+    bqn, bvn = bq.cpu().numpy(), bv.cpu().numpy()
+    xq, xv = O.lora_dropout_inputs_ref(xn, bqn, bvn, 1.0 / (1.0 - p), 1.0 / (1.0 - p))
+    gin = []
+    for x16, a, b, g, out, (wa, wb) in ((xq, a_q, b_q, gq, out_q, ws[:2]), (xv, a_v, b_v, gv, out_v, ws[2:])):
+        an, bn = a.cpu().numpy(), b.cpu().numpy()
+        u16, lo = O.lora_fwd_ref(x16, an, bn, s)
+        assert_close(out, lo, what="lora out")
+        gu16, da, db, _ = O.lora_bwd_ref(g.cpu().numpy(), x16, u16, an, bn, s)
+        assert_close(wa.grad, da, what="dA")
+        assert_close(wb.grad, db, what="dB")
+        gin.append((O._f64(gu16) @ O._f64(an)).astype(np.float16))
+    ref_dx = O.lora_input_grad_ref(gin[0], gin[1], bqn, bvn, 1.0 / (1.0 - p), 1.0 / (1.0 - p))
+    assert xin.grad.dtype == torch.float32
+    assert_close(xin.grad, ref_dx, what="dX through dropout")

@@ -280,3 +280,33 @@ def test_tolerance_metric():
     y = np.array([1.0, -2.0, 4.04])
     mx, mean = O.tolerance(y, ref)
     assert abs(mx - 0.01) < 1e-12 and abs(mean - 0.04 / 7.0) < 1e-12
+
+
+def test_keep_pack_matches_numpy_packbits():
+    """The oracle's bit packer against numpy's independent one (little bit order: bit j of a
+    byte is column 8 c + j, solution/attn.py:138-141); unpacking inverts it."""
+    rng = np.random.default_rng(3)
+    keep = rng.random((37, 128)) > 0.05
+    bits = O.keep_pack(keep)
+    assert bits.dtype == np.uint8 and bits.shape == (37, 16)
+    assert np.array_equal(bits, np.packbits(keep, axis=1, bitorder="little"))
+    assert np.array_equal(O.keep_unpack(bits, 128), keep.astype(np.float32))
+
+
+def test_dropout_refs_closed_forms():
+    """All-keep masks with scale 1 give fp16(x) and x itself back as the gradient; empty masks
+    give zeros carrying x's sign; the scale multiplies after the mask, in fp32."""
+    rng = np.random.default_rng(4)
+    x = (rng.standard_normal((8, 64)) * 3).astype(np.float32)
+    ones = O.keep_pack(np.ones((8, 64), dtype=bool))
+    zeros = O.keep_pack(np.zeros((8, 64), dtype=bool))
+    xq, xv = O.lora_dropout_inputs_ref(x, ones, zeros, 1.0, 1.0)
+    assert np.array_equal(xq, x.astype(np.float16))
+    assert np.all(xv == 0) and np.array_equal(np.signbit(xv), np.signbit(x))
+    xq2, _ = O.lora_dropout_inputs_ref(x, ones, ones, 1.0 / 0.95, 1.0)
+    assert np.array_equal(xq2, (x * np.float32(1.0 / 0.95)).astype(np.float16))
+    g16 = x.astype(np.float16)
+    out = O.lora_input_grad_ref(g16, g16, ones, zeros, 1.0, 2.0)
+    assert np.array_equal(out, g16.astype(np.float32))
+    out2 = O.lora_input_grad_ref(g16, g16, ones, ones, 2.0, 2.0)
+    assert np.array_equal(out2, g16.astype(np.float32) * 4)
