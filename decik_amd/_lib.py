@@ -59,6 +59,10 @@ EXPORTS = {
     "dk_lora_dropout_inputs": ([c_vp, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp], c_i32),
     "dk_lora_input_grad": ([c_vp, c_vp, c_vp, c_vp, c_f32, c_f32, c_vp, c_i64, c_i64, c_vp], c_i32),
     "dk_lora_up": ([c_vp, c_vp, c_i32, c_vp, c_i64, c_i64, c_vp], c_i32),
+    "dk_rope_qk_fwd": ([c_vp, c_vp, c_i64, c_i64, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_i64, c_i32, c_i32,
+                        c_i32, c_vp], c_i32),
+    "dk_rope_qk_bwd": ([c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_i32, c_i32, c_i32, c_vp],
+                       c_i32),
     "dk_swiglu_fwd": ([c_vp, c_vp, c_vp, c_i64, c_vp], c_i32),
     "dk_swiglu_bwd": ([c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp], c_i32),
     "dk_last_error": ([], ctypes.c_char_p),

@@ -689,6 +689,68 @@ int dk_lora_up(const uint16_t* gu, const uint16_t* a, int rank, uint16_t* out, i
                      "dk_lora_up launch");
 }
 
+int dk_rope_qk_fwd(const uint16_t* q_base, const uint16_t* q_lora, int64_t ldq, int64_t ldl, const uint16_t* k,
+                   int64_t ldk, const float* cos, const float* sin, uint16_t* q_out, uint16_t* k_out, int64_t n_tok,
+                   int n_heads, int n_kv_heads, int head_dim, void* stream) {
+    g_error.clear();
+    if (n_tok < 0 || n_heads < 0 || n_kv_heads < 0 || head_dim <= 0 || (head_dim % 16) != 0)
+        return fail("dk_rope_qk_fwd: head_dim must be a positive multiple of 16");
+    if (n_tok == 0) return 0;
+    if (q_base == nullptr || k == nullptr || cos == nullptr || sin == nullptr || q_out == nullptr || k_out == nullptr)
+        return fail("dk_rope_qk_fwd: null pointer");
+    if (ldq < (int64_t)n_heads * head_dim || ldk < (int64_t)n_kv_heads * head_dim || (ldq % 8) || (ldk % 8) ||
+        (q_lora != nullptr && (ldl < (int64_t)n_heads * head_dim || (ldl % 8))))
+        return fail("dk_rope_qk_fwd: row strides must cover the heads and be multiples of 8");
+    if (!aligned(q_base, 16) || !aligned(k, 16) || !aligned(cos, 16) || !aligned(sin, 16) || !aligned(q_out, 16) ||
+        !aligned(k_out, 16) || (q_lora != nullptr && !aligned(q_lora, 16)))
+        return fail("dk_rope_qk_fwd: tensors must be 16-byte aligned");
+    RopeArgs a{};
+    a.q_base = reinterpret_cast<const _Float16*>(q_base);
+    a.q_lora = reinterpret_cast<const _Float16*>(q_lora);
+    a.k = reinterpret_cast<const _Float16*>(k);
+    a.ldq = ldq;
+    a.ldl = ldl;
+    a.ldk = ldk;
+    a.cos = cos;
+    a.sin = sin;
+    a.q_out = reinterpret_cast<_Float16*>(q_out);
+    a.k_out = reinterpret_cast<_Float16*>(k_out);
+    a.n_tok = n_tok;
+    a.hq = n_heads;
+    a.hk = n_kv_heads;
+    a.d = head_dim;
+    return check_hip(launch_rope(a, false, static_cast<hipStream_t>(stream)), "dk_rope_qk_fwd launch");
+}
+
+int dk_rope_qk_bwd(const uint16_t* grad_q, const uint16_t* grad_k, const float* cos, const float* sin, uint16_t* dq,
+                   int64_t lddq, uint16_t* dk, int64_t lddk, int64_t n_tok, int n_heads, int n_kv_heads, int head_dim,
+                   void* stream) {
+    g_error.clear();
+    if (n_tok < 0 || n_heads < 0 || n_kv_heads < 0 || head_dim <= 0 || (head_dim % 16) != 0)
+        return fail("dk_rope_qk_bwd: head_dim must be a positive multiple of 16");
+    if (n_tok == 0) return 0;
+    if (grad_q == nullptr || grad_k == nullptr || cos == nullptr || sin == nullptr || dq == nullptr || dk == nullptr)
+        return fail("dk_rope_qk_bwd: null pointer");
+    if (lddq < (int64_t)n_heads * head_dim || lddk < (int64_t)n_kv_heads * head_dim || (lddq % 8) || (lddk % 8))
+        return fail("dk_rope_qk_bwd: row strides must cover the heads and be multiples of 8");
+    if (!aligned(grad_q, 16) || !aligned(grad_k, 16) || !aligned(dq, 16) || !aligned(dk, 16))
+        return fail("dk_rope_qk_bwd: tensors must be 16-byte aligned");
+    RopeArgs a{};
+    a.cos = cos;
+    a.sin = sin;
+    a.grad_q = reinterpret_cast<const _Float16*>(grad_q);
+    a.grad_k = reinterpret_cast<const _Float16*>(grad_k);
+    a.dq = reinterpret_cast<_Float16*>(dq);
+    a.dk = reinterpret_cast<_Float16*>(dk);
+    a.lddq = lddq;
+    a.lddk = lddk;
+    a.n_tok = n_tok;
+    a.hq = n_heads;
+    a.hk = n_kv_heads;
+    a.d = head_dim;
+    return check_hip(launch_rope(a, true, static_cast<hipStream_t>(stream)), "dk_rope_qk_bwd launch");
+}
+
 int dk_swiglu_fwd(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n, void* stream) {
     g_error.clear();
     if (n < 0 || (n > 0 && (gate == nullptr || up == nullptr || out == nullptr)))

@@ -151,6 +151,26 @@ hipError_t launch_lora_input_grad(const _Float16* gq, const _Float16* gv, const 
                                   float sq, float sv, float* out, int64_t nbytes, hipStream_t s);
 hipError_t launch_lora_up(const _Float16* gu, const _Float16* a, int rank, _Float16* out, int64_t m, int64_t k,
                           hipStream_t s);
+// RoPE of the attention inputs (rope.hip): q [T, hq*d] (+ LoRA) and k [T, hk*d] token-major in,
+// head-major [h, T, d] out; backward the transpose.
+struct RopeArgs {
+    const _Float16* q_base;
+    const _Float16* q_lora;  // may be null
+    const _Float16* k;
+    int64_t ldq, ldl, ldk;
+    const float* cos;        // fp32 [T, d]
+    const float* sin;
+    _Float16* q_out;
+    _Float16* k_out;
+    const _Float16* grad_q;  // head-major
+    const _Float16* grad_k;
+    _Float16* dq;            // token-major
+    _Float16* dk;
+    int64_t lddq, lddk;
+    int64_t n_tok;
+    int32_t hq, hk, d;
+};
+hipError_t launch_rope(const RopeArgs& a, bool backward, hipStream_t s);
 hipError_t launch_swiglu_fwd(const _Float16* g, const _Float16* u, _Float16* o, int64_t n,
                              hipStream_t s);
 hipError_t launch_swiglu_bwd(const _Float16* gr, const _Float16* g, const _Float16* u,

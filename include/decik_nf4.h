@@ -34,6 +34,8 @@
  *   dk_lora_input_grad                        <- skc_lora_input_grad_kernel (solution/attn.py:168-180)
  *   dk_lora_up                                <- grad_u.mm(a16) of LoRAPairFromNorm.backward
  *                                               (solution/attn.py:257)
+ *   dk_rope_qk_fwd / dk_rope_qk_bwd           <- skc_rope_fwd_kernel / skc_rope_bwd_kernel and
+ *                                               FusedQKRope (solution/attn.py:27-126)
  *   dk_swiglu_fwd / dk_swiglu_bwd             <- example_swiglu_fwd/bwd_kernel
  *                                               (solution/swiglu.py:15-37)
  */
@@ -182,6 +184,21 @@ int dk_lora_input_grad(const uint16_t* gq, const uint16_t* gv, const uint8_t* bi
 /* A branch's input gradient before its dropout mask: out = fp16(GU . A) [m, k], GU fp16 [m, rank],
  * A fp16 [rank, k] (rank 16 or 32, k % 8 == 0). */
 int dk_lora_up(const uint16_t* gu, const uint16_t* a, int rank, uint16_t* out, int64_t m, int64_t k, void* stream);
+
+/* RoPE of the attention inputs, q and k in one launch: q = fp32(q_base) + fp32(q_lora) (q_lora may
+ * be NULL: no addition), out = q * cos + rotate_half(q) * sin in fp32, stored fp16 head-major
+ * q_out [n_heads, n_tok, head_dim], k_out [n_kv_heads, n_tok, head_dim]; k likewise without LoRA.
+ * q_base / q_lora / k: fp16 token-major with row strides ldq / ldl / ldk; cos, sin: fp32
+ * [n_tok, head_dim]; head_dim % 16 == 0. */
+int dk_rope_qk_fwd(const uint16_t* q_base, const uint16_t* q_lora, int64_t ldq, int64_t ldl, const uint16_t* k,
+                   int64_t ldk, const float* cos, const float* sin, uint16_t* q_out, uint16_t* k_out, int64_t n_tok,
+                   int n_heads, int n_kv_heads, int head_dim, void* stream);
+
+/* Its transpose: d = g * cos + rotate_half^T(g * sin) in fp32, rounded to fp16 once; grad_q / grad_k
+ * head-major fp16, dq / dk token-major with row strides lddq / lddk. */
+int dk_rope_qk_bwd(const uint16_t* grad_q, const uint16_t* grad_k, const float* cos, const float* sin, uint16_t* dq,
+                   int64_t lddq, uint16_t* dk, int64_t lddk, int64_t n_tok, int n_heads, int n_kv_heads, int head_dim,
+                   void* stream);
 
 /* out = fp16(silu(gate) * up), computed in fp32 (n elements). */
 int dk_swiglu_fwd(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n,

@@ -22,6 +22,10 @@ What each function restates, and what pins it (the tests live in tests/test_orac
 - `keep_pack`, `lora_dropout_inputs_ref`, `lora_input_grad_ref`: the LoRA dropout steps of
   solution/attn.py:129-180, elementwise fp32 in the reference's order (exact). Pinned by
   numpy.packbits (an independent bit packer) and closed forms (all-keep / no-keep masks, scale 1).
+- `rope_fwd_ref`, `rope_bwd_ref`: RoPE of q/k (solution/attn.py:27-86), elementwise fp32 in the
+  reference's order (exact). Pinned by closed forms (cos 1 / sin 0 is the identity, cos 0 /
+  sin 1 is rotate_half) and by the backward being the forward's transpose (float64 inner
+  products).
 - `linear_ref`, `lora_*_ref`, `swiglu_*_ref`, `mlp_ref`: float64 accumulation of the exact fp16
   operands, rounded where the reference rounds (solution/nf4.py:93-104, solution/mlp.py:62-110,
   solution/swiglu.py:15-37, solution/attn.py:206-273). Pinned by closed forms in the tests
@@ -289,6 +293,42 @@ def lora_input_grad_ref(gq16, gv16, bits_q, bits_v, scale_q, scale_v):
     tq = (np.asarray(gq16).astype(np.float32) * keep_unpack(bits_q, w)) * np.float32(scale_q)
     tv = (np.asarray(gv16).astype(np.float32) * keep_unpack(bits_v, w)) * np.float32(scale_v)
     return (tq + tv).astype(np.float32)
+
+
+def rotate_half(x):
+    """[-x[D/2:], x[:D/2]] along the last axis (transformers' rotate_half)."""
+    h = x.shape[-1] // 2
+    return np.concatenate([-x[..., h:], x[..., :h]], axis=-1)
+
+
+def rope_fwd_ref(q_base16, q_lora16, k16, cos, sin, n_heads, n_kv_heads):
+    """skc_rope_fwd_kernel (solution/attn.py:27-66): q = fp32(base) + fp32(lora); q cos +
+    rotate_half(q) sin in fp32 (no FMA); fp16 head-major [H, T, D]. q_lora16 None: no add."""
+    t = q_base16.shape[0]
+    d = cos.shape[-1]
+    c, s = np.asarray(cos, np.float32), np.asarray(sin, np.float32)
+    def one(x, heads):
+        x = x.reshape(t, heads, d).transpose(1, 0, 2)  # [H, T, D] fp32
+        return ((x * c[None]) + (rotate_half(x) * s[None])).astype(np.float16)
+    q = np.asarray(q_base16).astype(np.float32)
+    if q_lora16 is not None:
+        q = q + np.asarray(q_lora16).astype(np.float32)
+    return one(q, n_heads), one(np.asarray(k16).astype(np.float32), n_kv_heads)
+
+
+def rope_bwd_ref(grad_q16, grad_k16, cos, sin):
+    """skc_rope_bwd_kernel (solution/attn.py:69-86): d = g cos + rotate_half^T(g sin) in fp32,
+    fp16 token-major [T, H*D]; rotate_half^T(y)[d] = y[d + D/2] for d < D/2, -y[d - D/2] after."""
+    c, s = np.asarray(cos, np.float32), np.asarray(sin, np.float32)
+    def one(g):
+        g = np.asarray(g).astype(np.float32)  # [H, T, D]
+        a = g * c[None]
+        b = g * s[None]
+        h = g.shape[-1] // 2
+        bt = np.concatenate([b[..., h:], -b[..., :h]], axis=-1)
+        out = (a + bt).astype(np.float16)
+        return out.transpose(1, 0, 2).reshape(g.shape[1], -1)
+    return one(grad_q16), one(grad_k16)
 
 
 def _sigmoid64(x):

@@ -310,3 +310,31 @@ def test_dropout_refs_closed_forms():
     assert np.array_equal(out, g16.astype(np.float32))
     out2 = O.lora_input_grad_ref(g16, g16, ones, ones, 2.0, 2.0)
     assert np.array_equal(out2, g16.astype(np.float32) * 4)
+
+
+def test_rope_refs_closed_forms_and_transpose():
+    """cos 1 / sin 0 leaves q + lora (rounded to fp16) unchanged; cos 0 / sin 1 is rotate_half;
+    the backward is the transpose of the forward's linear map: <R x, g> = <x, R^T g> in float64
+    for the same cos/sin (checked on the fp32 values before rounding, through tiny exact inputs)."""
+    rng = np.random.default_rng(5)
+    t, h, hk, d = 5, 3, 1, 16
+    qb = rng.standard_normal((t, h * d)).astype(np.float16)
+    ql = (rng.standard_normal((t, h * d)) * 0.1).astype(np.float16)
+    k = rng.standard_normal((t, hk * d)).astype(np.float16)
+    one, zero = np.ones((t, d), np.float32), np.zeros((t, d), np.float32)
+    q_out, k_out = O.rope_fwd_ref(qb, ql, k, one, zero, h, hk)
+    want = (qb.astype(np.float32) + ql.astype(np.float32)).astype(np.float16).reshape(t, h, d).transpose(1, 0, 2)
+    assert np.array_equal(q_out, want)
+    assert np.array_equal(k_out, k.reshape(t, hk, d).transpose(1, 0, 2))
+    _, k_rot = O.rope_fwd_ref(qb, None, k, zero, one, h, hk)
+    assert np.array_equal(k_rot, O.rotate_half(k.astype(np.float32).reshape(t, hk, d).transpose(1, 0, 2)).astype(np.float16))
+    # transpose identity with small-integer inputs (every product and sum exact in fp32)
+    xi = rng.integers(-4, 5, (t, hk * d)).astype(np.float16)
+    gi = rng.integers(-4, 5, (hk, t, d)).astype(np.float16)
+    ci = rng.integers(-2, 3, (t, d)).astype(np.float32)
+    si = rng.integers(-2, 3, (t, d)).astype(np.float32)
+    _, rx = O.rope_fwd_ref(np.zeros((t, h * d), np.float16), None, xi, ci, si, h, hk)
+    _, rtg = O.rope_bwd_ref(np.zeros((h, t, d), np.float16), gi, ci, si)
+    lhs = float((rx.astype(np.float64) * gi.astype(np.float64)).sum())
+    rhs = float((xi.astype(np.float64) * rtg.astype(np.float64)).sum())
+    assert lhs == rhs
