@@ -6,7 +6,7 @@ the modules are decik_amd's, registered under the reference's names."""
 import sys
 
 import decik_amd as _impl
-from decik_amd import _state, _enabled, apply, lora, mlp, nf4, swiglu, warmup  # noqa: F401
+from decik_amd import _state, _enabled, apply, attn, lora, mlp, nf4, rope, swiglu, warmup  # noqa: F401
 
-for _name in ("nf4", "mlp", "swiglu", "warmup", "_state", "lora"):
+for _name in ("nf4", "mlp", "swiglu", "warmup", "_state", "lora", "attn", "rope"):
     sys.modules[f"{__name__}.{_name}"] = getattr(_impl, _name)
