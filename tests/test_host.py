@@ -65,6 +65,11 @@ def test_solution_names_are_decik_modules():
 
     t = torch.zeros(1)
     assert st.on_gpu(t) is False
+    # the NF4-path names of solution/attn.py (RoPE, LoRA dropout helpers)
+    import solution.attn
+    from solution.attn import FusedQKRope, _lora_inputs, pack_keep  # noqa: F401
+
+    assert solution.attn is decik_amd.attn
 
 
 def test_apply_without_bitsandbytes_is_a_no_op(monkeypatch):
