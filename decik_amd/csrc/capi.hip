@@ -206,9 +206,15 @@ constexpr VariantCost kBwdVariants[] = {{2, 4, 256, 2, 3.20, 0.90},
                                        {2, 8, 512, 1, 2.60, 1.0},
                                        {4, 8, 512, 1, 3.40, 1.0}};
 
+// The eight-wave variants come last: nf4_fwd8_kernel advances its load descriptors by whole
+// steps, so it needs k % 64 == 0 and blocks that do not straddle rows (k % blocksize == 0).
+constexpr int kNumFwd4Variants = 4;
+static_assert(kFwdVariants[kNumFwd4Variants - 1].waves == 4 && kFwdVariants[kNumFwd4Variants].waves == 8,
+              "four-wave variants first");
+
 // glu: two weights of ns[0] rows, a tile takes 128 rows of each; never split (the epilogue
-// needs the finished sums).
-GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool glu,
+// needs the finished sums). fwd8_ok: the eight-wave kernel may run (see above).
+GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool glu, bool fwd8_ok,
                   bool no_split = false) {
     GemmPlan p{};
     p.steps = (int)((k + kFwdBK - 1) / kFwdBK);
@@ -223,11 +229,12 @@ GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool glu
             ncols += ns[g];
         }
     }
-    const VariantCost* v = plan_override("DECIK_FWD_PLAN", kFwdVariants, kNumFwdVariants, p.steps, &p.splits);
+    const int nv = fwd8_ok ? kNumFwdVariants : kNumFwd4Variants;
+    const VariantCost* v = plan_override("DECIK_FWD_PLAN", kFwdVariants, nv, p.steps, &p.splits);
     if (v != nullptr && (glu || no_split)) p.splits = 1;
     if (v == nullptr) {
         const int64_t nt = p.n_tiles;
-        v = choose_plan(kFwdVariants, kNumFwdVariants, m, ncols, p.steps, [nt](const VariantCost&) { return nt; },
+        v = choose_plan(kFwdVariants, nv, m, ncols, p.steps, [nt](const VariantCost&) { return nt; },
                         &p.splits, (glu || no_split) ? 1 : 32);
     }
     p.mt = v->rows_blocks;
@@ -319,7 +326,9 @@ int dk_nf4_block_scales(const dk_nf4_weight* w, float* scales, void* stream) {
 
 int64_t dk_nf4_linear_fwd_workspace(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
     if (ngroups < 1 || ngroups > kMaxGroups || ns == nullptr || m <= 0 || k <= 0) return 0;
-    return workspace_bytes(plan_fwd(m, k, ns, ngroups, false));
+    // the plan also depends on the block sizes (eight-wave kernel or not): cover both
+    return std::max(workspace_bytes(plan_fwd(m, k, ns, ngroups, false, true)),
+                    workspace_bytes(plan_fwd(m, k, ns, ngroups, false, false)));
 }
 
 int64_t dk_nf4_linear_bwd_workspace(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
@@ -388,7 +397,9 @@ static int linear_fwd_impl(const std::string& name, const uint16_t* x, int64_t m
                 groups[0].w.blocksize != groups[1].w.blocksize))
         return fail(name + ": GLU mode needs two plain weights of one shape, blocksize >= 64, k % 64 == 0");
     if (m == 0 || tile == 0) return 0;
-    const GemmPlan p = plan_fwd(m, k, ns, ngroups, glu, no_split);
+    bool fwd8_ok = k % 64 == 0;
+    for (int g = 0; g < ngroups; ++g) fwd8_ok = fwd8_ok && k % groups[g].w.blocksize == 0;
+    const GemmPlan p = plan_fwd(m, k, ns, ngroups, glu, fwd8_ok, no_split);
     const int64_t need = workspace_bytes(p);
     if (need > 0 && (workspace == nullptr || workspace_bytes_ < need || !aligned(workspace, 256)))
         return fail(name + ": workspace too small (need " + std::to_string(need) + " bytes)");

@@ -94,7 +94,7 @@ __global__ __launch_bounds__(kLoraThreads) void lora_gu_kernel(const _Float16* _
     }
     float tot;
     block_reduce<R>(acc, red, &tot);
-    if (threadIdx.x < R) gu[m * R + threadIdx.x] = (_Float16)(scale * tot);
+    if (threadIdx.x < R) gu[m * R + threadIdx.x] = to_half(scale * tot);
 }
 
 // C[c, t] = scale * sum_m Q[m, c] P[m, t] over all m, for 16 columns c per work-group:

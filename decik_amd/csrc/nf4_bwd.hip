@@ -87,90 +87,6 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void nf4_bwd_kernel(const Bw
 
     uint8_t* wring = dring + 3 * DBUF + wave * (3 * kBwdWSlot);
     float* scales = (float*)(dring + 3 * DBUF + WAVES * 3 * kBwdWSlot + wave * kBwdScaleBytes);
-    auto ring = [&](int t) __attribute__((always_inline)) { return (t - cs0) % 3; };
-    auto group_of_step = [&](int t) __attribute__((always_inline)) {
-        int gi = 0;
-#pragma unroll
-        for (int i = 1; i < kMaxGroups; ++i)
-            if (i < a.ngroups && t >= a.g[i].step_begin) gi = i;
-        return __builtin_amdgcn_readfirstlane(gi);
-    };
-
-    // Loads of step t: the shared dY tile (cooperative), then this wave's packed bytes
-    // (transposed to dword-columns) and its rows' statistics for both 32-column halves.
-    // `live` false: every load reads zeros (steps past the split's end keep the ring's load
-    // count uniform without a branch).
-    auto load_step = [&](int t, bool live) __attribute__((always_inline)) {
-        const int gi = group_of_step(t);
-        const BwdGroupDev& G = a.g[gi];
-        const int n0 = (t - G.step_begin) * kBwdBC;
-        const int N = (int)G.w.n;
-        const rsrc_t drs = make_rsrc(G.dy, G.dy_bytes);
-        uint8_t* db = dring + ring(t) * DBUF;
-#pragma unroll
-        for (int h = 0; h < DPT; ++h) {
-            const int q = tid + NT * h;
-            const int row = q >> 3, pc = q & 7;
-            const int c = pc ^ ((row >> 1) & 7);
-            const int gm = m0 + row, gn = n0 + 8 * c;
-            bload128_lds(drs, db + (NT * h + 64 * wave) * 16,
-                         off_if(live && gm < M && gn < N, (uint32_t)(gm * G.lddy + gn) * 2u));
-        }
-        uint8_t* slot = wring + ring(t) * kBwdWSlot;
-        const rsrc_t wrs = make_rsrc(G.w.packed, G.w.packed_bytes);
-        {
-            // instruction d fetches rows 8 d .. 8 d + 7, all 8 dwords (32 contiguous bytes) of
-            // each; lane -> (row quad, dword-column, row) lands at dword 72 d + 32 rq + 4 cg + rho
-            const int rq = lane >> 5, cg = (lane >> 2) & 7, rho = lane & 3;
-            const bool cok = live && kw0 + 8 * cg < K;
-            const uint32_t cbyte = (uint32_t)((kw0 + 8 * cg) >> 1);
-#pragma unroll
-            for (int d = 0; d < 8; ++d) {
-                const int r = n0 + 8 * d + 4 * rq + rho;
-                bload32_lds(wrs, slot + d * kBwdPkStride * 4,
-                            off_if(cok && r < N, (uint32_t)r * (uint32_t)(K >> 1) + cbyte));
-            }
-        }
-        const int row = n0 + lane;  // weight row this lane fetches statistics for
-        const bool rok = live && row < N;
-        const rsrc_t ars = make_rsrc(NESTED ? (const void*)G.w.absmax8 : (const void*)G.w.absmaxf,
-                                     G.w.absmax_bytes);
-        const rsrc_t a2rs = make_rsrc(G.w.absmax2, G.w.absmax2_bytes);
-        const uint32_t bs_shift = (uint32_t)G.w.bs_shift, bs2_shift = (uint32_t)G.w.bs2_shift;
-        for (int hh = 0; hh < (wide ? 2 : 1); ++hh) {
-            const bool ok = rok && kw0 + 32 * hh < K;
-            const uint32_t blk = ((uint32_t)row * (uint32_t)K + (uint32_t)(kw0 + 32 * hh)) >> bs_shift;
-            if constexpr (NESTED) {
-                bload8_lds(ars, slot + kBwdPkBytes + 256 * hh, off_if(ok, blk));
-                bload32_lds(a2rs, slot + kBwdPkBytes + 512 + 256 * hh, off_if(ok, (blk >> bs2_shift) * 4u));
-            } else {
-                bload32_lds(ars, slot + kBwdPkBytes + 256 * hh, off_if(ok, blk * 4u));
-            }
-        }
-    };
-    // Row scales of step t (this lane's row, both halves) into the per-wave table. The
-    // statistics were fetched by this same wave, so its own wait suffices (no barrier).
-    auto make_scales = [&](int t) __attribute__((always_inline)) {
-        const int gi = group_of_step(t);
-        const BwdGroupDev& G = a.g[gi];
-        const int row = (t - G.step_begin) * kBwdBC + lane;
-        const uint8_t* slot = wring + ring(t) * kBwdWSlot;
-        const float* c2 = (const float*)(smem + gi * kBwdTableBytes);
-        const float offset = NESTED ? *G.w.offset : 0.0f;
-        float* dst = scales + ((t - cs0) & 1) * 128;
-        for (int hh = 0; hh < (wide ? 2 : 1); ++hh) {
-            const bool ok = row < (int)G.w.n && kw0 + 32 * hh < K;
-            float sc;
-            if constexpr (NESTED) {
-                const uint32_t q = slot[kBwdPkBytes + 256 * hh + 4 * lane];
-                const float a2 = *(const float*)(slot + kBwdPkBytes + 512 + 256 * hh + 4 * lane);
-                sc = c2[q] * a2 + offset;
-            } else {
-                sc = *(const float*)(slot + kBwdPkBytes + 256 * hh + 4 * lane);
-            }
-            dst[64 * hh + lane] = ok ? sc : 0.0f;
-        }
-    };
 
     float16_t acc[MB * 2];  // [token block i][column block cb] at i * 2 + cb
 #pragma unroll
@@ -208,14 +124,6 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void nf4_bwd_kernel(const Bw
         }
     }
 
-    // Prologue: three steps in flight; wait for the first.
-    load_step(cs0, cs0 < cs1);
-    load_step(cs0 + 1, cs0 + 1 < cs1);
-    load_step(cs0 + 2, cs0 + 2 < cs1);
-    wait_vmcnt<2 * NL>();
-    lds_barrier();  // dY(cs0) from every wave, code tables
-    make_scales(cs0);
-
     // Software pipeline over 16-row slices, as in the forward kernel: while the 2*MB MFMAs of
     // slice j run, the wave prepares slice j + 1 in stages placed between them (sched_barrier
     // keeps each stage next to its MFMA): A = reads of its packed dwords, row scales and dY
@@ -228,115 +136,211 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void nf4_bwd_kernel(const Bw
     constexpr int qC1 = qC0 + (nm >= 4 ? 1 : 0);
     constexpr int qBar = nm >= 8 ? 2 : (nm >= 4 ? qC0 : 0);
 
-    half8_t xf[MB], w0, w1;      // operands of the current slice
-    half8_t xn[MB], wn0, wn1;    // ... of the next slice
-    u32x4_t d0, d1;              // next slice: packed dwords of rows r0 .. r0 + 3, r0 + 4 .. r0 + 7
-    float4_t s0, s1;             // ... and their row scales
-    float vh[8], vl[8];          // ... code-book values of the high and low nibbles
-    auto pk_of = [&](int t) __attribute__((always_inline)) {
-        return (const uint32_t*)(wring + ring(t) * kBwdWSlot) + 4 * (beta >> 2);
-    };
-    auto sc_of = [&](int t) __attribute__((always_inline)) {
-        return scales + ((t - cs0) & 1) * 128 + (wide ? 64 * half : 0);
-    };
-    auto stage_A = [&](int t, int j) __attribute__((always_inline)) {
-        const uint32_t* pk = pk_of(t);
-        const float* sc = sc_of(t);
-        const int r0 = 32 * g + 8 * j, dg = 4 * g + j;
-        d0 = *(const u32x4_t*)(pk + kBwdPkStride * dg);
-        d1 = *(const u32x4_t*)(pk + kBwdPkStride * dg + 32);
-        s0 = *(const float4_t*)(sc + r0);
-        s1 = *(const float4_t*)(sc + r0 + 4);
-    };
-    auto stage_X = [&](int t, int j) __attribute__((always_inline)) {
-        const uint8_t* db = dring + ring(t) * DBUF;
-#pragma unroll
-        for (int i = 0; i < MB; ++i)
-            xn[i] = *(const half8_t*)(db + (32 * i + l32) * 128 + (((4 * g + j) ^ xsw) << 4));
-    };
-    auto stage_B = [&](int t) __attribute__((always_inline)) {
-        const uint32_t gbase4 = (uint32_t)(64 * group_of_step(t)) * 0x01010101u;
-        // this lane's byte of rows r0 .. r0 + 3 and r0 + 4 .. r0 + 7, gathered into two dwords
-        const uint32_t rb0 = __builtin_amdgcn_perm(d0[1], d0[0], bsel) | (__builtin_amdgcn_perm(d0[3], d0[2], bsel) << 16);
-        const uint32_t rb1 = __builtin_amdgcn_perm(d1[1], d1[0], bsel) | (__builtin_amdgcn_perm(d1[3], d1[2], bsel) << 16);
-        uint32_t ah0, al0, ah1, al1;
-        nib_addrs(rb0, gbase4, ah0, al0);
-        nib_addrs(rb1, gbase4, ah1, al1);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            vh[e] = lut_at(luts, ah0, e);
-            vl[e] = lut_at(luts, al0, e);
-            vh[e + 4] = lut_at(luts, ah1, e);
-            vl[e + 4] = lut_at(luts, al1, e);
-        }
-    };
-    auto stage_C = [&](const float* v) __attribute__((always_inline)) -> half8_t {
-        u32x4_t o;
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            o[q] = pack_half2(v[2 * q] * s0[2 * q], v[2 * q + 1] * s0[2 * q + 1]);
-            o[q + 2] = pack_half2(v[2 * q + 4] * s1[2 * q], v[2 * q + 5] * s1[2 * q + 1]);
-        }
-        return __builtin_bit_cast(half8_t, o);
-    };
-    auto mfma_q = [&](int q) __attribute__((always_inline)) {
-        const int i = q >> 1;
-        if (q & 1)
-            acc[i * 2 + 1] = mfma32x32x16(w1, xf[i], acc[i * 2 + 1]);
-        else
-            acc[i * 2 + 0] = mfma32x32x16(w0, xf[i], acc[i * 2 + 0]);
-    };
+    // One weight group at a time: the group's operands (pointers, sizes, block-size shifts, the
+    // nested offset) are read once before its steps, so the per-step code issues no scalar
+    // memory loads -- their out-of-order returns would make every later wait drain all
+    // outstanding LDS reads. The pipeline drains between groups.
+    for (int gi = 0; gi < a.ngroups; ++gi) {
+        const BwdGroupDev& G = a.g[gi];
+        const int sb = sgpr(G.step_begin);
+        const int t0 = max(cs0, sb), t1 = min(cs1, sb + sgpr(G.nsteps));
+        if (t0 >= t1) continue;
+        const int N = sgpr((int)G.w.n);
+        const int lddy = sgpr(G.lddy);
+        const rsrc_t drs = make_rsrc(G.dy, G.dy_bytes);
+        const rsrc_t wrs = make_rsrc(G.w.packed, G.w.packed_bytes);
+        const rsrc_t ars = make_rsrc(NESTED ? (const void*)G.w.absmax8 : (const void*)G.w.absmaxf, G.w.absmax_bytes);
+        const rsrc_t a2rs = make_rsrc(G.w.absmax2, G.w.absmax2_bytes);
+        const uint32_t bs_shift = sgpr((uint32_t)G.w.bs_shift), bs2_shift = sgpr((uint32_t)G.w.bs2_shift);
+        const float offset = NESTED ? *G.w.offset : 0.0f;
+        const float* c2 = (const float*)(smem + gi * kBwdTableBytes);
+        const uint32_t gbase4 = (uint32_t)(64 * gi) * 0x01010101u;  // this group's code book
+        auto ring = [&](int t) __attribute__((always_inline)) { return (t - t0) % 3; };
 
-    // slice 0 of the first step
-    stage_A(cs0, 0);
-    stage_X(cs0, 0);
-    stage_B(cs0);
-    w0 = stage_C(vh);
-    w1 = stage_C(vl);
+        // Loads of step t: the shared dY tile (cooperative), then this wave's packed bytes
+        // (transposed to dword-columns) and its rows' statistics for both 32-column halves.
+        // `live` false: every load reads zeros (steps past the segment's end keep the ring's
+        // load count uniform without a branch).
+        auto load_step = [&](int t, bool live) __attribute__((always_inline)) {
+            const int n0 = (t - sb) * kBwdBC;
+            uint8_t* db = dring + ring(t) * DBUF;
 #pragma unroll
-    for (int i = 0; i < MB; ++i) xf[i] = xn[i];
-
-    for (int t = cs0; t < cs1; ++t) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-#pragma unroll
-            for (int q = 0; q < nm; ++q) {
-                mfma_q(q);
-                if (j < 3) {
-                    if (q == 0) {
-                        if (j == 2) {
-                            // step t+1's loads have landed (only step t+2's may be in flight):
-                            // its row scales from its statistics (this wave's own loads)
-                            wait_vmcnt<NL>();
-                            make_scales(t + 1);
-                        }
-                        stage_A(t, j + 1);
-                        stage_X(t, j + 1);
-                    }
-                    if (q == qB) stage_B(t);
-                } else {
-                    if (q == 0) stage_A(t + 1, 0);
-                    if (q == qB) stage_B(t + 1);
-                    if (q == qBar) {
-                        // every wave is past step t's slots: refill them with step t+3 (zeros
-                        // past the split's end). Past the last step the reads of this slice see
-                        // stale slots and their values go unused.
-                        lds_barrier();
-                        load_step(t + 3, t + 3 < cs1);
-                        stage_X(t + 1, 0);
-                    }
-                }
-                if (q == qC0) wn0 = stage_C(vh);
-                if (q == qC1) wn1 = stage_C(vl);
-                __builtin_amdgcn_sched_barrier(0);
+            for (int h = 0; h < DPT; ++h) {
+                const int q = tid + NT * h;
+                const int row = q >> 3, pc = q & 7;
+                const int c = pc ^ ((row >> 1) & 7);
+                const int gm = m0 + row, gn = n0 + 8 * c;
+                bload128_lds(drs, db + (NT * h + 64 * wave) * 16,
+                             off_if(live && gm < M && gn < N, (uint32_t)(gm * lddy + gn) * 2u));
             }
+            uint8_t* slot = wring + ring(t) * kBwdWSlot;
+            {
+                // instruction d fetches rows 8 d .. 8 d + 7, all 8 dwords (32 contiguous bytes) of
+                // each; lane -> (row quad, dword-column, row) lands at dword 72 d + 32 rq + 4 cg + rho
+                const int rq = lane >> 5, cg = (lane >> 2) & 7, rho = lane & 3;
+                const bool cok = live && kw0 + 8 * cg < K;
+                const uint32_t cbyte = (uint32_t)((kw0 + 8 * cg) >> 1);
 #pragma unroll
-            for (int i = 0; i < MB; ++i) xf[i] = xn[i];
-            w0 = wn0;
-            w1 = wn1;
+                for (int d = 0; d < 8; ++d) {
+                    const int r = n0 + 8 * d + 4 * rq + rho;
+                    bload32_lds(wrs, slot + d * kBwdPkStride * 4,
+                                off_if(cok && r < N, (uint32_t)r * (uint32_t)(K >> 1) + cbyte));
+                }
+            }
+            const int row = n0 + lane;  // weight row this lane fetches statistics for
+            const bool rok = live && row < N;
+            for (int hh = 0; hh < (wide ? 2 : 1); ++hh) {
+                const bool ok = rok && kw0 + 32 * hh < K;
+                const uint32_t blk = ((uint32_t)row * (uint32_t)K + (uint32_t)(kw0 + 32 * hh)) >> bs_shift;
+                if constexpr (NESTED) {
+                    bload8_lds(ars, slot + kBwdPkBytes + 256 * hh, off_if(ok, blk));
+                    bload32_lds(a2rs, slot + kBwdPkBytes + 512 + 256 * hh, off_if(ok, (blk >> bs2_shift) * 4u));
+                } else {
+                    bload32_lds(ars, slot + kBwdPkBytes + 256 * hh, off_if(ok, blk * 4u));
+                }
+            }
+        };
+        // Row scales of step t (this lane's row, both halves) into the per-wave table. The
+        // statistics were fetched by this same wave, so its own wait suffices (no barrier).
+        auto make_scales = [&](int t) __attribute__((always_inline)) {
+            const int row = (t - sb) * kBwdBC + lane;
+            const uint8_t* slot = wring + ring(t) * kBwdWSlot;
+            float* dst = scales + ((t - t0) & 1) * 128;
+            for (int hh = 0; hh < (wide ? 2 : 1); ++hh) {
+                const bool ok = row < N && kw0 + 32 * hh < K;
+                float sc;
+                if constexpr (NESTED) {
+                    const uint32_t q = slot[kBwdPkBytes + 256 * hh + 4 * lane];
+                    const float a2 = *(const float*)(slot + kBwdPkBytes + 512 + 256 * hh + 4 * lane);
+                    sc = c2[q] * a2 + offset;
+                } else {
+                    sc = *(const float*)(slot + kBwdPkBytes + 256 * hh + 4 * lane);
+                }
+                dst[64 * hh + lane] = ok ? sc : 0.0f;
+            }
+        };
+
+        // Prologue: three steps in flight; wait for the first.
+        load_step(t0, true);
+        load_step(t0 + 1, t0 + 1 < t1);
+        load_step(t0 + 2, t0 + 2 < t1);
+        wait_vmcnt<2 * NL>();
+        lds_barrier();  // dY(t0) from every wave, code tables
+        make_scales(t0);
+
+        half8_t xf[MB], w0, w1;      // operands of the current slice
+        half8_t xn[MB], wn0, wn1;    // ... of the next slice
+        u32x4_t d0, d1;              // next slice: packed dwords of rows r0 .. r0 + 3, r0 + 4 .. r0 + 7
+        float4_t s0, s1;             // ... and their row scales
+        float vh[8], vl[8];          // ... code-book values of the high and low nibbles
+        auto pk_of = [&](int t) __attribute__((always_inline)) {
+            return (const uint32_t*)(wring + ring(t) * kBwdWSlot) + 4 * (beta >> 2);
+        };
+        auto sc_of = [&](int t) __attribute__((always_inline)) {
+            return scales + ((t - t0) & 1) * 128 + (wide ? 64 * half : 0);
+        };
+        auto stage_A = [&](int t, int j) __attribute__((always_inline)) {
+            const uint32_t* pk = pk_of(t);
+            const float* sc = sc_of(t);
+            const int r0 = 32 * g + 8 * j, dg = 4 * g + j;
+            d0 = *(const u32x4_t*)(pk + kBwdPkStride * dg);
+            d1 = *(const u32x4_t*)(pk + kBwdPkStride * dg + 32);
+            s0 = *(const float4_t*)(sc + r0);
+            s1 = *(const float4_t*)(sc + r0 + 4);
+        };
+        auto stage_X = [&](int t, int j) __attribute__((always_inline)) {
+            const uint8_t* db = dring + ring(t) * DBUF;
+#pragma unroll
+            for (int i = 0; i < MB; ++i)
+                xn[i] = *(const half8_t*)(db + (32 * i + l32) * 128 + (((4 * g + j) ^ xsw) << 4));
+        };
+        auto stage_B = [&]() __attribute__((always_inline)) {
+            // this lane's byte of rows r0 .. r0 + 3 and r0 + 4 .. r0 + 7, gathered into two dwords
+            const uint32_t rb0 = __builtin_amdgcn_perm(d0[1], d0[0], bsel) | (__builtin_amdgcn_perm(d0[3], d0[2], bsel) << 16);
+            const uint32_t rb1 = __builtin_amdgcn_perm(d1[1], d1[0], bsel) | (__builtin_amdgcn_perm(d1[3], d1[2], bsel) << 16);
+            uint32_t ah0, al0, ah1, al1;
+            nib_addrs(rb0, gbase4, ah0, al0);
+            nib_addrs(rb1, gbase4, ah1, al1);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                vh[e] = lut_at(luts, ah0, e);
+                vl[e] = lut_at(luts, al0, e);
+                vh[e + 4] = lut_at(luts, ah1, e);
+                vl[e + 4] = lut_at(luts, al1, e);
+            }
+        };
+        auto stage_C = [&](const float* v) __attribute__((always_inline)) -> half8_t {
+            u32x4_t o;
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                o[q] = pack_half2(v[2 * q] * s0[2 * q], v[2 * q + 1] * s0[2 * q + 1]);
+                o[q + 2] = pack_half2(v[2 * q + 4] * s1[2 * q], v[2 * q + 5] * s1[2 * q + 1]);
+            }
+            return __builtin_bit_cast(half8_t, o);
+        };
+        auto mfma_q = [&](int q) __attribute__((always_inline)) {
+            const int i = q >> 1;
+            if (q & 1)
+                acc[i * 2 + 1] = mfma32x32x16(w1, xf[i], acc[i * 2 + 1]);
+            else
+                acc[i * 2 + 0] = mfma32x32x16(w0, xf[i], acc[i * 2 + 0]);
+        };
+
+        // slice 0 of the first step
+        stage_A(t0, 0);
+        stage_X(t0, 0);
+        stage_B();
+        w0 = stage_C(vh);
+        w1 = stage_C(vl);
+#pragma unroll
+        for (int i = 0; i < MB; ++i) xf[i] = xn[i];
+
+        for (int t = t0; t < t1; ++t) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                for (int q = 0; q < nm; ++q) {
+                    mfma_q(q);
+                    if (j < 3) {
+                        if (q == 0) {
+                            if (j == 2) {
+                                // step t+1's loads have landed (only step t+2's may be in
+                                // flight): its row scales from its statistics (this wave's own
+                                // loads)
+                                wait_vmcnt<NL>();
+                                make_scales(t + 1);
+                            }
+                            stage_A(t, j + 1);
+                            stage_X(t, j + 1);
+                        }
+                        if (q == qB) stage_B();
+                    } else {
+                        if (q == 0) stage_A(t + 1, 0);
+                        if (q == qB) stage_B();
+                        if (q == qBar) {
+                            // every wave is past step t's slots: refill them with step t+3
+                            // (zeros past the segment's end). Past the last step the reads of
+                            // this slice see stale slots and their values go unused.
+                            lds_barrier();
+                            load_step(t + 3, t + 3 < t1);
+                            stage_X(t + 1, 0);
+                        }
+                    }
+                    if (q == qC0) wn0 = stage_C(vh);
+                    if (q == qC1) wn1 = stage_C(vl);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+#pragma unroll
+                for (int i = 0; i < MB; ++i) xf[i] = xn[i];
+                w0 = wn0;
+                w1 = wn1;
+            }
         }
+        // every load has landed and every wave is done with the rings before the next group's
+        // prologue refills them
+        wait_vmcnt<0>();
+        lds_barrier();
     }
-    wait_vmcnt<0>();
 
     // ---- epilogue: lane (l32, g) holds columns kw0 + 32 g + c, c = 2 r + cb, of token rows
     // m0 + 32 i + l32 (acc[i * 2 + cb][r]).

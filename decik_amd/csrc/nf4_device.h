@@ -112,12 +112,21 @@ __device__ __forceinline__ int64_t group_of(const NF4Dev& w, int64_t block) {
     return w.bs2_shift >= 0 ? (block >> w.bs2_shift) : block / w.blocksize2;
 }
 
-// fp32 -> two fp16 (round to nearest even) packed with `a` in the low half.
+// fp32 -> two fp16 (round to nearest even) packed with `a` in the low half. The empty asm hides
+// a product feeding the conversion from the compiler, which would otherwise fold fp16(x * y)
+// into v_fma_mix*_f16 with a +0 addend -- that turns a -0 product into +0.
 __device__ __forceinline__ uint32_t pack_half2(float a, float b) {
+    asm("" : "+v"(a), "+v"(b));
     half2_t h;
     h.x = (_Float16)a;
     h.y = (_Float16)b;
     return __builtin_bit_cast(uint32_t, h);
+}
+
+// fp32 -> fp16 (round to nearest even), the value opaque to the compiler (see pack_half2).
+__device__ __forceinline__ _Float16 to_half(float x) {
+    asm("" : "+v"(x));
+    return (_Float16)x;
 }
 
 // The fp32 scale of the block `block` (solution/nf4.py:37-43). `code2` may point to LDS.
@@ -198,6 +207,7 @@ __device__ __forceinline__ void swiglu_bwd1(float G, float g, float u, float& dg
     const float s = swiglu_sigmoid(g);
     du = G * g * s;
     dg = G * u * s * (1.0f + g * (1.0f - s));
+    asm("" : "+v"(du), "+v"(dg));  // keep a later fp16 conversion off v_fma_mix (see pack_half2)
 }
 
 __device__ __forceinline__ float4_t mfma16x16x32(half8_t a, half8_t b, float4_t c) {

@@ -97,54 +97,58 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
     // addresses (see nib_addrs)
     const uint32_t book4 = (uint32_t)(glu ? 64 * (wave >> 2) : 0) * 0x01010101u;
 
-    const rsrc_t xrs = make_rsrc(a.x, a.x_bytes);
-    const rsrc_t wrs = make_rsrc(W.packed, W.packed_bytes);
-    const rsrc_t ars = make_rsrc(NESTED ? (const void*)W.absmax8 : (const void*)W.absmaxf, W.absmax_bytes);
-    const rsrc_t a2rs = make_rsrc(W.absmax2, W.absmax2_bytes);
     const int wrow = nw0 + arow_to_n(l32);  // this lane's A row
     const bool rowok = wrow < N;
     const int xsw = (l32 >> 1) & 7;          // LDS swizzle of this lane's X rows
 
-    uint8_t* wring = xs + 3 * XBUF + wave * (3 * wslot_bytes);
-    auto ring = [&](int t) __attribute__((always_inline)) { return (t - ks0) % 3; };
-    auto xbuf = [&](int t) -> uint8_t* { return xs + ring(t) * XBUF; };
-    auto wslot = [&](int t) -> uint8_t* { return wring + ring(t) * wslot_bytes; };
-
-    // Loads of step t (`live` false: zeros, keeping the ring's load count uniform).
-    auto load_step = [&](int t, bool live) __attribute__((always_inline)) {
-        const int k0 = t * kFwdBK;
-        uint8_t* xd = xbuf(t);
+    // Loads use loop-invariant per-lane offsets (a lane outside the tile or the weight has bit 31
+    // set: it reads zeros) against buffer descriptors whose base advances with the step, so a step
+    // costs scalar additions only. This needs k % 64 == 0 and blocks that do not straddle rows
+    // (k % blocksize == 0), which the planner checks before choosing this kernel. A step past the
+    // split's end loads from descriptors of size 0 (zeros), keeping the ring's load count uniform.
+    uint32_t xo[XPT];       // X chunk h of this thread: row (tid + 512 h) / 8 of the tile
+    int xdst[XPT];          // ... and its wave's LDS destination within a ring buffer
 #pragma unroll
-        for (int h = 0; h < XPT; ++h) {
-            // chunk q lands at q * 16 = row * 128 + pc * 16; waves past the tile load zeros
-            // into the dummy area
-            const int q = tid + kF8Threads * h;
-            const int row = q >> 3, pc = q & 7;
-            const int c = pc ^ ((row >> 1) & 7);
-            const int gm = m0 + row, gk = k0 + 8 * c;
-            const int wq0 = kF8Threads * h + 64 * wave;  // the wave's first chunk (uniform)
-            uint8_t* dst = wq0 < XCH ? xd + wq0 * 16 : dummy;
-            bload128_lds(xrs, dst, off_if(live && q < XCH && gm < M && gk < K, (uint32_t)(gm * ldx + gk) * 2u));
-        }
-        const int krun = k0 + 32 * g;
-        uint8_t* slot = wslot(t);
-        bload128_lds(wrs, slot, off_if(live && rowok && krun < K, ((uint32_t)wrow * (uint32_t)K + (uint32_t)krun) >> 1));
-        // statistics: narrow -- lanes g = 0 fetch their row's block at k0 (g = 1 lanes load zeros
-        // into unused slots); wide -- every lane its row's block at its own k half
-        const int kb = wide ? krun : k0;
-        const bool sok = live && rowok && kb < K && (wide || g == 0);
-        const uint32_t blk = ((uint32_t)wrow * (uint32_t)K + (uint32_t)kb) >> bs_shift;
+    for (int h = 0; h < XPT; ++h) {
+        const int q = tid + kF8Threads * h;
+        const int row = q >> 3, pc = q & 7;
+        const int c = pc ^ ((row >> 1) & 7);
+        const int gm = m0 + row;
+        xo[h] = off_if(q < XCH && gm < M, (uint32_t)(gm * ldx + 8 * c) * 2u);
+        const int wq0 = kF8Threads * h + 64 * wave;  // the wave's first chunk (uniform)
+        xdst[h] = wq0 < XCH ? wq0 * 16 : -1;         // waves past the tile load into the dummy area
+    }
+    const uint32_t wo = off_if(rowok, ((uint32_t)wrow * (uint32_t)K + 32u * (uint32_t)g) >> 1);
+    // statistics: narrow -- lanes g = 0 fetch their row's block (g = 1 lanes load zeros into
+    // unused slots); wide (blocksize 32) -- every lane its row's block at its own k half
+    const uint32_t blk0 = ((uint32_t)wrow * (uint32_t)K + (wide ? 32u * (uint32_t)g : 0u)) >> bs_shift;
+    const bool sok = rowok && (wide || g == 0);
+    const uint32_t so = off_if(sok, NESTED ? blk0 : blk0 * 4u);
+
+    uint8_t* wring = xs + 3 * XBUF + wave * (3 * wslot_bytes);
+    auto load_step = [&](int t, int rx, int rw, bool live) __attribute__((always_inline)) {
+        const uint32_t k0 = (uint32_t)t * kFwdBK;
+        const rsrc_t xrs = make_rsrc((const uint8_t*)a.x + 2u * k0, live ? a.x_bytes - 2u * k0 : 0u);
+#pragma unroll
+        for (int h = 0; h < XPT; ++h)
+            bload128_lds(xrs, xdst[h] >= 0 ? xs + rx + xdst[h] : dummy, xo[h]);
+        uint8_t* slot = wring + rw;
+        const rsrc_t wrs = make_rsrc(W.packed + k0 / 2u, live ? W.packed_bytes - k0 / 2u : 0u);
+        bload128_lds(wrs, slot, wo);
+        const uint32_t kb = k0 >> bs_shift;  // blocks of a row before this step
         if constexpr (NESTED) {
-            bload8_lds(ars, slot + 1024, off_if(sok, blk));
-            bload32_lds(a2rs, slot + 1280, off_if(sok, (blk >> bs2_shift) * 4u));
+            const rsrc_t ars = make_rsrc(W.absmax8 + kb, live ? W.absmax_bytes - kb : 0u);
+            const rsrc_t a2rs = make_rsrc(W.absmax2, live ? W.absmax2_bytes : 0u);
+            bload8_lds(ars, slot + 1024, so);
+            bload32_lds(a2rs, slot + 1280, off_if(sok, ((blk0 + kb) >> bs2_shift) * 4u));
         } else {
-            bload32_lds(ars, slot + 1024, off_if(sok, blk * 4u));
+            const rsrc_t ars = make_rsrc(W.absmaxf + kb, live ? W.absmax_bytes - 4u * kb : 0u);
+            bload32_lds(ars, slot + 1024, so);
         }
     };
     // fp32 scale of this lane's row at step t (0 outside the weight)
-    auto scale_of = [&](const uint8_t* slot, int t) __attribute__((always_inline)) -> float {
+    auto scale_of = [&](const uint8_t* slot) __attribute__((always_inline)) -> float {
         const int si = wide ? lane : l32;
-        const bool ok = rowok && t * kFwdBK + 32 * g < K;
         float sc;
         if constexpr (NESTED) {
             const uint32_t q = slot[1024 + 4 * si];
@@ -153,7 +157,7 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
         } else {
             sc = *(const float*)(slot + 1024 + 4 * si);
         }
-        return ok ? sc : 0.0f;
+        return rowok ? sc : 0.0f;
     };
     auto xfrag = [&](const uint8_t* xb, int i, int j) __attribute__((always_inline)) -> half8_t {
         return *(const half8_t*)(xb + (32 * i + l32) * 128 + (((4 * g + j) ^ xsw) << 4));
@@ -182,26 +186,29 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
         }
     }
 
+    // Ring buffers: step t uses X buffer rx0 (byte offset in the X ring) and weight slot rw0;
+    // step t + 1 uses rx1 / rw1; step t + 3 reuses step t's.
+    int rx0 = 0, rw0 = 0, rx1 = XBUF, rw1 = wslot_bytes;
     // Prologue: three steps in flight; wait for the first.
-    load_step(ks0, true);
-    load_step(ks0 + 1, ks0 + 1 < ks1);
-    load_step(ks0 + 2, ks0 + 2 < ks1);
+    load_step(ks0, 0, 0, true);
+    load_step(ks0 + 1, XBUF, wslot_bytes, ks0 + 1 < ks1);
+    load_step(ks0 + 2, 2 * XBUF, 2 * wslot_bytes, ks0 + 2 < ks1);
     wait_vmcnt<2 * NL>();
     lds_barrier();
 
     u32x4_t p;  // packed weights of the current step (slice j: dword j)
     float s;    // their scale
-    auto fetch_step = [&](int t) __attribute__((always_inline)) {
-        const uint8_t* ws = wslot(t);
+    auto fetch_step = [&](int rw) __attribute__((always_inline)) {
+        const uint8_t* ws = wring + rw;
         p = *(const u32x4_t*)(ws + 16 * lane);
-        s = scale_of(ws, t);
+        s = scale_of(ws);
     };
     half8_t xf[MB], w, wn;
     uint32_t ah, al;  // code-book byte addresses of the next slice (see nib_addrs)
     float v[8];       // its code-book values
-    fetch_step(ks0);
+    fetch_step(rw0);
 #pragma unroll
-    for (int i = 0; i < MB; ++i) xf[i] = xfrag(xbuf(ks0), i, 0);
+    for (int i = 0; i < MB; ++i) xf[i] = xfrag(xs + rx0, i, 0);
     {
         nib_addrs(p[0], book4, ah, al);
         u32x4_t o;
@@ -224,12 +231,12 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
                     // slots again: refill them with step t+3. Past the last step these reads
                     // see stale slots and their values go unused.
                     wait_vmcnt<NL>();
-                    fetch_step(t + 1);
+                    fetch_step(rw1);
                     lds_barrier();
-                    load_step(t + 3, t + 3 < ks1);
+                    load_step(t + 3, rx0, rw0, t + 3 < ks1);
                 }
                 // refill the X fragment the MFMA above has read (slice j + 1)
-                xf[q] = xfrag(j < 3 ? xbuf(t) : xbuf(t + 1), q, jn);
+                xf[q] = xfrag(xs + (j < 3 ? rx0 : rx1), q, jn);
                 if (q == (j < 3 ? qA : qA + 1)) nib_addrs(p[jn], book4, ah, al);
                 if (q == (j < 3 ? qB : qB + 1)) {
 #pragma unroll
@@ -248,6 +255,11 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
             }
             w = wn;
         }
+        // rotate the rings: step t + 1's buffers become the current ones
+        rx0 = rx1;
+        rw0 = rw1;
+        rx1 = rx1 == 2 * XBUF ? 0 : rx1 + XBUF;
+        rw1 = rw1 == 2 * wslot_bytes ? 0 : rw1 + wslot_bytes;
     }
     wait_vmcnt<0>();
     lds_barrier();  // every wave is done with the X ring: it becomes the staging area
