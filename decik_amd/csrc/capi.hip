@@ -75,6 +75,8 @@ int gemm_weight_ok(const dk_nf4_weight& w, const char* who) {
         return fail(std::string(who) + ": blocksize must be a power of two >= 32");
     if (w.nested && log2_exact(w.blocksize2) < 0)
         return fail(std::string(who) + ": blocksize2 must be a power of two");
+    // the kernels advance block indices by whole 64-row / 64-column steps
+    if ((64 * w.k) % w.blocksize != 0) return fail(std::string(who) + ": blocksize must divide 64 * k");
     if (w.n > INT32_MAX / 2) return fail(std::string(who) + ": too many weight rows");
     return 0;
 }

@@ -12,11 +12,13 @@ __device__ __forceinline__ int xcd_logical_id() {
     return (bid & 7) * (nwg >> 3) + (bid >> 3);
 }
 
-// Pin a wave-uniform 32-bit value in an SGPR: the empty asm hides where the value came from, so
-// the compiler can neither re-load it from memory later nor move it to a VGPR.
+// Pin a wave-uniform 32- or 64-bit value (a pointer: an SGPR pair) in scalar registers: the empty
+// asm hides where the value came from, so the compiler can neither re-load it from memory later
+// -- inside a loop that would be a scalar load, whose out-of-order return forces a wait on every
+// outstanding LDS read -- nor move it to a VGPR.
 template <typename T>
 __device__ __forceinline__ T sgpr(T v) {
-    static_assert(sizeof(T) == 4, "32-bit values only");
+    static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32- or 64-bit values only");
     asm volatile("" : "+s"(v));
     return v;
 }

@@ -55,7 +55,8 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void nf4_bwd_kernel(const Bw
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     uint8_t* dring = smem + kBwdHeader;
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS bases stay scalar
     const int l32 = lane & 31, g = lane >> 5;
     const int beta = arow_to_n(l32);      // this lane's packed byte within the wave's 32
     const int half = beta >> 4;           // ... and its 32-column half (scale)
@@ -147,67 +148,101 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void nf4_bwd_kernel(const Bw
         if (t0 >= t1) continue;
         const int N = sgpr((int)G.w.n);
         const int lddy = sgpr(G.lddy);
-        const rsrc_t drs = make_rsrc(G.dy, G.dy_bytes);
-        const rsrc_t wrs = make_rsrc(G.w.packed, G.w.packed_bytes);
-        const rsrc_t ars = make_rsrc(NESTED ? (const void*)G.w.absmax8 : (const void*)G.w.absmaxf, G.w.absmax_bytes);
-        const rsrc_t a2rs = make_rsrc(G.w.absmax2, G.w.absmax2_bytes);
+        // the group's buffers, held in scalar registers for the whole segment
+        const _Float16* const gdy = sgpr(G.dy);
+        const uint32_t dy_bytes = sgpr(G.dy_bytes);
+        const uint8_t* const gpk = sgpr(G.w.packed);
+        const uint32_t pk_bytes = sgpr(G.w.packed_bytes);
+        const uint8_t* const gam8 = NESTED ? sgpr(G.w.absmax8) : nullptr;
+        const float* const gamf = NESTED ? nullptr : sgpr(G.w.absmaxf);
+        const uint32_t am_bytes = sgpr(G.w.absmax_bytes);
+        const float* const gam2 = NESTED ? sgpr(G.w.absmax2) : nullptr;
+        const uint32_t am2_bytes = NESTED ? sgpr(G.w.absmax2_bytes) : 0u;
         const uint32_t bs_shift = sgpr((uint32_t)G.w.bs_shift), bs2_shift = sgpr((uint32_t)G.w.bs2_shift);
         const float offset = NESTED ? *G.w.offset : 0.0f;
         const float* c2 = (const float*)(smem + gi * kBwdTableBytes);
         const uint32_t gbase4 = (uint32_t)(64 * gi) * 0x01010101u;  // this group's code book
-        auto ring = [&](int t) __attribute__((always_inline)) { return (t - t0) % 3; };
 
-        // Loads of step t: the shared dY tile (cooperative), then this wave's packed bytes
-        // (transposed to dword-columns) and its rows' statistics for both 32-column halves.
-        // `live` false: every load reads zeros (steps past the segment's end keep the ring's
-        // load count uniform without a branch).
-        auto load_step = [&](int t, bool live) __attribute__((always_inline)) {
+        // Loads use per-lane offsets fixed for the group (bit 31 set where the lane's data lies
+        // outside the tile or the weight: it reads zeros) against buffer descriptors whose base
+        // advances by whole steps, so a step costs scalar additions. Only a group's last step,
+        // when its row count is not a multiple of 64, also checks rows per lane. A step past the
+        // segment's end loads from descriptors of size 0 (zeros), keeping the load count uniform.
+        uint32_t dyo[DPT];  // dY chunk h of this thread: token row (tid + NT h) / 8 of the tile
+        int dyc[DPT];       // ... its first column within the step
+#pragma unroll
+        for (int h = 0; h < DPT; ++h) {
+            const int q = tid + NT * h;
+            const int row = q >> 3, pc = q & 7;
+            const int c = pc ^ ((row >> 1) & 7);
+            const int gm = m0 + row;
+            dyc[h] = 8 * c;
+            dyo[h] = off_if(gm < M, (uint32_t)(gm * lddy + 8 * c) * 2u);
+        }
+        // packed bytes: instruction d fetches rows 8 d .. 8 d + 7, all 8 dwords (32 contiguous
+        // bytes) of each; lane -> (row quad, dword-column, row) lands at dword
+        // 72 d + 32 rq + 4 cg + rho
+        const int rq = lane >> 5, cg = (lane >> 2) & 7, rho = lane & 3;
+        const uint32_t po = off_if(kw0 + 8 * cg < K, (uint32_t)(4 * rq + rho) * (uint32_t)(K >> 1) + (uint32_t)((kw0 + 8 * cg) >> 1));
+        const uint32_t prow8 = 8u * (uint32_t)(K >> 1);  // bytes of 8 weight rows
+        // statistics: lane = weight row of the step, one block per 32-column half
+        uint32_t blk0[2], so[2];
+        bool cok[2];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            cok[hh] = kw0 + 32 * hh < K;
+            blk0[hh] = ((uint32_t)lane * (uint32_t)K + (uint32_t)(kw0 + 32 * hh)) >> bs_shift;
+            so[hh] = off_if(cok[hh], NESTED ? blk0[hh] : blk0[hh] * 4u);
+        }
+
+        auto load_step = [&](int t, int rd, int rw, bool live) __attribute__((always_inline)) {
             const int n0 = (t - sb) * kBwdBC;
-            uint8_t* db = dring + ring(t) * DBUF;
+            const bool tail = n0 + kBwdBC > N;  // uniform
+            const rsrc_t drs = make_rsrc(gdy + n0, live ? dy_bytes - 2u * (uint32_t)n0 : 0u);
+            uint8_t* slot = wring + rw;
+            const uint32_t pskip = (uint32_t)n0 * (uint32_t)(K >> 1);
+            const rsrc_t wrs = make_rsrc(gpk + pskip, live ? pk_bytes - pskip : 0u);
+            if (!tail) {
 #pragma unroll
-            for (int h = 0; h < DPT; ++h) {
-                const int q = tid + NT * h;
-                const int row = q >> 3, pc = q & 7;
-                const int c = pc ^ ((row >> 1) & 7);
-                const int gm = m0 + row, gn = n0 + 8 * c;
-                bload128_lds(drs, db + (NT * h + 64 * wave) * 16,
-                             off_if(live && gm < M && gn < N, (uint32_t)(gm * lddy + gn) * 2u));
-            }
-            uint8_t* slot = wring + ring(t) * kBwdWSlot;
-            {
-                // instruction d fetches rows 8 d .. 8 d + 7, all 8 dwords (32 contiguous bytes) of
-                // each; lane -> (row quad, dword-column, row) lands at dword 72 d + 32 rq + 4 cg + rho
-                const int rq = lane >> 5, cg = (lane >> 2) & 7, rho = lane & 3;
-                const bool cok = live && kw0 + 8 * cg < K;
-                const uint32_t cbyte = (uint32_t)((kw0 + 8 * cg) >> 1);
+                for (int h = 0; h < DPT; ++h) bload128_lds(drs, dring + rd + (NT * h + 64 * wave) * 16, dyo[h]);
 #pragma unroll
-                for (int d = 0; d < 8; ++d) {
-                    const int r = n0 + 8 * d + 4 * rq + rho;
+                for (int d = 0; d < 8; ++d) bload32_lds(wrs, slot + d * kBwdPkStride * 4, po + (uint32_t)d * prow8);
+            } else {
+                // the group's last step with fewer than 64 rows left: rows and dY columns past N
+                // read zeros
+#pragma unroll
+                for (int h = 0; h < DPT; ++h)
+                    bload128_lds(drs, dring + rd + (NT * h + 64 * wave) * 16, off_if(n0 + dyc[h] < N, dyo[h]));
+#pragma unroll
+                for (int d = 0; d < 8; ++d)
                     bload32_lds(wrs, slot + d * kBwdPkStride * 4,
-                                off_if(cok && r < N, (uint32_t)r * (uint32_t)(K >> 1) + cbyte));
-                }
+                                off_if(n0 + 8 * d + 4 * rq + rho < N, po + (uint32_t)d * prow8));
             }
-            const int row = n0 + lane;  // weight row this lane fetches statistics for
-            const bool rok = live && row < N;
-            for (int hh = 0; hh < (wide ? 2 : 1); ++hh) {
-                const bool ok = rok && kw0 + 32 * hh < K;
-                const uint32_t blk = ((uint32_t)row * (uint32_t)K + (uint32_t)(kw0 + 32 * hh)) >> bs_shift;
+            const uint32_t kb = ((uint32_t)n0 * (uint32_t)K) >> bs_shift;  // blocks before this step
+            const bool rok = !tail || n0 + lane < N;
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                if (hh == 1 && !wide) break;
                 if constexpr (NESTED) {
-                    bload8_lds(ars, slot + kBwdPkBytes + 256 * hh, off_if(ok, blk));
-                    bload32_lds(a2rs, slot + kBwdPkBytes + 512 + 256 * hh, off_if(ok, (blk >> bs2_shift) * 4u));
+                    const rsrc_t ars = make_rsrc(gam8 + kb, live ? am_bytes - kb : 0u);
+                    const rsrc_t a2rs = make_rsrc(gam2, live ? am2_bytes : 0u);
+                    bload8_lds(ars, slot + kBwdPkBytes + 256 * hh, off_if(rok, so[hh]));
+                    bload32_lds(a2rs, slot + kBwdPkBytes + 512 + 256 * hh,
+                                off_if(rok && cok[hh], ((blk0[hh] + kb) >> bs2_shift) * 4u));
                 } else {
-                    bload32_lds(ars, slot + kBwdPkBytes + 256 * hh, off_if(ok, blk * 4u));
+                    const rsrc_t ars = make_rsrc(gamf + kb, live ? am_bytes - 4u * kb : 0u);
+                    bload32_lds(ars, slot + kBwdPkBytes + 256 * hh, off_if(rok, so[hh]));
                 }
             }
         };
-        // Row scales of step t (this lane's row, both halves) into the per-wave table. The
-        // statistics were fetched by this same wave, so its own wait suffices (no barrier).
-        auto make_scales = [&](int t) __attribute__((always_inline)) {
+        // Row scales of step t (this lane's row, both halves) from slot rw into scale table sidx.
+        // The statistics were fetched by this same wave, so its own wait suffices (no barrier).
+        auto make_scales = [&](int t, int rw, int sidx) __attribute__((always_inline)) {
             const int row = (t - sb) * kBwdBC + lane;
-            const uint8_t* slot = wring + ring(t) * kBwdWSlot;
-            float* dst = scales + ((t - t0) & 1) * 128;
+            const uint8_t* slot = wring + rw;
+            float* dst = scales + sidx * 128;
             for (int hh = 0; hh < (wide ? 2 : 1); ++hh) {
-                const bool ok = row < N && kw0 + 32 * hh < K;
+                const bool ok = row < N && cok[hh];
                 float sc;
                 if constexpr (NESTED) {
                     const uint32_t q = slot[kBwdPkBytes + 256 * hh + 4 * lane];
@@ -220,36 +255,33 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void nf4_bwd_kernel(const Bw
             }
         };
 
+        // Ring buffers: step t uses dY buffer rd0 (byte offset in the dY ring), weight slot rw0
+        // and scale table si0; step t + 1 uses rd1 / rw1 / 1 - si0; step t + 3 reuses step t's.
+        int rd0 = 0, rw0 = 0, rd1 = DBUF, rw1 = kBwdWSlot, si0 = 0;
         // Prologue: three steps in flight; wait for the first.
-        load_step(t0, true);
-        load_step(t0 + 1, t0 + 1 < t1);
-        load_step(t0 + 2, t0 + 2 < t1);
+        load_step(t0, 0, 0, true);
+        load_step(t0 + 1, DBUF, kBwdWSlot, t0 + 1 < t1);
+        load_step(t0 + 2, 2 * DBUF, 2 * kBwdWSlot, t0 + 2 < t1);
         wait_vmcnt<2 * NL>();
         lds_barrier();  // dY(t0) from every wave, code tables
-        make_scales(t0);
+        make_scales(t0, 0, 0);
 
         half8_t xf[MB], w0, w1;      // operands of the current slice
         half8_t xn[MB], wn0, wn1;    // ... of the next slice
         u32x4_t d0, d1;              // next slice: packed dwords of rows r0 .. r0 + 3, r0 + 4 .. r0 + 7
         float4_t s0, s1;             // ... and their row scales
         float vh[8], vl[8];          // ... code-book values of the high and low nibbles
-        auto pk_of = [&](int t) __attribute__((always_inline)) {
-            return (const uint32_t*)(wring + ring(t) * kBwdWSlot) + 4 * (beta >> 2);
-        };
-        auto sc_of = [&](int t) __attribute__((always_inline)) {
-            return scales + ((t - t0) & 1) * 128 + (wide ? 64 * half : 0);
-        };
-        auto stage_A = [&](int t, int j) __attribute__((always_inline)) {
-            const uint32_t* pk = pk_of(t);
-            const float* sc = sc_of(t);
+        auto stage_A = [&](int rw, int sidx, int j) __attribute__((always_inline)) {
+            const uint32_t* pk = (const uint32_t*)(wring + rw) + 4 * (beta >> 2);
+            const float* sc = scales + sidx * 128 + (wide ? 64 * half : 0);
             const int r0 = 32 * g + 8 * j, dg = 4 * g + j;
             d0 = *(const u32x4_t*)(pk + kBwdPkStride * dg);
             d1 = *(const u32x4_t*)(pk + kBwdPkStride * dg + 32);
             s0 = *(const float4_t*)(sc + r0);
             s1 = *(const float4_t*)(sc + r0 + 4);
         };
-        auto stage_X = [&](int t, int j) __attribute__((always_inline)) {
-            const uint8_t* db = dring + ring(t) * DBUF;
+        auto stage_X = [&](int rd, int j) __attribute__((always_inline)) {
+            const uint8_t* db = dring + rd;
 #pragma unroll
             for (int i = 0; i < MB; ++i)
                 xn[i] = *(const half8_t*)(db + (32 * i + l32) * 128 + (((4 * g + j) ^ xsw) << 4));
@@ -287,8 +319,8 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void nf4_bwd_kernel(const Bw
         };
 
         // slice 0 of the first step
-        stage_A(t0, 0);
-        stage_X(t0, 0);
+        stage_A(rw0, si0, 0);
+        stage_X(rd0, 0);
         stage_B();
         w0 = stage_C(vh);
         w1 = stage_C(vl);
@@ -308,22 +340,22 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void nf4_bwd_kernel(const Bw
                                 // flight): its row scales from its statistics (this wave's own
                                 // loads)
                                 wait_vmcnt<NL>();
-                                make_scales(t + 1);
+                                make_scales(t + 1, rw1, 1 - si0);
                             }
-                            stage_A(t, j + 1);
-                            stage_X(t, j + 1);
+                            stage_A(rw0, si0, j + 1);
+                            stage_X(rd0, j + 1);
                         }
                         if (q == qB) stage_B();
                     } else {
-                        if (q == 0) stage_A(t + 1, 0);
+                        if (q == 0) stage_A(rw1, 1 - si0, 0);
                         if (q == qB) stage_B();
                         if (q == qBar) {
                             // every wave is past step t's slots: refill them with step t+3
                             // (zeros past the segment's end). Past the last step the reads of
                             // this slice see stale slots and their values go unused.
                             lds_barrier();
-                            load_step(t + 3, t + 3 < t1);
-                            stage_X(t + 1, 0);
+                            load_step(t + 3, rd0, rw0, t + 3 < t1);
+                            stage_X(rd1, 0);
                         }
                     }
                     if (q == qC0) wn0 = stage_C(vh);
@@ -335,6 +367,12 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void nf4_bwd_kernel(const Bw
                 w0 = wn0;
                 w1 = wn1;
             }
+            // rotate the rings: step t + 1's buffers become the current ones
+            rd0 = rd1;
+            rw0 = rw1;
+            rd1 = rd1 == 2 * DBUF ? 0 : rd1 + DBUF;
+            rw1 = rw1 == 2 * kBwdWSlot ? 0 : rw1 + kBwdWSlot;
+            si0 = 1 - si0;
         }
         // every load has landed and every wave is done with the rings before the next group's
         // prologue refills them

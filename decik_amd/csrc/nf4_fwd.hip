@@ -53,7 +53,8 @@ __global__ __launch_bounds__(kGemmThreads, MB <= 4 ? 2 : 1) void nf4_fwd_kernel(
     float* c2 = (float*)smem;
     uint8_t* xs = smem + kFwdSmemHeader;
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS bases stay scalar
     const int l32 = lane & 31, g = lane >> 5;
     const bool wide = a.wide_stats != 0;
     const bool glu = a.glu != 0;  // (host: plain narrow statistics, two weights of one shape)

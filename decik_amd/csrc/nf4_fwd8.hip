@@ -57,7 +57,8 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
     uint8_t* dummy = smem + kF8Header;
     uint8_t* xs = dummy + kF8Dummy;
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS bases stay scalar
     const int l32 = lane & 31, g = lane >> 5;
     const bool wide = a.wide_stats != 0;
     const bool glu = a.glu != 0;
@@ -125,24 +126,34 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
     const bool sok = rowok && (wide || g == 0);
     const uint32_t so = off_if(sok, NESTED ? blk0 : blk0 * 4u);
 
+    // the buffers, held in scalar registers for the whole loop
+    const uint8_t* const gx = sgpr((const uint8_t*)a.x);
+    const uint32_t x_bytes = sgpr(a.x_bytes);
+    const uint8_t* const gpk = sgpr(W.packed);
+    const uint32_t pk_bytes = sgpr(W.packed_bytes);
+    const uint8_t* const gam8 = NESTED ? sgpr(W.absmax8) : nullptr;
+    const float* const gamf = NESTED ? nullptr : sgpr(W.absmaxf);
+    const uint32_t am_bytes = sgpr(W.absmax_bytes);
+    const float* const gam2 = NESTED ? sgpr(W.absmax2) : nullptr;
+    const uint32_t am2_bytes = NESTED ? sgpr(W.absmax2_bytes) : 0u;
     uint8_t* wring = xs + 3 * XBUF + wave * (3 * wslot_bytes);
     auto load_step = [&](int t, int rx, int rw, bool live) __attribute__((always_inline)) {
         const uint32_t k0 = (uint32_t)t * kFwdBK;
-        const rsrc_t xrs = make_rsrc((const uint8_t*)a.x + 2u * k0, live ? a.x_bytes - 2u * k0 : 0u);
+        const rsrc_t xrs = make_rsrc(gx + 2u * k0, live ? x_bytes - 2u * k0 : 0u);
 #pragma unroll
         for (int h = 0; h < XPT; ++h)
             bload128_lds(xrs, xdst[h] >= 0 ? xs + rx + xdst[h] : dummy, xo[h]);
         uint8_t* slot = wring + rw;
-        const rsrc_t wrs = make_rsrc(W.packed + k0 / 2u, live ? W.packed_bytes - k0 / 2u : 0u);
+        const rsrc_t wrs = make_rsrc(gpk + k0 / 2u, live ? pk_bytes - k0 / 2u : 0u);
         bload128_lds(wrs, slot, wo);
         const uint32_t kb = k0 >> bs_shift;  // blocks of a row before this step
         if constexpr (NESTED) {
-            const rsrc_t ars = make_rsrc(W.absmax8 + kb, live ? W.absmax_bytes - kb : 0u);
-            const rsrc_t a2rs = make_rsrc(W.absmax2, live ? W.absmax2_bytes : 0u);
+            const rsrc_t ars = make_rsrc(gam8 + kb, live ? am_bytes - kb : 0u);
+            const rsrc_t a2rs = make_rsrc(gam2, live ? am2_bytes : 0u);
             bload8_lds(ars, slot + 1024, so);
             bload32_lds(a2rs, slot + 1280, off_if(sok, ((blk0 + kb) >> bs2_shift) * 4u));
         } else {
-            const rsrc_t ars = make_rsrc(W.absmaxf + kb, live ? W.absmax_bytes - 4u * kb : 0u);
+            const rsrc_t ars = make_rsrc(gamf + kb, live ? am_bytes - 4u * kb : 0u);
             bload32_lds(ars, slot + 1024, so);
         }
     };

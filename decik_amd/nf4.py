@@ -86,7 +86,7 @@ def fused_ok(quant_state, k=None):
     n, kk = (int(s) for s in qs.shape)
     pow2 = lambda v: v > 0 and (v & (v - 1)) == 0  # noqa: E731
     bs = int(qs.blocksize)
-    return (kk % 32 == 0 and bs % 32 == 0 and pow2(bs) and n % 8 == 0 and n * kk < 2 ** 32
+    return (kk % 32 == 0 and bs % 32 == 0 and pow2(bs) and (64 * kk) % bs == 0 and n % 8 == 0 and n * kk < 2 ** 32
             and (not qs.nested or pow2(int(qs.state2.blocksize)))
             and (k is None or k == kk))
 
