@@ -102,7 +102,8 @@ int pad8(int g) { return (g + 7) & ~7; }
 // Launch planning. A plan picks the kernel variant (token rows per tile) and the number of
 // contraction splits by an estimate of the launch time:
 //   full rounds of resident work-groups x steps per split x step time (all slots busy)
-//   + a last, partial round, whose work-groups run faster on less loaded CUs
+//   + a last, partial round: a full round's time if some CU holds two of its work-groups,
+//     else faster (one work-group per CU)
 //   + the split-K cost, proportional to the fp32 partial tiles written and read back.
 // Resident work-groups per CU and the step times are per-variant constants measured on MI355X
 // (Qwen2.5-1.5B MLP launches at M = 830).
@@ -112,10 +113,10 @@ struct VariantCost {
     int bn;            // output columns per tile
     int per_cu;        // resident work-groups per CU
     double step_us;    // one 64-wide contraction step of one work-group, every slot busy
-    double lone;       // step time relative to step_us with few work-groups per CU
+    double lone;       // step time relative to step_us with one work-group per CU
 };
 
-constexpr double kPartialUsPerMB = 0.45;  // split-K: partial slabs written, then read and summed
+constexpr double kPartialUsPerMB = 0.36;  // split-K: partial slabs written, then read and summed
 constexpr double kReduceLaunchUs = 4.0;   // split-K: the reduction launch
 constexpr int kRowUnit = 32;              // token rows per row block
 
@@ -129,9 +130,12 @@ double plan_time(const VariantCost& v, int64_t m, int64_t col_tiles, int64_t nco
     const int64_t wgs = tiles * splits;
     const int64_t full = wgs / slots, rem = wgs - full * slots;
     double t = (double)full * per * v.step_us;
-    if (rem > 0) {
-        const double load = (double)rem / (double)slots;
-        t += per * v.step_us * (load > v.lone ? load : v.lone);
+    if (rem > num_cus()) {
+        // some CU holds two work-groups of the last round: it takes a full round's time
+        t += per * v.step_us;
+    } else if (rem > 0) {
+        // one work-group per CU at most: each runs faster than with a busy neighbour
+        t += per * v.step_us * v.lone;
     }
     if (splits > 1) t += (double)splits * m * ncols * 4.0 * 1e-6 * kPartialUsPerMB + kReduceLaunchUs;
     return t;
@@ -201,10 +205,10 @@ constexpr VariantCost kFwdVariants[] = {{1, 4, kFwdBN, 3, 2.35, 0.65},
                                        {2, 4, kFwdBN, 2, 2.23, 0.65},
                                        {4, 4, kFwdBN, 2, 3.10, 0.65},
                                        {8, 4, kFwdBN, 1, 2.94, 0.85},
-                                       {8, 8, kFwdBN, 1, 2.60, 0.80},
-                                       {9, 8, kFwdBN, 1, 2.95, 0.80}};
+                                       {8, 8, kFwdBN, 1, 2.25, 0.90},
+                                       {9, 8, kFwdBN, 1, 2.45, 0.90}};
 constexpr int kNumFwdVariants = sizeof(kFwdVariants) / sizeof(kFwdVariants[0]);
-constexpr VariantCost kBwdVariants[] = {{2, 4, 256, 2, 3.20, 0.90},
+constexpr VariantCost kBwdVariants[] = {{2, 4, 256, 2, 2.55, 0.90},
                                        {2, 8, 512, 1, 2.60, 1.0},
                                        {4, 8, 512, 1, 3.40, 1.0}};
 
