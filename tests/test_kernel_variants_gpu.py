@@ -1,0 +1,67 @@
+"""Every fused GEMM kernel variant on weights the Python layer would otherwise route through cached
+fp32 block scales: nested double-quant statistics read by the kernels themselves (blocks of 64,
+128 and 256 weights, so a block spans one to four 64-wide steps), plain blocksize-32 statistics
+(two scales per lane), and weights whose row count leaves a partial last step in the backward
+kernel. Plans are forced so that each kernel and its split-K path run (solution/nf4.py:93-104;
+the summed input gradient of solution/mlp.py:106-109)."""
+import pytest
+
+from helpers import O, assert_close, make_weight, randn16
+
+pytestmark = pytest.mark.gpu
+
+CASES = [(True, 64), (True, 128), (True, 256), (False, 32)]
+
+
+@pytest.fixture
+def raw_statistics(monkeypatch):
+    """Describe nested weights to the kernels as they are (no cached block scales)."""
+    from decik_amd import nf4
+
+    monkeypatch.setattr(nf4, "_scales", lambda packed, qs, device: None)
+
+
+@pytest.mark.parametrize("plan", ["4,1,4", "2,3,4", "8,1,8", "9,2,8"])
+@pytest.mark.parametrize("nested,blocksize", CASES)
+def test_forward_variants(nested, blocksize, plan, device, monkeypatch, raw_statistics):
+    from decik_amd.nf4 import linear_forward
+
+    monkeypatch.setenv("DECIK_FWD_PLAN", plan)
+    packed, qs, w16 = make_weight((320, 1024), seed=blocksize + 7, device=device, nested=nested,
+                                  blocksize=blocksize)
+    x = randn16((300, 1024), seed=9, device=device)
+    b = randn16((320,), seed=10, device=device, std=0.1)
+    (y,) = linear_forward(x, [dict(packed=packed, qs=qs, bias=b)])
+    assert_close(y, O.linear_ref(x.cpu().numpy(), w16, b.cpu().numpy()),
+                 what=f"fwd {plan} nested={nested} bs={blocksize}")
+
+
+@pytest.mark.parametrize("plan", ["2,1,4", "2,2,8", "4,1,8", "4,3,8"])
+@pytest.mark.parametrize("nested,blocksize", CASES)
+def test_backward_variants_partial_last_step(nested, blocksize, plan, device, monkeypatch, raw_statistics):
+    """264 weight rows: the last 64-row step has 8 rows; dY columns and weight rows past them read
+    zeros."""
+    from decik_amd.nf4 import linear_backward
+
+    monkeypatch.setenv("DECIK_BWD_PLAN", plan)
+    packed, qs, w16 = make_weight((264, 1024), seed=blocksize + 11, device=device, nested=nested,
+                                  blocksize=blocksize)
+    dy = randn16((300, 264), seed=12, device=device, std=1e-2)
+    dx = linear_backward([dict(packed=packed, qs=qs, dy=dy)], 300, 1024)
+    assert_close(dx, O.linear_dx_ref(dy.cpu().numpy(), w16), what=f"bwd {plan} nested={nested} bs={blocksize}")
+
+
+@pytest.mark.parametrize("plan", ["2,1,8", "2,3,4", "4,2,8"])
+def test_grouped_backward_partial_steps(plan, device, monkeypatch, raw_statistics):
+    """Two weights of 264 and 200 rows in one launch: both groups end in a partial step, and the
+    split boundaries fall inside and between groups."""
+    from decik_amd.nf4 import linear_backward
+
+    monkeypatch.setenv("DECIK_BWD_PLAN", plan)
+    (p1, q1, w1), (p2, q2, w2) = (make_weight((n, 512), seed=60 + n, device=device, nested=True, blocksize=128)
+                                  for n in (264, 200))
+    d1 = randn16((130, 264), seed=13, device=device, std=1e-2)
+    d2 = randn16((130, 200), seed=14, device=device, std=1e-2)
+    dx = linear_backward([dict(packed=p1, qs=q1, dy=d1), dict(packed=p2, qs=q2, dy=d2)], 130, 512, dx_fp32=True)
+    ref = O.linear_dx_ref(d1.cpu().numpy(), w1) + O.linear_dx_ref(d2.cpu().numpy(), w2)
+    assert_close(dx, ref, max_rel=1e-4, mean_rel=1e-5, what=f"grouped bwd {plan}")
