@@ -6,8 +6,9 @@ double quant), X [830, 1536] ~ N(0, 1), dY ~ N(0, 1e-2), SwiGLU between the proj
 through the dequantized weights. Per step: 4 fused dequant-GEMM launches = 6 GEMMs of
 2*830*8960*1536 flops: gate+up forward with SwiGLU in its epilogue, down forward, down backward
 with the SwiGLU backward in its epilogue, gate+up backward. gate/up are kept from the forward (no
-recompute). Weights rotate over several
-layers' worth of seeded weights (seed = 7 * layer + projection).
+recompute). Weights rotate over enough layers' worth of seeded weights (seed = 7 * layer +
+projection) to total more than 512 MB of NF4 data, so the 256 MB Infinity Cache cannot serve
+repeats.
 
 Also measured: the standalone NF4 dequantization of all seven Qwen2.5-1.5B projections (q, k, v,
 o, gate, up, down) over 8 layers per iteration (942 MB of algorithmic traffic, more than the
@@ -15,7 +16,9 @@ o, gate, up, down) over 8 layers per iteration (942 MB of algorithmic traffic, m
 
 Prints one JSON line. `value` = whole-step dequant-GEMM throughput in TFLOP/s (inputs resident in
 HBM). `roofline` describes the kernel symbol with the largest share of the step time (launch
-durations from HIP events on the launch stream). `cpu_baseline` times the CPU restatement of the
+durations from HIP events on the launch stream). `measured_peaks` gives this device's ceilings as
+measured here (a large device copy; a dense loop of the same MFMA instruction), and the roofline
+objects also give their fractions of those. `cpu_baseline` times the CPU restatement of the
 reference algorithm (dequantize the whole weight, then an fp32 GEMM) on this host.
 """
 
@@ -89,11 +92,24 @@ def split_launch(kind):
     return fn(M, k, arr, len(ns)) > 0
 
 
-def bench_mlp(steps, warmup, device, n_sets=4, only=None):
+def nf4_bytes(n, k):
+    """Bytes of one NF4 weight in HBM: packed codes, absmax codes, absmax2, tables."""
+    w = n * k
+    return w // 2 + w // 64 + 4 * -(-w // 16384) + 1092
+
+
+def mlp_weight_sets(min_bytes=512 << 20):
+    """Weight sets (gate, up, down) the MLP bench rotates through: more than `min_bytes` in all."""
+    per_set = 2 * nf4_bytes(INTER, HIDDEN) + nf4_bytes(HIDDEN, INTER)
+    return max(4, -(-min_bytes // per_set) + 1)
+
+
+def bench_mlp(steps, warmup, device, n_sets=None, only=None):
     import torch
 
     from decik_amd import nf4
 
+    n_sets = n_sets or mlp_weight_sets()
     layers = make_layers(n_sets, ["gate", "up", "down"], device)
     x = seeded_fp16((M, HIDDEN), 1001, 1.0, device)
     dy = seeded_fp16((M, HIDDEN), 1002, 1e-2, device)
@@ -117,6 +133,11 @@ def bench_mlp(steps, warmup, device, n_sets=4, only=None):
                                   dict(packed=u[0], qs=u[1], dy=dup)], M, HIDDEN)
         return out, dx
 
+    # setup: one pass over every weight set fills the per-weight block-scale cache (computed once
+    # per frozen weight) before the warm-up steps
+    for i in range(n_sets):
+        step(i)
+    torch.cuda.synchronize()
     ms_step = None
     if only is None:
         for i in range(warmup):
@@ -168,7 +189,7 @@ def bench_mlp(steps, warmup, device, n_sets=4, only=None):
     launch_ms = per
     step_flops = sum(flops.values())
     return dict(ms_step=ms_step, launch_ms=launch_ms, flops=flops, symbol=symbol,
-                step_flops=step_flops)
+                step_flops=step_flops, n_sets=n_sets)
 
 
 def bench_dequant(iters, warmup, device, n_layers=8):
@@ -212,6 +233,47 @@ def bench_dequant(iters, warmup, device, n_layers=8):
     total_bytes = n_layers * sum(dequant_bytes(n, k) for _, n, k in QWEN15_SHAPES)
     launches = -(-len(descs) // 8)
     return dict(ms=ms, bytes=total_bytes, gbs=total_bytes / ms / 1e6, launches=launches)
+
+
+def measured_peaks(device):
+    """This device's ceilings as measured here: HBM bandwidth of a device-to-device copy of 512 MiB
+    (bytes read + written / time, median of 10), and the dense fp16 MFMA rate of a register-only
+    loop of v_mfma_f32_32x32x16_f16 (dk_probe_mfma_f16, 1024 work-groups of 8 waves)."""
+    import torch
+
+    from decik_amd import _lib
+
+    src = torch.empty(128 << 20, dtype=torch.float32, device=device).fill_(1.0)
+    dst = torch.empty_like(src)
+    times = []
+    for i in range(12):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        dst.copy_(src)
+        b.record()
+        torch.cuda.synchronize()
+        if i >= 2:
+            times.append(a.elapsed_time(b))
+    copy_gbs = 2 * src.numel() * 4 / statistics.median(times) / 1e6
+    del src, dst
+    wgs, iters = 1024, 4096
+    out = torch.empty(wgs * 512, dtype=torch.float32, device=device)
+    L = _lib.lib()
+    stream = _lib.stream_of(device)
+    _lib.check(L.dk_probe_mfma_f16(wgs, 64, out.data_ptr(), stream))
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(3):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        _lib.check(L.dk_probe_mfma_f16(wgs, iters, out.data_ptr(), stream))
+        b.record()
+        torch.cuda.synchronize()
+        times.append(a.elapsed_time(b))
+    flops = wgs * 8 * iters * 8 * 2 * 32 * 32 * 16
+    mfma_tf = flops / statistics.median(times) / 1e9
+    return dict(hbm_copy_gbs=round(copy_gbs, 1), mfma_f16_tflops=round(mfma_tf, 1),
+                method="512 MiB device copy; register-only v_mfma_f32_32x32x16_f16 loop")
 
 
 def cpu_baseline(sample_steps=3):
@@ -334,6 +396,8 @@ def main():
         print(json.dumps(dict(only=args.only, roofline=roofline)))
         return
     value = mlp["step_flops"] / (mlp["ms_step"] * 1e-3) / 1e12
+    peaks = measured_peaks(device)
+    roofline["frac_of_measured"] = round(achieved / peaks["mfma_f16_tflops"], 4)
     line = dict(
         metric=METRIC, value=round(value, 2), unit="TFLOP/s", n_gpus=1, steps=args.steps,
         warmup=args.warmup, ms_per_step=round(mlp["ms_step"], 4), higher_is_better=True,
@@ -341,8 +405,9 @@ def main():
         config=dict(workload="Qwen2.5-1.5B MLP block fwd+bwd on NF4 weights: gate/up [8960,1536], "
                              "down [1536,8960], blocksize 64, double quant; X [830,1536]; SwiGLU; "
                              "dX through W; gate/up kept from the forward",
-                    m=M, hidden=HIDDEN, intermediate=INTER, weight_sets=4),
+                    m=M, hidden=HIDDEN, intermediate=INTER, weight_sets=mlp["n_sets"]),
         roofline=roofline,
+        measured_peaks=peaks,
         kernels={k: dict(ms=round(v, 4),
                          tflops=round(mlp["flops"][k] / (v * 1e-3) / 1e12, 1) if mlp["flops"][k] else None)
                  for k, v in mlp["launch_ms"].items()},
@@ -353,7 +418,8 @@ def main():
                                workload="all 7 Qwen2.5-1.5B projections x 8 layers per iteration",
                                roofline=dict(bound="hbm", achieved=round(deq["gbs"], 1),
                                              peak=HBM_PEAK_GBS, unit="GB/s",
-                                             frac=round(deq["gbs"] / HBM_PEAK_GBS, 4)))
+                                             frac=round(deq["gbs"] / HBM_PEAK_GBS, 4),
+                                             frac_of_measured=round(deq["gbs"] / peaks["hbm_copy_gbs"], 4)))
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
     else:

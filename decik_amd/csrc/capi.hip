@@ -798,4 +798,12 @@ int dk_swiglu_bwd(const uint16_t* grad, const uint16_t* gate, const uint16_t* up
                      "dk_swiglu_bwd launch");
 }
 
+int dk_probe_mfma_f16(int64_t work_groups, int32_t iters, float* out, void* stream) {
+    g_error.clear();
+    if (work_groups <= 0 || work_groups > INT32_MAX / 512 || iters <= 0 || out == nullptr)
+        return fail("dk_probe_mfma_f16: bad arguments");
+    return check_hip(launch_mfma_peak(work_groups, iters, out, static_cast<hipStream_t>(stream)),
+                     "dk_probe_mfma_f16 launch");
+}
+
 }  // extern "C"

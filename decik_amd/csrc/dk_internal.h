@@ -171,6 +171,9 @@ struct RopeArgs {
     int32_t hq, hk, d;
 };
 hipError_t launch_rope(const RopeArgs& a, bool backward, hipStream_t s);
+
+// diagnostics
+hipError_t launch_mfma_peak(int64_t work_groups, int iters, float* out, hipStream_t s);
 hipError_t launch_swiglu_fwd(const _Float16* g, const _Float16* u, _Float16* o, int64_t n,
                              hipStream_t s);
 hipError_t launch_swiglu_bwd(const _Float16* gr, const _Float16* g, const _Float16* u,

@@ -209,6 +209,12 @@ int dk_swiglu_fwd(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64
 int dk_swiglu_bwd(const uint16_t* grad, const uint16_t* gate, const uint16_t* up,
                   uint16_t* dgate, uint16_t* dup, int64_t n, void* stream);
 
+/* Diagnostic, no counterpart in the reference: the device's dense fp16 MFMA rate, for reporting
+ * the GEMM kernels against a measured ceiling. Runs work_groups x 8 waves, each `iters` rounds of
+ * 8 v_mfma_f32_32x32x16_f16 on register operands (work_groups * 8 * iters * 8 * 32768 flops);
+ * out: work_groups * 512 floats (written, values meaningless). Allocates nothing. */
+int dk_probe_mfma_f16(int64_t work_groups, int32_t iters, float* out, void* stream);
+
 /* Description of the last error on the calling thread ("" if none). */
 const char* dk_last_error(void);
 
