@@ -231,7 +231,7 @@ def bench_dequant(iters, warmup, device, n_layers=8):
         times.append(a.elapsed_time(b))
     ms = statistics.median(times)
     total_bytes = n_layers * sum(dequant_bytes(n, k) for _, n, k in QWEN15_SHAPES)
-    launches = -(-len(descs) // 8)
+    launches = -(-len(descs) // 24)  # dk_nf4_dequant_batched: up to 24 weights per launch
     return dict(ms=ms, bytes=total_bytes, gbs=total_bytes / ms / 1e6, launches=launches)
 
 
