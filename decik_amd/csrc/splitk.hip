@@ -1,19 +1,24 @@
 // Split-K epilogue of the fused GEMMs: sums the per-split fp32 partial slabs in split order
 // (deterministic: the same additions in the same order on every run, whatever order the
 // work-groups of the GEMM ran in), adds the bias, rounds once and stores fp16 (or fp32).
-// One work-group per output row; each thread takes 8 consecutive columns at a time, so every
-// load and store instruction is contiguous across the wave.
+// One thread per 8 consecutive output columns of one row (rows are ncols / 8 threads apart in
+// the flat index), so every thread has work whatever the row length, and every load and store
+// instruction is contiguous across the wave.
 #include "dk_internal.h"
 
 namespace dk {
 
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(const ReduceArgs a) {
-    const int row = blockIdx.x;
+constexpr int kReduceThreads = 256;
+
+__global__ __launch_bounds__(kReduceThreads) void splitk_reduce_kernel(const ReduceArgs a) {
     const int chunks = a.ncols >> 3;
+    const int64_t item = (int64_t)blockIdx.x * kReduceThreads + threadIdx.x;
+    if (item >= (int64_t)a.m * chunks) return;
+    const int row = (int)(item / chunks);
     const float* base = a.partials + (int64_t)row * a.ncols;
-    constexpr int kBatch = 8;  // splits whose loads are in flight together
-    for (int c = threadIdx.x; c < chunks; c += 256) {
-        const int col = c << 3;
+    constexpr int kBatch = 16;  // splits whose loads are in flight together
+    {
+        const int col = (int)(item - (int64_t)row * chunks) << 3;
         float4_t v0 = {0.f, 0.f, 0.f, 0.f}, v1 = v0;
         for (int s0 = 0; s0 < a.splits; s0 += kBatch) {
             float4_t l0[kBatch], l1[kBatch];
@@ -62,7 +67,9 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const ReduceArgs a) 
 
 hipError_t launch_splitk_reduce(const ReduceArgs& a, hipStream_t s) {
     if (a.m <= 0 || a.ncols <= 0) return hipSuccess;
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(a.m), dim3(256), 0, s, a);
+    const int64_t items = (int64_t)a.m * (a.ncols >> 3);
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((items + kReduceThreads - 1) / kReduceThreads)),
+                       dim3(kReduceThreads), 0, s, a);
     return hipGetLastError();
 }
 
