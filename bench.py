@@ -116,8 +116,11 @@ def bench_mlp(steps, warmup, device, n_sets=None, only=None):
     launches = ["fwd_gate_up", "fwd_down", "bwd_down", "bwd_gate_up"]
     if only is not None:
         launches = [only]
-    symbol = {"fwd_gate_up": "nf4_fwd_kernel", "fwd_down": "nf4_fwd_kernel",
-              "bwd_down": "nf4_bwd_kernel", "bwd_gate_up": "nf4_bwd_kernel"}
+    # the GEMM kernel each launch runs, as the library's planner chooses it for these shapes
+    symbol = {"fwd_gate_up": nf4.launch_plan(False, M, HIDDEN, [INTER, INTER], glu=True)["kernel"],
+              "fwd_down": nf4.launch_plan(False, M, INTER, [HIDDEN])["kernel"],
+              "bwd_down": nf4.launch_plan(True, M, INTER, [HIDDEN], glu=True)["kernel"],
+              "bwd_gate_up": nf4.launch_plan(True, M, HIDDEN, [INTER, INTER])["kernel"]}
     flops = {"fwd_gate_up": 2 * gemm_flops(INTER, HIDDEN), "fwd_down": gemm_flops(HIDDEN, INTER),
              "bwd_down": gemm_flops(INTER, HIDDEN), "bwd_gate_up": 2 * gemm_flops(INTER, HIDDEN)}
 

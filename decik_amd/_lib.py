@@ -14,6 +14,9 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libdecik_nf4.so")
 MAX_GROUPS = 4
+# dk_nf4_linear_plan flags and kernel ids (include/decik_nf4.h)
+PLAN_GLU, PLAN_LORA, PLAN_NO_SPLIT = 1, 2, 4
+PLAN_KERNELS = ("nf4_fwd_kernel", "nf4_fwd8_kernel", "nf4_bwd_kernel", "nf4_bwd8_kernel")
 
 _lib = None
 _lock = threading.Lock()
@@ -42,6 +45,8 @@ EXPORTS = {
     "dk_nf4_dequant": ([ctypes.POINTER(NF4Weight), c_vp, c_vp], c_i32),
     "dk_nf4_dequant_batched": ([ctypes.POINTER(NF4Weight), ctypes.POINTER(c_vp), c_i32, c_vp], c_i32),
     "dk_probe_mfma_f16": ([ctypes.c_int64, ctypes.c_int32, c_vp, c_vp], c_i32),
+    "dk_nf4_linear_plan": ([c_i32, c_i64, c_i64, ctypes.POINTER(c_i64), c_i32, c_i32, c_i32,
+                            ctypes.POINTER(ctypes.c_int32)], c_i32),
     "dk_nf4_block_scales": ([ctypes.POINTER(NF4Weight), c_vp, c_vp], c_i32),
     "dk_nf4_linear_fwd_workspace": ([c_i64, c_i64, ctypes.POINTER(c_i64), c_i32], c_i64),
     "dk_nf4_linear_fwd": ([c_vp, c_i64, c_i64, c_i64, ctypes.POINTER(LinearFwdGroup), c_i32, c_i32,

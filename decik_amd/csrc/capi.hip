@@ -208,9 +208,17 @@ constexpr VariantCost kFwdVariants[] = {{1, 4, kFwdBN, 3, 2.35, 0.65},
                                        {8, 8, kFwdBN, 1, 2.25, 0.90},
                                        {9, 8, kFwdBN, 1, 2.45, 0.90}};
 constexpr int kNumFwdVariants = sizeof(kFwdVariants) / sizeof(kFwdVariants[0]);
+// rows_blocks 8 and 9: nf4_bwd8_kernel (eight waves of 32 output columns; no LoRA terms, no
+// SwiGLU epilogue), listed last
 constexpr VariantCost kBwdVariants[] = {{2, 4, 256, 2, 2.55, 0.90},
                                        {2, 8, 512, 1, 2.60, 1.0},
-                                       {4, 8, 512, 1, 3.40, 1.0}};
+                                       {4, 8, 512, 1, 3.40, 1.0},
+                                       {8, 8, 256, 1, 2.25, 0.90},
+                                       {9, 8, 256, 1, 2.85, 0.85}};
+constexpr int kNumBwdVariants = sizeof(kBwdVariants) / sizeof(kBwdVariants[0]);
+constexpr int kNumBwd4Variants = 3;
+static_assert(kBwdVariants[kNumBwd4Variants - 1].rows_blocks < 8 && kBwdVariants[kNumBwd4Variants].rows_blocks >= 8,
+              "nf4_bwd_kernel variants first");
 
 // The eight-wave variants come last: nf4_fwd8_kernel advances its load descriptors by whole
 // steps, so it needs k % 64 == 0 and blocks that do not straddle rows (k % blocksize == 0).
@@ -250,14 +258,16 @@ GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool glu
     return p;
 }
 
-GemmPlan plan_bwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool no_split = false) {
+// bwd8_ok: nf4_bwd8_kernel may run (no group with LoRA terms, no SwiGLU epilogue).
+GemmPlan plan_bwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool bwd8_ok, bool no_split = false) {
     GemmPlan p{};
     p.steps = 0;
     for (int g = 0; g < ngroups; ++g) p.steps += (int)((ns[g] + kBwdBC - 1) / kBwdBC);
-    const VariantCost* v = plan_override("DECIK_BWD_PLAN", kBwdVariants, 3, p.steps, &p.splits);
+    const int nv = bwd8_ok ? kNumBwdVariants : kNumBwd4Variants;
+    const VariantCost* v = plan_override("DECIK_BWD_PLAN", kBwdVariants, nv, p.steps, &p.splits);
     if (v != nullptr && no_split) p.splits = 1;
     if (v == nullptr)
-        v = choose_plan(kBwdVariants, 3, m, k, p.steps,
+        v = choose_plan(kBwdVariants, nv, m, k, p.steps,
                         [k](const VariantCost& c) { return (k + c.bn - 1) / c.bn; }, &p.splits,
                         no_split ? 1 : 32);
     p.mt = v->rows_blocks;
@@ -337,9 +347,35 @@ int64_t dk_nf4_linear_fwd_workspace(int64_t m, int64_t k, const int64_t* ns, int
                     workspace_bytes(plan_fwd(m, k, ns, ngroups, false, false)));
 }
 
+int dk_nf4_linear_plan(int backward, int64_t m, int64_t k, const int64_t* ns, int ngroups, int flags,
+                       int blocksize, int32_t* out) {
+    g_error.clear();
+    if (ngroups < 1 || ngroups > kMaxGroups || ns == nullptr || out == nullptr || m <= 0 || k <= 0 ||
+        blocksize < 32 || log2_exact(blocksize) < 0)
+        return fail("dk_nf4_linear_plan: bad arguments");
+    const bool glu = (flags & DK_PLAN_GLU) != 0, lora = (flags & DK_PLAN_LORA) != 0;
+    const bool single = (flags & DK_PLAN_NO_SPLIT) != 0;
+    GemmPlan p;
+    int kernel;
+    if (backward) {
+        p = plan_bwd(m, k, ns, ngroups, !glu && !lora, glu || single);
+        kernel = p.mt >= 8 ? 3 : 2;
+    } else {
+        p = plan_fwd(m, k, ns, ngroups, glu, k % 64 == 0 && k % blocksize == 0, single);
+        kernel = p.waves == 8 ? 1 : 0;
+    }
+    out[0] = p.mt;
+    out[1] = p.waves;
+    out[2] = p.splits;
+    out[3] = kernel;
+    return 0;
+}
+
 int64_t dk_nf4_linear_bwd_workspace(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
     if (ngroups < 1 || ngroups > kMaxGroups || ns == nullptr || m <= 0 || k <= 0) return 0;
-    return workspace_bytes(plan_bwd(m, k, ns, ngroups));
+    // the plan also depends on LoRA terms (eight-wave kernel or not): cover both
+    return std::max(workspace_bytes(plan_bwd(m, k, ns, ngroups, true)),
+                    workspace_bytes(plan_bwd(m, k, ns, ngroups, false)));
 }
 
 }  // extern "C"
@@ -547,7 +583,9 @@ static int linear_bwd_impl(const std::string& name, const dk_linear_bwd_group* g
         ns[g] = G.w.n;
     }
     if (m == 0) return 0;
-    const GemmPlan p = plan_bwd(m, k, ns, ngroups, sw != nullptr);
+    bool bwd8_ok = sw == nullptr;
+    for (int g = 0; g < ngroups; ++g) bwd8_ok = bwd8_ok && groups[g].lora_gu == nullptr;
+    const GemmPlan p = plan_bwd(m, k, ns, ngroups, bwd8_ok, sw != nullptr);
     const int64_t need = workspace_bytes(p);
     if (need > 0 && (workspace == nullptr || workspace_bytes_ < need || !aligned(workspace, 256)))
         return fail(name + ": workspace too small (need " + std::to_string(need) + " bytes)");
@@ -577,7 +615,9 @@ static int linear_bwd_impl(const std::string& name, const dk_linear_bwd_group* g
     const int64_t wgs = (int64_t)p.m_tiles * p.n_tiles * p.splits;
     if (wgs > INT32_MAX / 2) return fail(name + ": problem too large");
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    if (check_hip(launch_bwd(a, p.mt, p.waves, pad8((int)wgs), st), "dk_nf4_linear_bwd launch")) return 1;
+    const hipError_t le = p.mt >= 8 ? launch_bwd8(a, p.mt, pad8((int)wgs), st)
+                                    : launch_bwd(a, p.mt, p.waves, pad8((int)wgs), st);
+    if (check_hip(le, "dk_nf4_linear_bwd launch")) return 1;
     if (p.splits <= 1) return 0;
     ReduceArgs r{};
     r.partials = a.partials;

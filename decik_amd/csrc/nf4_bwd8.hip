@@ -1,0 +1,405 @@
+// Fused NF4 dequant x fp16 GEMM, input gradient, for launches with many token rows: the same
+// product as nf4_bwd_kernel (dX = sum_g dY_g . W_g, solution/nf4.py:99-104, summed over several
+// weights as the gate and up projections of solution/mlp.py:106-109), for launches without LoRA
+// terms or the SwiGLU epilogue.
+//
+// Why a second kernel: nf4_bwd_kernel's waves own 64 output columns (two A operands, both
+// nibbles of a byte per lane) and at most 4 token blocks, so each dequantized weight feeds at
+// most four MFMAs and the dequant costs far more issue slots than the matrix pipe leaves free.
+// Here a work-group is 8 waves (two per SIMD, one work-group per CU) on a tile of 32*MB tokens
+// (MB = 8 or 9) x 256 output columns; each wave owns 32 columns -- one A operand, one nibble per
+// lane and weight row -- and all 32*MB tokens, so each dequantized weight feeds MB MFMAs.
+//
+// A operand (A = W^T): lane l (l32 = l % 32, g = l / 32) serves A row l32 = output column
+// c = arow_to_n(l32) of the wave's 32 (packed byte c / 2; high nibble for even c). Its eight
+// contraction slots of slice j are the weight rows 32 g + 8 j + e of the 64-row step; dY's B
+// operand uses the same order. Lane l ends with the 16 consecutive columns 16 g + r of token row
+// l32 of every 32-token block.
+//
+// Per wave and step: the wave's 16 packed bytes of each of the 64 rows (four 256-byte DMA loads,
+// stored as 16-row groups of [dword column][16 rows], so a lane reads its 8 rows of one dword
+// column with two 16-byte loads) and one block statistic per row (32 aligned columns of a row
+// always lie in one block: k % 32 == 0 and blocks are powers of two >= 32). The dY tile (32*MB x
+// 64 fp16) is shared by the work-group through a ring three steps deep, as in nf4_bwd_kernel.
+// Row scales of step t + 1 are computed during slice 2 of step t, one row per lane, and read back
+// through a per-wave LDS table. The loop is software-pipelined one slice ahead, as in the forward
+// kernels: stage A (packed dwords and row scales of the next slice) after the slice's first MFMA,
+// stage B (byte gather, code-book addresses and reads) after the third, stage C (scaling and fp16
+// packing) after the last but one, and each dY fragment refilled right after its MFMA read it.
+//
+// Epilogue: each token block's 32 x 256 fp32 tile goes through LDS (the dY ring, after a
+// barrier) and leaves as whole rows: split-K partial slabs (reduced by splitk_reduce_kernel) or
+// dX in fp32 or fp16.
+#include "gemm_common.h"
+
+namespace dk {
+
+constexpr int kB8Waves = 8;
+constexpr int kB8Threads = 64 * kB8Waves;
+constexpr int kB8BN = 32 * kB8Waves;          // output columns per tile
+constexpr int kB8Tables = kMaxGroups * 1024;  // code2 tables (nested statistics), 1 KB per group
+constexpr int kB8Dummy = 1024;                // target of the dY loads of waves past the tile
+// Per-wave ring slot of one step: 1 KB packed bytes (4 x [4 dword columns][16 rows]), then one
+// statistics dword slot per row (codes or fp32 absmax at +1024, absmax2 at +1280).
+constexpr int kB8WSlot = 1536;
+constexpr int kB8ScaleBytes = 2 * 64 * 4;  // per wave: row-scale tables of two steps
+
+__host__ __device__ constexpr size_t bwd8_smem_bytes(int mb) {
+    return kB8Tables + kB8Dummy + 3 * (size_t)(32 * mb * 128) +
+           kB8Waves * (3 * (size_t)kB8WSlot + kB8ScaleBytes);
+}
+
+template <int MB, bool NESTED>
+__global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a) {
+    constexpr int BM = 32 * MB;
+    constexpr int DBUF = BM * 128;                             // bytes of one dY ring buffer
+    constexpr int DCH = BM * 8;                                // its 16-byte chunks
+    constexpr int DPT = (DCH + kB8Threads - 1) / kB8Threads;   // dY loads per thread and step
+    constexpr int NL = DPT + 4 + (NESTED ? 2 : 1);             // loads per thread and step
+    static_assert(DCH % 64 == 0, "a wave's dY load is wholly inside or past the tile");
+    static_assert(2 * 32 * (kB8BN * 4 + 16) <= 3 * DBUF, "epilogue staging fits the dY ring");
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ float luts[16 * kMaxGroups];  // code books, group g at byte 64 g
+    uint8_t* dummy = smem + kB8Tables;
+    uint8_t* dring = dummy + kB8Dummy;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS bases stay scalar
+    const int l32 = lane & 31, g = lane >> 5;
+    const int c = arow_to_n(l32);      // this lane's output column within the wave's 32
+    const int xsw = (l32 >> 1) & 7;    // LDS swizzle of this lane's dY rows
+
+    const int L = xcd_logical_id();
+    if (L >= a.m_tiles * a.k_tiles * a.splits) return;
+    const int m_tile = L % a.m_tiles;
+    const int rest = L / a.m_tiles;
+    const int k_tile = rest % a.k_tiles;
+    const int split = rest / a.k_tiles;
+    const int M = sgpr(a.m), K = sgpr(a.k);
+    const int m0 = m_tile * BM;
+    const int tile_k0 = k_tile * kB8BN;
+    const int kw0 = tile_k0 + 32 * wave;  // the wave's first output column
+    const bool cok = kw0 < K;             // k % 32 == 0: the wave's columns are all in or all out
+    const int cs0 = split * a.csteps_per_split;
+    const int cs1 = min(a.csteps, cs0 + a.csteps_per_split);
+
+    for (int gg = 0; gg < a.ngroups; ++gg) {
+        if (tid < 16) luts[16 * gg + tid] = a.g[gg].w.code[tid];
+        if (NESTED && tid < 256) ((float*)smem)[256 * gg + tid] = a.g[gg].w.code2[tid];
+    }
+    // v_perm selector that gathers byte (c / 2) % 4 of two dwords into the low two bytes
+    const uint32_t bb = (uint32_t)((c >> 1) & 3);
+    const uint32_t bsel = bb | ((bb + 4u) << 8) | 0x0C0C0000u;
+    // rotation (right) that moves this lane's nibble of every byte to bits 2..5, i.e. to the
+    // code-book byte address 4 * nibble: 2 for the high nibble, 30 (left by 2) for the low one
+    const uint32_t nrot = (c & 1) ? 30u : 2u;
+    uint8_t* wring = dring + 3 * DBUF + wave * (3 * kB8WSlot);
+    float* stab = (float*)(dring + 3 * DBUF + kB8Waves * 3 * kB8WSlot + wave * kB8ScaleBytes);
+    // this lane's packed reads: 16-row group 2 g + j / 2, dword column c / 8, rows 8 (j % 2) ..
+    const int pkl = 512 * g + 64 * (c >> 3);
+
+    float16_t acc[MB];  // token block i
+#pragma unroll
+    for (int i = 0; i < MB; ++i) acc[i] = float16_t{};
+
+    // stage positions (MFMA index after which a stage runs)
+    constexpr int qB = 2, qC = MB - 2;
+    constexpr int qS1 = 1, qS2 = 3, qS3 = 5;  // row scales of the next step (slice 2)
+    static_assert(qS3 < MB, "scale stages inside the slice");
+
+    // One weight group at a time, as in nf4_bwd_kernel: the group's operands are pinned in
+    // scalar registers for its steps and the pipeline drains between groups.
+    for (int gi = 0; gi < a.ngroups; ++gi) {
+        const BwdGroupDev& G = a.g[gi];
+        const int sb = sgpr(G.step_begin);
+        const int t0 = max(cs0, sb), t1 = min(cs1, sb + sgpr(G.nsteps));
+        if (t0 >= t1) continue;
+        const int N = sgpr((int)G.w.n);
+        const int lddy = sgpr(G.lddy);
+        const _Float16* const gdy = sgpr(G.dy);
+        const uint32_t dy_bytes = sgpr(G.dy_bytes);
+        const uint8_t* const gpk = sgpr(G.w.packed);
+        const uint32_t pk_bytes = sgpr(G.w.packed_bytes);
+        const uint8_t* const gam8 = NESTED ? sgpr(G.w.absmax8) : nullptr;
+        const float* const gamf = NESTED ? nullptr : sgpr(G.w.absmaxf);
+        const uint32_t am_bytes = sgpr(G.w.absmax_bytes);
+        const float* const gam2 = NESTED ? sgpr(G.w.absmax2) : nullptr;
+        const uint32_t am2_bytes = NESTED ? sgpr(G.w.absmax2_bytes) : 0u;
+        const uint32_t bs_shift = sgpr((uint32_t)G.w.bs_shift), bs2_shift = sgpr((uint32_t)G.w.bs2_shift);
+        const float offset = NESTED ? *G.w.offset : 0.0f;
+        const float* c2 = (const float*)smem + 256 * gi;
+        const uint32_t gbase4 = (uint32_t)(64 * gi) * 0x01010101u;  // this group's code book
+
+        // Loads use per-lane offsets fixed for the group (bit 31 set where the lane's data lies
+        // outside the tile or the weight: it reads zeros) against buffer descriptors whose base
+        // advances by whole steps. Only a group's last step, when its row count is not a
+        // multiple of 64, also checks rows and dY columns per lane. A step past the segment's
+        // end loads from descriptors of size 0 (zeros), keeping the load count uniform.
+        // dY chunk h of this thread: token row (tid + 512 h) / 8 of the tile, 16-byte column
+        // dy_col(h) of the step (the LDS swizzle applied to the thread's position in the row)
+        auto dy_col = [&](int h) __attribute__((always_inline)) -> int {
+            const int q = tid + kB8Threads * h;
+            return (q & 7) ^ ((q >> 4) & 7);
+        };
+        uint32_t dyo[DPT];
+#pragma unroll
+        for (int h = 0; h < DPT; ++h) {
+            const int q = tid + kB8Threads * h;
+            const int gm = m0 + (q >> 3);
+            dyo[h] = off_if(q < DCH && gm < M, (uint32_t)(gm * lddy + 8 * dy_col(h)) * 2u);
+        }
+        // the LDS destination of a wave's dY load h within ring buffer rd (waves past the tile:
+        // the dummy area)
+        auto dy_dst = [&](int rd, int h) __attribute__((always_inline)) -> uint8_t* {
+            const int wq0 = kB8Threads * h + 64 * wave;  // the wave's first chunk (uniform)
+            return wq0 < DCH ? dring + rd + wq0 * 16 : dummy;
+        };
+        // packed bytes: DMA instruction d fetches rows 16 d .. 16 d + 15, the wave's 4 dwords of
+        // each; lane l -> (dword column l / 16, row l % 16) lands at byte 256 d + 4 l
+        const int prr = lane & 15;
+        const uint32_t po = off_if(cok, (uint32_t)prr * (uint32_t)(K >> 1) + (uint32_t)(kw0 >> 1) + 4u * (uint32_t)(lane >> 4));
+        const uint32_t prow16 = 16u * (uint32_t)(K >> 1);  // bytes of 16 weight rows
+        // statistics: lane = weight row of the step
+        const uint32_t blk0 = ((uint32_t)lane * (uint32_t)K + (uint32_t)kw0) >> bs_shift;
+        const uint32_t so = off_if(cok, NESTED ? blk0 : blk0 * 4u);
+
+        auto load_step = [&](int t, int rd, int rw, bool live) __attribute__((always_inline)) {
+            const int n0 = (t - sb) * kBwdBC;
+            const bool tail = n0 + kBwdBC > N;  // uniform
+            const rsrc_t drs = make_rsrc(gdy + n0, live ? dy_bytes - 2u * (uint32_t)n0 : 0u);
+            uint8_t* slot = wring + rw;
+            const uint32_t pskip = (uint32_t)n0 * (uint32_t)(K >> 1);
+            const rsrc_t wrs = make_rsrc(gpk + pskip, live ? pk_bytes - pskip : 0u);
+            if (!tail) {
+#pragma unroll
+                for (int h = 0; h < DPT; ++h) bload128_lds(drs, dy_dst(rd, h), dyo[h]);
+#pragma unroll
+                for (int d = 0; d < 4; ++d) bload32_lds(wrs, slot + 256 * d, po + (uint32_t)d * prow16);
+            } else {
+                // rows and dY columns past N read zeros
+#pragma unroll
+                for (int h = 0; h < DPT; ++h)
+                    bload128_lds(drs, dy_dst(rd, h), off_if(n0 + 8 * dy_col(h) < N, dyo[h]));
+#pragma unroll
+                for (int d = 0; d < 4; ++d)
+                    bload32_lds(wrs, slot + 256 * d, off_if(n0 + 16 * d + prr < N, po + (uint32_t)d * prow16));
+            }
+            const uint32_t kb = ((uint32_t)n0 * (uint32_t)K) >> bs_shift;  // blocks before this step
+            const bool rok = !tail || n0 + lane < N;
+            if constexpr (NESTED) {
+                const rsrc_t ars = make_rsrc(gam8 + kb, live ? am_bytes - kb : 0u);
+                const rsrc_t a2rs = make_rsrc(gam2, live ? am2_bytes : 0u);
+                bload8_lds(ars, slot + 1024, off_if(rok, so));
+                bload32_lds(a2rs, slot + 1280, off_if(rok && cok, ((blk0 + kb) >> bs2_shift) * 4u));
+            } else {
+                const rsrc_t ars = make_rsrc(gamf + kb, live ? am_bytes - 4u * kb : 0u);
+                bload32_lds(ars, slot + 1024, off_if(rok, so));
+            }
+        };
+
+        // Row scale of step t (lane = row) from this wave's statistics in slot rw, into table
+        // sidx, in three parts spread over slice 2's MFMAs (the loads were this wave's own, so its
+        // own wait suffices: no barrier).
+        uint32_t sq = 0;
+        float sa = 0.0f;
+        auto scales_1 = [&](int rw) __attribute__((always_inline)) {
+            const uint8_t* slot = wring + rw;
+            if constexpr (NESTED) {
+                sq = slot[1024 + 4 * lane];
+                sa = *(const float*)(slot + 1280 + 4 * lane);
+            } else {
+                sa = *(const float*)(slot + 1024 + 4 * lane);
+            }
+        };
+        auto scales_2 = [&]() __attribute__((always_inline)) {
+            if constexpr (NESTED) sa = c2[sq] * sa;
+        };
+        auto scales_3 = [&](int t, int sidx) __attribute__((always_inline)) {
+            const int row = (t - sb) * kBwdBC + lane;
+            const float sc = NESTED ? sa + offset : sa;
+            stab[64 * sidx + lane] = (row < N && cok) ? sc : 0.0f;
+        };
+
+        // Ring buffers: step t uses dY buffer rd0 (byte offset in the dY ring), weight slot rw0
+        // and scale table si0; step t + 1 uses rd1 / rw1 / 1 - si0; step t + 3 reuses step t's.
+        int rd0 = 0, rw0 = 0, rd1 = DBUF, rw1 = kB8WSlot, si0 = 0;
+        // Prologue: three steps in flight; wait for the first.
+        load_step(t0, 0, 0, true);
+        load_step(t0 + 1, DBUF, kB8WSlot, t0 + 1 < t1);
+        load_step(t0 + 2, 2 * DBUF, 2 * kB8WSlot, t0 + 2 < t1);
+        wait_vmcnt<2 * NL>();
+        lds_barrier();  // dY(t0) from every wave, code tables
+        scales_1(0);
+        scales_2();
+        scales_3(t0, 0);
+
+        half8_t xf[MB], w, wn;
+        u32x4_t d0, d1;  // next slice: packed dwords of rows r0 .. r0 + 3 and r0 + 4 .. r0 + 7
+        float4_t s0, s1; // ... their row scales
+        float v[8];      // ... their code-book values
+        auto stage_A = [&](int rw, int sidx, int j) __attribute__((always_inline)) {
+            const uint8_t* pk = wring + rw + pkl + 256 * (j >> 1) + 32 * (j & 1);
+            d0 = *(const u32x4_t*)pk;
+            d1 = *(const u32x4_t*)(pk + 16);
+            const float* sc = stab + 64 * sidx + 32 * g + 8 * j;
+            s0 = *(const float4_t*)sc;
+            s1 = *(const float4_t*)(sc + 4);
+        };
+        auto stage_B = [&]() __attribute__((always_inline)) {
+            // this lane's byte of rows r0 .. r0 + 3 and r0 + 4 .. r0 + 7, gathered into two dwords
+            const uint32_t rb0 = __builtin_amdgcn_perm(d0[1], d0[0], bsel) | (__builtin_amdgcn_perm(d0[3], d0[2], bsel) << 16);
+            const uint32_t rb1 = __builtin_amdgcn_perm(d1[1], d1[0], bsel) | (__builtin_amdgcn_perm(d1[3], d1[2], bsel) << 16);
+            uint32_t a0 = (__builtin_amdgcn_alignbit(rb0, rb0, nrot) & 0x3C3C3C3Cu) | gbase4;
+            uint32_t a1 = (__builtin_amdgcn_alignbit(rb1, rb1, nrot) & 0x3C3C3C3Cu) | gbase4;
+            asm("" : "+v"(a0), "+v"(a1));  // one v_bfe per lookup (see nib_addrs)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[e] = lut_at(luts, a0, e);
+                v[e + 4] = lut_at(luts, a1, e);
+            }
+        };
+        auto stage_C = [&]() __attribute__((always_inline)) -> half8_t {
+            u32x4_t o;
+            o[0] = pack_half2(v[0] * s0[0], v[1] * s0[1]);
+            o[1] = pack_half2(v[2] * s0[2], v[3] * s0[3]);
+            o[2] = pack_half2(v[4] * s1[0], v[5] * s1[1]);
+            o[3] = pack_half2(v[6] * s1[2], v[7] * s1[3]);
+            return __builtin_bit_cast(half8_t, o);
+        };
+        auto xfrag = [&](int rd, int i, int j) __attribute__((always_inline)) -> half8_t {
+            return *(const half8_t*)(dring + rd + (32 * i + l32) * 128 + (((4 * g + j) ^ xsw) << 4));
+        };
+
+        // slice 0 of the first step
+        stage_A(rw0, si0, 0);
+#pragma unroll
+        for (int i = 0; i < MB; ++i) xf[i] = xfrag(rd0, i, 0);
+        stage_B();
+        w = stage_C();
+
+        for (int t = t0; t < t1; ++t) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int jn = (j + 1) & 3;
+#pragma unroll
+                for (int q = 0; q < MB; ++q) {
+                    acc[q] = mfma32x32x16(w, xf[q], acc[q]);
+                    if (j == 3 && q == 0) {
+                        // every wave's loads of step t+1 have landed (each waited in slice 2)
+                        // and every wave is past step t's slots: refill them with step t+3
+                        // (zeros past the segment's end). Past the last step the reads below
+                        // see stale slots and their values go unused.
+                        lds_barrier();
+                        load_step(t + 3, rd0, rw0, t + 3 < t1);
+                    }
+                    // refill the dY fragment the MFMA above has read (slice j + 1)
+                    xf[q] = xfrag(j < 3 ? rd0 : rd1, q, jn);
+                    if (q == 0) {
+                        if (j == 2) wait_vmcnt<NL>();  // step t+1's loads (this wave's) landed
+                        if (j < 3) stage_A(rw0, si0, j + 1);
+                        else stage_A(rw1, 1 - si0, 0);
+                    }
+                    if (j == 2) {
+                        if (q == qS1) scales_1(rw1);
+                        if (q == qS2) scales_2();
+                        if (q == qS3) scales_3(t + 1, 1 - si0);
+                    }
+                    if (q == qB) stage_B();
+                    if (q == qC) wn = stage_C();
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                w = wn;
+            }
+            // rotate the rings: step t + 1's buffers become the current ones
+            rd0 = rd1;
+            rw0 = rw1;
+            rd1 = rd1 == 2 * DBUF ? 0 : rd1 + DBUF;
+            rw1 = rw1 == 2 * kB8WSlot ? 0 : rw1 + kB8WSlot;
+            si0 = 1 - si0;
+        }
+        // every load has landed and every wave is done with the rings before the next group's
+        // prologue refills them
+        wait_vmcnt<0>();
+        lds_barrier();
+    }
+    lds_barrier();  // the dY ring becomes the staging area (also when no group had steps here)
+
+    // ---- epilogue. Lane (l32, g) holds, for token block i, token row m0 + 32 i + l32 and the 16
+    // consecutive columns colw + r of the tile (acc[i][r]).
+    const int colw = 32 * wave + 16 * g;
+    const bool out32 = a.splits > 1 || a.dx_fp32;
+    if (out32) {
+        // 32 x 256 fp32 tiles (rows 1040 bytes apart) -> whole 1 KB rows of the split's partial
+        // slab or of dX
+        float* dst = a.splits > 1 ? a.partials + (int64_t)split * M * K : (float*)a.dx;
+        const int64_t ld = a.splits > 1 ? (int64_t)K : a.lddx;
+        constexpr int RB = kB8BN * 4 + 16;
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+            uint8_t* buf = dring + (i & 1) * 32 * RB;
+            uint8_t* lp = buf + l32 * RB + colw * 4;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) *(float4_t*)(lp + 16 * q) = chunk4(acc[i], q);
+            lds_barrier();
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                const int ch = tid + kB8Threads * h, row = ch >> 6, cc = ch & 63;
+                const float4_t val = *(const float4_t*)(buf + row * RB + cc * 16);
+                const int m = m0 + 32 * i + row, col = tile_k0 + 4 * cc;
+                if (m < M && col < K) *(float4_t*)(dst + (int64_t)m * ld + col) = val;
+            }
+        }
+        return;
+    }
+    {
+        // 32 x 256 fp16 tiles (rows 528 bytes apart) -> whole 512-byte rows of dX
+        _Float16* dst = (_Float16*)a.dx;
+        constexpr int RB = kB8BN * 2 + 16;
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+            uint8_t* buf = dring + (i & 1) * 32 * RB;
+            uint8_t* lp = buf + l32 * RB + colw * 2;
+            uint32_t o[8];
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) o[r >> 1] = pack_half2(acc[i][r], acc[i][r + 1]);
+            *(u32x4_t*)lp = u32x4_t{o[0], o[1], o[2], o[3]};
+            *(u32x4_t*)(lp + 16) = u32x4_t{o[4], o[5], o[6], o[7]};
+            lds_barrier();
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int ch = tid + kB8Threads * h, row = ch >> 5, cc = ch & 31;
+                const u32x4_t val = *(const u32x4_t*)(buf + row * RB + cc * 16);
+                const int m = m0 + 32 * i + row, col = tile_k0 + 8 * cc;
+                if (m < M && col < K) *(u32x4_t*)(dst + (int64_t)m * a.lddx + col) = val;
+            }
+        }
+    }
+}
+
+template <int MB, bool NESTED>
+static hipError_t launch_bwd8_t(const BwdArgs& a, int grid, hipStream_t s) {
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute((const void*)nf4_bwd8_kernel<MB, NESTED>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)bwd8_smem_bytes(MB));
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    hipLaunchKernelGGL((nf4_bwd8_kernel<MB, NESTED>), dim3(grid), dim3(kB8Threads),
+                       bwd8_smem_bytes(MB), s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_bwd8(const BwdArgs& a, int mb, int grid, hipStream_t s) {
+    if (a.swiglu) return hipErrorInvalidValue;  // not in this kernel
+    for (int g = 0; g < a.ngroups; ++g)
+        if (a.g[g].lora_gu != nullptr) return hipErrorInvalidValue;
+#define X(T) \
+    if (mb == T) return a.nested ? launch_bwd8_t<T, true>(a, grid, s) : launch_bwd8_t<T, false>(a, grid, s);
+    X(8) X(9)
+#undef X
+    return hipErrorInvalidValue;
+}
+
+}  // namespace dk

@@ -209,6 +209,21 @@ int dk_swiglu_fwd(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64
 int dk_swiglu_bwd(const uint16_t* grad, const uint16_t* gate, const uint16_t* up,
                   uint16_t* dgate, uint16_t* dup, int64_t n, void* stream);
 
+/* Diagnostic, no counterpart in the reference: the launch plan that dk_nf4_linear_fwd
+ * (backward = 0) or dk_nf4_linear_bwd (backward = 1) chooses for these shapes, for reports and
+ * tuning. flags: DK_PLAN_GLU (forward: the fused GLU mode of dk_nf4_glu_fwd; backward: the SwiGLU
+ * epilogue of dk_nf4_linear_bwd_swiglu), DK_PLAN_LORA (some group has LoRA terms),
+ * DK_PLAN_NO_SPLIT (a single pass). blocksize: the largest block size of the groups' weights.
+ * out[0] = 32-token row blocks per tile, out[1] = waves per work-group, out[2] = contraction
+ * splits, out[3] = kernel (0 nf4_fwd_kernel, 1 nf4_fwd8_kernel, 2 nf4_bwd_kernel,
+ * 3 nf4_bwd8_kernel). Host-only (no GPU call); honours DECIK_FWD_PLAN / DECIK_BWD_PLAN like the
+ * launches. Returns 0, or nonzero with dk_last_error() on bad arguments. */
+#define DK_PLAN_GLU 1
+#define DK_PLAN_LORA 2
+#define DK_PLAN_NO_SPLIT 4
+int dk_nf4_linear_plan(int backward, int64_t m, int64_t k, const int64_t* ns, int ngroups, int flags,
+                       int blocksize, int32_t* out);
+
 /* Diagnostic, no counterpart in the reference: the device's dense fp16 MFMA rate, for reporting
  * the GEMM kernels against a measured ceiling. Runs work_groups x 8 waves, each `iters` rounds of
  * 8 v_mfma_f32_32x32x16_f16 on register operands (work_groups * 8 * iters * 8 * 32768 flops);

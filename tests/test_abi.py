@@ -84,3 +84,39 @@ def test_workspace_sizes():
     # split-K plans need counters + partial tiles; plans without a split need nothing
     assert L.dk_nf4_linear_bwd_workspace(830, 8960, ns, 1) >= 0
     assert L.dk_nf4_linear_fwd_workspace(0, 1536, ns, 1) == 0
+
+
+def test_launch_plans():
+    """dk_nf4_linear_plan (host-only): the eight-wave input-gradient kernel serves the MLP's
+    gate/up input gradient at M = 830 and never a launch with LoRA terms or the SwiGLU epilogue
+    (it has neither); the fused GLU forward never splits; forced plans apply only where their
+    kernel may run; bad arguments are reported."""
+    from decik_amd import _lib
+    from decik_amd.nf4 import launch_plan
+
+    gu = launch_plan(True, 830, 1536, [8960, 8960])
+    assert gu["kernel"] == "nf4_bwd8_kernel" and gu["splits"] > 1
+    assert launch_plan(True, 830, 1536, [8960, 8960], lora=True)["kernel"] == "nf4_bwd_kernel"
+    sw = launch_plan(True, 830, 8960, [1536], glu=True)
+    assert sw["kernel"] == "nf4_bwd_kernel" and sw["splits"] == 1
+    glu = launch_plan(False, 830, 1536, [8960, 8960], glu=True)
+    assert glu["splits"] == 1 and glu["kernel"] == "nf4_fwd8_kernel"
+    # k % blocksize != 0: the eight-wave forward kernel may not run
+    assert launch_plan(False, 830, 1536, [8960], blocksize=1024)["kernel"] == "nf4_fwd_kernel"
+    assert launch_plan(True, 830, 1536, [8960, 8960], no_split=True)["splits"] == 1
+    old = os.environ.get("DECIK_BWD_PLAN")
+    try:
+        os.environ["DECIK_BWD_PLAN"] = "9,3,8"
+        assert launch_plan(True, 830, 1536, [8960]) == dict(rows_blocks=9, waves=8, splits=3,
+                                                             kernel="nf4_bwd8_kernel")
+        assert launch_plan(True, 830, 1536, [8960], lora=True)["kernel"] == "nf4_bwd_kernel"
+    finally:
+        if old is None:
+            os.environ.pop("DECIK_BWD_PLAN", None)
+        else:
+            os.environ["DECIK_BWD_PLAN"] = old
+    L = _lib.lib()
+    out = (ctypes.c_int32 * 4)()
+    ns = (ctypes.c_int64 * 1)(64)
+    assert L.dk_nf4_linear_plan(1, 8, 64, ns, 1, 0, 48, out) != 0
+    assert b"bad arguments" in L.dk_last_error()

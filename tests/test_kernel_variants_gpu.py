@@ -36,7 +36,7 @@ def test_forward_variants(nested, blocksize, plan, device, monkeypatch, raw_stat
                  what=f"fwd {plan} nested={nested} bs={blocksize}")
 
 
-@pytest.mark.parametrize("plan", ["2,1,4", "2,2,8", "4,1,8", "4,3,8"])
+@pytest.mark.parametrize("plan", ["2,1,4", "2,2,8", "4,1,8", "4,3,8", "8,1,8", "9,2,8"])
 @pytest.mark.parametrize("nested,blocksize", CASES)
 def test_backward_variants_partial_last_step(nested, blocksize, plan, device, monkeypatch, raw_statistics):
     """264 weight rows: the last 64-row step has 8 rows; dY columns and weight rows past them read
@@ -51,7 +51,7 @@ def test_backward_variants_partial_last_step(nested, blocksize, plan, device, mo
     assert_close(dx, O.linear_dx_ref(dy.cpu().numpy(), w16), what=f"bwd {plan} nested={nested} bs={blocksize}")
 
 
-@pytest.mark.parametrize("plan", ["2,1,8", "2,3,4", "4,2,8"])
+@pytest.mark.parametrize("plan", ["2,1,8", "2,3,4", "4,2,8", "8,2,8", "9,1,8", "9,3,8"])
 def test_grouped_backward_partial_steps(plan, device, monkeypatch, raw_statistics):
     """Two weights of 264 and 200 rows in one launch: both groups end in a partial step, and the
     split boundaries fall inside and between groups."""
@@ -65,3 +65,42 @@ def test_grouped_backward_partial_steps(plan, device, monkeypatch, raw_statistic
     dx = linear_backward([dict(packed=p1, qs=q1, dy=d1), dict(packed=p2, qs=q2, dy=d2)], 130, 512, dx_fp32=True)
     ref = O.linear_dx_ref(d1.cpu().numpy(), w1) + O.linear_dx_ref(d2.cpu().numpy(), w2)
     assert_close(dx, ref, max_rel=1e-4, mean_rel=1e-5, what=f"grouped bwd {plan}")
+
+
+@pytest.mark.parametrize("plan", ["8,2,8", "9,1,8"])
+@pytest.mark.parametrize("nested,blocksize", CASES)
+@pytest.mark.parametrize("dx_fp32", [False, True])
+def test_eight_wave_backward_edges(nested, blocksize, plan, dx_fp32, device, monkeypatch, raw_statistics):
+    """The eight-wave input-gradient kernel (256-column tiles of 32 columns per wave) at
+    k = 1056: the last column tile holds one wave's 32 columns and seven waves past k; 200 weight
+    rows (a partial last step); 300 tokens (a partial last token tile)."""
+    from decik_amd.nf4 import linear_backward
+
+    monkeypatch.setenv("DECIK_BWD_PLAN", plan)
+    packed, qs, w16 = make_weight((200, 1056), seed=blocksize + 21, device=device, nested=nested,
+                                  blocksize=blocksize)
+    dy = randn16((300, 200), seed=22, device=device, std=1e-2)
+    dx = linear_backward([dict(packed=packed, qs=qs, dy=dy)], 300, 1056, dx_fp32=dx_fp32)
+    ref = O.linear_dx_ref(dy.cpu().numpy(), w16)
+    if dx_fp32:
+        assert_close(dx, ref, max_rel=1e-4, mean_rel=1e-5, what=f"bwd8 {plan} fp32 nested={nested} bs={blocksize}")
+    else:
+        assert_close(dx, ref, what=f"bwd8 {plan} nested={nested} bs={blocksize}")
+
+
+def test_eight_wave_plan_ignored_with_lora(device, monkeypatch):
+    """A forced eight-wave plan does not apply to launches with LoRA terms (that kernel has none):
+    the planner falls back to nf4_bwd_kernel and the result includes the LoRA gradient."""
+    import torch
+    from decik_amd.nf4 import linear_backward
+
+    monkeypatch.setenv("DECIK_BWD_PLAN", "9,1,8")
+    packed, qs, w16 = make_weight((256, 512), seed=31, device=device, nested=True, blocksize=64)
+    dy = randn16((200, 256), seed=32, device=device, std=1e-2)
+    gu = randn16((200, 16), seed=33, device=device, std=1e-2)
+    la = randn16((16, 512), seed=34, device=device, std=1e-1)
+    dx = linear_backward([dict(packed=packed, qs=qs, dy=dy, lora_gu=gu, lora_a=la)], 200, 512, dx_fp32=True,
+                         lora_rank=16)
+    ref = O.linear_dx_ref(dy.cpu().numpy(), w16) + gu.cpu().float().numpy() @ la.cpu().float().numpy()
+    assert_close(dx, ref, max_rel=1e-4, mean_rel=1e-5, what="bwd lora with forced bwd8 plan")
+    assert torch.isfinite(dx).all()
