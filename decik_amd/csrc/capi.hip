@@ -175,17 +175,18 @@ void no_split(GemmPlan& p) {
     p.partial_floats = 0;
 }
 
-// Tuning hook: DECIK_FWD_PLAN / DECIK_BWD_PLAN = "rows_blocks,splits[,waves]" forces a plan
-// (a compiled variant and 1 <= splits <= steps; waves defaults to the variant list's first match).
+// Tuning hook: DECIK_FWD_PLAN / DECIK_BWD_PLAN = "rows_blocks,splits[,waves[,columns]]" forces a
+// plan (a compiled variant and 1 <= splits <= steps; waves and columns per tile default to the
+// variant list's first match).
 // Unset in normal use; read on every call so a sweep can change it between calls.
 const VariantCost* plan_override(const char* var, const VariantCost* vs, int nv, int steps, int* splits) {
     const char* v = std::getenv(var);
     if (v == nullptr || *v == 0) return nullptr;
-    int a = 0, b = 0, w = 0;
-    const int got = std::sscanf(v, "%d,%d,%d", &a, &b, &w);
+    int a = 0, b = 0, w = 0, c = 0;
+    const int got = std::sscanf(v, "%d,%d,%d,%d", &a, &b, &w, &c);
     if (got < 2 || b < 1 || b > (steps > 0 ? steps : 1)) return nullptr;
     for (int i = 0; i < nv; ++i)
-        if (vs[i].rows_blocks == a && (got < 3 || vs[i].waves == w)) {
+        if (vs[i].rows_blocks == a && (got < 3 || vs[i].waves == w) && (got < 4 || vs[i].bn == c)) {
             *splits = b;
             return &vs[i];
         }
@@ -208,17 +209,21 @@ constexpr VariantCost kFwdVariants[] = {{1, 4, kFwdBN, 3, 2.35, 0.65},
                                        {8, 8, kFwdBN, 1, 2.25, 0.90},
                                        {9, 8, kFwdBN, 1, 2.45, 0.90}};
 constexpr int kNumFwdVariants = sizeof(kFwdVariants) / sizeof(kFwdVariants[0]);
-// rows_blocks 8 and 9: nf4_bwd8_kernel (eight waves of 32 output columns; no LoRA terms, no
-// SwiGLU epilogue), listed last
+// waves 8 with 256 columns: nf4_bwd8_kernel (eight waves of 32 output columns), listed after
+// nf4_bwd_kernel's; its SwiGLU epilogue exists for rows_blocks 4 only, which comes first.
 constexpr VariantCost kBwdVariants[] = {{2, 4, 256, 2, 2.55, 0.90},
                                        {2, 8, 512, 1, 2.60, 1.0},
                                        {4, 8, 512, 1, 3.40, 1.0},
+                                       {4, 8, 256, 1, 1.40, 0.90},
                                        {8, 8, 256, 1, 2.25, 0.90},
                                        {9, 8, 256, 1, 2.85, 0.85}};
 constexpr int kNumBwdVariants = sizeof(kBwdVariants) / sizeof(kBwdVariants[0]);
-constexpr int kNumBwd4Variants = 3;
-static_assert(kBwdVariants[kNumBwd4Variants - 1].rows_blocks < 8 && kBwdVariants[kNumBwd4Variants].rows_blocks >= 8,
-              "nf4_bwd_kernel variants first");
+constexpr int kNumBwdSwigluVariants = 4;  // nf4_bwd_kernel's and nf4_bwd8_kernel<4>
+static_assert(kBwdVariants[kNumBwdSwigluVariants - 1].bn == 256 && kBwdVariants[kNumBwdSwigluVariants - 1].rows_blocks == 4 &&
+              kBwdVariants[kNumBwdSwigluVariants].rows_blocks > 4, "SwiGLU-capable variants first");
+
+// nf4_bwd8_kernel variants: eight waves, 256-column tiles
+constexpr bool is_bwd8(const VariantCost& v) { return v.waves == 8 && v.bn == 256; }
 
 // The eight-wave variants come last: nf4_fwd8_kernel advances its load descriptors by whole
 // steps, so it needs k % 64 == 0 and blocks that do not straddle rows (k % blocksize == 0).
@@ -258,12 +263,13 @@ GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool glu
     return p;
 }
 
-// bwd8_ok: nf4_bwd8_kernel may run (no group with LoRA terms, no SwiGLU epilogue).
-GemmPlan plan_bwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool bwd8_ok, bool no_split = false) {
+// swiglu: the SwiGLU epilogue of dk_nf4_linear_bwd_swiglu (never split; the variants that have it).
+GemmPlan plan_bwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool swiglu, bool no_split = false) {
     GemmPlan p{};
     p.steps = 0;
     for (int g = 0; g < ngroups; ++g) p.steps += (int)((ns[g] + kBwdBC - 1) / kBwdBC);
-    const int nv = bwd8_ok ? kNumBwdVariants : kNumBwd4Variants;
+    const int nv = swiglu ? kNumBwdSwigluVariants : kNumBwdVariants;
+    no_split = no_split || swiglu;
     const VariantCost* v = plan_override("DECIK_BWD_PLAN", kBwdVariants, nv, p.steps, &p.splits);
     if (v != nullptr && no_split) p.splits = 1;
     if (v == nullptr)
@@ -272,6 +278,7 @@ GemmPlan plan_bwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool bwd
                         no_split ? 1 : 32);
     p.mt = v->rows_blocks;
     p.waves = v->waves;
+    p.bwd8 = is_bwd8(*v);
     p.n_tiles = (int)((k + v->bn - 1) / v->bn);
     p.m_tiles = (int)((m + kRowUnit * p.mt - 1) / (kRowUnit * p.mt));
     finish_plan(p, m, k);
@@ -357,9 +364,10 @@ int dk_nf4_linear_plan(int backward, int64_t m, int64_t k, const int64_t* ns, in
     const bool single = (flags & DK_PLAN_NO_SPLIT) != 0;
     GemmPlan p;
     int kernel;
+    (void)lora;  // every variant takes LoRA terms
     if (backward) {
-        p = plan_bwd(m, k, ns, ngroups, !glu && !lora, glu || single);
-        kernel = p.mt >= 8 ? 3 : 2;
+        p = plan_bwd(m, k, ns, ngroups, glu, single);
+        kernel = p.bwd8 ? 3 : 2;
     } else {
         p = plan_fwd(m, k, ns, ngroups, glu, k % 64 == 0 && k % blocksize == 0, single);
         kernel = p.waves == 8 ? 1 : 0;
@@ -373,9 +381,7 @@ int dk_nf4_linear_plan(int backward, int64_t m, int64_t k, const int64_t* ns, in
 
 int64_t dk_nf4_linear_bwd_workspace(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
     if (ngroups < 1 || ngroups > kMaxGroups || ns == nullptr || m <= 0 || k <= 0) return 0;
-    // the plan also depends on LoRA terms (eight-wave kernel or not): cover both
-    return std::max(workspace_bytes(plan_bwd(m, k, ns, ngroups, true)),
-                    workspace_bytes(plan_bwd(m, k, ns, ngroups, false)));
+    return workspace_bytes(plan_bwd(m, k, ns, ngroups, false));
 }
 
 }  // extern "C"
@@ -583,9 +589,7 @@ static int linear_bwd_impl(const std::string& name, const dk_linear_bwd_group* g
         ns[g] = G.w.n;
     }
     if (m == 0) return 0;
-    bool bwd8_ok = sw == nullptr;
-    for (int g = 0; g < ngroups; ++g) bwd8_ok = bwd8_ok && groups[g].lora_gu == nullptr;
-    const GemmPlan p = plan_bwd(m, k, ns, ngroups, bwd8_ok, sw != nullptr);
+    const GemmPlan p = plan_bwd(m, k, ns, ngroups, sw != nullptr);
     const int64_t need = workspace_bytes(p);
     if (need > 0 && (workspace == nullptr || workspace_bytes_ < need || !aligned(workspace, 256)))
         return fail(name + ": workspace too small (need " + std::to_string(need) + " bytes)");
@@ -615,8 +619,8 @@ static int linear_bwd_impl(const std::string& name, const dk_linear_bwd_group* g
     const int64_t wgs = (int64_t)p.m_tiles * p.n_tiles * p.splits;
     if (wgs > INT32_MAX / 2) return fail(name + ": problem too large");
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    const hipError_t le = p.mt >= 8 ? launch_bwd8(a, p.mt, pad8((int)wgs), st)
-                                    : launch_bwd(a, p.mt, p.waves, pad8((int)wgs), st);
+    const hipError_t le = p.bwd8 ? launch_bwd8(a, p.mt, pad8((int)wgs), st)
+                                 : launch_bwd(a, p.mt, p.waves, pad8((int)wgs), st);
     if (check_hip(le, "dk_nf4_linear_bwd launch")) return 1;
     if (p.splits <= 1) return 0;
     ReduceArgs r{};

@@ -1,14 +1,14 @@
-// Fused NF4 dequant x fp16 GEMM, input gradient, for launches with many token rows: the same
-// product as nf4_bwd_kernel (dX = sum_g dY_g . W_g, solution/nf4.py:99-104, summed over several
-// weights as the gate and up projections of solution/mlp.py:106-109), for launches without LoRA
-// terms or the SwiGLU epilogue.
+// Fused NF4 dequant x fp16 GEMM, input gradient: the same product as nf4_bwd_kernel
+// (dX = sum_g dY_g . W_g + sum_g GU_g . A_g, solution/nf4.py:99-104, summed over several weights
+// as the gate and up projections of solution/mlp.py:106-109), including the SwiGLU epilogue of
+// dk_nf4_linear_bwd_swiglu (solution/mlp.py:97-105: dgate / dup from fp16(dY . W_down)).
 //
 // Why a second kernel: nf4_bwd_kernel's waves own 64 output columns (two A operands, both
 // nibbles of a byte per lane) and at most 4 token blocks, so each dequantized weight feeds at
 // most four MFMAs and the dequant costs far more issue slots than the matrix pipe leaves free.
 // Here a work-group is 8 waves (two per SIMD, one work-group per CU) on a tile of 32*MB tokens
-// (MB = 8 or 9) x 256 output columns; each wave owns 32 columns -- one A operand, one nibble per
-// lane and weight row -- and all 32*MB tokens, so each dequantized weight feeds MB MFMAs.
+// (MB = 4, 8 or 9) x 256 output columns; each wave owns 32 columns -- one A operand, one nibble
+// per lane and weight row -- and all 32*MB tokens, so each dequantized weight feeds MB MFMAs.
 //
 // A operand (A = W^T): lane l (l32 = l % 32, g = l / 32) serves A row l32 = output column
 // c = arow_to_n(l32) of the wave's 32 (packed byte c / 2; high nibble for even c). Its eight
@@ -27,9 +27,10 @@
 // stage B (byte gather, code-book addresses and reads) after the third, stage C (scaling and fp16
 // packing) after the last but one, and each dY fragment refilled right after its MFMA read it.
 //
-// Epilogue: each token block's 32 x 256 fp32 tile goes through LDS (the dY ring, after a
-// barrier) and leaves as whole rows: split-K partial slabs (reduced by splitk_reduce_kernel) or
-// dX in fp32 or fp16.
+// Epilogue: each token block's 32 x 256 tile goes through LDS (the rings, after a barrier) and
+// leaves as whole rows: split-K partial slabs (reduced by splitk_reduce_kernel), dX in fp32 or
+// fp16, or (SwiGLU mode, MB = 4) dgate / dup from the tile rounded to fp16 and the matching gate
+// and up tiles, which every thread fetches for all its token blocks as the kernel starts.
 #include "gemm_common.h"
 
 namespace dk {
@@ -57,7 +58,9 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
     constexpr int DPT = (DCH + kB8Threads - 1) / kB8Threads;   // dY loads per thread and step
     constexpr int NL = DPT + 4 + (NESTED ? 2 : 1);             // loads per thread and step
     static_assert(DCH % 64 == 0, "a wave's dY load is wholly inside or past the tile");
-    static_assert(2 * 32 * (kB8BN * 4 + 16) <= 3 * DBUF, "epilogue staging fits the dY ring");
+    // epilogue staging area: the dY ring, the weight rings and the scale tables (contiguous)
+    constexpr int STAGE = 3 * DBUF + kB8Waves * (3 * kB8WSlot + kB8ScaleBytes);
+    static_assert(2 * 32 * (kB8BN * 4 + 16) <= STAGE, "epilogue staging fits the rings");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ float luts[16 * kMaxGroups];  // code books, group g at byte 64 g
     uint8_t* dummy = smem + kB8Tables;
@@ -103,9 +106,59 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
     for (int i = 0; i < MB; ++i) acc[i] = float16_t{};
 
     // stage positions (MFMA index after which a stage runs)
-    constexpr int qB = 2, qC = MB - 2;
-    constexpr int qS1 = 1, qS2 = 3, qS3 = 5;  // row scales of the next step (slice 2)
-    static_assert(qS3 < MB, "scale stages inside the slice");
+    constexpr int qB = MB >= 8 ? 2 : 1, qC = MB >= 8 ? MB - 2 : MB - 1;
+    constexpr int qS1 = 1, qS2 = MB >= 8 ? 3 : 2, qS3 = MB >= 8 ? 5 : 3;  // next step's row scales
+    static_assert(qS3 < MB && qB < qC, "stages inside the slice");
+
+    // SwiGLU mode: this thread's two 16-byte chunks (row ch / 32, columns 8 (ch % 32) ..) of
+    // every token block's gate and up tiles, requested as the kernel starts so that their reads
+    // overlap the main loop (the tiles are read before any output is written: dgate / dup may
+    // alias gate / up). The main loop's waits count its own loads only; these are older, so they
+    // only make the first wait stricter.
+    constexpr int SWB = MB <= 4 ? MB : 1;
+    u32x4_t gv[SWB][2], uv[SWB][2];
+    if constexpr (MB <= 4) {
+        if (a.swiglu) {
+#pragma unroll
+            for (int i = 0; i < MB; ++i)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int ch = tid + kB8Threads * h, row = ch >> 5, cc = ch & 31;
+                    const int m = m0 + 32 * i + row, col = tile_k0 + 8 * cc;
+                    gv[i][h] = uv[i][h] = u32x4_t{0u, 0u, 0u, 0u};
+                    if (m < M && col < K) {
+                        gv[i][h] = *(const u32x4_t*)(a.gate + (int64_t)m * a.ldgu + col);
+                        uv[i][h] = *(const u32x4_t*)(a.up + (int64_t)m * a.ldgu + col);
+                    }
+                }
+        }
+    }
+
+    // LoRA input-gradient terms GU_g . A_g first (split 0 only; trip count 0 without LoRA): A row
+    // l32 (output column kw0 + c) of rank slots t0 + 8 g + e, B = GU^T.
+    {
+        const int R = split == 0 ? sgpr(a.lora_rank) : 0;
+        for (int gg = 0; gg < a.ngroups; ++gg) {
+            const BwdGroupDev& G = a.g[gg];
+            if (G.lora_gu == nullptr || R == 0) continue;
+            const rsrc_t ars = make_rsrc(G.lora_a, (uint32_t)R * (uint32_t)K * 2u);
+            const rsrc_t grs = make_rsrc(G.lora_gu, (uint32_t)M * (uint32_t)R * 2u);
+            for (int t0 = 0; t0 < R; t0 += 16) {
+                half8_t al;
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    al[e] = __builtin_bit_cast(
+                        _Float16, (uint16_t)bload16(ars, off_if(cok, (uint32_t)((t0 + 8 * g + e) * K + kw0 + c) * 2u)));
+#pragma unroll
+                for (int i = 0; i < MB; ++i) {
+                    const int m = m0 + 32 * i + l32;
+                    const half8_t gu = __builtin_bit_cast(
+                        half8_t, bload128(grs, off_if(m < M, (uint32_t)(m * R + t0 + 8 * g) * 2u)));
+                    acc[i] = mfma32x32x16(al, gu, acc[i]);
+                }
+            }
+        }
+    }
 
     // One weight group at a time, as in nf4_bwd_kernel: the group's operands are pinned in
     // scalar registers for its steps and the pipeline drains between groups.
@@ -322,11 +375,55 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
         wait_vmcnt<0>();
         lds_barrier();
     }
-    lds_barrier();  // the dY ring becomes the staging area (also when no group had steps here)
+    lds_barrier();  // the rings become the staging area (also when no group had steps here)
 
     // ---- epilogue. Lane (l32, g) holds, for token block i, token row m0 + 32 i + l32 and the 16
     // consecutive columns colw + r of the tile (acc[i][r]).
     const int colw = 32 * wave + 16 * g;
+    if constexpr (MB <= 4) {
+        if (a.swiglu) {
+            // dgate / dup from G = fp16(dY . W) and the gate / up chunks fetched at the start
+            constexpr int RB = kB8BN * 2 + 16;
+#pragma unroll
+            for (int i = 0; i < MB; ++i) {
+                // G = fp16(dY . W) through LDS as 32 x 256 fp16 rows
+                uint8_t* buf = dring + (i & 1) * 32 * RB;
+                uint8_t* lp = buf + l32 * RB + colw * 2;
+                uint32_t o[8];
+#pragma unroll
+                for (int r = 0; r < 16; r += 2) o[r >> 1] = pack_half2(acc[i][r], acc[i][r + 1]);
+                *(u32x4_t*)lp = u32x4_t{o[0], o[1], o[2], o[3]};
+                *(u32x4_t*)(lp + 16) = u32x4_t{o[4], o[5], o[6], o[7]};
+                lds_barrier();
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int ch = tid + kB8Threads * h, row = ch >> 5, cc = ch & 31;
+                    const u32x4_t Gv = *(const u32x4_t*)(buf + row * RB + cc * 16);
+                    const int m = m0 + 32 * i + row, col = tile_k0 + 8 * cc;
+                    u32x4_t dg, du;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        // elements copied to scalars first: hipcc compiles __builtin_bit_cast of
+                        // a vector element (vec[q]) as element 0 whatever q is
+                        const uint32_t Gq = Gv[q], gq = gv[i][h][q], uq = uv[i][h][q];
+                        const half2_t G2 = __builtin_bit_cast(half2_t, Gq);
+                        const half2_t g2 = __builtin_bit_cast(half2_t, gq);
+                        const half2_t u2 = __builtin_bit_cast(half2_t, uq);
+                        float d0, d1, e0, e1;
+                        swiglu_bwd1((float)G2.x, (float)g2.x, (float)u2.x, d0, e0);
+                        swiglu_bwd1((float)G2.y, (float)g2.y, (float)u2.y, d1, e1);
+                        dg[q] = pack_half2(d0, d1);
+                        du[q] = pack_half2(e0, e1);
+                    }
+                    if (m < M && col < K) {
+                        *(u32x4_t*)(a.dgate + (int64_t)m * a.ldd + col) = dg;
+                        *(u32x4_t*)(a.dup + (int64_t)m * a.ldd + col) = du;
+                    }
+                }
+            }
+            return;
+        }
+    }
     const bool out32 = a.splits > 1 || a.dx_fp32;
     if (out32) {
         // 32 x 256 fp32 tiles (rows 1040 bytes apart) -> whole 1 KB rows of the split's partial
@@ -392,12 +489,10 @@ static hipError_t launch_bwd8_t(const BwdArgs& a, int grid, hipStream_t s) {
 }
 
 hipError_t launch_bwd8(const BwdArgs& a, int mb, int grid, hipStream_t s) {
-    if (a.swiglu) return hipErrorInvalidValue;  // not in this kernel
-    for (int g = 0; g < a.ngroups; ++g)
-        if (a.g[g].lora_gu != nullptr) return hipErrorInvalidValue;
+    if (a.swiglu && (mb > 4 || a.splits > 1)) return hipErrorInvalidValue;  // SwiGLU: MB <= 4, no split
 #define X(T) \
     if (mb == T) return a.nested ? launch_bwd8_t<T, true>(a, grid, s) : launch_bwd8_t<T, false>(a, grid, s);
-    X(8) X(9)
+    X(4) X(8) X(9)
 #undef X
     return hipErrorInvalidValue;
 }

@@ -88,17 +88,18 @@ def test_workspace_sizes():
 
 def test_launch_plans():
     """dk_nf4_linear_plan (host-only): the eight-wave input-gradient kernel serves the MLP's
-    gate/up input gradient at M = 830 and never a launch with LoRA terms or the SwiGLU epilogue
-    (it has neither); the fused GLU forward never splits; forced plans apply only where their
-    kernel may run; bad arguments are reported."""
+    gate/up input gradient at M = 830; SwiGLU-epilogue launches never split and use that kernel
+    only with 4 token blocks; the fused GLU forward never splits; forced plans apply only where
+    their kernel may run; bad arguments are reported."""
     from decik_amd import _lib
     from decik_amd.nf4 import launch_plan
 
     gu = launch_plan(True, 830, 1536, [8960, 8960])
     assert gu["kernel"] == "nf4_bwd8_kernel" and gu["splits"] > 1
-    assert launch_plan(True, 830, 1536, [8960, 8960], lora=True)["kernel"] == "nf4_bwd_kernel"
+    # the SwiGLU epilogue: never split, and in the eight-wave kernel only with 4 token blocks
     sw = launch_plan(True, 830, 8960, [1536], glu=True)
-    assert sw["kernel"] == "nf4_bwd_kernel" and sw["splits"] == 1
+    assert sw["splits"] == 1
+    assert sw["kernel"] == "nf4_bwd_kernel" or sw["rows_blocks"] == 4
     glu = launch_plan(False, 830, 1536, [8960, 8960], glu=True)
     assert glu["splits"] == 1 and glu["kernel"] == "nf4_fwd8_kernel"
     # k % blocksize != 0: the eight-wave forward kernel may not run
@@ -109,7 +110,13 @@ def test_launch_plans():
         os.environ["DECIK_BWD_PLAN"] = "9,3,8"
         assert launch_plan(True, 830, 1536, [8960]) == dict(rows_blocks=9, waves=8, splits=3,
                                                              kernel="nf4_bwd8_kernel")
-        assert launch_plan(True, 830, 1536, [8960], lora=True)["kernel"] == "nf4_bwd_kernel"
+        # no SwiGLU epilogue with 9 token blocks: the forced plan does not apply
+        assert launch_plan(True, 830, 1536, [8960], glu=True)["rows_blocks"] != 9
+        os.environ["DECIK_BWD_PLAN"] = "4,2,8"
+        assert launch_plan(True, 830, 1536, [8960])["kernel"] == "nf4_bwd_kernel"
+        os.environ["DECIK_BWD_PLAN"] = "4,2,8,256"
+        assert launch_plan(True, 830, 1536, [8960]) == dict(rows_blocks=4, waves=8, splits=2,
+                                                             kernel="nf4_bwd8_kernel")
     finally:
         if old is None:
             os.environ.pop("DECIK_BWD_PLAN", None)

@@ -36,7 +36,7 @@ def test_forward_variants(nested, blocksize, plan, device, monkeypatch, raw_stat
                  what=f"fwd {plan} nested={nested} bs={blocksize}")
 
 
-@pytest.mark.parametrize("plan", ["2,1,4", "2,2,8", "4,1,8", "4,3,8", "8,1,8", "9,2,8"])
+@pytest.mark.parametrize("plan", ["2,1,4", "2,2,8", "4,1,8", "4,3,8", "4,2,8,256", "8,1,8", "9,2,8"])
 @pytest.mark.parametrize("nested,blocksize", CASES)
 def test_backward_variants_partial_last_step(nested, blocksize, plan, device, monkeypatch, raw_statistics):
     """264 weight rows: the last 64-row step has 8 rows; dY columns and weight rows past them read
@@ -67,7 +67,7 @@ def test_grouped_backward_partial_steps(plan, device, monkeypatch, raw_statistic
     assert_close(dx, ref, max_rel=1e-4, mean_rel=1e-5, what=f"grouped bwd {plan}")
 
 
-@pytest.mark.parametrize("plan", ["8,2,8", "9,1,8"])
+@pytest.mark.parametrize("plan", ["4,1,8,256", "8,2,8", "9,1,8"])
 @pytest.mark.parametrize("nested,blocksize", CASES)
 @pytest.mark.parametrize("dx_fp32", [False, True])
 def test_eight_wave_backward_edges(nested, blocksize, plan, dx_fp32, device, monkeypatch, raw_statistics):
@@ -88,19 +88,17 @@ def test_eight_wave_backward_edges(nested, blocksize, plan, dx_fp32, device, mon
         assert_close(dx, ref, what=f"bwd8 {plan} nested={nested} bs={blocksize}")
 
 
-def test_eight_wave_plan_ignored_with_lora(device, monkeypatch):
-    """A forced eight-wave plan does not apply to launches with LoRA terms (that kernel has none):
-    the planner falls back to nf4_bwd_kernel and the result includes the LoRA gradient."""
-    import torch
+@pytest.mark.parametrize("plan", ["4,1,8,256", "8,2,8", "9,3,8"])
+def test_eight_wave_backward_lora(plan, device, monkeypatch):
+    """LoRA input-gradient terms GU . A (rank 16) in the eight-wave kernel, split 0 only."""
     from decik_amd.nf4 import linear_backward
 
-    monkeypatch.setenv("DECIK_BWD_PLAN", "9,1,8")
+    monkeypatch.setenv("DECIK_BWD_PLAN", plan)
     packed, qs, w16 = make_weight((256, 512), seed=31, device=device, nested=True, blocksize=64)
     dy = randn16((200, 256), seed=32, device=device, std=1e-2)
     gu = randn16((200, 16), seed=33, device=device, std=1e-2)
     la = randn16((16, 512), seed=34, device=device, std=1e-1)
     dx = linear_backward([dict(packed=packed, qs=qs, dy=dy, lora_gu=gu, lora_a=la)], 200, 512, dx_fp32=True,
                          lora_rank=16)
-    ref = O.linear_dx_ref(dy.cpu().numpy(), w16) + gu.cpu().float().numpy() @ la.cpu().float().numpy()
-    assert_close(dx, ref, max_rel=1e-4, mean_rel=1e-5, what="bwd lora with forced bwd8 plan")
-    assert torch.isfinite(dx).all()
+    ref = O.linear_dx_ref(dy.cpu().numpy(), w16) + gu.cpu().double().numpy() @ la.cpu().double().numpy()
+    assert_close(dx, ref, max_rel=1e-4, mean_rel=1e-5, what=f"bwd8 lora {plan}")
