@@ -52,7 +52,9 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
     static_assert(XCH % 64 == 0, "a wave's X load is wholly inside or past the tile");
     static_assert(2 * 32 * (256 * 4 + 16) <= 3 * XBUF, "epilogue staging fits the X ring");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    __shared__ float lut[32];  // code books (gate, up in GLU mode; the same book otherwise)
+    // byte-pair code books (gate, up in GLU mode; the same book otherwise): entry 256 b + byte
+    // holds (code_b[byte >> 4], code_b[byte & 15]), the two weights of one packed byte
+    __shared__ float2_t lut2[512];
     float* c2 = (float*)smem;
     uint8_t* dummy = smem + kF8Header;
     uint8_t* xs = dummy + kF8Dummy;
@@ -89,14 +91,23 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
     const int ks0 = split * a.ksteps_per_split;
     const int ks1 = min(a.ksteps, ks0 + a.ksteps_per_split);
 
-    if (tid < 32) lut[tid] = a.g[glu ? (tid >> 4) : gi].w.code[tid & 15];
+    {
+        const float* book = a.g[glu ? (tid >> 8) : gi].w.code;
+        lut2[tid] = float2_t{book[(tid >> 4) & 15], book[tid & 15]};
+    }
     if constexpr (NESTED) {
         if (tid < 256) c2[tid] = W.code2[tid];
     }
     const float offset = NESTED ? *W.offset : 0.0f;
-    // this wave's code book (bytes 64 * book of the static table), folded into the lookup
-    // addresses (see nib_addrs)
-    const uint32_t book4 = (uint32_t)(glu ? 64 * (wave >> 2) : 0) * 0x01010101u;
+    // byte offset of this wave's byte-pair code book in lut2
+    const uint32_t book8 = (uint32_t)(glu ? 2048 * (wave >> 2) : 0);
+    // LDS byte address of the code-book pair of byte e of a packed dword
+    auto pair_addr = [&](uint32_t w, int e) __attribute__((always_inline)) -> uint32_t {
+        return (((w >> (8 * e)) & 0xFFu) << 3) + book8;
+    };
+    auto pair_at = [&](uint32_t addr) __attribute__((always_inline)) -> float2_t {
+        return *(const float2_t*)((const char*)lut2 + addr);
+    };
 
     const int wrow = nw0 + arow_to_n(l32);  // this lane's A row
     const bool rowok = wrow < N;
@@ -215,16 +226,18 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
         s = scale_of(ws);
     };
     half8_t xf[MB], w, wn;
-    uint32_t ah, al;  // code-book byte addresses of the next slice (see nib_addrs)
+    uint32_t pa[4];   // code-book pair addresses of the next slice's 4 packed bytes
     float v[8];       // its code-book values
     fetch_step(rw0);
 #pragma unroll
     for (int i = 0; i < MB; ++i) xf[i] = xfrag(xs + rx0, i, 0);
     {
-        nib_addrs(p[0], book4, ah, al);
         u32x4_t o;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = pack_half2(lut_at(lut, ah, e) * s, lut_at(lut, al, e) * s);
+        for (int e = 0; e < 4; ++e) {
+            const float2_t cv = pair_at(pair_addr(p[0], e));
+            o[e] = pack_half2(cv.x * s, cv.y * s);
+        }
         w = __builtin_bit_cast(half8_t, o);
     }
     // stage positions (MFMA index after which a stage runs)
@@ -248,12 +261,16 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
                 }
                 // refill the X fragment the MFMA above has read (slice j + 1)
                 xf[q] = xfrag(xs + (j < 3 ? rx0 : rx1), q, jn);
-                if (q == (j < 3 ? qA : qA + 1)) nib_addrs(p[jn], book4, ah, al);
+                if (q == (j < 3 ? qA : qA + 1)) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) pa[e] = pair_addr(p[jn], e);
+                }
                 if (q == (j < 3 ? qB : qB + 1)) {
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        v[2 * e] = lut_at(lut, ah, e);
-                        v[2 * e + 1] = lut_at(lut, al, e);
+                        const float2_t cv = pair_at(pa[e]);
+                        v[2 * e] = cv.x;
+                        v[2 * e + 1] = cv.y;
                     }
                 }
                 if (q == qC) {
