@@ -105,7 +105,11 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
 #pragma unroll
     for (int i = 0; i < MB; ++i) acc[i] = float16_t{};
 
-    // stage positions (MFMA index after which a stage runs)
+    // stage positions (MFMA index after which a stage runs). With few MFMAs per slice (P2) the
+    // packed dwords and row scales are read two slices ahead (LA = 2), so the next step's row
+    // scales are made in slice 1 (JW) instead of slice 2.
+    constexpr bool P2 = MB <= 4;
+    constexpr int LA = P2 ? 2 : 1, JW = P2 ? 1 : 2;
     constexpr int qB = MB >= 8 ? 2 : 1, qC = MB >= 8 ? MB - 2 : MB - 1;
     constexpr int qS1 = 1, qS2 = MB >= 8 ? 3 : 2, qS3 = MB >= 8 ? 5 : 3;  // next step's row scales
     static_assert(qS3 < MB && qB < qC, "stages inside the slice");
@@ -290,13 +294,31 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
         u32x4_t d0, d1;  // next slice: packed dwords of rows r0 .. r0 + 3 and r0 + 4 .. r0 + 7
         float4_t s0, s1; // ... their row scales
         float v[8];      // ... their code-book values
+        u32x4_t e0, e1;  // two-slice pipeline: the packed dwords and scales of the slice after
+        float4_t t0s, t1s;
         auto stage_A = [&](int rw, int sidx, int j) __attribute__((always_inline)) {
             const uint8_t* pk = wring + rw + pkl + 256 * (j >> 1) + 32 * (j & 1);
-            d0 = *(const u32x4_t*)pk;
-            d1 = *(const u32x4_t*)(pk + 16);
             const float* sc = stab + 64 * sidx + 32 * g + 8 * j;
-            s0 = *(const float4_t*)sc;
-            s1 = *(const float4_t*)(sc + 4);
+            if constexpr (P2) {
+                e0 = *(const u32x4_t*)pk;
+                e1 = *(const u32x4_t*)(pk + 16);
+                t0s = *(const float4_t*)sc;
+                t1s = *(const float4_t*)(sc + 4);
+            } else {
+                d0 = *(const u32x4_t*)pk;
+                d1 = *(const u32x4_t*)(pk + 16);
+                s0 = *(const float4_t*)sc;
+                s1 = *(const float4_t*)(sc + 4);
+            }
+        };
+        // two-slice pipeline: the slice after next becomes the next one
+        auto advance = [&]() __attribute__((always_inline)) {
+            if constexpr (P2) {
+                d0 = e0;
+                d1 = e1;
+                s0 = t0s;
+                s1 = t1s;
+            }
         };
         auto stage_B = [&]() __attribute__((always_inline)) {
             // this lane's byte of rows r0 .. r0 + 3 and r0 + 4 .. r0 + 7, gathered into two dwords
@@ -323,12 +345,17 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
             return *(const half8_t*)(dring + rd + (32 * i + l32) * 128 + (((4 * g + j) ^ xsw) << 4));
         };
 
-        // slice 0 of the first step
+        // slice 0 of the first step (and, two slices deep, slice 1's packed dwords and scales)
         stage_A(rw0, si0, 0);
+        advance();
 #pragma unroll
         for (int i = 0; i < MB; ++i) xf[i] = xfrag(rd0, i, 0);
         stage_B();
         w = stage_C();
+        if constexpr (P2) {
+            stage_A(rw0, si0, 1);
+            advance();
+        }
 
         for (int t = t0; t < t1; ++t) {
 #pragma unroll
@@ -338,7 +365,7 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
                 for (int q = 0; q < MB; ++q) {
                     acc[q] = mfma32x32x16(w, xf[q], acc[q]);
                     if (j == 3 && q == 0) {
-                        // every wave's loads of step t+1 have landed (each waited in slice 2)
+                        // every wave's loads of step t+1 have landed (each waited in slice 1 or 2)
                         // and every wave is past step t's slots: refill them with step t+3
                         // (zeros past the segment's end). Past the last step the reads below
                         // see stale slots and their values go unused.
@@ -348,11 +375,14 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
                     // refill the dY fragment the MFMA above has read (slice j + 1)
                     xf[q] = xfrag(j < 3 ? rd0 : rd1, q, jn);
                     if (q == 0) {
-                        if (j == 2) wait_vmcnt<NL>();  // step t+1's loads (this wave's) landed
-                        if (j < 3) stage_A(rw0, si0, j + 1);
-                        else stage_A(rw1, 1 - si0, 0);
+                        // step t+1's loads (this wave's) landed; its row scales follow in this
+                        // slice, before any stage A reads them
+                        if (j == JW) wait_vmcnt<NL>();
+                        const int ja = j + LA;  // the slice stage A prepares
+                        if (ja < 4) stage_A(rw0, si0, ja);
+                        else stage_A(rw1, 1 - si0, ja - 4);
                     }
-                    if (j == 2) {
+                    if (j == JW) {
                         if (q == qS1) scales_1(rw1);
                         if (q == qS2) scales_2();
                         if (q == qS3) scales_3(t + 1, 1 - si0);
@@ -362,6 +392,7 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
                     __builtin_amdgcn_sched_barrier(0);
                 }
                 w = wn;
+                advance();
             }
             // rotate the rings: step t + 1's buffers become the current ones
             rd0 = rd1;
