@@ -26,8 +26,10 @@ __global__ __launch_bounds__(kReduceThreads) void splitk_reduce_kernel(const Red
             for (int u = 0; u < kBatch; ++u) {
                 if (s0 + u < a.splits) {
                     const float4_t* p = (const float4_t*)(base + (int64_t)(s0 + u) * a.slab + col);
-                    l0[u] = __builtin_nontemporal_load(p);
-                    l1[u] = __builtin_nontemporal_load(p + 1);
+                    // plain loads: the slabs were written just before and are read back from
+                    // the caches (non-temporal loads measured 2-3.5 us slower per reduction)
+                    l0[u] = *p;
+                    l1[u] = *(p + 1);
                 }
             }
             // the additions stay in split order
