@@ -233,7 +233,10 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
 #pragma unroll
                 for (int d = 0; d < 4; ++d) bload32_lds(wrs, slot + 256 * d, po + (uint32_t)d * prow16);
             } else {
-                // rows and dY columns past N read zeros
+                // rows and dY columns past N read zeros. The empty volatile asm keeps this a
+                // branch taken only on a group's last, partial step: merged with the plain loads
+                // above, the per-lane checks became selects on every step (~8% of the loop).
+                asm volatile("");
 #pragma unroll
                 for (int h = 0; h < DPT; ++h)
                     bload128_lds(drs, dy_dst(rd, h), off_if(n0 + 8 * dy_col(h) < N, dyo[h]));
