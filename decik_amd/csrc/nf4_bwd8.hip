@@ -209,7 +209,8 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
         // the dummy area)
         auto dy_dst = [&](int rd, int h) __attribute__((always_inline)) -> uint8_t* {
             const int wq0 = kB8Threads * h + 64 * wave;  // the wave's first chunk (uniform)
-            return wq0 < DCH ? dring + rd + wq0 * 16 : dummy;
+            // loads h < DPT - 1 never pass the tile (folded at compile time: no scalar select)
+            return ((h + 1) * kB8Threads <= DCH || wq0 < DCH) ? dring + rd + wq0 * 16 : dummy;
         };
         // packed bytes: DMA instruction d fetches rows 16 d .. 16 d + 15, the wave's 4 dwords of
         // each; lane l -> (dword column l / 16, row l % 16) lands at byte 256 d + 4 l

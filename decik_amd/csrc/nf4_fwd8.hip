@@ -153,7 +153,8 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
         const rsrc_t xrs = make_rsrc(gx + 2u * k0, live ? x_bytes - 2u * k0 : 0u);
 #pragma unroll
         for (int h = 0; h < XPT; ++h)
-            bload128_lds(xrs, xdst[h] >= 0 ? xs + rx + xdst[h] : dummy, xo[h]);
+            // loads h < XPT - 1 never pass the tile (folded at compile time: no scalar select)
+            bload128_lds(xrs, ((h + 1) * kF8Threads <= XCH || xdst[h] >= 0) ? xs + rx + xdst[h] : dummy, xo[h]);
         uint8_t* slot = wring + rw;
         const rsrc_t wrs = make_rsrc(gpk + k0 / 2u, live ? pk_bytes - k0 / 2u : 0u);
         bload128_lds(wrs, slot, wo);
