@@ -102,3 +102,28 @@ def test_eight_wave_backward_lora(plan, device, monkeypatch):
                          lora_rank=16)
     ref = O.linear_dx_ref(dy.cpu().numpy(), w16) + gu.cpu().double().numpy() @ la.cpu().double().numpy()
     assert_close(dx, ref, max_rel=1e-4, mean_rel=1e-5, what=f"bwd8 lora {plan}")
+
+
+@pytest.mark.parametrize("plan", ["4,2,8,256", "8,3,8", "9,4,8"])
+def test_eight_wave_backward_three_groups_lora(plan, device, monkeypatch):
+    """Three weights of 1536, 256 and 264 rows (the last ends in a partial step) in one launch,
+    LoRA terms on the first and last: every split adds its share of the contraction, split 0 the
+    LoRA terms (the q/k/v input gradient of solution/attn.py:396-418)."""
+    from decik_amd.nf4 import linear_backward
+
+    monkeypatch.setenv("DECIK_BWD_PLAN", plan)
+    m, k = 300, 512
+    items, ref = [], 0.0
+    for i, n in enumerate((1536, 256, 264)):
+        packed, qs, w16 = make_weight((n, k), seed=90 + i, device=device, nested=True, blocksize=64)
+        dy = randn16((m, n), seed=95 + i, device=device, std=1e-2)
+        it = dict(packed=packed, qs=qs, dy=dy)
+        ref = ref + O.linear_dx_ref(dy.cpu().numpy(), w16)
+        if i != 1:
+            gu = randn16((m, 16), seed=97 + i, device=device, std=1e-2)
+            la = randn16((16, k), seed=99 + i, device=device, std=1e-1)
+            it.update(lora_gu=gu, lora_a=la)
+            ref = ref + gu.cpu().double().numpy() @ la.cpu().double().numpy()
+        items.append(it)
+    dx = linear_backward(items, m, k, dx_fp32=True, lora_rank=16)
+    assert_close(dx, ref, max_rel=1e-4, mean_rel=1e-5, what=f"bwd8 three groups {plan}")
