@@ -201,3 +201,28 @@ def test_scale_cache_follows_in_place_updates(device):
     assert s2 is not s1 and not torch.equal(y1, y2)
     w16b = O.dequant_nf4(oracle_state(packed, qs), nthreads=0)
     assert_close(y2, O.linear_ref(x.cpu().numpy(), w16b), what="after in-place update")
+
+
+def test_large_m_planned_launches(device):
+    """M = 4096 tokens with the planner's own choices (eight-wave kernels, splits as planned):
+    gate/up forward with the SwiGLU epilogue and the summed gate/up input gradient, against fp32
+    GEMMs on the GPU of the oracle's bit-exact dequantized weights (fp32 reference of the same
+    fp16 operands; the float64 CPU reference is too slow at this size)."""
+    from decik_amd.nf4 import glu_forward, launch_plan, linear_backward
+
+    m, n, k = 4096, 1024, 1536
+    (pg, qg, wg), (pu, qu, wu) = (make_weight((n, k), seed=110 + i, device=device, nested=False) for i in range(2))
+    x = randn16((m, k), seed=111, device=device)
+    gate, up, h = glu_forward(x, dict(packed=pg, qs=qg), dict(packed=pu, qs=qu))
+    wg32 = torch.from_numpy(wg.astype(np.float32)).to(device)
+    wu32 = torch.from_numpy(wu.astype(np.float32)).to(device)
+    g_ref = x.float() @ wg32.t()
+    u_ref = x.float() @ wu32.t()
+    assert_close(gate, g_ref.cpu().numpy(), what="large-M gate")
+    assert_close(up, u_ref.cpu().numpy(), what="large-M up")
+    dg = randn16((m, n), seed=112, device=device, std=1e-2)
+    du = randn16((m, n), seed=113, device=device, std=1e-2)
+    assert launch_plan(True, m, k, [n, n])["kernel"] == "nf4_bwd8_kernel"
+    dx = linear_backward([dict(packed=pg, qs=qg, dy=dg), dict(packed=pu, qs=qu, dy=du)], m, k, dx_fp32=True)
+    ref = dg.float() @ wg32 + du.float() @ wu32
+    assert_close(dx, ref.cpu().numpy(), max_rel=1e-4, mean_rel=1e-5, what="large-M grouped bwd")
