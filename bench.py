@@ -23,6 +23,8 @@ reference algorithm (dequantize the whole weight, then an fp32 GEMM) on this hos
 """
 
 import argparse
+import contextlib
+import gc
 import json
 import os
 import statistics
@@ -102,6 +104,18 @@ def mlp_weight_sets(min_bytes=512 << 20):
     """Weight sets (gate, up, down) the MLP bench rotates through: more than `min_bytes` in all."""
     per_set = 2 * nf4_bytes(INTER, HIDDEN) + nf4_bytes(HIDDEN, INTER)
     return max(4, -(-min_bytes // per_set) + 1)
+
+
+@contextlib.contextmanager
+def no_gc():
+    """Python's garbage collector off while timing (as the timeit module does): a collection
+    pause in the host loop stalls the launch queue and would be charged to the GPU work."""
+    gc.collect()
+    gc.disable()
+    try:
+        yield
+    finally:
+        gc.enable()
 
 
 def bench_mlp(steps, warmup, device, n_sets=None, only=None):
@@ -372,7 +386,8 @@ def main():
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
 
-    mlp = bench_mlp(args.steps, args.warmup, device, only=args.only)
+    with no_gc():
+        mlp = bench_mlp(args.steps, args.warmup, device, only=args.only)
     if args.copy_probe:
         src = torch.ones(128 << 20, dtype=torch.float32, device=device)
         dst = torch.empty(128 << 20, dtype=torch.float16, device=device)
@@ -380,7 +395,8 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    deq = None if (args.skip_dequant or args.only) else bench_dequant(max(args.steps, 10), args.warmup, device)
+    with no_gc():
+        deq = None if (args.skip_dequant or args.only) else bench_dequant(max(args.steps, 10), args.warmup, device)
 
     # Dominant launch: the fused GEMM call with the largest time. Its kernels: the GEMM kernel,
     # plus splitk_reduce_kernel when the call takes the split-K path. `achieved` = the call's
