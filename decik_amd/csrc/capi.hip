@@ -364,10 +364,15 @@ int dk_nf4_linear_plan(int backward, int64_t m, int64_t k, const int64_t* ns, in
     const bool single = (flags & DK_PLAN_NO_SPLIT) != 0;
     GemmPlan p;
     int kernel;
-    (void)lora;  // every variant takes LoRA terms
     if (backward) {
         p = plan_bwd(m, k, ns, ngroups, glu, single);
         kernel = p.bwd8 ? 3 : 2;
+    } else if (!glu && !lora && m <= kGemvMaxM && (std::getenv("DECIK_FWD_PLAN") == nullptr ||
+                                                    *std::getenv("DECIK_FWD_PLAN") == 0)) {
+        p = GemmPlan{};
+        p.waves = 4;
+        p.splits = 1;
+        kernel = 4;  // nf4_gemv_kernel
     } else {
         p = plan_fwd(m, k, ns, ngroups, glu, k % 64 == 0 && k % blocksize == 0, single);
         kernel = p.waves == 8 ? 1 : 0;
@@ -385,6 +390,17 @@ int64_t dk_nf4_linear_bwd_workspace(int64_t m, int64_t k, const int64_t* ns, int
 }
 
 }  // extern "C"
+
+// The GEMV kernel takes forward launches of at most kGemvMaxM token rows without LoRA terms or
+// the GLU epilogue, unless DECIK_FWD_PLAN forces an MFMA plan (tuning and the variant tests).
+static bool use_gemv(int64_t m, bool glu, const dk_linear_fwd_group* groups, int ngroups) {
+    if (glu || m > kGemvMaxM || m < 1) return false;
+    const char* forced = std::getenv("DECIK_FWD_PLAN");
+    if (forced != nullptr && *forced != 0) return false;
+    for (int g = 0; g < ngroups; ++g)
+        if (groups[g].lora_u != nullptr) return false;
+    return true;
+}
 
 // The forward launch behind dk_nf4_linear_fwd and dk_nf4_glu_fwd. h != NULL: GLU mode (two groups
 // of one shape, plain narrow statistics; gate/up outputs optional). no_split: a single pass
@@ -445,13 +461,25 @@ static int linear_fwd_impl(const std::string& name, const uint16_t* x, int64_t m
                 groups[0].w.blocksize != groups[1].w.blocksize))
         return fail(name + ": GLU mode needs two plain weights of one shape, blocksize >= 64, k % 64 == 0");
     if (m == 0 || tile == 0) return 0;
+    if ((m - 1) * ldx + k >= INT32_MAX / 2) return fail(name + ": x too large");
+    if (use_gemv(m, glu, groups, ngroups)) {
+        // few token rows, no LoRA terms: one pass over the packed weights (no workspace)
+        a.x = reinterpret_cast<const _Float16*>(x);
+        a.ldx = ldx;
+        a.m = (int)m;
+        a.k = (int)k;
+        a.ngroups = ngroups;
+        a.nested = nested;
+        a.ncols = (int32_t)ncols;
+        if (ncols > INT32_MAX / 2) return fail(name + ": problem too large");
+        return check_hip(launch_gemv(a, static_cast<hipStream_t>(stream)), "dk_nf4_linear_fwd GEMV launch");
+    }
     bool fwd8_ok = k % 64 == 0;
     for (int g = 0; g < ngroups; ++g) fwd8_ok = fwd8_ok && k % groups[g].w.blocksize == 0;
     const GemmPlan p = plan_fwd(m, k, ns, ngroups, glu, fwd8_ok, no_split);
     const int64_t need = workspace_bytes(p);
     if (need > 0 && (workspace == nullptr || workspace_bytes_ < need || !aligned(workspace, 256)))
         return fail(name + ": workspace too small (need " + std::to_string(need) + " bytes)");
-    if ((m - 1) * ldx + k >= INT32_MAX / 2) return fail(name + ": x too large");
     a.x = reinterpret_cast<const _Float16*>(x);
     a.ldx = ldx;
     a.x_bytes = (uint32_t)(((m - 1) * ldx + k) * 2);

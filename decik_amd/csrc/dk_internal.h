@@ -133,6 +133,9 @@ struct GemmPlan {
 };
 
 hipError_t launch_fwd(const FwdArgs& a, int mb, int grid, hipStream_t s);
+// GEMV for launches of at most kGemvMaxM token rows (no LoRA terms, no GLU epilogue, no split)
+constexpr int kGemvMaxM = 2;  // measured: the MFMA kernels are faster from 3 token rows on 7B shapes
+hipError_t launch_gemv(const FwdArgs& a, hipStream_t s);
 // 8-wave forward kernel (32 weight rows x 32*mb tokens per wave), mb = 8 or 9
 hipError_t launch_fwd8(const FwdArgs& a, int mb, int grid, hipStream_t s);
 hipError_t launch_bwd(const BwdArgs& a, int mb, int waves, int grid, hipStream_t s);

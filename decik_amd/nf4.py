@@ -16,6 +16,7 @@ No path runs on the CPU: the HIP library must be built (`python -m decik_amd.bui
 """
 
 import ctypes
+import os
 
 import torch
 
@@ -100,6 +101,25 @@ def _scales(packed, qs, device):
     return _lib.SCALES.get(packed, qs, device) if qs.nested else None
 
 
+_NEED = {}
+
+
+def _workspace_need(forward, m, k, ns):
+    """dk_nf4_linear_{fwd,bwd}_workspace for these shapes, remembered per shape and forced plan
+    (the query runs the planner; a step repeats the same few shapes)."""
+    var = "DECIK_FWD_PLAN" if forward else "DECIK_BWD_PLAN"
+    key = (forward, m, k, tuple(ns), os.environ.get(var))
+    need = _NEED.get(key)
+    if need is None:
+        ns_arr = (ctypes.c_int64 * len(ns))(*ns)
+        fn = lib().dk_nf4_linear_fwd_workspace if forward else lib().dk_nf4_linear_bwd_workspace
+        need = int(fn(m, k, ns_arr, len(ns)))
+        if len(_NEED) > 4096:
+            _NEED.clear()
+        _NEED[key] = need
+    return need
+
+
 def linear_forward(x16, items, lora_rank=0):
     """Fused forward for weights that share x16 [M, K] (fp16, contiguous rows).
 
@@ -133,8 +153,7 @@ def linear_forward(x16, items, lora_rank=0):
         keep += [bias, u, b, out]
         outs.append(out)
         ns.append(n)
-    ns_arr = (ctypes.c_int64 * len(ns))(*ns)
-    need = lib().dk_nf4_linear_fwd_workspace(m, k, ns_arr, len(ns))
+    need = _workspace_need(True, m, k, ns)
     ws, ws_bytes = _lib.WORKSPACE.get(need, dev)
     check(lib().dk_nf4_linear_fwd(ptr(x2), m, k, x2.stride(0), groups, len(items), int(lora_rank),
                                   ptr(ws), ws_bytes, stream_of(dev)))
@@ -176,8 +195,7 @@ def linear_backward(items, m, k, dx=None, dx_fp32=False, lora_rank=0):
         groups[g].lora_a = None if a is None else a.data_ptr()
         keep += [dy, gu, a]
         ns.append(int(qs.shape[0]))
-    ns_arr = (ctypes.c_int64 * len(ns))(*ns)
-    need = lib().dk_nf4_linear_bwd_workspace(m, k, ns_arr, len(ns))
+    need = _workspace_need(False, m, k, ns)
     ws, ws_bytes = _lib.WORKSPACE.get(need, dev)
     check(lib().dk_nf4_linear_bwd(groups, len(items), m, k, ptr(dx), dx.stride(0),
                                   1 if dx.dtype == torch.float32 else 0, int(lora_rank), ptr(ws),

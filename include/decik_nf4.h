@@ -216,7 +216,8 @@ int dk_swiglu_bwd(const uint16_t* grad, const uint16_t* gate, const uint16_t* up
  * DK_PLAN_NO_SPLIT (a single pass). blocksize: the largest block size of the groups' weights.
  * out[0] = 32-token row blocks per tile, out[1] = waves per work-group, out[2] = contraction
  * splits, out[3] = kernel (0 nf4_fwd_kernel, 1 nf4_fwd8_kernel, 2 nf4_bwd_kernel,
- * 3 nf4_bwd8_kernel). Host-only (no GPU call); honours DECIK_FWD_PLAN / DECIK_BWD_PLAN like the
+ * 3 nf4_bwd8_kernel, 4 nf4_gemv_kernel: forward launches of at most 2 token rows without LoRA
+ * terms or the GLU epilogue, one wave per weight row). Host-only (no GPU call); honours DECIK_FWD_PLAN / DECIK_BWD_PLAN like the
  * launches. Returns 0, or nonzero with dk_last_error() on bad arguments. */
 #define DK_PLAN_GLU 1
 #define DK_PLAN_LORA 2

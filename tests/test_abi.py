@@ -100,6 +100,11 @@ def test_launch_plans():
     sw = launch_plan(True, 830, 8960, [1536], glu=True)
     assert sw["splits"] == 1
     assert sw["kernel"] == "nf4_bwd_kernel" or sw["rows_blocks"] == 4
+    # at most 2 token rows, no LoRA, no GLU epilogue: the GEMV kernel
+    assert launch_plan(False, 1, 3584, [18944])["kernel"] == "nf4_gemv_kernel"
+    assert launch_plan(False, 2, 3584, [18944])["kernel"] == "nf4_gemv_kernel"
+    assert launch_plan(False, 3, 3584, [18944])["kernel"] != "nf4_gemv_kernel"
+    assert launch_plan(False, 1, 3584, [18944], lora=True)["kernel"] != "nf4_gemv_kernel"
     glu = launch_plan(False, 830, 1536, [8960, 8960], glu=True)
     assert glu["splits"] == 1 and glu["kernel"] == "nf4_fwd8_kernel"
     # k % blocksize != 0: the eight-wave forward kernel may not run
@@ -127,3 +132,23 @@ def test_launch_plans():
     ns = (ctypes.c_int64 * 1)(64)
     assert L.dk_nf4_linear_plan(1, 8, 64, ns, 1, 0, 48, out) != 0
     assert b"bad arguments" in L.dk_last_error()
+
+
+def test_no_bit_cast_of_vector_elements():
+    """hipcc compiles __builtin_bit_cast(T, v[i]) of an ext_vector_type element as element 0
+    whatever i is (found twice in this library); the kernels copy elements to scalars first.
+    Flags any bit_cast whose operand is a subscript of a variable declared as one of the
+    library's vector types."""
+    import glob
+
+    csrc = os.path.join(ROOT, "decik_amd", "csrc")
+    vec_types = r"(?:u32x4_t|u32x2_t|half2_t|half4_t|half8_t|float2_t|float4_t|float16_t)"
+    bad = []
+    for path in sorted(glob.glob(os.path.join(csrc, "*.hip")) + glob.glob(os.path.join(csrc, "*.h"))):
+        text = open(path).read()
+        vec_vars = set(re.findall(vec_types + r"\s+(\w+)(?:\s*\[[^\]]*\])*\s*[=;,{)]", text))
+        vec_vars |= set(re.findall(vec_types + r"\s+\w+(?:\s*\[[^\]]*\])*\s*(?:=[^,;()]*)?,\s*(\w+)", text))
+        for mt in re.finditer(r"__builtin_bit_cast\(\s*\w+\s*,\s*(\w+)((?:\s*\[[^\]]*\])+)\s*\)", text):
+            if mt.group(1) in vec_vars:
+                bad.append(f"{os.path.basename(path)}: {mt.group(0)}")
+    assert not bad, bad

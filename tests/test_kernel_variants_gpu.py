@@ -127,3 +127,41 @@ def test_eight_wave_backward_three_groups_lora(plan, device, monkeypatch):
         items.append(it)
     dx = linear_backward(items, m, k, dx_fp32=True, lora_rank=16)
     assert_close(dx, ref, max_rel=1e-4, mean_rel=1e-5, what=f"bwd8 three groups {plan}")
+
+
+@pytest.mark.parametrize("m", [1, 2])
+@pytest.mark.parametrize("nested,blocksize", CASES)
+def test_gemv_small_m(m, nested, blocksize, device, raw_statistics):
+    """The GEMV kernel (forward launches of at most 2 token rows without LoRA terms): three
+    weights in one launch (q/k/v-like, with bias), statistics read raw, k = 1056 (a row of 33
+    16-byte chunks: lane 0 takes two)."""
+    from decik_amd.nf4 import launch_plan, linear_forward
+
+    assert launch_plan(False, m, 1056, [320, 64, 64])["kernel"] == "nf4_gemv_kernel"
+    items, refs = [], []
+    x = randn16((m, 1056), seed=120 + m, device=device)
+    for i, n in enumerate((320, 64, 64)):
+        packed, qs, w16 = make_weight((n, 1056), seed=121 + i + blocksize, device=device, nested=nested,
+                                      blocksize=blocksize)
+        b = randn16((n,), seed=125 + i, device=device, std=0.1)
+        items.append(dict(packed=packed, qs=qs, bias=b))
+        refs.append(O.linear_ref(x.cpu().numpy(), w16, b.cpu().numpy()))
+    ys = linear_forward(x, items)
+    for y, ref in zip(ys, refs):
+        assert_close(y, ref, what=f"gemv m={m} nested={nested} bs={blocksize}")
+
+
+def test_gemv_not_used_with_lora_or_forced_plan(device, monkeypatch):
+    """LoRA terms or a forced plan keep small launches on the MFMA kernels (same results)."""
+    from decik_amd.nf4 import launch_plan, linear_forward
+
+    assert launch_plan(False, 2, 512, [256], lora=True)["kernel"] != "nf4_gemv_kernel"
+    packed, qs, w16 = make_weight((256, 512), seed=130, device=device)
+    x = randn16((2, 512), seed=131, device=device)
+    (y0,) = linear_forward(x, [dict(packed=packed, qs=qs)])
+    monkeypatch.setenv("DECIK_FWD_PLAN", "1,2,4")
+    assert launch_plan(False, 2, 512, [256])["kernel"] == "nf4_fwd_kernel"
+    (y1,) = linear_forward(x, [dict(packed=packed, qs=qs)])
+    ref = O.linear_ref(x.cpu().numpy(), w16)
+    assert_close(y0, ref, what="gemv")
+    assert_close(y1, ref, what="mfma at m=2")
