@@ -206,6 +206,7 @@ constexpr VariantCost kFwdVariants[] = {{1, 4, kFwdBN, 3, 2.35, 0.65},
                                        {2, 4, kFwdBN, 2, 2.23, 0.65},
                                        {4, 4, kFwdBN, 2, 3.10, 0.65},
                                        {8, 4, kFwdBN, 1, 2.94, 0.85},
+                                       {7, 8, kFwdBN, 1, 2.00, 0.90},
                                        {8, 8, kFwdBN, 1, 2.25, 0.90},
                                        {9, 8, kFwdBN, 1, 2.45, 0.90}};
 constexpr int kNumFwdVariants = sizeof(kFwdVariants) / sizeof(kFwdVariants[0]);

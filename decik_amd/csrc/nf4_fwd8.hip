@@ -6,7 +6,7 @@
 // tokens, and the dequant (code-book address, code-book read, fp32 multiply, fp16 pack per
 // weight) is ~6 VALU instructions per 32x32x16 MFMA -- more than the SIMD co-issues with the
 // matrix pipe (~4). Here a work-group is 8 waves (two per SIMD, one work-group per CU) on a tile
-// of 32*MB tokens (MB = 8 or 9: 256 or 288 tokens) x 256 weight rows; each wave owns 32 weight
+// of 32*MB tokens (MB = 7, 8 or 9: 224, 256 or 288 tokens) x 256 weight rows; each wave owns 32 weight
 // rows and all 32*MB tokens, so each dequantized weight feeds MB MFMAs (~3 VALU per MFMA), and
 // the X tile, staged once per step for all eight waves, is read by each wave at one 16-byte
 // fragment per MFMA.
@@ -402,7 +402,7 @@ static hipError_t launch_fwd8_t(const FwdArgs& a, int grid, hipStream_t s) {
 hipError_t launch_fwd8(const FwdArgs& a, int mb, int grid, hipStream_t s) {
 #define X(T) \
     if (mb == T) return a.nested ? launch_fwd8_t<T, true>(a, grid, s) : launch_fwd8_t<T, false>(a, grid, s);
-    X(8) X(9)
+    X(7) X(8) X(9)
 #undef X
     return hipErrorInvalidValue;
 }

@@ -21,7 +21,7 @@ def raw_statistics(monkeypatch):
     monkeypatch.setattr(nf4, "_scales", lambda packed, qs, device: None)
 
 
-@pytest.mark.parametrize("plan", ["4,1,4", "2,3,4", "8,1,8", "9,2,8"])
+@pytest.mark.parametrize("plan", ["4,1,4", "2,3,4", "7,2,8", "8,1,8", "9,2,8"])
 @pytest.mark.parametrize("nested,blocksize", CASES)
 def test_forward_variants(nested, blocksize, plan, device, monkeypatch, raw_statistics):
     from decik_amd.nf4 import linear_forward
