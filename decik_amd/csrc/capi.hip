@@ -216,6 +216,7 @@ constexpr VariantCost kBwdVariants[] = {{2, 4, 256, 2, 2.55, 0.90},
                                        {2, 8, 512, 1, 2.60, 1.0},
                                        {4, 8, 512, 1, 3.40, 1.0},
                                        {4, 8, 256, 1, 1.75, 0.90},
+                                       {7, 8, 256, 1, 2.10, 0.90},
                                        {8, 8, 256, 1, 2.25, 0.90},
                                        {9, 8, 256, 1, 2.85, 0.85}};
 constexpr int kNumBwdVariants = sizeof(kBwdVariants) / sizeof(kBwdVariants[0]);

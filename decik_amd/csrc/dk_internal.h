@@ -139,7 +139,7 @@ hipError_t launch_gemv(const FwdArgs& a, hipStream_t s);
 // 8-wave forward kernel (32 weight rows x 32*mb tokens per wave), mb = 8 or 9
 hipError_t launch_fwd8(const FwdArgs& a, int mb, int grid, hipStream_t s);
 hipError_t launch_bwd(const BwdArgs& a, int mb, int waves, int grid, hipStream_t s);
-// 8-wave input-gradient kernel (32 output columns x 32*mb tokens per wave), mb = 4, 8 or 9; the
+// 8-wave input-gradient kernel (32 output columns x 32*mb tokens per wave), mb = 4, 7, 8 or 9; the
 // SwiGLU epilogue with mb = 4 only
 hipError_t launch_bwd8(const BwdArgs& a, int mb, int grid, hipStream_t s);
 hipError_t launch_splitk_reduce(const ReduceArgs& a, hipStream_t s);

@@ -67,7 +67,7 @@ def test_grouped_backward_partial_steps(plan, device, monkeypatch, raw_statistic
     assert_close(dx, ref, max_rel=1e-4, mean_rel=1e-5, what=f"grouped bwd {plan}")
 
 
-@pytest.mark.parametrize("plan", ["4,1,8,256", "8,2,8", "9,1,8"])
+@pytest.mark.parametrize("plan", ["4,1,8,256", "7,3,8", "8,2,8", "9,1,8"])
 @pytest.mark.parametrize("nested,blocksize", CASES)
 @pytest.mark.parametrize("dx_fp32", [False, True])
 def test_eight_wave_backward_edges(nested, blocksize, plan, dx_fp32, device, monkeypatch, raw_statistics):
