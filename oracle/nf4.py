@@ -29,7 +29,10 @@ What each function restates, and what pins it (the tests live in tests/test_orac
 - `linear_ref`, `lora_*_ref`, `swiglu_*_ref`, `mlp_ref`: float64 accumulation of the exact fp16
   operands, rounded where the reference rounds (solution/nf4.py:93-104, solution/mlp.py:62-110,
   solution/swiglu.py:15-37, solution/attn.py:206-273). Pinned by closed forms in the tests
-  (identity and permutation weights, rank-one inputs, sigmoid identities).
+  (identity and permutation weights, rank-one inputs, sigmoid identities) and, for every
+  backward (swiglu_bwd_ref, lora_bwd_ref's gu/dA/dB/dX, mlp_ref's dx), by torch's float64
+  autograd of the forward formulas, with planted mistakes (a dropped factor, a wrong scale, a
+  swapped operand) shown to fail those checks.
 """
 
 import ctypes
@@ -246,15 +249,37 @@ def lora_fwd_ref(x16, a16, b16, scaling):
     return u16, out.astype(np.float32)
 
 
-def lora_bwd_ref(dy16, x16, u16, a16, b16, scaling):
-    """The products autograd forms for out = (u . B^T) * s, u = x . A^T (solution/attn.py:251-257):
-    g = dY*s; dB = g^T u; gu = g . B; dA = gu^T x; dX_lora = gu . A. fp32 results; gu rounded
-    to fp16 as the reference's fp16 matmul leaves it."""
-    g = _f64(dy16) * float(scaling)
-    db = g.T @ _f64(u16)
-    gu16 = (g @ _f64(b16)).astype(np.float32).astype(np.float16)
-    da = _f64(gu16).T @ _f64(x16)
-    dx = _f64(gu16) @ _f64(a16)
+def _f16(a):
+    """Round to fp16 (through fp32, as a torch fp16 matmul stores its fp32 accumulator)."""
+    return np.asarray(a).astype(np.float32).astype(np.float16)
+
+
+def lora_bwd_ref(dy16, x16, u16, a16, b16, scaling, exact=False):
+    """The products LoRAPairFromNorm.backward forms for out = (u . B^T) * s, u = x . A^T
+    (solution/attn.py:251-257), with the reference's fp16 tensors rounded where it rounds them:
+      g = fp16(dY * s)                  (:252, fp16 tensor times a Python float)
+      dB = fp32(fp16(g^T . u))          (:254, fp16 mm, then .to(float32) at :256)
+      gu = fp16(g . B16)                (:255)
+      dA = fp32(fp16(gu^T . x16))       (:256)
+      dX_lora = fp16(gu . A16)          (:257, before the dropout-mask step)
+    Returns (gu16, dA, dB, dX_lora) as (fp16, fp32, fp32, fp32).
+
+    exact=True: the same chain without the roundings of g, dA, dB and dX_lora (gu stays fp16: it
+    is an fp16 operand of the next product in both implementations) -- what the fused kernels
+    compute (fp32 accumulators stored once); the reference's roundings are within the bar of it."""
+    s = float(scaling)
+    if exact:
+        g = _f64(dy16) * s
+        gu16 = _f16(g @ _f64(b16))
+        db = g.T @ _f64(u16)
+        da = _f64(gu16).T @ _f64(x16)
+        dx = _f64(gu16) @ _f64(a16)
+        return gu16, da.astype(np.float32), db.astype(np.float32), dx.astype(np.float32)
+    g16 = _f16(_f64(dy16).astype(np.float32) * np.float32(s))
+    gu16 = _f16(_f64(g16) @ _f64(b16))
+    db = _f16(_f64(g16).T @ _f64(u16))
+    da = _f16(_f64(gu16).T @ _f64(x16))
+    dx = _f16(_f64(gu16) @ _f64(a16))
     return gu16, da.astype(np.float32), db.astype(np.float32), dx.astype(np.float32)
 
 
@@ -352,8 +377,15 @@ def swiglu_bwd_ref(grad16, gate16, up16):
 
 def mlp_ref(x16, wg16, wu16, wd16, dy16):
     """Qwen2 MLP forward and input gradient as RecomputedMLP computes it (solution/mlp.py:62-110):
-    gate, up, h, out rounded to fp16 where the fp16 matmuls round; dX = fp32(dgate.Wg) +
-    fp32(dup.Wu). Returns dict of fp32 arrays (gate, up, h, out, gh, dgate, dup, dx)."""
+    gate, up, h rounded to fp16 where the fp16 matmuls and the SwiGLU kernel round (:69-71);
+    out = the fp32-accumulated down projection (:73; the reference stores it as fp16);
+    gh = fp16(dY . Wd) (:95); dgate / dup from the SwiGLU backward, fp16 (:104); and
+    dx = fp32(fp16(dgate . Wg)) + fp32(fp16(dup . Wu)) -- two fp16 matmul results, each cast to
+    fp32, then summed (:106-109).
+    dx_exact = fp32(dgate . Wg + dup . Wu) with no rounding of the two products: the fused kernel
+    accumulates both in one fp32 tile and rounds once, so this measures its own accuracy; dx (the
+    reference's two roundings) lies within the bar of it.
+    Returns a dict of fp32 arrays (gate, up, h, out, gh, dgate, dup, dx, dx_exact)."""
     gate = linear_ref(x16, wg16).astype(np.float16)
     up = linear_ref(x16, wu16).astype(np.float16)
     h = swiglu_fwd_ref(gate, up).astype(np.float16)
@@ -361,10 +393,13 @@ def mlp_ref(x16, wg16, wu16, wd16, dy16):
     gh = linear_dx_ref(dy16, wd16).astype(np.float16)
     dgate, dup = swiglu_bwd_ref(gh, gate, up)
     dgate16, dup16 = dgate.astype(np.float16), dup.astype(np.float16)
-    dx = (_f64(dgate16) @ _f64(wg16) + _f64(dup16) @ _f64(wu16)).astype(np.float32)
+    pg = _f64(dgate16) @ _f64(wg16)
+    pu = _f64(dup16) @ _f64(wu16)
+    dx = (_f64(_f16(pg)) + _f64(_f16(pu))).astype(np.float32)
+    dx_exact = (pg + pu).astype(np.float32)
     return dict(gate=gate.astype(np.float32), up=up.astype(np.float32),
                 h=h.astype(np.float32), out=out, gh=gh.astype(np.float32),
-                dgate=dgate, dup=dup, dx=dx)
+                dgate=dgate, dup=dup, dx=dx, dx_exact=dx_exact)
 
 
 def tolerance(y, ref):

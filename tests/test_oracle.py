@@ -268,11 +268,20 @@ def test_lora_refs_closed_forms():
     assert np.array_equal(out[:, :r], 2.0 * x[:, :r].astype(np.float32))
     assert np.all(out[:, r:] == 0)
     dy = rng.standard_normal((3, n)).astype(np.float16)
-    gu, da, db, dx = O.lora_bwd_ref(dy, x, u, a, b, 2.0)
+    gu, da, db, dx = O.lora_bwd_ref(dy, x, u, a, b, 2.0, exact=True)
     g = 2.0 * dy.astype(np.float64)
     assert np.allclose(db, g.T @ u.astype(np.float64))
+    # B = [I; 0]: gu = g[:, :r] (exact: a power-of-two scale of fp16 values)
     assert np.array_equal(gu.astype(np.float32), (g[:, :r]).astype(np.float16).astype(np.float32))
-    assert np.all(dx[:, r:] == 0)
+    # A = [I | 0]: dA = gu^T x in its first r columns is gu^T x[:, :r]; dX_lora = [gu | 0]
+    gu64 = gu.astype(np.float64)
+    assert np.allclose(da, gu64.T @ x.astype(np.float64), rtol=1e-6, atol=0)
+    assert np.array_equal(dx[:, :r], gu.astype(np.float32)) and np.all(dx[:, r:] == 0)
+    # the reference's roundings (fp16 dA, dB, dX_lora) of the same products
+    gu_r, da_r, db_r, dx_r = O.lora_bwd_ref(dy, x, u, a, b, 2.0)
+    assert np.array_equal(gu_r, gu)
+    assert np.array_equal(da_r, (gu64.T @ x.astype(np.float64)).astype(np.float32).astype(np.float16).astype(np.float32))
+    assert np.array_equal(dx_r, dx) and np.array_equal(db_r, db.astype(np.float16).astype(np.float32))
 
 
 def test_tolerance_metric():
@@ -338,3 +347,161 @@ def test_rope_refs_closed_forms_and_transpose():
     lhs = float((rx.astype(np.float64) * gi.astype(np.float64)).sum())
     rhs = float((xi.astype(np.float64) * rtg.astype(np.float64)).sum())
     assert lhs == rhs
+
+
+# ---- float64 autograd pins of the backward references ---------------------------------------
+# torch's autograd differentiates the forward formulas mechanically (product rule, sigmoid',
+# matmul transposes), so a dropped term, a wrong scale or a transposed operand in the oracle's
+# hand-written backward shows up as a mismatch. The oracle's own fp16 roundings (where the
+# reference rounds) keep it within a few 1e-4 of the unrounded float64 chain; the checks below
+# allow 2e-3, while the planted mistakes of test_pins_catch_planted_mistakes move them by 0.1 or
+# more.
+
+def _t(a, grad=False):
+    import torch
+
+    return torch.tensor(np.asarray(a).astype(np.float64), requires_grad=grad)
+
+
+def _check_swiglu_bwd(fn):
+    """swiglu_bwd_ref(G, g, u) against autograd of g * sigmoid(g) * u (solution/swiglu.py:15-37),
+    over g in [-8, 8] (every sigmoid regime, not only where 1 + g (1 - s) is 1)."""
+    import torch
+
+    rng = np.random.default_rng(8)
+    g = rng.uniform(-8, 8, 4096).astype(np.float16)
+    u = rng.standard_normal(4096).astype(np.float16)
+    G = rng.standard_normal(4096).astype(np.float16)
+    gt, ut = _t(g, True), _t(u, True)
+    dgate, dup = torch.autograd.grad(gt * torch.sigmoid(gt) * ut, (gt, ut), _t(G))
+    og, ou = fn(G, g, u)
+    np.testing.assert_allclose(og, dgate.numpy(), rtol=1e-6, atol=1e-9)
+    np.testing.assert_allclose(ou, dup.numpy(), rtol=1e-6, atol=1e-9)
+
+
+def _lora_case(seed=31, m=64, k=256, n=192, r=16):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    a = ((rng.random((r, k)) * 2 - 1) / np.sqrt(k)).astype(np.float16)
+    b = (rng.standard_normal((n, r)) * 0.05).astype(np.float16)
+    dy = rng.standard_normal((m, n)).astype(np.float16)
+    return x, a, b, dy
+
+
+def _check_lora_bwd(fn, scaling):
+    """lora_bwd_ref against autograd: out = (U . B^T) s with U the forward's fp16 u gives dU and
+    dB; U = x . A^T, back-propagated from fp16(dU) (the reference's fp16 grad_u,
+    solution/attn.py:255), gives dA and dX_lora. Both roundings of the oracle (reference) and its
+    exact variant are checked: every output of both, each against its own bar."""
+    import torch
+
+    x, a, b, dy = _lora_case()
+    u16, _ = O.lora_fwd_ref(x, a, b, scaling)
+    U, B = _t(u16, True), _t(b, True)
+    dU, dB = torch.autograd.grad((U @ B.T) * scaling, (U, B), _t(dy))
+    gu = dU.numpy().astype(np.float32).astype(np.float16)
+    X, A = _t(x, True), _t(a, True)
+    dX, dA = torch.autograd.grad(X @ A.T, (X, A), _t(gu))
+    for exact, bar in ((False, 2e-3), (True, 1e-6)):
+        gu16, da, db, dxl = fn(dy, x, u16, a, b, scaling, exact=exact)
+        for name, got, want in (("gu", gu16, dU.numpy()), ("dA", da, dA.numpy()), ("dB", db, dB.numpy()),
+                                ("dX", dxl, dX.numpy())):
+            mx, mean = O.tolerance(got, want)
+            lim = 2e-3 if name == "gu" else bar  # gu is fp16 in both variants
+            assert mx <= lim and mean <= lim, f"{name} exact={exact}: {mx:.2e} {mean:.2e}"
+
+
+def _check_mlp(fn):
+    """mlp_ref's out and dx against autograd of down(silu(gate(x)) * up(x)) in float64."""
+    import torch
+
+    rng = np.random.default_rng(31)
+    m, k, n = 64, 128, 256
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    wg, wu = ((rng.standard_normal((n, k)) * 0.1).astype(np.float16) for _ in range(2))
+    wd = (rng.standard_normal((k, n)) * 0.1).astype(np.float16)
+    dy = rng.standard_normal((m, k)).astype(np.float16)
+    ref = fn(x, wg, wu, wd, dy)
+    X = _t(x, True)
+    gate, up = X @ _t(wg).T, X @ _t(wu).T
+    out = (gate * torch.sigmoid(gate) * up) @ _t(wd).T
+    (dx,) = torch.autograd.grad(out, (X,), _t(dy))
+    for name, got, want in (("out", ref["out"], out.detach().numpy()), ("dx", ref["dx"], dx.numpy()),
+                            ("dx_exact", ref["dx_exact"], dx.numpy())):
+        mx, mean = O.tolerance(got, want)
+        assert mx <= 2e-3 and mean <= 2e-3, f"{name}: {mx:.2e} {mean:.2e}"
+
+
+def test_swiglu_bwd_ref_matches_autograd():
+    _check_swiglu_bwd(O.swiglu_bwd_ref)
+
+
+def test_swiglu_fwd_ref_matches_torch():
+    import torch
+
+    rng = np.random.default_rng(9)
+    g = rng.uniform(-8, 8, 4096).astype(np.float16)
+    u = rng.standard_normal(4096).astype(np.float16)
+    want = (torch.nn.functional.silu(_t(g)) * _t(u)).numpy()
+    np.testing.assert_allclose(O.swiglu_fwd_ref(g, u), want, rtol=1e-6, atol=1e-9)
+
+
+@pytest.mark.parametrize("scaling", [2.0, 0.75])
+def test_lora_bwd_ref_matches_autograd(scaling):
+    _check_lora_bwd(O.lora_bwd_ref, scaling)
+
+
+def test_lora_fwd_ref_matches_torch_fp16_matmul():
+    """u = fp16(x . A^T) and out = fp16(u . B^T) * s, as torch's fp16 linear (fp32 accumulate,
+    one rounding) computes them; the oracle's out stays fp32 before the scale's rounding."""
+    import torch
+
+    x, a, b, _ = _lora_case(seed=5)
+    u16, out = O.lora_fwd_ref(x, a, b, 2.0)
+    tu = (_t(x) @ _t(a).T).float().half()
+    assert np.array_equal(u16.view(np.uint16), tu.numpy().view(np.uint16))
+    tout = (tu.double() @ _t(b).T) * 2.0
+    mx, mean = O.tolerance(out, tout.numpy())
+    assert mx <= 1e-6 and mean <= 1e-6
+
+
+def test_mlp_ref_matches_autograd():
+    _check_mlp(O.mlp_ref)
+
+
+def test_pins_catch_planted_mistakes(monkeypatch):
+    """The checks above fail on plausible mistakes planted in the oracle (on the CPU): dgate
+    without its (1 + g (1 - s)) factor, dup with u for g, dA doubled, dX_lora tripled, dB from the
+    unscaled gradient, and the MLP built on the broken SwiGLU backward."""
+    def dgate_no_factor(G, g, u):
+        G, g, u = O._f64(G), O._f64(g), O._f64(u)
+        s = 1.0 / (1.0 + np.exp(-g))
+        return (G * u * s).astype(np.float32), (G * g * s).astype(np.float32)
+
+    def dup_swapped(G, g, u):
+        dg, _ = O.swiglu_bwd_ref(G, g, u)
+        G, g, u = O._f64(G), O._f64(g), O._f64(u)
+        return dg, (G * u / (1.0 + np.exp(-g))).astype(np.float32)
+
+    good_lora = O.lora_bwd_ref
+
+    def scaled(i, f):
+        def fn(*args, **kw):
+            out = list(good_lora(*args, **kw))
+            out[i] = (out[i] * f).astype(out[i].dtype)
+            return tuple(out)
+        return fn
+
+    def db_unscaled(dy, x, u, a, b, s, exact=False):
+        gu, da, db, dx = good_lora(dy, x, u, a, b, s, exact=exact)
+        return gu, da, (db / np.float32(s)).astype(np.float32), dx
+
+    for bad in (dgate_no_factor, dup_swapped):
+        with pytest.raises(AssertionError):
+            _check_swiglu_bwd(bad)
+    for bad in (scaled(1, 2.0), scaled(3, 3.0), db_unscaled):
+        with pytest.raises(AssertionError):
+            _check_lora_bwd(bad, 2.0)
+    monkeypatch.setattr(O, "swiglu_bwd_ref", dgate_no_factor)
+    with pytest.raises(AssertionError):
+        _check_mlp(O.mlp_ref)
