@@ -1,10 +1,9 @@
 """The NF4-path pieces of the reference's attention module (solution/attn.py) under its names:
 RoPE of q/k (FusedQKRope, solution/attn.py:89-126) and the LoRA dropout helpers (pack_keep,
-_lora_inputs, solution/attn.py:183-203), backed by this package's HIP kernels. LoRAPairFromNorm
-itself also rebuilds its input from the RMSNorm (out of this package's scope); LoRAPair in
-decik_amd.lora is the same branch computation with the input passed in."""
+_lora_inputs, solution/attn.py:183-203) and LoRAPairFromNorm (solution/attn.py:206-273, same
+`apply` signature), backed by this package's HIP kernels."""
 
-from .lora import LoRAPair, lora_input_grad, lora_inputs, pack_keep  # noqa: F401
+from .lora import LoRAPair, LoRAPairFromNorm, lora_input_grad, lora_inputs, pack_keep  # noqa: F401
 from .rope import FusedQKRope, rope_qk_backward, rope_qk_forward  # noqa: F401
 
 

@@ -432,6 +432,9 @@ static int linear_fwd_impl(const std::string& name, const uint16_t* x, int64_t m
         if (G.w.k != k) return fail(name + ": weight k differs from x");
         if (gemm_weight_ok(G.w, name.c_str())) return 1;
         if (!aligned(G.w.packed, 16)) return fail(name + ": packed weights must be 16-byte aligned");
+        // every epilogue (direct stores, split-K partial slabs and their reduction, the GLU
+        // tile) moves whole 8-column chunks: a chunk must lie wholly inside a group's rows
+        if ((G.w.n % 8) != 0) return fail(name + ": weight rows must be a multiple of 8");
         if (nested >= 0 && nested != G.w.nested)
             return fail(name + ": all groups must be nested or all plain");
         nested = G.w.nested;

@@ -139,6 +139,80 @@ class LoRAPair(torch.autograd.Function):
                 None, None, None, None)
 
 
+def _branch_input(x, scaled=None, mask=None, scale=None):
+    """fp16(x * dropout) of one branch on the reference's unpacked path (solution/attn.py:219-223,
+    240-243): the forward multiplies by `scaled` (the dropout output of ones, x-shaped), the
+    backward rebuilds it from the mask and its kept value; no dropout: fp16(x)."""
+    width = x.shape[-1]
+    if scaled is not None:
+        return (x * scaled).to(torch.float16).reshape(-1, width).contiguous()
+    if mask is not None:
+        return (x * (mask * scale)).to(torch.float16).reshape(-1, width).contiguous()
+    return x.to(torch.float16).reshape(-1, width).contiguous()
+
+
+class LoRAPairFromNorm(torch.autograd.Function):
+    """The reference's LoRAPairFromNorm.apply(x, h, norm_weight, eps, scaled_q, mask_q, scale_q,
+    scaled_v, mask_v, scale_v, a_q, b_q, a_v, b_v, scaling_q, scaling_v, p_q, p_v, packed)
+    (solution/attn.py:206-273): peft's q and v LoRA branches, lora_B(lora_A(dropout(x))) *
+    scaling, on this package's kernels.
+
+    packed=True: mask_q / mask_v are bit-packed keep-masks (pack_keep) and scale_q / scale_v fp32
+    device scalars; the dropped-out inputs and the input gradient through both masks are the HIP
+    kernels of LoRAPair (bit-exact restatements). packed=False: the reference's elementwise
+    torch ops on the GPU (`scaled_*` in the forward, mask * scale in the backward; a branch with
+    no dropout passes None). The reference rebuilds x in backward from the RMSNorm input h
+    (bit-identically, :240); the RMSNorm kernel is outside this package, so x is saved instead and
+    h, norm_weight and eps are accepted unused. Returns (out_q, out_v) fp16; gradients flow to x
+    (fp32) and the four adapter weights (their dtype)."""
+
+    @staticmethod
+    def forward(ctx, x, h, norm_weight, eps, scaled_q, mask_q, scale_q, scaled_v, mask_v, scale_v,
+                a_q, b_q, a_v, b_v, scaling_q, scaling_v, p_q, p_v, packed):
+        if packed:
+            inputs = lora_inputs(x, mask_q, mask_v, scale_q, scale_v)
+        else:
+            inputs = (_branch_input(x, scaled_q), _branch_input(x, scaled_v))
+        outs, us = [], []
+        for x16, a, b, s in zip(inputs, (a_q, a_v), (b_q, b_v), (scaling_q, scaling_v)):
+            u = lora_down(x16, a.to(torch.float16).contiguous())
+            outs.append(lora_up(u, b.to(torch.float16).t().contiguous()) * s)
+            us.append(u)
+        ctx.save_for_backward(x, mask_q, scale_q, mask_v, scale_v, us[0], us[1], a_q, b_q, a_v, b_v)
+        ctx.scalings, ctx.ps, ctx.packed = (scaling_q, scaling_v), (p_q, p_v), packed
+        lead = x.shape[:-1]
+        return outs[0].reshape(*lead, -1), outs[1].reshape(*lead, -1)
+
+    @staticmethod
+    def backward(ctx, grad_q, grad_v):
+        x, mask_q, scale_q, mask_v, scale_v, u_q, u_v, a_q, b_q, a_v, b_v = ctx.saved_tensors
+        width = x.shape[-1]
+        if ctx.packed:
+            inputs = lora_inputs(x, mask_q, mask_v, scale_q, scale_v)
+        else:
+            inputs = (_branch_input(x, None, mask_q, scale_q), _branch_input(x, None, mask_v, scale_v))
+        grads, input_grads = [], []
+        branches = ((grad_q, u_q, a_q, b_q, ctx.scalings[0]), (grad_v, u_v, a_v, b_v, ctx.scalings[1]))
+        for (grad, u, a, b, s), x16 in zip(branches, inputs):
+            if grad is None:
+                grad = torch.zeros(u.shape[:-1] + (b.shape[0],), dtype=torch.float16, device=u.device)
+            g16 = grad.to(torch.float16).reshape(-1, grad.shape[-1]).contiguous()
+            gu, da, db = lora_grads(g16, u, x16, b.to(torch.float16).contiguous(), s)
+            grads += [da.to(a.dtype), db.to(b.dtype)]
+            input_grads.append(lora_up(gu, a.to(torch.float16).contiguous()))
+        if ctx.packed:
+            grad_x = lora_input_grad(input_grads[0], input_grads[1], mask_q, mask_v,
+                                     1.0 / (1.0 - ctx.ps[0]), 1.0 / (1.0 - ctx.ps[1]))
+        else:
+            grad_x = None
+            for gx16, m, p in zip(input_grads, (mask_q, mask_v), ctx.ps):
+                gx = gx16.to(torch.float32)
+                if m is not None:
+                    gx = gx * m.reshape(-1, width) * (1.0 / (1.0 - p))
+                grad_x = gx if grad_x is None else grad_x + gx
+        return ((grad_x.view(x.shape),) + (None,) * 9 + tuple(grads) + (None,) * 5)
+
+
 class NF4LoRALinear(torch.autograd.Function):
     """Y = x16 . dequant(W)^T + bias + scaling * fp16(x16 . A^T) . B^T in one fused launch.
 
@@ -188,6 +262,10 @@ class QKVProjection(torch.autograd.Function):
     def forward(ctx, x16, projections, *adapters):
         x2 = x16.reshape(-1, x16.shape[-1]).contiguous()
         items, saved, rank = [], [], 0
+        ranks = {int(p["lora_a"].shape[0]) for p in projections if p.get("lora_a") is not None}
+        if len(ranks) > 1:
+            # one launch runs one rank (its LoRA slices and the U / B row strides)
+            raise ValueError(f"QKVProjection: LoRA ranks differ within one launch: {sorted(ranks)}")
         for p in projections:
             it = dict(packed=p["packed"], qs=p["qs"], bias=p.get("bias"))
             if p.get("lora_a") is not None:
@@ -226,7 +304,29 @@ class QKVProjection(torch.autograd.Function):
         return (grad_x, None, *adapter_grads)
 
 
+FUSED_RANKS = (16, 32)  # LoRA ranks the GEMM kernels' rank-16 MFMA slices take
+
+
+def _project_one(x16, p):
+    """One projection on its own: NF4Linear, NF4LoRALinear, or (a rank the kernels do not take)
+    NF4Linear plus peft's fp16 LoRA products, summed in fp32 as the base sums them."""
+    if p.get("lora_a") is None:
+        return _nf4.NF4Linear.apply(x16, p["packed"], p.get("bias"), p["qs"])
+    if int(p["lora_a"].shape[0]) in FUSED_RANKS:
+        return NF4LoRALinear.apply(x16, p["packed"], p.get("bias"), p["qs"], p["lora_a"], p["lora_b"],
+                                   p["scaling"])
+    base = _nf4.NF4Linear.apply(x16, p["packed"], p.get("bias"), p["qs"])
+    u = torch.nn.functional.linear(x16, p["lora_a"].to(torch.float16))
+    lora = torch.nn.functional.linear(u, p["lora_b"].to(torch.float16)) * p["scaling"]
+    return (base.float() + lora.float()).to(torch.float16)
+
+
 def qkv_projection(x16, projections):
+    """q, k, v (+ LoRA) of x16 in one fused launch each way when every LoRA term has one rank the
+    kernels take (16 or 32); otherwise each projection runs on its own."""
+    ranks = {int(p["lora_a"].shape[0]) for p in projections if p.get("lora_a") is not None}
+    if len(ranks) > 1 or not ranks <= set(FUSED_RANKS):
+        return tuple(_project_one(x16, p) for p in projections)
     adapters = []
     for p in projections:
         if p.get("lora_a") is not None:

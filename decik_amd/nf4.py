@@ -22,7 +22,7 @@ import torch
 
 from . import _lib, warmup
 from ._lib import LinearBwdGroup, LinearFwdGroup, check, lib, ptr, stream_of, weight_desc
-from ._state import on_gpu
+from . import _state
 
 # Work shape of the dequantization kernel: packed bytes per work-group (256 threads x 16 bytes)
 # and waves (wavefronts of 64) per work-group.
@@ -304,37 +304,73 @@ class NF4Linear(torch.autograd.Function):
         return grad_x, None, None, None
 
 
+# ---- bitsandbytes' Linear4bit.forward, patched (solution/nf4.py:107-138) ------------------------
+# The fast path's conditions are the reference's (solution/nf4.py:125-131), one predicate each;
+# when any fails the original forward runs unchanged.
+
+def _gpu_input(x):
+    return isinstance(x, torch.Tensor) and _state.on_gpu(x) and x.numel() > 0
+
+
+def _frozen_nf4_bytes(weight):
+    return (weight is not None and _state.on_gpu(weight) and weight.dtype == torch.uint8
+            and not weight.requires_grad)
+
+
+def _fp16_compute(module):
+    return getattr(module, "compute_dtype", None) == torch.float16
+
+
+def _frozen_or_absent(bias):
+    return bias is None or not bias.requires_grad
+
+
+def _takes_fast_path(module, x):
+    weight = getattr(module, "weight", None)
+    return (_gpu_input(x) and _frozen_nf4_bytes(weight) and _fp16_compute(module)
+            and _frozen_or_absent(module.bias)
+            and supported(getattr(weight, "quant_state", None), x.shape[-1]))
+
+
+def _quant_state_repair():
+    """bitsandbytes' helper that restores a Params4bit's lost quant_state from its module (the
+    reference calls it first, solution/nf4.py:115-122); None on versions without it."""
+    import importlib
+
+    try:
+        modules = importlib.import_module("bitsandbytes.nn.modules")
+    except ImportError:
+        return None
+    return getattr(modules, "fix_4bit_weight_quant_state_from_module", None)
+
+
+def _fast_forward(module, x):
+    """NF4Linear on the fp16 input bitsandbytes itself would make, with an fp16 bias; the output
+    comes back in x's dtype as bitsandbytes returns it (solution/nf4.py:132-135)."""
+    bias = module.bias
+    out = NF4Linear.apply(x.to(torch.float16), module.weight.data,
+                          None if bias is None else bias.to(torch.float16), module.weight.quant_state)
+    return out.to(x.dtype)
+
+
 def patch():
-    """Send bitsandbytes' Linear4bit.forward through NF4Linear (solution/nf4.py:107-138): same
-    gate, same fallback to the original for anything else."""
+    """Route bitsandbytes' Linear4bit.forward through NF4Linear where the reference does
+    (solution/nf4.py:107-138). Idempotent: the installed forward carries `_skc`."""
     import bitsandbytes as bnb
 
     cls = bnb.nn.Linear4bit
     if getattr(cls.forward, "_skc", False):
         return
-    original = cls.forward
-    try:
-        from bitsandbytes.nn.modules import fix_4bit_weight_quant_state_from_module as fix_state
-    except ImportError:  # pragma: no cover - older bitsandbytes
-        fix_state = None
+    bnb_forward = cls.forward
+    repair = _quant_state_repair()
 
     def forward(self, x):
         weight = getattr(self, "weight", None)
-        if fix_state is not None and weight is not None and getattr(weight, "quant_state", None) is None:
-            fix_state(self)
-        qs = getattr(weight, "quant_state", None)
-        bias = self.bias
-        if not (isinstance(x, torch.Tensor) and on_gpu(x) and x.numel() > 0
-                and weight is not None and on_gpu(weight) and weight.dtype == torch.uint8
-                and not weight.requires_grad
-                and getattr(self, "compute_dtype", None) == torch.float16
-                and (bias is None or not bias.requires_grad)
-                and supported(qs, x.shape[-1])):
-            return original(self, x)
-        inp_dtype = x.dtype
-        bias16 = None if bias is None else bias.to(torch.float16)
-        out = NF4Linear.apply(x.to(torch.float16), weight.data, bias16, qs)
-        return out.to(inp_dtype)
+        if repair is not None and weight is not None and getattr(weight, "quant_state", None) is None:
+            repair(self)
+        if _takes_fast_path(self, x):
+            return _fast_forward(self, x)
+        return bnb_forward(self, x)
 
     forward._skc = True
     cls.forward = forward

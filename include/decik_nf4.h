@@ -115,7 +115,10 @@ int dk_nf4_block_scales(const dk_nf4_weight* w, float* scales, void* stream);
 int64_t dk_nf4_linear_fwd_workspace(int64_t m, int64_t k, const int64_t* ns, int ngroups);
 
 /* Fused dequant x fp16 GEMM, forward, for up to DK_MAX_GROUPS weights that share X
- * (fp16 [m, k], row stride ldx). fp32 accumulation, one fp16 rounding per output. */
+ * (fp16 [m, k], row stride ldx). fp32 accumulation, one fp16 rounding per output.
+ * Shapes: k % 32 == 0, every weight's n % 8 == 0 (outputs move in 8-column chunks), blocksize a
+ * power of two >= 32 dividing 64 * k; x, y, bias, packed 16-byte aligned, ldx / ldy % 8 == 0.
+ * Anything else returns an error (the Python layer sends such weights to dequant + F.linear). */
 int dk_nf4_linear_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
                       const dk_linear_fwd_group* groups, int ngroups, int lora_rank,
                       void* workspace, int64_t workspace_bytes, void* stream);
@@ -135,7 +138,7 @@ int64_t dk_nf4_linear_bwd_workspace(int64_t m, int64_t k, const int64_t* ns, int
 
 /* Fused dequant x fp16 GEMM, input gradient: dX = sum over groups of dY_g.W_g (+ GU_g.A_g),
  * accumulated in fp32 across all groups and rounded once. dx is fp16 (dx_fp32 = 0) or fp32
- * (dx_fp32 = 1), row stride lddx. */
+ * (dx_fp32 = 1), row stride lddx. Shapes as for dk_nf4_linear_fwd (k % 32 == 0, n % 8 == 0). */
 int dk_nf4_linear_bwd(const dk_linear_bwd_group* groups, int ngroups, int64_t m, int64_t k,
                       void* dx, int64_t lddx, int dx_fp32, int lora_rank, void* workspace,
                       int64_t workspace_bytes, void* stream);

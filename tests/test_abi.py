@@ -76,6 +76,42 @@ def test_argument_errors_are_reported():
         _lib.check(1)
 
 
+def _fake_weight(n, k):
+    """A descriptor with aligned non-null fake device pointers: only argument checks run."""
+    from decik_amd import _lib
+
+    w = _lib.NF4Weight()
+    w.packed = w.absmax = w.code = 256
+    w.n, w.k, w.blocksize, w.blocksize2, w.nested = n, k, 64, 256, 0
+    return w
+
+
+@pytest.mark.parametrize("m", [1, 830])  # the GEMV path and the (split-K) MFMA path
+def test_forward_rejects_rows_not_multiple_of_8(m):
+    """n % 8 != 0 would move 8-column output chunks across a group's end (the caller's row
+    padding, the next group's partial-slab columns, bias read past its end): every forward entry
+    rejects it before any GPU call, whatever ldy leaves room for."""
+    from decik_amd import _lib
+
+    L = _lib.lib()
+    g = (_lib.LinearFwdGroup * 2)()
+    for i in range(2):
+        g[i].w = _fake_weight(67, 1536)
+        g[i].y, g[i].ldy = 4096, 72  # padded rows: room for the chunk, still rejected
+    ws = ctypes.c_void_p(1 << 20)
+    rc = L.dk_nf4_linear_fwd(ctypes.c_void_p(16), m, 1536, 1536, g, 1, 0, ws, 1 << 40, None)
+    assert rc != 0 and b"multiple of 8" in L.dk_last_error()
+    rc = L.dk_nf4_linear_fwd(ctypes.c_void_p(16), m, 1536, 1536, g, 2, 0, ws, 1 << 40, None)
+    assert rc != 0 and b"multiple of 8" in L.dk_last_error()
+    rc = L.dk_nf4_glu_fwd(ctypes.c_void_p(16), m, 1536, 1536, g, 0, ctypes.c_void_p(8192), 72, None)
+    assert rc != 0 and b"multiple of 8" in L.dk_last_error()
+    b = (_lib.LinearBwdGroup * 1)()
+    b[0].w = _fake_weight(67, 1536)
+    b[0].dy, b[0].lddy = 4096, 72
+    rc = L.dk_nf4_linear_bwd(b, 1, m, 1536, ctypes.c_void_p(8192), 1536, 0, 0, ws, 1 << 40, None)
+    assert rc != 0 and b"multiple of 8" in L.dk_last_error()
+
+
 def test_workspace_sizes():
     from decik_amd import _lib
 

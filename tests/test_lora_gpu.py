@@ -182,3 +182,42 @@ def test_lora_pair_with_dropout(device):
     ref_dx = O.lora_input_grad_ref(gin[0], gin[1], bqn, bvn, 1.0 / (1.0 - p), 1.0 / (1.0 - p))
     assert xin.grad.dtype == torch.float32
     assert_close(xin.grad, ref_dx, what="dX through dropout")
+
+
+@pytest.mark.parametrize("ranks", [(16, 32), (16, 8)])
+def test_qkv_projection_mixed_ranks(ranks, device):
+    """LoRA ranks that differ between q and v (or one the kernels do not take) run each
+    projection on its own; outputs and gradients still match the oracle."""
+    from decik_amd.lora import qkv_projection
+
+    m, k, s = 256, 1536, 2.0
+    x = randn16((m, k), seed=90, device=device).requires_grad_(True)
+    projs, refs = [], []
+    for i, (n, r) in enumerate([(1536, ranks[0]), (256, None), (256, ranks[1])]):
+        packed, qs, w16 = make_weight((n, k), seed=91 + i, device=device)
+        p = dict(packed=packed, qs=qs, bias=None, lora_a=None, lora_b=None, scaling=s)
+        if r is not None:
+            a, b = adapters(n, k, seed=95 + i, device=device, r=r)
+            p["lora_a"], p["lora_b"] = a.float().requires_grad_(True), (b.float() * 20).requires_grad_(True)
+        projs.append(p)
+        refs.append(w16)
+    outs = qkv_projection(x, projs)
+    grads = [randn16(o.shape, seed=99 + i, device=device, std=1e-2) for i, o in enumerate(outs)]
+    torch.autograd.backward(outs, grads)
+    xn = x.detach().cpu().numpy()
+    dx_ref = np.zeros((m, k), np.float64)
+    for p, w16, o, g in zip(projs, refs, outs, grads):
+        gn = g.cpu().numpy()
+        y_ref = O.linear_ref(xn, w16)
+        dx_ref += O.linear_dx_ref(gn, w16)
+        if p["lora_a"] is not None:
+            an = p["lora_a"].detach().half().cpu().numpy()
+            bn = p["lora_b"].detach().half().cpu().numpy()
+            u16, lora = O.lora_fwd_ref(xn, an, bn, s)
+            y_ref = y_ref + lora
+            _, da, db, dxl = O.lora_bwd_ref(gn, xn, u16, an, bn, s)
+            dx_ref += dxl
+            assert_close(p["lora_a"].grad, da, what=f"dA r={an.shape[0]}")
+            assert_close(p["lora_b"].grad, db, what=f"dB r={an.shape[0]}")
+        assert_close(o, y_ref, what="Y")
+    assert_close(x.grad, dx_ref, what="dX")

@@ -1,0 +1,161 @@
+"""The patched entry points on the GPU, through a stand-in bitsandbytes package
+(tests/standin_bnb.py) and transformers' Qwen2MLP: bitsandbytes' Linear4bit.forward
+(solution/nf4.py:107-138), Qwen2MLP.forward (solution/mlp.py:113-162), the reference-named
+RecomputedMLP (solution/mlp.py:62-110) and LoRAPairFromNorm (solution/attn.py:206-273), each
+against the oracle. Bar: max|err| <= 1e-2 max|ref|, sum|err| / sum|ref| <= 1e-3."""
+
+import numpy as np
+import pytest
+import torch
+
+import standin_bnb
+from helpers import assert_close, make_weight, oracle_state, randn16
+from oracle import nf4 as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture
+def bnb(monkeypatch):
+    return standin_bnb.install(monkeypatch)
+
+
+@pytest.fixture
+def qwen_mlp_restored(monkeypatch):
+    from transformers.models.qwen2 import modeling_qwen2
+
+    monkeypatch.setattr(modeling_qwen2.Qwen2MLP, "forward", modeling_qwen2.Qwen2MLP.forward)
+    return modeling_qwen2.Qwen2MLP
+
+
+def _module(bnb, shape, seed, device, bias=False, **kw):
+    packed, qs, w16 = make_weight(shape, seed=seed, device=device)
+    b = randn16((shape[0],), seed=seed + 1000, device=device, std=0.1) if bias else None
+    return bnb.nn.Linear4bit(packed, qs, bias=b, **kw).to(device), w16
+
+
+@pytest.mark.parametrize("xdtype", [torch.float32, torch.float16])
+def test_patched_linear4bit_forward_backward(xdtype, bnb, device):
+    """q_proj-shaped Linear4bit with bias: the patched forward returns x's dtype, and values and
+    the input gradient match the oracle; bitsandbytes' own forward never runs."""
+    from decik_amd import nf4
+
+    nf4.patch()
+    layer, w16 = _module(bnb, (1536, 1536), 41, device, bias=True)
+    x = randn16((830, 1536), seed=42, device=device).to(xdtype).requires_grad_(True)
+    y = layer(x)
+    assert y.dtype == xdtype and bnb.nn.Linear4bit.original_calls == 0
+    dy = randn16((830, 1536), seed=43, device=device, std=1e-2).to(xdtype)
+    y.backward(dy)
+    xn = x.detach().half().cpu().numpy()
+    assert_close(y, O.linear_ref(xn, w16, layer.bias.detach().cpu().numpy()), what="Y")
+    assert x.grad.dtype == xdtype
+    assert_close(x.grad, O.linear_dx_ref(dy.half().cpu().numpy(), w16), what="dX")
+
+
+def test_patched_linear4bit_falls_back_on_fp32_compute(bnb, device):
+    from decik_amd import nf4
+
+    nf4.patch()
+    layer, _ = _module(bnb, (256, 1536), 44, device, compute_dtype=torch.float32)
+    out = layer(randn16((8, 1536), seed=45, device=device).float())
+    assert bnb.nn.Linear4bit.original_calls == 1 and torch.all(out == -7.0)
+
+
+@pytest.mark.parametrize("recompute", [True, False])
+def test_patched_qwen2_mlp(recompute, bnb, qwen_mlp_restored, device):
+    """transformers' Qwen2MLP with NF4 Linear4bit projections at Qwen2.5-1.5B shapes, patched:
+    fp32 input, fp16 output, fp32 input gradient, all against the oracle's RecomputedMLP."""
+    from decik_amd import mlp
+
+    mlp.patch(recompute=recompute)
+    weights = {}
+
+    def make(o, i):
+        mod, w16 = _module(bnb, (o, i), seed=o + 3 * i + len(weights), device=device)
+        weights[len(weights)] = w16
+        return mod
+
+    m = standin_bnb.qwen2_mlp(1536, 8960, make).to(device)
+    x = randn16((830, 1536), seed=46, device=device).float().requires_grad_(True)
+    out = m(x)
+    assert out.dtype == torch.float16 and bnb.nn.Linear4bit.original_calls == 0
+    dy = randn16((830, 1536), seed=47, device=device, std=1e-2)
+    out.backward(dy)
+    ref = O.mlp_ref(x.detach().half().cpu().numpy(), weights[0], weights[1], weights[2], dy.cpu().numpy())
+    assert_close(out, ref["out"], what="out")
+    assert x.grad.dtype == torch.float32
+    assert_close(x.grad, ref["dx"], what="dX")
+
+
+def test_recomputed_mlp_reference_signature_and_fallback(bnb, device):
+    """RecomputedMLP.apply(x, gate_proj, up_proj, down_proj) on modules: the fused launches for
+    Qwen shapes, and the reference's own dequantize + fp16 matmul chain (on the GPU) for a width
+    the fused kernels do not take (k = 40); both against the oracle."""
+    from decik_amd.mlp import RecomputedMLP
+
+    for hidden, inter, seed in ((1536, 8960, 50), (40, 96, 60)):
+        mods = [_module(bnb, s, seed + i, device) for i, s in
+                enumerate(((inter, hidden), (inter, hidden), (hidden, inter)))]
+        x = randn16((64, hidden), seed=seed + 5, device=device).float().requires_grad_(True)
+        out = RecomputedMLP.apply(x, mods[0][0], mods[1][0], mods[2][0])
+        dy = randn16((64, hidden), seed=seed + 6, device=device, std=1e-2)
+        out.backward(dy)
+        ref = O.mlp_ref(x.detach().half().cpu().numpy(), mods[0][1], mods[1][1], mods[2][1], dy.cpu().numpy())
+        assert_close(out, ref["out"], what=f"out hidden={hidden}")
+        assert_close(x.grad, ref["dx"], what=f"dX hidden={hidden}")
+
+
+@pytest.mark.parametrize("packed", [True, False])
+def test_lora_pair_from_norm(packed, device):
+    """LoRAPairFromNorm with the reference's 19 arguments, packed-mask and unpacked paths
+    (q with p = 0.05, v without dropout on the unpacked path): outputs, dA/dB and the fp32 input
+    gradient against the oracle's restatement of solution/attn.py:206-273."""
+    from decik_amd.attn import LoRAPairFromNorm, pack_keep
+
+    rows, width, p, s = 830, 1536, 0.05, 2.0
+    g = torch.Generator().manual_seed(71)
+    kq = (torch.rand((rows, width), generator=g) >= p).to(device)
+    kv = (torch.rand((rows, width), generator=g) >= p).to(device)
+    x = torch.randn((rows, width), generator=torch.Generator().manual_seed(72)).to(device)
+    gen = torch.Generator().manual_seed(73)
+    ad = []
+    for n in (1536, 256):
+        a = ((torch.rand((16, width), generator=gen) * 2 - 1) / np.sqrt(width)).half().float().to(device)
+        b = (torch.randn((n, 16), generator=gen) * 3e-2).half().float().to(device)
+        ad += [a.requires_grad_(True), b.requires_grad_(True)]
+    keep_val = 1.0 / (1.0 - p)
+    sc = torch.tensor(keep_val, dtype=torch.float32, device=device)
+    xin = x.clone().requires_grad_(True)
+    if packed:
+        mq, mv = pack_keep(kq, kv)
+        args = (None, mq, sc, None, mv, sc)
+        pv = p
+    else:
+        scaled_q = kq.float() * keep_val
+        args = (scaled_q, kq.float(), sc, None, None, None)
+        pv = 0.0
+    out_q, out_v = LoRAPairFromNorm.apply(xin, None, None, None, *args, *ad, s, s, p, pv, packed)
+    gq = randn16((rows, 1536), seed=74, device=device, std=1e-2)
+    gvv = randn16((rows, 256), seed=75, device=device, std=1e-2)
+    torch.autograd.backward([out_q, out_v], [gq, gvv])
+
+    xn = x.cpu().numpy()
+    ones = np.ones((rows, width), bool)
+    kqn = kq.cpu().numpy()
+    kvn = kv.cpu().numpy() if packed else ones
+    bq, bv = O.keep_pack(kqn), O.keep_pack(kvn)
+    sv = keep_val if packed else 1.0
+    xq, xv = O.lora_dropout_inputs_ref(xn, bq, bv, keep_val, sv)
+    gin = []
+    for x16, (wa, wb), out, gr in ((xq, ad[:2], out_q, gq), (xv, ad[2:], out_v, gvv)):
+        an, bn = wa.detach().half().cpu().numpy(), wb.detach().half().cpu().numpy()
+        u16, lo = O.lora_fwd_ref(x16, an, bn, s)
+        assert_close(out, lo, what="out")
+        gu16, da, db, dxl = O.lora_bwd_ref(gr.cpu().numpy(), x16, u16, an, bn, s)
+        assert_close(wa.grad, da, what="dA")
+        assert_close(wb.grad, db, what="dB")
+        gin.append(dxl.astype(np.float16))
+    ref_dx = O.lora_input_grad_ref(gin[0], gin[1], bq, bv, keep_val, sv)
+    assert xin.grad.dtype == torch.float32
+    assert_close(xin.grad, ref_dx, what="dX")
