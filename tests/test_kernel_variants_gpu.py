@@ -154,15 +154,15 @@ def test_gemv_small_m(m, nested, blocksize, device, raw_statistics):
 @pytest.mark.parametrize("m", [1, 2])
 def test_gemv_short_k_no_bias(m, device):
     """GEMV edges: k = 64 (two 16-byte chunks per row: lanes 2-63 hold no weights), two weights
-    of 72 and 8 rows, no bias. Output rows must be a multiple of 8 (ldy % 8 == 0): a 67-row weight
-    is rejected with that message before anything runs."""
+    of 72 and 8 rows, no bias. Weight rows must be a multiple of 8: a 67-row weight is rejected
+    with that message before anything runs."""
     from decik_amd import _lib
     from decik_amd.nf4 import launch_plan, linear_forward
 
     assert launch_plan(False, m, 64, [72, 8])["kernel"] == "nf4_gemv_kernel"
     x = randn16((m, 64), seed=140 + m, device=device)
     packed, qs, _ = make_weight((67, 64), seed=141, device=device)
-    with pytest.raises(_lib.DecikError, match="ldy % 8 == 0"):
+    with pytest.raises(_lib.DecikError, match="multiple of 8"):
         linear_forward(x, [dict(packed=packed, qs=qs)])
     items, refs = [], []
     for i, n in enumerate((72, 8)):
