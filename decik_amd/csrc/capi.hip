@@ -142,9 +142,11 @@ double plan_time(const VariantCost& v, int64_t m, int64_t col_tiles, int64_t nco
 }
 
 // Best (variant, splits) for a launch; col_tiles_of(v) gives the column tiles for variant v.
+// max_partial_bytes: plans whose fp32 partial slabs exceed it are not considered.
 template <typename ColTiles>
 const VariantCost* choose_plan(const VariantCost* vs, int nv, int64_t m, int64_t ncols, int steps,
-                               ColTiles col_tiles_of, int* splits, int max_splits = 32) {
+                               ColTiles col_tiles_of, int* splits, int max_splits = 32,
+                               int64_t max_partial_bytes = INT64_MAX) {
     double best = 1e300;
     const VariantCost* pick = &vs[0];
     *splits = 1;
@@ -154,6 +156,7 @@ const VariantCost* choose_plan(const VariantCost* vs, int nv, int64_t m, int64_t
         for (int s = 1; s <= (max_s > 0 ? max_s : 1); ++s) {
             const int per = steps > 0 ? (steps + s - 1) / s : 0;
             if (steps > 0 && (steps + per - 1) / per != s) continue;  // s splits must all get work
+            if (s > 1 && (double)s * m * ncols * 4.0 > (double)max_partial_bytes) continue;
             const double t = plan_time(v, m, col_tiles_of(v), ncols, steps, s);
             if (t < best * 0.999) {
                 best = t;
@@ -266,7 +269,9 @@ GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool glu
 }
 
 // swiglu: the SwiGLU epilogue of dk_nf4_linear_bwd_swiglu (never split; the variants that have it).
-GemmPlan plan_bwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool swiglu, bool no_split = false) {
+// max_partial_bytes: the split-K partial slabs must fit in that many bytes.
+GemmPlan plan_bwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool swiglu, bool no_split = false,
+                  int64_t max_partial_bytes = INT64_MAX) {
     GemmPlan p{};
     p.steps = 0;
     for (int g = 0; g < ngroups; ++g) p.steps += (int)((ns[g] + kBwdBC - 1) / kBwdBC);
@@ -274,10 +279,11 @@ GemmPlan plan_bwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool swi
     no_split = no_split || swiglu;
     const VariantCost* v = plan_override("DECIK_BWD_PLAN", kBwdVariants, nv, p.steps, &p.splits);
     if (v != nullptr && no_split) p.splits = 1;
+    if (v != nullptr && p.splits > 1 && (double)p.splits * m * k * 4.0 > (double)max_partial_bytes) v = nullptr;
     if (v == nullptr)
         v = choose_plan(kBwdVariants, nv, m, k, p.steps,
                         [k](const VariantCost& c) { return (k + c.bn - 1) / c.bn; }, &p.splits,
-                        no_split ? 1 : 32);
+                        no_split ? 1 : 32, max_partial_bytes);
     p.mt = v->rows_blocks;
     p.waves = v->waves;
     p.bwd8 = is_bwd8(*v);
@@ -576,10 +582,11 @@ struct SwigluBwdOut {
 
 // The input-gradient launch behind dk_nf4_linear_bwd and dk_nf4_linear_bwd_swiglu (sw != NULL:
 // no dX; the epilogue turns fp16(dY.W) into dgate / dup; never split).
+// max_partial_bytes: a cap on the split-K workspace the plan may use (the static-scratch entry).
 static int linear_bwd_impl(const std::string& name, const dk_linear_bwd_group* groups, int ngroups,
                            int64_t m, int64_t k, void* dx, int64_t lddx, int dx_fp32, int lora_rank,
                            void* workspace, int64_t workspace_bytes_, void* stream,
-                           const SwigluBwdOut* sw) {
+                           const SwigluBwdOut* sw, int64_t max_partial_bytes = INT64_MAX) {
     if (ngroups < 1 || ngroups > kMaxGroups || groups == nullptr)
         return fail(name + ": need 1..4 groups");
     if (m < 0 || k <= 0 || (k % 32) != 0)
@@ -622,7 +629,7 @@ static int linear_bwd_impl(const std::string& name, const dk_linear_bwd_group* g
         ns[g] = G.w.n;
     }
     if (m == 0) return 0;
-    const GemmPlan p = plan_bwd(m, k, ns, ngroups, sw != nullptr);
+    const GemmPlan p = plan_bwd(m, k, ns, ngroups, sw != nullptr, false, max_partial_bytes);
     const int64_t need = workspace_bytes(p);
     if (need > 0 && (workspace == nullptr || workspace_bytes_ < need || !aligned(workspace, 256)))
         return fail(name + ": workspace too small (need " + std::to_string(need) + " bytes)");
@@ -676,6 +683,58 @@ int dk_nf4_linear_bwd(const dk_linear_bwd_group* groups, int ngroups, int64_t m,
     g_error.clear();
     return linear_bwd_impl("dk_nf4_linear_bwd", groups, ngroups, m, k, dx, lddx, dx_fp32, lora_rank,
                            workspace, workspace_bytes_, stream, nullptr);
+}
+
+}  // extern "C"
+
+// ---- input gradient without allocation -----------------------------------------------------
+// The split-K partial slabs of dk_nf4_linear_bwd_noalloc live in this file-scope device array.
+// Every GPU the library runs on holds its own copy (kNoAllocScratchBytes) until the process
+// ends. Host code never uses the array's name as an address (on the host it is a stand-in, not a
+// device pointer): each device's copy is looked up once, with that device current, and kept.
+constexpr int64_t kNoAllocScratchBytes = DK_NOALLOC_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+static void* g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// This device's copy of `scratch` (nullptr with g_error set on failure).
+static void* device_scratch(const char* who) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        fail(std::string(who) + ": no current device");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            fail(std::string(who) + ": hipGetSymbolAddress(scratch): " + hipGetErrorString(e));
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    return g_scratch_ptr[dev];
+}
+
+extern "C" {
+
+int dk_nf4_linear_bwd_noalloc(const dk_linear_bwd_group* groups, int ngroups, int64_t m, int64_t k, void* dx,
+                              int64_t lddx, int dx_fp32, int lora_rank, void* stream) {
+    g_error.clear();
+    const char* who = "dk_nf4_linear_bwd_noalloc";
+    void* ws = device_scratch(who);
+    if (ws == nullptr) return 1;
+    // plans are capped to the scratch size (fewer splits, or none), so no shape needs more; the
+    // check below guards that contract
+    const int rc = linear_bwd_impl(who, groups, ngroups, m, k, dx, lddx, dx_fp32, lora_rank, ws,
+                                   kNoAllocScratchBytes, stream, nullptr, kNoAllocScratchBytes);
+    if (rc != 0 && g_error.find("workspace too small") != std::string::npos)
+        return fail(std::string(who) + ": split-K partials exceed the " +
+                    std::to_string(kNoAllocScratchBytes) + "-byte scratch");
+    return rc;
 }
 
 int dk_nf4_linear_bwd_swiglu(const dk_linear_bwd_group* group, int64_t m, int64_t k, int lora_rank,

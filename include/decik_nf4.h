@@ -143,6 +143,20 @@ int dk_nf4_linear_bwd(const dk_linear_bwd_group* groups, int ngroups, int64_t m,
                       void* dx, int64_t lddx, int dx_fp32, int lora_rank, void* workspace,
                       int64_t workspace_bytes, void* stream);
 
+/* No counterpart in the reference: dk_nf4_linear_bwd for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments and results as dk_nf4_linear_bwd, without the workspace: the split-K partial
+ * sums live in a static device array of DK_NOALLOC_SCRATCH_BYTES per GPU, held from the first
+ * call on that GPU until the process ends. Launch plans are capped so that their partials fit
+ * (fewer splits, or none), so every shape dk_nf4_linear_bwd takes runs here; when the allocating
+ * entry's plan fits, both run the same plan and give the same bits. Nothing carries over
+ * between calls. Calls and graph replays on one GPU share the array: calls that overlap in time
+ * on one GPU (different streams, concurrent replays) race and must be serialised by the caller.
+ * Allocates nothing (no hipMalloc, hipFree or allocating library routine). */
+#define DK_NOALLOC_SCRATCH_BYTES (64ll << 20)
+int dk_nf4_linear_bwd_noalloc(const dk_linear_bwd_group* groups, int ngroups, int64_t m, int64_t k,
+                              void* dx, int64_t lddx, int dx_fp32, int lora_rank, void* stream);
+
 /* Input gradient of one weight (the MLP's down projection, group->w [n, k]) with the SwiGLU
  * backward in its epilogue: G = fp16(dY . W) [m, k] is never stored; dgate =
  * fp16(G up s (1 + gate (1 - s))), dup = fp16(G gate s), s = sigmoid(gate) -- the same bits as
