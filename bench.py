@@ -340,6 +340,197 @@ def cpu_baseline(sample_steps=3):
                        f"{sec * 1e3:.0f} ms/step")
 
 
+# ---- config C4: the full Qwen2.5-1.5B frozen-linear stack, one training step ------------------
+
+LORA_R, LORA_ALPHA = 16, 32
+
+
+def make_stack(n_layers, device, base_seed=20_000):
+    """n_layers Qwen2.5-1.5B layers: the seven NF4 weights (seed = base + 7 * layer + projection),
+    fp16 biases on q/k/v (Qwen2), LoRA r=16 on q and v (A Kaiming-uniform, B ~ N(0, 1e-3), fp16)."""
+    import torch
+
+    from decik_amd.quant import quantize_nf4
+
+    bound = 1.0 / (HIDDEN ** 0.5)
+    layers = []
+    for layer in range(n_layers):
+        d = {}
+        for j, (name, n, k) in enumerate(QWEN15_SHAPES):
+            w = seeded_fp16((n, k), base_seed + 7 * layer + j, 0.02, device)
+            d[name] = quantize_nf4(w, blocksize=64, compress_statistics=True)
+            del w
+        for j, name in enumerate(("q", "k", "v")):
+            d[name + "_bias"] = seeded_fp16((d[name][1].shape[0],), base_seed + 1000 + 3 * layer + j, 0.1, device)
+        g = torch.Generator(device="cpu").manual_seed(base_seed + 5000 + layer)
+        for name, n in (("q", 1536), ("v", 256)):
+            a = ((torch.rand((LORA_R, HIDDEN), generator=g) * 2 - 1) * bound).half().to(device)
+            b = (torch.randn((n, LORA_R), generator=g) * 1e-3).half().to(device)
+            d[name + "_lora"] = (a, b)
+        layers.append(d)
+    return layers
+
+
+def stack_flops(n_layers):
+    """Base GEMM flops of one training step of the stack (forward + input gradient), and the
+    LoRA products' flops (forward u, out; backward dB, gu, dA, dX)."""
+    base = 2 * sum(gemm_flops(n, k) for _, n, k in QWEN15_SHAPES) * n_layers
+    lora = sum(2 * M * LORA_R * (HIDDEN + n) + 2 * M * LORA_R * (2 * HIDDEN + 2 * n)
+               for n in (1536, 256)) * n_layers
+    return base, lora
+
+
+def bench_c4(steps, warmup, device, n_layers=28):
+    """One training step of the 28-layer stack (solution/varlen.py:254-257 -> attn.py:396-418,
+    mlp.py:62-110): per layer forward q/k/v with LoRA q/v (one fused launch, U from
+    dk_lora_down), o, gate+up+SwiGLU, down; backward down with the SwiGLU backward, gate+up, o,
+    q/k/v with the LoRA input-gradient terms (GU, dA, dB from dk_lora_bwd). Attention and the
+    norms are outside this path: each layer's attention output and MLP input are fixed synthetic
+    tensors; gate/up are kept from the forward (no recompute). Also timed: the same step with U
+    and GU precomputed (the dequant-GEMM launches alone)."""
+    import torch
+
+    from decik_amd import lora, nf4
+
+    layers = make_stack(n_layers, device)
+    s = LORA_ALPHA / LORA_R
+    x = seeded_fp16((M, HIDDEN), 2001, 1.0, device)
+    attn = seeded_fp16((M, HIDDEN), 2002, 1.0, device)
+    x2 = seeded_fp16((M, HIDDEN), 2003, 1.0, device)
+    dy = seeded_fp16((M, HIDDEN), 2004, 1e-2, device)
+    dq = seeded_fp16((M, 1536), 2005, 1e-2, device)
+    dkv = seeded_fp16((M, 256), 2006, 1e-2, device)
+    pre = {}  # U / GU per layer, for the GEMM-only step
+
+    def layer_step(L, li, lora_kernels):
+        (aq, bq), (av, bv) = L["q_lora"], L["v_lora"]
+        if lora_kernels:
+            uq, uv = lora.lora_down(x, aq), lora.lora_down(x, av)
+        else:
+            uq, uv = pre[li][0], pre[li][1]
+        items = [dict(packed=L["q"][0], qs=L["q"][1], bias=L["q_bias"], lora_u=uq, lora_b=bq, lora_scale=s),
+                 dict(packed=L["k"][0], qs=L["k"][1], bias=L["k_bias"]),
+                 dict(packed=L["v"][0], qs=L["v"][1], bias=L["v_bias"], lora_u=uv, lora_b=bv, lora_scale=s)]
+        nf4.linear_forward(x, items, lora_rank=LORA_R)
+        nf4.linear_forward(attn, [dict(packed=L["o"][0], qs=L["o"][1])])
+        gate, up, h = nf4.glu_forward(x2, dict(packed=L["gate"][0], qs=L["gate"][1]),
+                                      dict(packed=L["up"][0], qs=L["up"][1]))
+        nf4.linear_forward(h, [dict(packed=L["down"][0], qs=L["down"][1])])
+        return uq, uv, gate, up
+
+    def layer_back(L, li, saved, lora_kernels):
+        uq, uv, gate, up = saved
+        (aq, bq), (av, bv) = L["q_lora"], L["v_lora"]
+        dgate, dup = nf4.linear_backward_swiglu(dict(packed=L["down"][0], qs=L["down"][1], dy=dy), gate, up,
+                                                out=(gate, up))
+        nf4.linear_backward([dict(packed=L["gate"][0], qs=L["gate"][1], dy=dgate),
+                             dict(packed=L["up"][0], qs=L["up"][1], dy=dup)], M, HIDDEN)
+        nf4.linear_backward([dict(packed=L["o"][0], qs=L["o"][1], dy=dy)], M, HIDDEN)
+        if lora_kernels:
+            guq, _, _ = lora.lora_grads(dq, uq, x, bq, s)
+            guv, _, _ = lora.lora_grads(dkv, uv, x, bv, s)
+        else:
+            guq, guv = pre[li][2], pre[li][3]
+        nf4.linear_backward([dict(packed=L["q"][0], qs=L["q"][1], dy=dq, lora_gu=guq, lora_a=aq),
+                             dict(packed=L["k"][0], qs=L["k"][1], dy=dkv),
+                             dict(packed=L["v"][0], qs=L["v"][1], dy=dkv, lora_gu=guv, lora_a=av)],
+                            M, HIDDEN, lora_rank=LORA_R)
+
+    def step(lora_kernels=True):
+        saved = [layer_step(L, li, lora_kernels) for li, L in enumerate(layers)]
+        for li in reversed(range(n_layers)):
+            layer_back(layers[li], li, saved[li], lora_kernels)
+
+    for li, L in enumerate(layers):
+        (aq, bq), (av, bv) = L["q_lora"], L["v_lora"]
+        uq, uv = lora.lora_down(x, aq), lora.lora_down(x, av)
+        pre[li] = (uq, uv, lora.lora_grads(dq, uq, x, bq, s)[0], lora.lora_grads(dkv, uv, x, bv, s)[0])
+    step()  # fills the block-scale cache of every weight
+    torch.cuda.synchronize()
+    res = {}
+    for name, lk in (("step", True), ("gemm_only", False)):
+        for _ in range(warmup):
+            step(lk)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(steps):
+            step(lk)
+        b.record()
+        torch.cuda.synchronize()
+        res[name] = a.elapsed_time(b) / steps
+    base, lora_f = stack_flops(n_layers)
+    return dict(
+        workload=f"Qwen2.5-1.5B {n_layers} layers x {{q,k,v,o,gate,up,down}} NF4 (bs 64, double quant) + "
+                 f"LoRA r=16 on q/v, M={M}, one training step: 8 fused dequant-GEMM launches per layer "
+                 f"({7 * n_layers} forward + {7 * n_layers} input-gradient GEMMs) + 4 LoRA side launches",
+        ms_per_step=round(res["step"], 4), dequant_gemm_ms=round(res["gemm_only"], 4),
+        dequant_gemm_share=round(res["gemm_only"] / res["step"], 4),
+        tflops=round((base + lora_f) / (res["step"] * 1e-3) / 1e12, 1),
+        gemm_tflops=round(base / (res["gemm_only"] * 1e-3) / 1e12, 1),
+        frac=round(base / (res["gemm_only"] * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4),
+        step_gflops=round((base + lora_f) / 1e9, 1), launches_per_step=12 * n_layers)
+
+
+# ---- config C5: the Qwen2.5-7B sweep -----------------------------------------------------------
+
+QWEN7_SHAPES = [("q/o", 3584, 3584), ("k/v", 512, 3584), ("gate/up", 18944, 3584), ("down", 3584, 18944)]
+C5_M = (1, 8, 64, 830, 8192)
+
+
+def fused_bytes(n, k, m):
+    """Algorithmic HBM bytes of one fused call: the NF4 weight once, X in and Y out (fp16)."""
+    return nf4_bytes(n, k) + 2 * m * (n + k)
+
+
+def bench_c5(device, reps=7, flush_bytes=512 << 20):
+    """Each 7B projection shape at every M: forward Y = X.W^T (the GEMV kernel at M = 1, the MFMA
+    kernels above) and, for M >= 64, the input gradient dX = dY.W. Before every timed call a
+    512 MiB fill evicts the caches (L2 and the 256 MB Infinity Cache), so the weight comes from
+    HBM; the call is bracketed by HIP events on its stream (the fill also covers the host's
+    enqueue time). Median of `reps`."""
+    import torch
+
+    from decik_amd import nf4
+    from decik_amd.quant import quantize_nf4
+
+    flush = torch.empty(flush_bytes // 4, dtype=torch.float32, device=device)
+    rows = []
+    for si, (name, n, k) in enumerate(QWEN7_SHAPES):
+        packed, qs = quantize_nf4(seeded_fp16((n, k), 30_000 + si, 0.02, device), blocksize=64,
+                                  compress_statistics=True)
+        for m in C5_M:
+            x = seeded_fp16((m, k), 31_000 + m, 1.0, device)
+            dy = seeded_fp16((m, n), 32_000 + m, 1e-2, device)
+            calls = {"fwd": lambda: nf4.linear_forward(x, [dict(packed=packed, qs=qs)])}
+            if m >= 64:
+                calls["bwd"] = lambda: nf4.linear_backward([dict(packed=packed, qs=qs, dy=dy)], m, k)
+            for d, fn in calls.items():
+                fn()
+                times = []
+                for _ in range(reps):
+                    flush.fill_(1.0)
+                    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    a.record()
+                    fn()
+                    b.record()
+                    torch.cuda.synchronize()
+                    times.append(a.elapsed_time(b))
+                ms = statistics.median(times)
+                fl = gemm_flops(n, k, m)
+                by = fused_bytes(n, k, m)
+                plan = nf4.launch_plan(d == "bwd", m, k, [n])
+                rows.append(dict(shape=name, n=n, k=k, m=m, dir=d, us=round(ms * 1e3, 2),
+                                 gbs=round(by / (ms * 1e-3) / 1e9, 1), hbm_frac=round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                 tflops=round(fl / (ms * 1e-3) / 1e12, 2),
+                                 mfma_frac=round(fl / (ms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4),
+                                 kernel=plan["kernel"], splits=plan["splits"]))
+        del packed, qs
+    del flush
+    return dict(workload="Qwen2.5-7B projections (NF4 bs 64, double quant), one call per shape and M, "
+                         "caches flushed before each call", rows=rows)
+
+
 def load_traffic(kind):
     """HBM bytes per call of launch `kind`, from the committed rocprofv3 --pmc FETCH_SIZE /
     WRITE_SIZE summary (profiles/traffic.json, made with `bench.py --only <kind>`), or None if
@@ -360,6 +551,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-dequant", action="store_true")
+    ap.add_argument("--skip-configs", action="store_true",
+                    help="skip the 28-layer stack step (C4) and the Qwen2.5-7B sweep (C5)")
     ap.add_argument("--only", default=None,
                     choices=["fwd_gate_up", "fwd_down", "bwd_down", "bwd_gate_up"],
                     help="time only this launch kind (for counter runs); prints its roofline only")
@@ -397,6 +590,14 @@ def main():
         del src, dst
     with no_gc():
         deq = None if (args.skip_dequant or args.only) else bench_dequant(max(args.steps, 10), args.warmup, device)
+    c4 = c5 = None
+    if not (args.skip_configs or args.only):
+        with no_gc():
+            c4 = bench_c4(max(2, min(args.steps, 5)), 1, device)
+        torch.cuda.empty_cache()
+        with no_gc():
+            c5 = bench_c5(device)
+        torch.cuda.empty_cache()
 
     # Dominant launch: the fused GEMM call with the largest time. Its kernels: the GEMM kernel,
     # plus splitk_reduce_kernel when the call takes the split-K path. `achieved` = the call's
@@ -439,6 +640,10 @@ def main():
                                              peak=HBM_PEAK_GBS, unit="GB/s",
                                              frac=round(deq["gbs"] / HBM_PEAK_GBS, 4),
                                              frac_of_measured=round(deq["gbs"] / peaks["hbm_copy_gbs"], 4)))
+    if c4 is not None:
+        line["c4_stack_step"] = c4
+    if c5 is not None:
+        line["c5_qwen7b_sweep"] = c5
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
     else:
