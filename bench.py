@@ -463,13 +463,14 @@ def bench_c4(steps, warmup, device, n_layers=28):
     return dict(
         workload=f"Qwen2.5-1.5B {n_layers} layers x {{q,k,v,o,gate,up,down}} NF4 (bs 64, double quant) + "
                  f"LoRA r=16 on q/v, M={M}, one training step: 8 fused dequant-GEMM launches per layer "
-                 f"({7 * n_layers} forward + {7 * n_layers} input-gradient GEMMs) + 4 LoRA side launches",
+                 f"({7 * n_layers} forward + {7 * n_layers} input-gradient GEMMs) + 6 LoRA side launches "
+                 f"(U of q and v; GU with dB, then dA, of q and v)",
         ms_per_step=round(res["step"], 4), dequant_gemm_ms=round(res["gemm_only"], 4),
         dequant_gemm_share=round(res["gemm_only"] / res["step"], 4),
         tflops=round((base + lora_f) / (res["step"] * 1e-3) / 1e12, 1),
         gemm_tflops=round(base / (res["gemm_only"] * 1e-3) / 1e12, 1),
         frac=round(base / (res["gemm_only"] * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4),
-        step_gflops=round((base + lora_f) / 1e9, 1), launches_per_step=12 * n_layers)
+        step_gflops=round((base + lora_f) / 1e9, 1), launches_per_step=14 * n_layers)
 
 
 # ---- config C5: the Qwen2.5-7B sweep -----------------------------------------------------------

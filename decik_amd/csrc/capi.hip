@@ -759,6 +759,8 @@ int dk_lora_down(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const uin
         return fail("dk_lora_down: k and ldx must be multiples of 8");
     if (x == nullptr || a == nullptr || u == nullptr || !aligned(x, 16) || !aligned(a, 16))
         return fail("dk_lora_down: x and a must be 16-byte aligned");
+    // 32-bit byte offsets (with a 32-row margin for the tile past the last row)
+    if ((m + 32) * ldx * 2 >= INT32_MAX || k * rank * 2 >= INT32_MAX) return fail("dk_lora_down: tensors too large");
     return check_hip(launch_lora_down(reinterpret_cast<const _Float16*>(x), m, k, ldx,
                                       reinterpret_cast<const _Float16*>(a), rank,
                                       reinterpret_cast<_Float16*>(u), static_cast<hipStream_t>(stream)),
@@ -774,8 +776,13 @@ int dk_lora_bwd(const uint16_t* dy, int64_t lddy, const uint16_t* u, const uint1
         return fail("dk_lora_bwd: bad shapes");
     if (dy == nullptr || u == nullptr || x == nullptr || b == nullptr || gu == nullptr)
         return fail("dk_lora_bwd: null pointer");
-    if (!aligned(u, 16) || !aligned(b, 16) || !aligned(gu, 16))
-        return fail("dk_lora_bwd: u, b, gu must be 16-byte aligned");
+    if (!aligned(u, 16) || !aligned(b, 16) || !aligned(gu, 16) || !aligned(dy, 16))
+        return fail("dk_lora_bwd: dy, u, b, gu must be 16-byte aligned");
+    if ((n % 8) != 0 || (lddy % 8) != 0) return fail("dk_lora_bwd: n and lddy must be multiples of 8");
+    // 32-bit byte offsets (with a 32-row margin for the tile past the last row)
+    if ((m + 32) * lddy * 2 >= INT32_MAX || (m + 32) * ldx * 2 >= INT32_MAX || (m + 32) * rank * 2 >= INT32_MAX ||
+        n * rank * 2 >= INT32_MAX)
+        return fail("dk_lora_bwd: tensors too large");
     return check_hip(launch_lora_bwd(reinterpret_cast<const _Float16*>(dy), lddy,
                                      reinterpret_cast<const _Float16*>(u),
                                      reinterpret_cast<const _Float16*>(x), ldx,

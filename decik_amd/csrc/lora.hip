@@ -4,137 +4,215 @@
 // :251-257 backward). Here:
 //   lora_down:  U  = fp16(X . A^T)                 [m, r]   (the forward epilogue adds s U.B^T)
 //   lora_gu:    GU = fp16(s * dY . B)              [m, r]   (the backward epilogue adds GU.A)
-//   lora_wgrad: dB = s * dY^T . U  (fp32 [n, r]),  dA = GU^T . X  (fp32 [r, k])
-// These are ~2% of the flops of the projection they ride on. lora_down / lora_gu use one
-// work-group per token row (the contraction is spread over the 256 threads, then reduced with
-// cross-lane shuffles and LDS); the weight gradients reduce over tokens inside one work-group
-// per 16 output columns (16 token slices reduced through LDS), so no atomics and the summation
-// order is fixed.
+//   lora_db:    dB = s * dY^T . U                  fp32 [n, r]
+//   lora_da:    dA = GU^T . X                      fp32 [r, k]
+// All four are small (about 2% of the flops of the projection they ride on) and run on
+// v_mfma_f32_16x16x32_f16: a work-group of 8 waves owns one 16-row output tile (16 tokens for U
+// and GU, 16 weight rows for dB, 16 columns of A for dA) and all r rank columns; its waves take
+// the 32-wide contraction chunks in turn and their fp32 tiles are summed through LDS in wave
+// order, so the summation order is fixed (no atomics) and every call gives the same bits.
+// GU and dB are one launch (both read dY); dA, which needs GU, is a second one.
+//
+// MFMA operand layout (16x16x32, lane l, i = l % 16, g = l / 16): A operand A[i][8 g + e],
+// B operand B[8 g + e][i], result D[4 g + r][i], e = 0..7, r = 0..3. Operands whose 8 contraction
+// values are contiguous in memory are one 16-byte load; the others (the token-contracted products
+// dB and dA, and B's rows in GU) are gathered with 2-byte loads, all from the L2-resident
+// activations.
 #include "dk_internal.h"
 
 namespace dk {
 
-constexpr int kLoraThreads = 256;
+constexpr int kLoraWaves = 8;
+constexpr int kLoraThreads = 64 * kLoraWaves;
 
-// Sum `v[0..R)` over the 256 threads of the work-group; thread 0..R-1 returns the total of
-// component tid in *out.
-template <int R>
-__device__ __forceinline__ void block_reduce(float (&v)[R], float* red, float* out) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+__device__ __forceinline__ half8_t gather8(rsrc_t r, uint32_t off0, uint32_t stride, bool ok0, int valid) {
+    // 8 fp16 values at off0 + e * stride (bytes); element e reads zero unless ok0 && e < valid
+    half8_t v;
 #pragma unroll
-    for (int t = 0; t < R; ++t) {
-        float x = v[t];
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
-        v[t] = x;
-    }
-    if (lane == 0) {
-#pragma unroll
-        for (int t = 0; t < R; ++t) red[wave * R + t] = v[t];
-    }
-    __syncthreads();
-    if (tid < R) *out = ((red[tid] + red[R + tid]) + red[2 * R + tid]) + red[3 * R + tid];
+    for (int e = 0; e < 8; ++e)
+        v[e] = __builtin_bit_cast(_Float16, (uint16_t)bload16(r, off_if(ok0 && e < valid, off0 + (uint32_t)e * stride)));
+    return v;
 }
 
-// U[m, t] = fp16(sum_k X[m, k] A[t, k]); one work-group per row m, 8 consecutive k per thread.
+// Sum the 8 waves' 16 x R tiles (lane: rows 4 g + r, column 16 h + i) in wave order; thread t
+// of the work-group then holds element t of the tile (row t / R, column t % R) in *out for
+// t < 16 R. red: 8 x 16 x R floats.
 template <int R>
-__global__ __launch_bounds__(kLoraThreads) void lora_down_kernel(const _Float16* __restrict__ x,
-                                                                 int64_t k, int64_t ldx,
-                                                                 const _Float16* __restrict__ a,
+__device__ __forceinline__ void reduce_tiles(const float4_t (&acc)[R / 16], float* red, int wave, int lane) {
+    const int i = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int h = 0; h < R / 16; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[(wave * 16 + 4 * g + r) * R + 16 * h + i] = acc[h][r];
+    __syncthreads();
+}
+
+template <int R>
+__device__ __forceinline__ float tile_sum(const float* red, int t) {
+    float s = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kLoraWaves; ++w) s += red[w * 16 * R + t];
+    return s;
+}
+
+// U[m, t] = fp16(sum_k X[m, k] A[t, k]): A operand X (16 tokens), B operand A^T (rows of A).
+template <int R>
+__global__ __launch_bounds__(kLoraThreads) void lora_down_kernel(const _Float16* __restrict__ x, int m, int k,
+                                                                 int ldx, const _Float16* __restrict__ a,
                                                                  _Float16* __restrict__ u) {
-    __shared__ float red[4 * R];
-    const int64_t m = blockIdx.x;
-    const _Float16* xr = x + m * ldx;
-    float acc[R];
+    __shared__ float red[kLoraWaves * 16 * R];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int i = lane & 15, g = lane >> 4;
+    const int m0 = blockIdx.x * 16;
+    const rsrc_t xr = make_rsrc(x, (uint32_t)(((int64_t)(m - 1) * ldx + k) * 2));
+    const rsrc_t ar = make_rsrc(a, (uint32_t)R * (uint32_t)k * 2u);
+    const bool rok = m0 + i < m;
+    float4_t acc[R / 16];
 #pragma unroll
-    for (int t = 0; t < R; ++t) acc[t] = 0.0f;
-    for (int64_t k0 = 8 * threadIdx.x; k0 < k; k0 += 8 * kLoraThreads) {
-        if (k0 + 8 <= k) {
-            const half8_t xv = *(const half8_t*)(xr + k0);
+    for (int h = 0; h < R / 16; ++h) acc[h] = float4_t{};
+    const int nk = (k + 31) >> 5;
+    // two chunks per iteration (the second reads zeros past the end): their loads overlap
+    for (int kc = wave; kc < nk; kc += 2 * kLoraWaves) {
+        half8_t xa[2], ab[2][R / 16];
 #pragma unroll
-            for (int t = 0; t < R; ++t) {
-                const half8_t av = *(const half8_t*)(a + (int64_t)t * k + k0);
+        for (int q = 0; q < 2; ++q) {
+            const int kk = 32 * (kc + q * kLoraWaves) + 8 * g;  // k % 8 == 0: wholly inside or past the end
+            xa[q] = __builtin_bit_cast(half8_t, bload128(xr, off_if(rok && kk < k, (uint32_t)((m0 + i) * ldx + kk) * 2u)));
 #pragma unroll
-                for (int e = 0; e < 8; ++e) acc[t] = __builtin_fmaf((float)xv[e], (float)av[e], acc[t]);
-            }
-        } else {
-            for (int64_t kk = k0; kk < k; ++kk)
-#pragma unroll
-                for (int t = 0; t < R; ++t)
-                    acc[t] = __builtin_fmaf((float)xr[kk], (float)a[(int64_t)t * k + kk], acc[t]);
+            for (int h = 0; h < R / 16; ++h)
+                ab[q][h] = __builtin_bit_cast(half8_t, bload128(ar, off_if(kk < k, (uint32_t)((16 * h + i) * k + kk) * 2u)));
         }
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+            for (int h = 0; h < R / 16; ++h) acc[h] = mfma16x16x32(xa[q], ab[q][h], acc[h]);
     }
-    float tot;
-    block_reduce<R>(acc, red, &tot);
-    if (threadIdx.x < R) u[m * R + threadIdx.x] = (_Float16)tot;
+    reduce_tiles<R>(acc, red, wave, lane);
+    for (int t = threadIdx.x; t < 16 * R; t += kLoraThreads) {
+        const int row = m0 + t / R;
+        if (row < m) u[(int64_t)row * R + t % R] = to_half(tile_sum<R>(red, t));
+    }
 }
 
-// GU[m, t] = fp16(s * sum_n dY[m, n] B[n, t]); one work-group per row m.
+// Work-groups [0, m_tiles): GU tiles, GU[m, t] = fp16(s sum_n dY[m, n] B[n, t]);
+// work-groups [m_tiles, m_tiles + n_tiles): dB tiles, dB[n, t] = s sum_m dY[m, n] U[m, t].
 template <int R>
-__global__ __launch_bounds__(kLoraThreads) void lora_gu_kernel(const _Float16* __restrict__ dy,
-                                                               int64_t lddy, int64_t n,
-                                                               const _Float16* __restrict__ b,
-                                                               float scale,
-                                                               _Float16* __restrict__ gu) {
-    __shared__ float red[4 * R];
-    const int64_t m = blockIdx.x;
-    const _Float16* dr = dy + m * lddy;
-    float acc[R];
+__global__ __launch_bounds__(kLoraThreads) void lora_gu_db_kernel(const _Float16* __restrict__ dy, int lddy,
+                                                                  const _Float16* __restrict__ u,
+                                                                  const _Float16* __restrict__ b, int m, int n,
+                                                                  float scale, int m_tiles,
+                                                                  _Float16* __restrict__ gu,
+                                                                  float* __restrict__ db) {
+    __shared__ float red[kLoraWaves * 16 * R];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int i = lane & 15, g = lane >> 4;
+    const rsrc_t dr = make_rsrc(dy, (uint32_t)(((int64_t)(m - 1) * lddy + n) * 2));
+    float4_t acc[R / 16];
 #pragma unroll
-    for (int t = 0; t < R; ++t) acc[t] = 0.0f;
-    for (int64_t j = threadIdx.x; j < n; j += kLoraThreads) {
-        const float g = (float)dr[j];
-        const _Float16* br = b + j * R;
+    for (int h = 0; h < R / 16; ++h) acc[h] = float4_t{};
+    if ((int)blockIdx.x < m_tiles) {
+        const int m0 = blockIdx.x * 16;
+        const rsrc_t br = make_rsrc(b, (uint32_t)n * (uint32_t)R * 2u);
+        const bool rok = m0 + i < m;
+        const int nc = (n + 31) >> 5;
+        for (int c = wave; c < nc; c += 2 * kLoraWaves) {
+            half8_t ya[2], bb[2][R / 16];
 #pragma unroll
-        for (int t = 0; t < R; t += 8) {
-            const half8_t bv = *(const half8_t*)(br + t);
+            for (int q = 0; q < 2; ++q) {
+                const int nn = 32 * (c + q * kLoraWaves) + 8 * g;  // n % 8 == 0
+                ya[q] = __builtin_bit_cast(half8_t, bload128(dr, off_if(rok && nn < n, (uint32_t)((m0 + i) * lddy + nn) * 2u)));
+                // B[nn + e][16 h + i]: rows of B, R fp16 apart
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[t + e] = __builtin_fmaf(g, (float)bv[e], acc[t + e]);
+                for (int h = 0; h < R / 16; ++h)
+                    bb[q][h] = gather8(br, (uint32_t)(nn * R + 16 * h + i) * 2u, 2u * R, nn < n, 8);
+            }
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+#pragma unroll
+                for (int h = 0; h < R / 16; ++h) acc[h] = mfma16x16x32(ya[q], bb[q][h], acc[h]);
         }
+        reduce_tiles<R>(acc, red, wave, lane);
+        for (int t = threadIdx.x; t < 16 * R; t += kLoraThreads) {
+            const int row = m0 + t / R;
+            if (row < m) gu[(int64_t)row * R + t % R] = to_half(scale * tile_sum<R>(red, t));
+        }
+        return;
     }
-    float tot;
-    block_reduce<R>(acc, red, &tot);
-    if (threadIdx.x < R) gu[m * R + threadIdx.x] = to_half(scale * tot);
+    if (db == nullptr) return;
+    const int n0 = ((int)blockIdx.x - m_tiles) * 16;
+    const rsrc_t ur = make_rsrc(u, (uint32_t)m * (uint32_t)R * 2u);
+    const bool cok = n0 + i < n;
+    const int mc = (m + 31) >> 5;
+    for (int c = wave; c < mc; c += 2 * kLoraWaves) {
+        half8_t ya[2], ub[2][R / 16];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int mm = min(32 * (c + q * kLoraWaves) + 8 * g, m);  // rows past m: zeros
+            const int valid = m - mm;  // rows mm .. mm + 7 that exist
+            // A = dY^T: A[n0 + i][mm + e] = dY[mm + e][n0 + i]
+            ya[q] = gather8(dr, (uint32_t)(mm * lddy + n0 + i) * 2u, 2u * (uint32_t)lddy, cok, valid);
+#pragma unroll
+            for (int h = 0; h < R / 16; ++h)
+                ub[q][h] = gather8(ur, (uint32_t)(mm * R + 16 * h + i) * 2u, 2u * R, true, valid);
+        }
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+            for (int h = 0; h < R / 16; ++h) acc[h] = mfma16x16x32(ya[q], ub[q][h], acc[h]);
+    }
+    reduce_tiles<R>(acc, red, wave, lane);
+    for (int t = threadIdx.x; t < 16 * R; t += kLoraThreads) {
+        const int row = n0 + t / R;
+        if (row < n) db[(int64_t)row * R + t % R] = scale * tile_sum<R>(red, t);
+    }
 }
 
-// C[c, t] = scale * sum_m Q[m, c] P[m, t] over all m, for 16 columns c per work-group:
-// thread = (column c0 + tid % 16, token slice tid / 16); slices reduced in LDS in fixed order.
-// transpose_out: write C as [t][c] (row stride ldc) instead of [c][t].
+// dA[t, k] = sum_m GU[m, t] X[m, k]: work-group = 16 columns k (all R rows t); A operand GU^T,
+// B operand X, both gathered along the token dimension.
 template <int R>
-__global__ __launch_bounds__(kLoraThreads) void lora_wgrad_kernel(
-    const _Float16* __restrict__ q, int64_t ldq, const _Float16* __restrict__ p, int64_t m_rows,
-    int64_t ncols, float scale, float* __restrict__ c, int64_t ldc, int transpose_out) {
-    __shared__ float red[16][16][R + 1];
-    const int tid = threadIdx.x;
-    const int cl = tid & 15, slice = tid >> 4;
-    const int64_t col = (int64_t)blockIdx.x * 16 + cl;
-    float acc[R];
+__global__ __launch_bounds__(kLoraThreads) void lora_da_kernel(const _Float16* __restrict__ gu,
+                                                               const _Float16* __restrict__ x, int ldx, int m,
+                                                               int k, float* __restrict__ da) {
+    __shared__ float red[kLoraWaves * 16 * R];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int i = lane & 15, g = lane >> 4;
+    const int k0 = blockIdx.x * 16;
+    const rsrc_t gr = make_rsrc(gu, (uint32_t)m * (uint32_t)R * 2u);
+    const rsrc_t xr = make_rsrc(x, (uint32_t)(((int64_t)(m - 1) * ldx + k) * 2));
+    const bool cok = k0 + i < k;
+    // acc[h]: D[t = 16 h + 4 g + r][k0 + i]
+    float4_t acc[R / 16];
 #pragma unroll
-    for (int t = 0; t < R; ++t) acc[t] = 0.0f;
-    if (col < ncols) {
-        for (int64_t m = slice; m < m_rows; m += 16) {
-            const float qv = (float)q[m * ldq + col];
-            const _Float16* pr = p + m * R;
+    for (int h = 0; h < R / 16; ++h) acc[h] = float4_t{};
+    const int mc = (m + 31) >> 5;
+    for (int c = wave; c < mc; c += 2 * kLoraWaves) {
+        half8_t xb[2], ga[2][R / 16];
 #pragma unroll
-            for (int t = 0; t < R; t += 8) {
-                const half8_t pv = *(const half8_t*)(pr + t);
+        for (int q = 0; q < 2; ++q) {
+            const int mm = min(32 * (c + q * kLoraWaves) + 8 * g, m);  // rows past m: zeros
+            const int valid = m - mm;
+            xb[q] = gather8(xr, (uint32_t)(mm * ldx + k0 + i) * 2u, 2u * (uint32_t)ldx, cok, valid);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) acc[t + e] = __builtin_fmaf(qv, (float)pv[e], acc[t + e]);
-            }
+            for (int h = 0; h < R / 16; ++h)
+                ga[q][h] = gather8(gr, (uint32_t)(mm * R + 16 * h + i) * 2u, 2u * R, true, valid);
         }
-    }
 #pragma unroll
-    for (int t = 0; t < R; ++t) red[slice][cl][t] = acc[t];
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+            for (int h = 0; h < R / 16; ++h) acc[h] = mfma16x16x32(ga[q][h], xb[q], acc[h]);
+    }
+    // lane holds D[16 h + 4 g + r][k0 + i]: write as a [R][16] tile (row t, column i)
+#pragma unroll
+    for (int h = 0; h < R / 16; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[(wave * R + 16 * h + 4 * g + r) * 16 + i] = acc[h][r];
     __syncthreads();
-    // thread (cl, t-part) sums the 16 slices of column cl for t = tid / 16 (+16 ...)
-    for (int t = slice; t < R; t += 16) {
+    for (int t = threadIdx.x; t < 16 * R; t += kLoraThreads) {
+        const int row = t / 16, col = k0 + t % 16;  // row = rank index
         float s = 0.0f;
 #pragma unroll
-        for (int sl = 0; sl < 16; ++sl) s += red[sl][cl][t];
-        if (col < ncols) {
-            if (transpose_out) c[(int64_t)t * ldc + col] = scale * s;
-            else c[col * ldc + t] = scale * s;
-        }
+        for (int w = 0; w < kLoraWaves; ++w) s += red[w * 16 * R + t];
+        if (col < k) da[(int64_t)row * k + col] = s;
     }
 }
 
@@ -143,8 +221,13 @@ __global__ __launch_bounds__(kLoraThreads) void lora_wgrad_kernel(
 hipError_t launch_lora_down(const _Float16* x, int64_t m, int64_t k, int64_t ldx, const _Float16* a,
                             int rank, _Float16* u, hipStream_t s) {
     if (m == 0) return hipSuccess;
-#define X(R) \
-    if (rank == R) { hipLaunchKernelGGL((lora_down_kernel<R>), dim3(m), dim3(kLoraThreads), 0, s, x, k, ldx, a, u); return hipGetLastError(); }
+    const dim3 grid((unsigned)((m + 15) / 16));
+#define X(R)                                                                                           \
+    if (rank == R) {                                                                                   \
+        hipLaunchKernelGGL((lora_down_kernel<R>), grid, dim3(kLoraThreads), 0, s, x, (int)m, (int)k,   \
+                           (int)ldx, a, u);                                                            \
+        return hipGetLastError();                                                                      \
+    }
     DK_RANK_CASES(X)
 #undef X
     return hipErrorInvalidValue;
@@ -154,17 +237,16 @@ hipError_t launch_lora_bwd(const _Float16* dy, int64_t lddy, const _Float16* u, 
                            int64_t ldx, const _Float16* b, int64_t m, int64_t n, int64_t k, int rank,
                            float scale, _Float16* gu, float* da, float* db, hipStream_t s) {
     if (m == 0) return hipSuccess;
-#define X(R)                                                                                        \
-    if (rank == R) {                                                                                \
-        hipLaunchKernelGGL((lora_gu_kernel<R>), dim3(m), dim3(kLoraThreads), 0, s, dy, lddy, n, b,  \
-                           scale, gu);                                                              \
-        if (db != nullptr)                                                                          \
-            hipLaunchKernelGGL((lora_wgrad_kernel<R>), dim3((n + 15) / 16), dim3(kLoraThreads), 0, \
-                               s, dy, lddy, u, m, n, scale, db, (int64_t)R, 0);                     \
-        if (da != nullptr)                                                                          \
-            hipLaunchKernelGGL((lora_wgrad_kernel<R>), dim3((k + 15) / 16), dim3(kLoraThreads), 0, \
-                               s, x, ldx, gu, m, k, 1.0f, da, k, 1);                                \
-        return hipGetLastError();                                                                   \
+    const int m_tiles = (int)((m + 15) / 16);
+    const int n_tiles = db != nullptr ? (int)((n + 15) / 16) : 0;
+#define X(R)                                                                                           \
+    if (rank == R) {                                                                                   \
+        hipLaunchKernelGGL((lora_gu_db_kernel<R>), dim3(m_tiles + n_tiles), dim3(kLoraThreads), 0, s,  \
+                           dy, (int)lddy, u, b, (int)m, (int)n, scale, m_tiles, gu, db);               \
+        if (da != nullptr)                                                                             \
+            hipLaunchKernelGGL((lora_da_kernel<R>), dim3((unsigned)((k + 15) / 16)), dim3(kLoraThreads), \
+                               0, s, gu, x, (int)ldx, (int)m, (int)k, da);                             \
+        return hipGetLastError();                                                                      \
     }
     DK_RANK_CASES(X)
 #undef X

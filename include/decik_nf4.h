@@ -174,8 +174,9 @@ int dk_lora_down(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const uin
  *   GU = fp16(scale * dY . B)  [m, rank]
  *   dB = scale * dY^T . U      fp32 [n, rank]
  *   dA = GU^T . X              fp32 [rank, k]
- * dY fp16 [m, n] (row stride lddy), U fp16 [m, rank], X fp16 [m, k] (row stride ldx),
- * B fp16 [n, rank]. The input gradient GU . A is added by dk_nf4_linear_bwd. */
+ * dY fp16 [m, n] (row stride lddy; n and lddy multiples of 8), U fp16 [m, rank], X fp16 [m, k]
+ * (row stride ldx), B fp16 [n, rank]; da or db may be NULL (not computed). Fixed summation order:
+ * the same bits on every call. The input gradient GU . A is added by dk_nf4_linear_bwd. */
 int dk_lora_bwd(const uint16_t* dy, int64_t lddy, const uint16_t* u, const uint16_t* x,
                 int64_t ldx, const uint16_t* b, int64_t m, int64_t n, int64_t k, int rank,
                 float scale, uint16_t* gu, float* da, float* db, void* stream);

@@ -221,3 +221,32 @@ def test_qkv_projection_mixed_ranks(ranks, device):
             assert_close(p["lora_b"].grad, db, what=f"dB r={an.shape[0]}")
         assert_close(o, y_ref, what="Y")
     assert_close(x.grad, dx_ref, what="dX")
+
+
+@pytest.mark.parametrize("r", [16, 32])
+@pytest.mark.parametrize("m,k,n", [(1, 40, 8), (17, 1536, 256), (830, 104, 1536)])
+def test_lora_kernels_edge_shapes(r, m, k, n, device):
+    """dk_lora_down / dk_lora_bwd on shapes that leave partial tiles everywhere: token counts
+    below and past one 16-row tile, widths that are not multiples of 32; dA / dB may be omitted.
+    Against the oracle (exact variant: the kernels keep dA and dB in fp32)."""
+    from decik_amd.lora import lora_down, lora_grads
+
+    s = 2.0
+    x = randn16((m, k), seed=150 + m, device=device)
+    a = randn16((r, k), seed=151, device=device, std=0.05)
+    b = randn16((n, r), seed=152, device=device, std=0.05)
+    dy = randn16((m, n), seed=153, device=device, std=1e-2)
+    u = lora_down(x, a)
+    xn, an, bn, dyn = (t.cpu().numpy() for t in (x, a, b, dy))
+    u_ref, _ = O.lora_fwd_ref(xn, an, bn, s)
+    assert_close(u, u_ref.astype(np.float32), what="U")
+    gu, da, db = lora_grads(dy, u, x, b, s)
+    gu_ref, da_ref, db_ref, _ = O.lora_bwd_ref(dyn, xn, u.cpu().numpy(), an, bn, s, exact=True)
+    assert_close(gu, gu_ref.astype(np.float32), what="GU")
+    assert_close(da, da_ref, what="dA")
+    assert_close(db, db_ref, what="dB")
+    gu2, da2, db2 = lora_grads(dy, u, x, b, s, want_da=False, want_db=False)
+    assert da2 is None and db2 is None and torch.equal(gu2, gu)
+    # the same bits on a second call (fixed summation order)
+    gu3, da3, db3 = lora_grads(dy, u, x, b, s)
+    assert torch.equal(gu3, gu) and torch.equal(da3, da) and torch.equal(db3, db)
