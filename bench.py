@@ -485,17 +485,20 @@ def fused_bytes(n, k, m):
 
 
 def bench_c5(device, reps=7, flush_bytes=512 << 20):
-    """Each 7B projection shape at every M: forward Y = X.W^T (the GEMV kernel at M = 1, the MFMA
-    kernels above) and, for M >= 64, the input gradient dX = dY.W. Before every timed call a
-    512 MiB fill evicts the caches (L2 and the 256 MB Infinity Cache), so the weight comes from
-    HBM; the call is bracketed by HIP events on its stream (the fill also covers the host's
-    enqueue time). Median of `reps`."""
+    """Each 7B projection shape at every M: forward Y = X.W^T (the GEMV kernel at M = 1, the
+    small-M kernel at M = 8, the MFMA kernels above) and, for M >= 64, the input gradient
+    dX = dY.W. Before every timed call a sum over a 512 MiB buffer evicts the caches (L2 and the
+    256 MB Infinity Cache) by reading -- a fill would leave dirty lines whose write-back the timed
+    call would pay for (about 3 us on the large shapes) -- so the weight comes from HBM; the call
+    is bracketed by HIP events on its stream (the flush also covers the host's enqueue time).
+    Median of `reps`."""
     import torch
 
     from decik_amd import nf4
     from decik_amd.quant import quantize_nf4
 
-    flush = torch.empty(flush_bytes // 4, dtype=torch.float32, device=device)
+    flush = torch.ones(flush_bytes // 4, dtype=torch.float32, device=device)
+    sink = torch.empty(1, dtype=torch.float32, device=device)
     rows = []
     for si, (name, n, k) in enumerate(QWEN7_SHAPES):
         packed, qs = quantize_nf4(seeded_fp16((n, k), 30_000 + si, 0.02, device), blocksize=64,
@@ -510,7 +513,7 @@ def bench_c5(device, reps=7, flush_bytes=512 << 20):
                 fn()
                 times = []
                 for _ in range(reps):
-                    flush.fill_(1.0)
+                    torch.sum(flush, dim=0, out=sink[0])
                     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                     a.record()
                     fn()

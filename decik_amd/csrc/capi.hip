@@ -2,6 +2,8 @@
 #include <cstdio>
 #include <cstdlib>
 #include <mutex>
+#include <set>
+#include <tuple>
 #include <string>
 
 #include "dk_internal.h"
@@ -81,18 +83,23 @@ int gemm_weight_ok(const dk_nf4_weight& w, const char* who) {
     return 0;
 }
 
+// CUs of the current device (cached per device; 256, MI355X's count, when no device answers:
+// the planner also runs on hosts without a GPU).
 int num_cus() {
-    static int cus = 0;
+    constexpr int kDevs = 64;
+    static int cus[kDevs] = {};
     static std::mutex mu;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDevs) return 256;
     std::lock_guard<std::mutex> lock(mu);
-    if (cus == 0) {
-        int dev = 0;
+    if (cus[dev] == 0) {
         hipDeviceProp_t prop;
-        if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess)
-            cus = prop.multiProcessorCount;
-        if (cus <= 0) cus = 256;
+        if (hipGetDeviceProperties(&prop, dev) == hipSuccess && prop.multiProcessorCount > 0)
+            cus[dev] = prop.multiProcessorCount;
+        else
+            cus[dev] = 256;
     }
-    return cus;
+    return cus[dev];
 }
 
 int pad8(int g) { return (g + 7) & ~7; }
@@ -293,9 +300,64 @@ GemmPlan plan_bwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool swi
     return p;
 }
 
+// nf4_skinny_kernel (forward, m <= kSkinnyMaxM): 64-row groups; contraction splits so that the
+// launch has at least two work-groups per CU, while every split keeps at least two 128-wide
+// super-steps per wave (16 per work-group).
+constexpr int kSkinnyRows = 64, kSkinnyStep = 128, kSkinnyWaves = 8;
+GemmPlan plan_skinny(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
+    GemmPlan p{};
+    int64_t rgroups = 0, ncols = 0;
+    for (int g = 0; g < ngroups; ++g) {
+        rgroups += (ns[g] + kSkinnyRows - 1) / kSkinnyRows;
+        ncols += ns[g];
+    }
+    p.steps = (int)((k + kSkinnyStep - 1) / kSkinnyStep);
+    p.splits = 1;
+    while (p.splits < 32 && rgroups * p.splits < 2 * num_cus() &&
+           (p.steps + p.splits) / (p.splits + 1) >= 2 * kSkinnyWaves)
+        ++p.splits;
+    p.n_tiles = (int)rgroups;
+    p.m_tiles = 1;
+    p.mt = m <= 16 ? 1 : 2;
+    p.waves = kSkinnyWaves;
+    finish_plan(p, m, ncols);
+    return p;
+}
+
+// Forward launches of at most kSkinnyMaxM token rows without LoRA terms or the GLU epilogue run
+// the GEMV kernel (at most kGemvMaxM rows) or nf4_skinny_kernel, unless DECIK_FWD_PLAN forces an
+// MFMA plan. Measured on Qwen2.5-7B shapes: at 1-2 rows the GEMV is as fast on the large weights
+// and twice as fast on the small ones (fewer dependent steps per wave); from 3 rows on the
+// skinny kernel wins (7B gate at 8 rows: 26 us against 39 for the MFMA kernels). DECIK_SMALL_M
+// = gemv / skinny forces one of them for launches both may take (measurements, tests).
+bool small_m_forward(int64_t m, bool glu, bool lora) {
+    if (glu || lora || m < 1 || m > kSkinnyMaxM) return false;
+    const char* forced = std::getenv("DECIK_FWD_PLAN");
+    return forced == nullptr || *forced == 0;
+}
+bool gemv_requested(int64_t m) {
+    if (m > kGemvMaxM) return false;
+    const char* v = std::getenv("DECIK_SMALL_M");
+    return v == nullptr || std::string(v) != "skinny";
+}
+
 
 
 }  // namespace
+
+hipError_t allow_dynamic_lds(const void* fn, size_t bytes) {
+    static std::mutex mu;
+    static std::set<std::tuple<int, const void*, size_t>> done;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lock(mu);
+    if (done.count({dev, fn, bytes})) return hipSuccess;
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (e == hipSuccess) done.insert({dev, fn, bytes});
+    return e;
+}
+
 }  // namespace dk
 
 using namespace dk;
@@ -357,6 +419,7 @@ int dk_nf4_block_scales(const dk_nf4_weight* w, float* scales, void* stream) {
 
 int64_t dk_nf4_linear_fwd_workspace(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
     if (ngroups < 1 || ngroups > kMaxGroups || ns == nullptr || m <= 0 || k <= 0) return 0;
+    if (small_m_forward(m, false, false)) return workspace_bytes(plan_skinny(m, k, ns, ngroups));
     // the plan also depends on the block sizes (eight-wave kernel or not): cover both
     return std::max(workspace_bytes(plan_fwd(m, k, ns, ngroups, false, true)),
                     workspace_bytes(plan_fwd(m, k, ns, ngroups, false, false)));
@@ -375,12 +438,14 @@ int dk_nf4_linear_plan(int backward, int64_t m, int64_t k, const int64_t* ns, in
     if (backward) {
         p = plan_bwd(m, k, ns, ngroups, glu, single);
         kernel = p.bwd8 ? 3 : 2;
-    } else if (!glu && !lora && m <= kGemvMaxM && (std::getenv("DECIK_FWD_PLAN") == nullptr ||
-                                                    *std::getenv("DECIK_FWD_PLAN") == 0)) {
+    } else if (small_m_forward(m, glu, lora) && gemv_requested(m)) {
         p = GemmPlan{};
         p.waves = 4;
         p.splits = 1;
         kernel = 4;  // nf4_gemv_kernel
+    } else if (small_m_forward(m, glu, lora)) {
+        p = plan_skinny(m, k, ns, ngroups);
+        kernel = 5;  // nf4_skinny_kernel
     } else {
         p = plan_fwd(m, k, ns, ngroups, glu, k % 64 == 0 && k % blocksize == 0, single);
         kernel = p.waves == 8 ? 1 : 0;
@@ -399,16 +464,6 @@ int64_t dk_nf4_linear_bwd_workspace(int64_t m, int64_t k, const int64_t* ns, int
 
 }  // extern "C"
 
-// The GEMV kernel takes forward launches of at most kGemvMaxM token rows without LoRA terms or
-// the GLU epilogue, unless DECIK_FWD_PLAN forces an MFMA plan (tuning and the variant tests).
-static bool use_gemv(int64_t m, bool glu, const dk_linear_fwd_group* groups, int ngroups) {
-    if (glu || m > kGemvMaxM || m < 1) return false;
-    const char* forced = std::getenv("DECIK_FWD_PLAN");
-    if (forced != nullptr && *forced != 0) return false;
-    for (int g = 0; g < ngroups; ++g)
-        if (groups[g].lora_u != nullptr) return false;
-    return true;
-}
 
 // The forward launch behind dk_nf4_linear_fwd and dk_nf4_glu_fwd. h != NULL: GLU mode (two groups
 // of one shape, plain narrow statistics; gate/up outputs optional). no_split: a single pass
@@ -473,17 +528,49 @@ static int linear_fwd_impl(const std::string& name, const uint16_t* x, int64_t m
         return fail(name + ": GLU mode needs two plain weights of one shape, blocksize >= 64, k % 64 == 0");
     if (m == 0 || tile == 0) return 0;
     if ((m - 1) * ldx + k >= INT32_MAX / 2) return fail(name + ": x too large");
-    if (use_gemv(m, glu, groups, ngroups)) {
-        // few token rows, no LoRA terms: one pass over the packed weights (no workspace)
+    bool any_lora = false;
+    for (int g = 0; g < ngroups; ++g) any_lora = any_lora || groups[g].lora_u != nullptr;
+    if (small_m_forward(m, glu, any_lora)) {
+        // few token rows, no LoRA terms: one pass over the packed weights
         a.x = reinterpret_cast<const _Float16*>(x);
         a.ldx = ldx;
+        a.x_bytes = (uint32_t)(((m - 1) * ldx + k) * 2);
         a.m = (int)m;
         a.k = (int)k;
         a.ngroups = ngroups;
         a.nested = nested;
         a.ncols = (int32_t)ncols;
         if (ncols > INT32_MAX / 2) return fail(name + ": problem too large");
-        return check_hip(launch_gemv(a, static_cast<hipStream_t>(stream)), "dk_nf4_linear_fwd GEMV launch");
+        const hipStream_t st = static_cast<hipStream_t>(stream);
+        if (gemv_requested(m)) return check_hip(launch_gemv(a, st), "dk_nf4_linear_fwd GEMV launch");
+        const GemmPlan p = plan_skinny(m, k, ns, ngroups);
+        const int64_t need = workspace_bytes(p);
+        if (need > 0 && (workspace == nullptr || workspace_bytes_ < need || !aligned(workspace, 256)))
+            return fail(name + ": workspace too small (need " + std::to_string(need) + " bytes)");
+        int rg = 0;
+        for (int g = 0; g < ngroups; ++g) {
+            a.g[g].tile_begin = rg;
+            rg += (int)((ns[g] + kSkinnyRows - 1) / kSkinnyRows);
+        }
+        a.splits = p.splits;
+        a.ksteps = p.steps;
+        a.ksteps_per_split = p.steps_per_split;
+        if (need > 0) a.partials = static_cast<float*>(workspace);
+        const int64_t wgs = (int64_t)rg * p.splits;
+        if (wgs > INT32_MAX / 2) return fail(name + ": problem too large");
+        if (check_hip(launch_skinny(a, (int)wgs, st), "dk_nf4_linear_fwd small-M launch")) return 1;
+        if (p.splits <= 1) return 0;
+        ReduceArgs r{};
+        r.partials = a.partials;
+        r.slab = m * ncols;
+        r.splits = p.splits;
+        r.m = (int)m;
+        r.ncols = (int)ncols;
+        r.nout = ngroups;
+        r.out_fp32 = 0;
+        for (int g = 0; g < ngroups; ++g)
+            r.o[g] = ReduceOut{groups[g].y, groups[g].ldy, a.g[g].bias, a.g[g].col_begin, (int32_t)ns[g]};
+        return check_hip(launch_splitk_reduce(r, st), "dk_nf4_linear_fwd split-K reduction");
     }
     bool fwd8_ok = k % 64 == 0;
     for (int g = 0; g < ngroups; ++g) fwd8_ok = fwd8_ok && k % groups[g].w.blocksize == 0;

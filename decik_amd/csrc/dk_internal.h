@@ -136,6 +136,12 @@ hipError_t launch_fwd(const FwdArgs& a, int mb, int grid, hipStream_t s);
 // GEMV for launches of at most kGemvMaxM token rows (no LoRA terms, no GLU epilogue, no split)
 constexpr int kGemvMaxM = 2;  // measured: the MFMA kernels are faster from 3 token rows on 7B shapes
 hipError_t launch_gemv(const FwdArgs& a, hipStream_t s);
+// Forward launches of few token rows (no LoRA terms, no GLU epilogue): nf4_skinny_kernel. A
+// work-group owns 64 weight rows; a.splits work-groups share them along the contraction, each
+// covering a.ksteps_per_split 128-wide super-steps; g[].tile_begin = each group's first 64-row
+// group. splits > 1: fp32 partial slabs, then splitk_reduce_kernel.
+constexpr int kSkinnyMaxM = 32;
+hipError_t launch_skinny(const FwdArgs& a, int grid, hipStream_t s);
 // 8-wave forward kernel (32 weight rows x 32*mb tokens per wave), mb = 8 or 9
 hipError_t launch_fwd8(const FwdArgs& a, int mb, int grid, hipStream_t s);
 hipError_t launch_bwd(const BwdArgs& a, int mb, int waves, int grid, hipStream_t s);
@@ -179,6 +185,10 @@ struct RopeArgs {
     int32_t hq, hk, d;
 };
 hipError_t launch_rope(const RopeArgs& a, bool backward, hipStream_t s);
+
+// Let `fn` launch with `bytes` of dynamic LDS on the current device (hipFuncSetAttribute once per
+// device and kernel; thread-safe). Needed above 64 KB.
+hipError_t allow_dynamic_lds(const void* fn, size_t bytes);
 
 // diagnostics
 hipError_t launch_mfma_peak(int64_t work_groups, int iters, float* out, hipStream_t s);

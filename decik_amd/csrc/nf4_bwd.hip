@@ -498,14 +498,9 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void nf4_bwd_kernel(const Bw
 
 template <int MB, int WAVES, bool NESTED>
 static hipError_t launch_bwd_t(const BwdArgs& a, int grid, hipStream_t s) {
-    static bool attr = false;
     const size_t sm = bwd_smem_bytes(MB, WAVES);
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void*)nf4_bwd_kernel<MB, WAVES, NESTED>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
+    const hipError_t e = allow_dynamic_lds((const void*)nf4_bwd_kernel<MB, WAVES, NESTED>, sm);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL((nf4_bwd_kernel<MB, WAVES, NESTED>), dim3(grid), dim3(64 * WAVES), sm, s, a);
     return hipGetLastError();
 }

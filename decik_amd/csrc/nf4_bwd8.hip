@@ -510,14 +510,8 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
 
 template <int MB, bool NESTED>
 static hipError_t launch_bwd8_t(const BwdArgs& a, int grid, hipStream_t s) {
-    static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void*)nf4_bwd8_kernel<MB, NESTED>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int)bwd8_smem_bytes(MB));
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
+    const hipError_t e = allow_dynamic_lds((const void*)nf4_bwd8_kernel<MB, NESTED>, bwd8_smem_bytes(MB));
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL((nf4_bwd8_kernel<MB, NESTED>), dim3(grid), dim3(kB8Threads),
                        bwd8_smem_bytes(MB), s, a);
     return hipGetLastError();

@@ -449,14 +449,8 @@ __global__ __launch_bounds__(kGemmThreads, MB <= 4 ? 2 : 1) void nf4_fwd_kernel(
 
 template <int MB, bool NESTED>
 static hipError_t launch_fwd_t(const FwdArgs& a, int grid, hipStream_t s) {
-    static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void*)nf4_fwd_kernel<MB, NESTED>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int)fwd_smem_bytes(MB, true));
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
+    const hipError_t e = allow_dynamic_lds((const void*)nf4_fwd_kernel<MB, NESTED>, fwd_smem_bytes(MB, true));
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL((nf4_fwd_kernel<MB, NESTED>), dim3(grid), dim3(kGemmThreads),
                        fwd_smem_bytes(MB, a.wide_stats != 0), s, a);
     return hipGetLastError();

@@ -386,14 +386,8 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
 
 template <int MB, bool NESTED>
 static hipError_t launch_fwd8_t(const FwdArgs& a, int grid, hipStream_t s) {
-    static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void*)nf4_fwd8_kernel<MB, NESTED>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int)fwd8_smem_bytes(MB));
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
+    const hipError_t e = allow_dynamic_lds((const void*)nf4_fwd8_kernel<MB, NESTED>, fwd8_smem_bytes(MB));
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL((nf4_fwd8_kernel<MB, NESTED>), dim3(grid), dim3(kF8Threads),
                        fwd8_smem_bytes(MB), s, a);
     return hipGetLastError();

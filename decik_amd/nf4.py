@@ -108,7 +108,7 @@ def _workspace_need(forward, m, k, ns):
     """dk_nf4_linear_{fwd,bwd}_workspace for these shapes, remembered per shape and forced plan
     (the query runs the planner; a step repeats the same few shapes)."""
     var = "DECIK_FWD_PLAN" if forward else "DECIK_BWD_PLAN"
-    key = (forward, m, k, tuple(ns), os.environ.get(var))
+    key = (forward, m, k, tuple(ns), os.environ.get(var), os.environ.get("DECIK_SMALL_M"))
     need = _NEED.get(key)
     if need is None:
         ns_arr = (ctypes.c_int64 * len(ns))(*ns)

@@ -136,11 +136,26 @@ def test_launch_plans():
     sw = launch_plan(True, 830, 8960, [1536], glu=True)
     assert sw["splits"] == 1
     assert sw["kernel"] == "nf4_bwd_kernel" or sw["rows_blocks"] == 4
-    # at most 2 token rows, no LoRA, no GLU epilogue: the GEMV kernel
-    assert launch_plan(False, 1, 3584, [18944])["kernel"] == "nf4_gemv_kernel"
-    assert launch_plan(False, 2, 3584, [18944])["kernel"] == "nf4_gemv_kernel"
-    assert launch_plan(False, 3, 3584, [18944])["kernel"] != "nf4_gemv_kernel"
-    assert launch_plan(False, 1, 3584, [18944], lora=True)["kernel"] != "nf4_gemv_kernel"
+    # at most 32 token rows, no LoRA, no GLU epilogue: the small-M kernel, split along the
+    # contraction only where the rows cannot fill the GPU
+    for m in (1, 2):
+        assert launch_plan(False, m, 3584, [18944])["kernel"] == "nf4_gemv_kernel"
+    for m in (3, 8, 32):
+        assert launch_plan(False, m, 3584, [18944])["kernel"] == "nf4_skinny_kernel"
+    assert launch_plan(False, 8, 3584, [18944])["splits"] == 1
+    assert launch_plan(False, 8, 18944, [3584])["splits"] > 1
+    assert launch_plan(False, 33, 3584, [18944])["kernel"] != "nf4_skinny_kernel"
+    assert launch_plan(False, 1, 3584, [18944], lora=True)["kernel"] not in ("nf4_skinny_kernel", "nf4_gemv_kernel")
+    old_sm = os.environ.get("DECIK_SMALL_M")
+    try:
+        os.environ["DECIK_SMALL_M"] = "skinny"
+        assert launch_plan(False, 1, 3584, [18944])["kernel"] == "nf4_skinny_kernel"
+        assert launch_plan(False, 3, 3584, [18944])["kernel"] == "nf4_skinny_kernel"
+    finally:
+        if old_sm is None:
+            os.environ.pop("DECIK_SMALL_M", None)
+        else:
+            os.environ["DECIK_SMALL_M"] = old_sm
     glu = launch_plan(False, 830, 1536, [8960, 8960], glu=True)
     assert glu["splits"] == 1 and glu["kernel"] == "nf4_fwd8_kernel"
     # k % blocksize != 0: the eight-wave forward kernel may not run

@@ -129,12 +129,74 @@ def test_eight_wave_backward_three_groups_lora(plan, device, monkeypatch):
     assert_close(dx, ref, max_rel=1e-4, mean_rel=1e-5, what=f"bwd8 three groups {plan}")
 
 
+@pytest.fixture
+def gemv(monkeypatch):
+    """Forward launches of 1-2 token rows take the GEMV kernel (the default; DECIK_SMALL_M unset)."""
+    monkeypatch.delenv("DECIK_SMALL_M", raising=False)
+
+
+@pytest.fixture
+def skinny(monkeypatch):
+    """Send every small-M forward launch, 1-2 token rows included, to the skinny kernel."""
+    monkeypatch.setenv("DECIK_SMALL_M", "skinny")
+
+
+@pytest.mark.parametrize("m", [1, 2, 5, 16, 17, 32])
+@pytest.mark.parametrize("nested,blocksize", CASES)
+def test_skinny_small_m(m, nested, blocksize, device, raw_statistics, skinny):
+    """The small-M kernel (forward launches of at most 32 token rows without LoRA terms): three
+    weights in one launch (320, 64 and 72 rows: the last row group of the third is partial),
+    with bias, statistics read raw, k = 1056 (the last 128-wide super-step is a quarter full)."""
+    from decik_amd.nf4 import launch_plan, linear_forward
+
+    assert launch_plan(False, m, 1056, [320, 64, 72])["kernel"] == "nf4_skinny_kernel"
+    items, refs = [], []
+    x = randn16((m, 1056), seed=160 + m, device=device)
+    for i, n in enumerate((320, 64, 72)):
+        packed, qs, w16 = make_weight((n, 1056), seed=161 + i + blocksize, device=device, nested=nested,
+                                      blocksize=blocksize)
+        b = randn16((n,), seed=165 + i, device=device, std=0.1)
+        items.append(dict(packed=packed, qs=qs, bias=b))
+        refs.append(O.linear_ref(x.cpu().numpy(), w16, b.cpu().numpy()))
+    ys = linear_forward(x, items)
+    for y, ref in zip(ys, refs):
+        assert_close(y, ref, what=f"skinny m={m} nested={nested} bs={blocksize}")
+
+
+@pytest.mark.parametrize("m", [1, 8, 32])
+@pytest.mark.parametrize("raw", [False, True])
+def test_skinny_split_k(m, raw, device, monkeypatch, skinny):
+    """Few rows and a long contraction (two weights of 128 and 64 rows, k = 8192): the small-M
+    kernel splits the contraction over work-groups (fp32 partial slabs, then the split-K
+    reduction adds bias and rounds), with cached block scales or raw nested statistics; the same
+    bits on a second call."""
+    from decik_amd import nf4
+    from decik_amd.nf4 import launch_plan, linear_forward
+
+    if raw:
+        monkeypatch.setattr(nf4, "_scales", lambda packed, qs, device: None)
+    plan = launch_plan(False, m, 8192, [128, 64])
+    assert plan["kernel"] == "nf4_skinny_kernel" and plan["splits"] > 1
+    x = randn16((m, 8192), seed=170 + m, device=device)
+    items, refs = [], []
+    for i, n in enumerate((128, 64)):
+        packed, qs, w16 = make_weight((n, 8192), seed=171 + i, device=device)
+        b = randn16((n,), seed=173 + i, device=device, std=0.1)
+        items.append(dict(packed=packed, qs=qs, bias=b))
+        refs.append(O.linear_ref(x.cpu().numpy(), w16, b.cpu().numpy()))
+    ys = linear_forward(x, items)
+    for y, ref in zip(ys, refs):
+        assert_close(y, ref, what=f"skinny split m={m} raw={raw}")
+    ys2 = linear_forward(x, items)
+    assert all(bool((a == b).all()) for a, b in zip(ys, ys2))
+
+
 @pytest.mark.parametrize("m", [1, 2])
 @pytest.mark.parametrize("nested,blocksize", CASES)
-def test_gemv_small_m(m, nested, blocksize, device, raw_statistics):
-    """The GEMV kernel (forward launches of at most 2 token rows without LoRA terms): three
-    weights in one launch (q/k/v-like, with bias), statistics read raw, k = 1056 (a row of 33
-    16-byte chunks: lane 0 takes two)."""
+def test_gemv_small_m(m, nested, blocksize, device, raw_statistics, gemv):
+    """The GEMV kernel (forward launches of at most 2 token rows without LoRA terms, when asked
+    for): three weights in one launch (q/k/v-like, with bias), statistics read raw, k = 1056 (a
+    row of 33 16-byte chunks: lane 0 takes two)."""
     from decik_amd.nf4 import launch_plan, linear_forward
 
     assert launch_plan(False, m, 1056, [320, 64, 64])["kernel"] == "nf4_gemv_kernel"
@@ -152,7 +214,7 @@ def test_gemv_small_m(m, nested, blocksize, device, raw_statistics):
 
 
 @pytest.mark.parametrize("m", [1, 2])
-def test_gemv_short_k_no_bias(m, device):
+def test_gemv_short_k_no_bias(m, device, gemv):
     """GEMV edges: k = 64 (two 16-byte chunks per row: lanes 2-63 hold no weights), two weights
     of 72 and 8 rows, no bias. Weight rows must be a multiple of 8: a 67-row weight is rejected
     with that message before anything runs."""
