@@ -326,19 +326,22 @@ GemmPlan plan_skinny(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
 
 // Forward launches of at most kSkinnyMaxM token rows without LoRA terms or the GLU epilogue run
 // the GEMV kernel (at most kGemvMaxM rows) or nf4_skinny_kernel, unless DECIK_FWD_PLAN forces an
-// MFMA plan. Measured on Qwen2.5-7B shapes: at 1-2 rows the GEMV is as fast on the large weights
-// and twice as fast on the small ones (fewer dependent steps per wave); from 3 rows on the
-// skinny kernel wins (7B gate at 8 rows: 26 us against 39 for the MFMA kernels). DECIK_SMALL_M
-// = gemv / skinny forces one of them for launches both may take (measurements, tests).
+// MFMA plan. Measured on Qwen2.5-7B shapes: at one row the GEMV is faster on every shape (gate
+// 18 us against 25, q/o 10 against 16), and at two rows on all but the long contraction of down;
+// from 3 rows on the skinny kernel wins (7B gate at 8 rows: 28 us against 39 for the MFMA
+// kernels). DECIK_SMALL_M = gemv / skinny forces one of them for launches both may take.
 bool small_m_forward(int64_t m, bool glu, bool lora) {
     if (glu || lora || m < 1 || m > kSkinnyMaxM) return false;
     const char* forced = std::getenv("DECIK_FWD_PLAN");
     return forced == nullptr || *forced == 0;
 }
-bool gemv_requested(int64_t m) {
+bool gemv_requested(int64_t m, int64_t k) {
     if (m > kGemvMaxM) return false;
     const char* v = std::getenv("DECIK_SMALL_M");
-    return v == nullptr || std::string(v) != "skinny";
+    if (v != nullptr && std::string(v) == "gemv") return true;
+    if (v != nullptr && std::string(v) == "skinny") return false;
+    // two rows of a long contraction (7B down): the skinny kernel's split is faster (24 vs 31 us)
+    return m == 1 || k <= 8192;
 }
 
 
@@ -438,7 +441,7 @@ int dk_nf4_linear_plan(int backward, int64_t m, int64_t k, const int64_t* ns, in
     if (backward) {
         p = plan_bwd(m, k, ns, ngroups, glu, single);
         kernel = p.bwd8 ? 3 : 2;
-    } else if (small_m_forward(m, glu, lora) && gemv_requested(m)) {
+    } else if (small_m_forward(m, glu, lora) && gemv_requested(m, k)) {
         p = GemmPlan{};
         p.waves = 4;
         p.splits = 1;
@@ -542,7 +545,7 @@ static int linear_fwd_impl(const std::string& name, const uint16_t* x, int64_t m
         a.ncols = (int32_t)ncols;
         if (ncols > INT32_MAX / 2) return fail(name + ": problem too large");
         const hipStream_t st = static_cast<hipStream_t>(stream);
-        if (gemv_requested(m)) return check_hip(launch_gemv(a, st), "dk_nf4_linear_fwd GEMV launch");
+        if (gemv_requested(m, k)) return check_hip(launch_gemv(a, st), "dk_nf4_linear_fwd GEMV launch");
         const GemmPlan p = plan_skinny(m, k, ns, ngroups);
         const int64_t need = workspace_bytes(p);
         if (need > 0 && (workspace == nullptr || workspace_bytes_ < need || !aligned(workspace, 256)))
