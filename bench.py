@@ -204,9 +204,35 @@ def bench_mlp(steps, warmup, device, n_sets=None, only=None):
         torch.cuda.synchronize()
         per[kind] = a.elapsed_time(b) / steps
     launch_ms = per
+    # The same launches on the raw double-quant statistics (no cached fp32 block scales): each
+    # kernel then decodes code2[q] * absmax2 + offset per block itself, and the GLU forward runs as
+    # the grouped launch plus the SwiGLU kernel (its fused epilogue takes plain statistics only).
+    uncached = {}
+    saved_scales = nf4._scales
+    nf4._scales = lambda packed, qs, device: None
+    try:
+        if only is not None:
+            launches = []  # counter runs (--only) time the cached launch alone
+        gate0, up0, h0 = nf4.glu_forward(x, dict(packed=layers[0]["gate"][0], qs=layers[0]["gate"][1]),
+                                         dict(packed=layers[0]["up"][0], qs=layers[0]["up"][1]))
+        dg0, du0 = nf4.linear_backward_swiglu(dict(packed=layers[0]["down"][0], qs=layers[0]["down"][1], dy=dy),
+                                              gate0, up0)
+        for kind in launches:
+            for i in range(2):
+                one(kind, i)
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for i in range(steps):
+                one(kind, i)
+            b.record()
+            torch.cuda.synchronize()
+            uncached[kind] = a.elapsed_time(b) / steps
+    finally:
+        nf4._scales = saved_scales
     step_flops = sum(flops.values())
     return dict(ms_step=ms_step, launch_ms=launch_ms, flops=flops, symbol=symbol,
-                step_flops=step_flops, n_sets=n_sets)
+                step_flops=step_flops, n_sets=n_sets, uncached_ms=uncached)
 
 
 def bench_dequant(iters, warmup, device, n_layers=8):
@@ -248,35 +274,48 @@ def bench_dequant(iters, warmup, device, n_layers=8):
         times.append(a.elapsed_time(b))
     ms = statistics.median(times)
     total_bytes = n_layers * sum(dequant_bytes(n, k) for _, n, k in QWEN15_SHAPES)
+    write_bytes = n_layers * sum(2 * n * k for _, n, k in QWEN15_SHAPES)
     launches = -(-len(descs) // 24)  # dk_nf4_dequant_batched: up to 24 weights per launch
-    return dict(ms=ms, bytes=total_bytes, gbs=total_bytes / ms / 1e6, launches=launches)
+    return dict(ms=ms, bytes=total_bytes, gbs=total_bytes / ms / 1e6, launches=launches,
+                read=total_bytes - write_bytes, write=write_bytes)
 
 
 def measured_peaks(device):
-    """This device's ceilings as measured here: HBM bandwidth of a device-to-device copy of 512 MiB
-    (bytes read + written / time, median of 10), and the dense fp16 MFMA rate of a register-only
-    loop of v_mfma_f32_32x32x16_f16 (dk_probe_mfma_f16, 1024 work-groups of 8 waves)."""
+    """This device's ceilings as measured here: HBM read, write and copy rates of dk_probe_hbm (the
+    dequantization kernel's access pattern: 16-byte lanes, four chunks in flight per thread; stores
+    non-temporal or plain, whichever is faster) over 1 GiB buffers (past the 256 MB Infinity
+    Cache), median of 7; and the
+    dense fp16 MFMA rate of a register-only loop of v_mfma_f32_32x32x16_f16 (dk_probe_mfma_f16,
+    1024 work-groups of 8 waves)."""
     import torch
 
     from decik_amd import _lib
 
-    src = torch.empty(128 << 20, dtype=torch.float32, device=device).fill_(1.0)
-    dst = torch.empty_like(src)
-    times = []
-    for i in range(12):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        dst.copy_(src)
-        b.record()
-        torch.cuda.synchronize()
-        if i >= 2:
-            times.append(a.elapsed_time(b))
-    copy_gbs = 2 * src.numel() * 4 / statistics.median(times) / 1e6
-    del src, dst
-    wgs, iters = 1024, 4096
-    out = torch.empty(wgs * 512, dtype=torch.float32, device=device)
     L = _lib.lib()
     stream = _lib.stream_of(device)
+    nbytes = 1 << 30
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device=device)
+    dst = torch.empty_like(src)
+    sums = torch.zeros(nbytes // 16384 + 1, dtype=torch.float32, device=device)
+    rates = {}
+    # write and copy: the better of non-temporal and plain stores (mode + 4)
+    for name, modes, moved in (("read", (0,), nbytes), ("write", (1, 5), nbytes), ("copy", (2, 6), 2 * nbytes)):
+        best = 0.0
+        for mode in modes:
+            times = []
+            for i in range(9):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                _lib.check(L.dk_probe_hbm(src.data_ptr(), dst.data_ptr(), nbytes, mode, sums.data_ptr(), stream))
+                b.record()
+                torch.cuda.synchronize()
+                if i >= 2:
+                    times.append(a.elapsed_time(b))
+            best = max(best, moved / statistics.median(times) / 1e6)
+        rates[name] = best
+    del src, dst, sums
+    wgs, iters = 1024, 4096
+    out = torch.empty(wgs * 512, dtype=torch.float32, device=device)
     _lib.check(L.dk_probe_mfma_f16(wgs, 64, out.data_ptr(), stream))
     torch.cuda.synchronize()
     times = []
@@ -289,8 +328,17 @@ def measured_peaks(device):
         times.append(a.elapsed_time(b))
     flops = wgs * 8 * iters * 8 * 2 * 32 * 32 * 16
     mfma_tf = flops / statistics.median(times) / 1e9
-    return dict(hbm_copy_gbs=round(copy_gbs, 1), mfma_f16_tflops=round(mfma_tf, 1),
-                method="512 MiB device copy; register-only v_mfma_f32_32x32x16_f16 loop")
+    return dict(hbm_read_gbs=round(rates["read"], 1), hbm_write_gbs=round(rates["write"], 1),
+                hbm_copy_gbs=round(rates["copy"], 1), mfma_f16_tflops=round(mfma_tf, 1),
+                method="dk_probe_hbm over 1 GiB (read / write / copy, bytes moved per second); "
+                       "register-only v_mfma_f32_32x32x16_f16 loop")
+
+
+def mixed_ceiling(peaks, read_bytes, write_bytes):
+    """The measured ceiling of a stream that reads and writes these amounts: each byte at its own
+    measured rate, t = R / read + W / write."""
+    t = read_bytes / peaks["hbm_read_gbs"] + write_bytes / peaks["hbm_write_gbs"]
+    return (read_bytes + write_bytes) / t
 
 
 def cpu_baseline(sample_steps=3):
@@ -305,6 +353,15 @@ def cpu_baseline(sample_steps=3):
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
+    cpu_model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
     rng = np.random.default_rng(0)
     ws = {}
     for name, n, k in [("gate", INTER, HIDDEN), ("up", INTER, HIDDEN), ("down", HIDDEN, INTER)]:
@@ -334,7 +391,7 @@ def cpu_baseline(sample_steps=3):
         times.append(time.perf_counter() - t)
     sec = statistics.median(times)
     flops = 6 * gemm_flops(INTER, HIDDEN)
-    return dict(value=round(flops / sec / 1e12, 4), unit="TFLOP/s", cores=cores, kind="port",
+    return dict(value=round(flops / sec / 1e12, 4), unit="TFLOP/s", cores=cores, cpu=cpu_model, kind="port",
                 sample=f"{sample_steps} full MLP fwd+bwd steps (M=830, 3 NF4 weights dequantized by "
                        f"the C oracle with {cores} OpenMP threads + torch fp32 CPU GEMMs), median "
                        f"{sec * 1e3:.0f} ms/step")
@@ -629,12 +686,17 @@ def main():
         config=dict(workload="Qwen2.5-1.5B MLP block fwd+bwd on NF4 weights: gate/up [8960,1536], "
                              "down [1536,8960], blocksize 64, double quant; X [830,1536]; SwiGLU; "
                              "dX through W; gate/up kept from the forward",
-                    m=M, hidden=HIDDEN, intermediate=INTER, weight_sets=mlp["n_sets"]),
+                    m=M, hidden=HIDDEN, intermediate=INTER, weight_sets=mlp["n_sets"],
+                    block_scales="fp32 scale of every 64-weight block cached per frozen weight (4 B per 64 "
+                                 "weights: +12.5% of the packed bytes, 0.5 bit/weight), computed once "
+                                 "before timing; kernels_uncached_nested times the raw double-quant path"),
         roofline=roofline,
         measured_peaks=peaks,
         kernels={k: dict(ms=round(v, 4),
                          tflops=round(mlp["flops"][k] / (v * 1e-3) / 1e12, 1) if mlp["flops"][k] else None)
                  for k, v in mlp["launch_ms"].items()},
+        kernels_uncached_nested={k: dict(ms=round(v, 4), tflops=round(mlp["flops"][k] / (v * 1e-3) / 1e12, 1))
+                                 for k, v in mlp["uncached_ms"].items()},
     )
     if deq is not None:
         line["dequant"] = dict(value=round(deq["gbs"], 1), unit="GB/s", ms=round(deq["ms"], 4),
@@ -643,7 +705,8 @@ def main():
                                roofline=dict(bound="hbm", achieved=round(deq["gbs"], 1),
                                              peak=HBM_PEAK_GBS, unit="GB/s",
                                              frac=round(deq["gbs"] / HBM_PEAK_GBS, 4),
-                                             frac_of_measured=round(deq["gbs"] / peaks["hbm_copy_gbs"], 4)))
+                                             measured_ceiling=round(mixed_ceiling(peaks, deq["read"], deq["write"]), 1),
+                                             frac_of_measured=round(deq["gbs"] / mixed_ceiling(peaks, deq["read"], deq["write"]), 4)))
     if c4 is not None:
         line["c4_stack_step"] = c4
     if c5 is not None:

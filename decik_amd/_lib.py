@@ -46,6 +46,7 @@ EXPORTS = {
     "dk_nf4_dequant": ([ctypes.POINTER(NF4Weight), c_vp, c_vp], c_i32),
     "dk_nf4_dequant_batched": ([ctypes.POINTER(NF4Weight), ctypes.POINTER(c_vp), c_i32, c_vp], c_i32),
     "dk_probe_mfma_f16": ([ctypes.c_int64, ctypes.c_int32, c_vp, c_vp], c_i32),
+    "dk_probe_hbm": ([c_vp, c_vp, c_i64, c_i32, c_vp, c_vp], c_i32),
     "dk_nf4_linear_plan": ([c_i32, c_i64, c_i64, ctypes.POINTER(c_i64), c_i32, c_i32, c_i32,
                             ctypes.POINTER(ctypes.c_int32)], c_i32),
     "dk_nf4_block_scales": ([ctypes.POINTER(NF4Weight), c_vp, c_vp], c_i32),

@@ -212,10 +212,10 @@ void finish_plan(GemmPlan& p, int64_t m, int64_t ncols) {
 
 // waves 4: nf4_fwd_kernel (two work-groups per CU for mb <= 4); waves 8: nf4_fwd8_kernel (one
 // work-group of eight waves per CU, 32*mb tokens x 256 weight rows)
+// (nf4_fwd_kernel<8> and nf4_bwd8_kernel<9> are not offered: they spilled registers to scratch)
 constexpr VariantCost kFwdVariants[] = {{1, 4, kFwdBN, 3, 2.35, 0.65},
                                        {2, 4, kFwdBN, 2, 2.23, 0.65},
                                        {4, 4, kFwdBN, 2, 3.10, 0.65},
-                                       {8, 4, kFwdBN, 1, 2.94, 0.85},
                                        {7, 8, kFwdBN, 1, 2.00, 0.90},
                                        {8, 8, kFwdBN, 1, 2.25, 0.90},
                                        {9, 8, kFwdBN, 1, 2.45, 0.90}};
@@ -227,8 +227,7 @@ constexpr VariantCost kBwdVariants[] = {{2, 4, 256, 2, 2.55, 0.90},
                                        {4, 8, 512, 1, 3.40, 1.0},
                                        {4, 8, 256, 1, 1.75, 0.90},
                                        {7, 8, 256, 1, 2.10, 0.90},
-                                       {8, 8, 256, 1, 2.25, 0.90},
-                                       {9, 8, 256, 1, 2.85, 0.85}};
+                                       {8, 8, 256, 1, 2.25, 0.90}};
 constexpr int kNumBwdVariants = sizeof(kBwdVariants) / sizeof(kBwdVariants[0]);
 constexpr int kNumBwdSwigluVariants = 4;  // nf4_bwd_kernel's and nf4_bwd8_kernel<4>
 static_assert(kBwdVariants[kNumBwdSwigluVariants - 1].bn == 256 && kBwdVariants[kNumBwdSwigluVariants - 1].rows_blocks == 4 &&
@@ -239,7 +238,7 @@ constexpr bool is_bwd8(const VariantCost& v) { return v.waves == 8 && v.bn == 25
 
 // The eight-wave variants come last: nf4_fwd8_kernel advances its load descriptors by whole
 // steps, so it needs k % 64 == 0 and blocks that do not straddle rows (k % blocksize == 0).
-constexpr int kNumFwd4Variants = 4;
+constexpr int kNumFwd4Variants = 3;
 static_assert(kFwdVariants[kNumFwd4Variants - 1].waves == 4 && kFwdVariants[kNumFwd4Variants].waves == 8,
               "four-wave variants first");
 
@@ -1029,6 +1028,17 @@ int dk_swiglu_bwd(const uint16_t* grad, const uint16_t* gate, const uint16_t* up
                                        reinterpret_cast<_Float16*>(dgate), reinterpret_cast<_Float16*>(dup),
                                        n, static_cast<hipStream_t>(stream)),
                      "dk_swiglu_bwd launch");
+}
+
+int dk_probe_hbm(const void* src, void* dst, int64_t bytes, int mode, float* sums, void* stream) {
+    g_error.clear();
+    const int kind = mode & 3;
+    if (bytes <= 0 || (bytes % 16) != 0 || mode < 0 || (mode & ~7) != 0 || kind > 2 || bytes / 16 / 1024 >= INT32_MAX ||
+        (kind != 1 && (src == nullptr || !aligned(src, 16))) || (kind != 0 && (dst == nullptr || !aligned(dst, 16))) ||
+        (kind == 0 && sums == nullptr))
+        return fail("dk_probe_hbm: bad arguments");
+    return check_hip(launch_hbm_probe(src, dst, bytes, mode, sums, static_cast<hipStream_t>(stream)),
+                     "dk_probe_hbm launch");
 }
 
 int dk_probe_mfma_f16(int64_t work_groups, int32_t iters, float* out, void* stream) {

@@ -145,7 +145,7 @@ hipError_t launch_skinny(const FwdArgs& a, int grid, hipStream_t s);
 // 8-wave forward kernel (32 weight rows x 32*mb tokens per wave), mb = 8 or 9
 hipError_t launch_fwd8(const FwdArgs& a, int mb, int grid, hipStream_t s);
 hipError_t launch_bwd(const BwdArgs& a, int mb, int waves, int grid, hipStream_t s);
-// 8-wave input-gradient kernel (32 output columns x 32*mb tokens per wave), mb = 4, 7, 8 or 9; the
+// 8-wave input-gradient kernel (32 output columns x 32*mb tokens per wave), mb = 4, 7 or 8; the
 // SwiGLU epilogue with mb = 4 only
 hipError_t launch_bwd8(const BwdArgs& a, int mb, int grid, hipStream_t s);
 hipError_t launch_splitk_reduce(const ReduceArgs& a, hipStream_t s);
@@ -192,6 +192,7 @@ hipError_t allow_dynamic_lds(const void* fn, size_t bytes);
 
 // diagnostics
 hipError_t launch_mfma_peak(int64_t work_groups, int iters, float* out, hipStream_t s);
+hipError_t launch_hbm_probe(const void* src, void* dst, int64_t bytes, int mode, float* sums, hipStream_t s);
 hipError_t launch_swiglu_fwd(const _Float16* g, const _Float16* u, _Float16* o, int64_t n,
                              hipStream_t s);
 hipError_t launch_swiglu_bwd(const _Float16* gr, const _Float16* g, const _Float16* u,

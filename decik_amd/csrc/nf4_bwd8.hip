@@ -7,7 +7,7 @@
 // nibbles of a byte per lane) and at most 4 token blocks, so each dequantized weight feeds at
 // most four MFMAs and the dequant costs far more issue slots than the matrix pipe leaves free.
 // Here a work-group is 8 waves (two per SIMD, one work-group per CU) on a tile of 32*MB tokens
-// (MB = 4, 7, 8 or 9) x 256 output columns; each wave owns 32 columns -- one A operand, one nibble
+// (MB = 4, 7 or 8) x 256 output columns; each wave owns 32 columns -- one A operand, one nibble
 // per lane and weight row -- and all 32*MB tokens, so each dequantized weight feeds MB MFMAs.
 //
 // A operand (A = W^T): lane l (l32 = l % 32, g = l / 32) serves A row l32 = output column
@@ -521,7 +521,7 @@ hipError_t launch_bwd8(const BwdArgs& a, int mb, int grid, hipStream_t s) {
     if (a.swiglu && (mb > 4 || a.splits > 1)) return hipErrorInvalidValue;  // SwiGLU: MB <= 4, no split
 #define X(T) \
     if (mb == T) return a.nested ? launch_bwd8_t<T, true>(a, grid, s) : launch_bwd8_t<T, false>(a, grid, s);
-    X(4) X(7) X(8) X(9)
+    X(4) X(7) X(8)
 #undef X
     return hipErrorInvalidValue;
 }

@@ -459,7 +459,7 @@ static hipError_t launch_fwd_t(const FwdArgs& a, int grid, hipStream_t s) {
 hipError_t launch_fwd(const FwdArgs& a, int mb, int grid, hipStream_t s) {
 #define X(T) \
     if (mb == T) return a.nested ? launch_fwd_t<T, true>(a, grid, s) : launch_fwd_t<T, false>(a, grid, s);
-    X(1) X(2) X(4) X(8)
+    X(1) X(2) X(4)
 #undef X
     return hipErrorInvalidValue;
 }

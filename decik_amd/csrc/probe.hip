@@ -1,4 +1,6 @@
-// Dense fp16 MFMA rate of this device: a loop of v_mfma_f32_32x32x16_f16 on register operands,
+// Measured ceilings of this device, for reporting the kernels against them.
+//
+// Dense fp16 MFMA rate: a loop of v_mfma_f32_32x32x16_f16 on register operands,
 // 8 waves per work-group, two A fragments x four B fragments per wave (eight independent
 // accumulators, each MFMA reusing the B operand of the previous one). No memory traffic in the
 // loop; the sums are stored so nothing is removed. The bench reports the GEMM kernels' rates
@@ -39,6 +41,55 @@ __global__ __launch_bounds__(kProbeThreads, 1) void mfma_peak_kernel(float* __re
 
 hipError_t launch_mfma_peak(int64_t work_groups, int iters, float* out, hipStream_t s) {
     hipLaunchKernelGGL(mfma_peak_kernel, dim3((unsigned)work_groups), dim3(kProbeThreads), 0, s, out, iters);
+    return hipGetLastError();
+}
+
+// HBM streaming rate with the access pattern of the dequantization kernel: each thread handles 4
+// 16-byte chunks 4 KB apart (every load or store instruction covers 1 KB contiguous per wave),
+// issues all its loads first, and stores non-temporally (mode bit 4: plain stores). mode 0: read
+// only (one float per work-group is written, so the loads stay); mode 1: write only (fill);
+// mode 2: copy.
+constexpr int kHbmThreads = 256, kHbmUnits = 4;
+
+__global__ __launch_bounds__(kHbmThreads) void hbm_probe_kernel(const u32x4_t* __restrict__ src, u32x4_t* __restrict__ dst,
+                                                                int64_t chunks, int mode, float* __restrict__ sums) {
+    const bool plain = (mode & 4) != 0;
+    mode &= 3;
+    const int64_t base = (int64_t)blockIdx.x * kHbmThreads * kHbmUnits + threadIdx.x;
+    u32x4_t v[kHbmUnits];
+    if (mode != 1) {
+#pragma unroll
+        for (int u = 0; u < kHbmUnits; ++u) {
+            const int64_t c = base + (int64_t)u * kHbmThreads;
+            v[u] = c < chunks ? __builtin_nontemporal_load(src + c) : u32x4_t{0u, 0u, 0u, 0u};
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < kHbmUnits; ++u) v[u] = u32x4_t{(uint32_t)u, 1u, 2u, 3u};
+    }
+    if (mode == 0) {
+        uint32_t x = 0;
+#pragma unroll
+        for (int u = 0; u < kHbmUnits; ++u) x ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+        if (x == 0x9E3779B9u) sums[blockIdx.x] = (float)x;  // practically never: keeps the loads
+        return;
+    }
+#pragma unroll
+    for (int u = 0; u < kHbmUnits; ++u) {
+        const int64_t c = base + (int64_t)u * kHbmThreads;
+        if (c < chunks) {
+            if (plain) dst[c] = v[u];
+            else __builtin_nontemporal_store(v[u], dst + c);
+        }
+    }
+}
+
+hipError_t launch_hbm_probe(const void* src, void* dst, int64_t bytes, int mode, float* sums, hipStream_t s) {
+    const int64_t chunks = bytes / 16;
+    const int64_t per_wg = (int64_t)kHbmThreads * kHbmUnits;
+    const int64_t grid = (chunks + per_wg - 1) / per_wg;
+    hipLaunchKernelGGL(hbm_probe_kernel, dim3((unsigned)grid), dim3(kHbmThreads), 0, s, (const u32x4_t*)src,
+                       (u32x4_t*)dst, chunks, mode, sums);
     return hipGetLastError();
 }
 

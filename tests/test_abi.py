@@ -163,11 +163,14 @@ def test_launch_plans():
     assert launch_plan(True, 830, 1536, [8960, 8960], no_split=True)["splits"] == 1
     old = os.environ.get("DECIK_BWD_PLAN")
     try:
-        os.environ["DECIK_BWD_PLAN"] = "9,3,8"
-        assert launch_plan(True, 830, 1536, [8960]) == dict(rows_blocks=9, waves=8, splits=3,
+        os.environ["DECIK_BWD_PLAN"] = "8,3,8"
+        assert launch_plan(True, 830, 1536, [8960]) == dict(rows_blocks=8, waves=8, splits=3,
                                                              kernel="nf4_bwd8_kernel")
-        # no SwiGLU epilogue with 9 token blocks: the forced plan does not apply
-        assert launch_plan(True, 830, 1536, [8960], glu=True)["rows_blocks"] != 9
+        # no SwiGLU epilogue with 8 token blocks: the forced plan does not apply
+        assert launch_plan(True, 830, 1536, [8960], glu=True)["rows_blocks"] != 8
+        # variants that spilled registers are not offered: a forced plan naming one is ignored
+        os.environ["DECIK_BWD_PLAN"] = "9,3,8"
+        assert launch_plan(True, 830, 1536, [8960])["rows_blocks"] != 9
         os.environ["DECIK_BWD_PLAN"] = "4,2,8"
         assert launch_plan(True, 830, 1536, [8960])["kernel"] == "nf4_bwd_kernel"
         os.environ["DECIK_BWD_PLAN"] = "4,2,8,256"
