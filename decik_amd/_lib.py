@@ -56,6 +56,9 @@ EXPORTS = {
     "dk_nf4_linear_bwd_workspace": ([c_i64, c_i64, ctypes.POINTER(c_i64), c_i32], c_i64),
     "dk_nf4_linear_bwd": ([ctypes.POINTER(LinearBwdGroup), c_i32, c_i64, c_i64, c_vp, c_i64, c_i32,
                            c_i32, c_vp, c_i64, c_vp], c_i32),
+    "dk_nf4_linear_rope_fwd_workspace": ([c_i64, c_i64, ctypes.POINTER(c_i64), c_i32], c_i64),
+    "dk_nf4_linear_rope_fwd": ([c_vp, c_i64, c_i64, c_i64, ctypes.POINTER(LinearFwdGroup), c_i32, c_i32, c_vp,
+                                c_vp, c_i32, c_i32, ctypes.POINTER(c_vp), c_vp, c_i64, c_vp], c_i32),
     "dk_nf4_linear_bwd_noalloc": ([ctypes.POINTER(LinearBwdGroup), c_i32, c_i64, c_i64, c_vp, c_i64, c_i32,
                                    c_i32, c_vp], c_i32),
     "dk_nf4_glu_fwd": ([c_vp, c_i64, c_i64, c_i64, ctypes.POINTER(LinearFwdGroup), c_i32, c_vp, c_i64,

@@ -150,17 +150,19 @@ double plan_time(const VariantCost& v, int64_t m, int64_t col_tiles, int64_t nco
 
 // Best (variant, splits) for a launch; col_tiles_of(v) gives the column tiles for variant v.
 // max_partial_bytes: plans whose fp32 partial slabs exceed it are not considered.
+// min_splits: plans with fewer splits are not considered (the RoPE epilogue lives in the split-K
+// reduction), unless the contraction has fewer steps.
 template <typename ColTiles>
 const VariantCost* choose_plan(const VariantCost* vs, int nv, int64_t m, int64_t ncols, int steps,
                                ColTiles col_tiles_of, int* splits, int max_splits = 32,
-                               int64_t max_partial_bytes = INT64_MAX) {
+                               int64_t max_partial_bytes = INT64_MAX, int min_splits = 1) {
     double best = 1e300;
     const VariantCost* pick = &vs[0];
     *splits = 1;
     for (int i = 0; i < nv; ++i) {
         const VariantCost& v = vs[i];
         const int max_s = steps < max_splits ? steps : max_splits;
-        for (int s = 1; s <= (max_s > 0 ? max_s : 1); ++s) {
+        for (int s = min_splits < max_s ? min_splits : 1; s <= (max_s > 0 ? max_s : 1); ++s) {
             const int per = steps > 0 ? (steps + s - 1) / s : 0;
             if (steps > 0 && (steps + per - 1) / per != s) continue;  // s splits must all get work
             if (s > 1 && (double)s * m * ncols * 4.0 > (double)max_partial_bytes) continue;
@@ -245,7 +247,7 @@ static_assert(kFwdVariants[kNumFwd4Variants - 1].waves == 4 && kFwdVariants[kNum
 // glu: two weights of ns[0] rows, a tile takes 128 rows of each; never split (the epilogue
 // needs the finished sums). fwd8_ok: the eight-wave kernel may run (see above).
 GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool glu, bool fwd8_ok,
-                  bool no_split = false) {
+                  bool no_split = false, int min_splits = 1) {
     GemmPlan p{};
     p.steps = (int)((k + kFwdBK - 1) / kFwdBK);
     p.n_tiles = 0;
@@ -262,10 +264,11 @@ GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool glu
     const int nv = fwd8_ok ? kNumFwdVariants : kNumFwd4Variants;
     const VariantCost* v = plan_override("DECIK_FWD_PLAN", kFwdVariants, nv, p.steps, &p.splits);
     if (v != nullptr && (glu || no_split)) p.splits = 1;
+    if (v != nullptr && p.splits < min_splits && p.steps >= min_splits) v = nullptr;
     if (v == nullptr) {
         const int64_t nt = p.n_tiles;
         v = choose_plan(kFwdVariants, nv, m, ncols, p.steps, [nt](const VariantCost&) { return nt; },
-                        &p.splits, (glu || no_split) ? 1 : 32);
+                        &p.splits, (glu || no_split) ? 1 : 32, INT64_MAX, min_splits);
     }
     p.mt = v->rows_blocks;
     p.waves = v->waves;
@@ -467,13 +470,23 @@ int64_t dk_nf4_linear_bwd_workspace(int64_t m, int64_t k, const int64_t* ns, int
 }  // extern "C"
 
 
-// The forward launch behind dk_nf4_linear_fwd and dk_nf4_glu_fwd. h != NULL: GLU mode (two groups
-// of one shape, plain narrow statistics; gate/up outputs optional). no_split: a single pass
-// (no workspace).
+// The RoPE epilogue of dk_nf4_linear_rope_fwd: groups in `mask` are rotated and stored head-major.
+struct RopeSpec {
+    const float* cos;
+    const float* sin;
+    int head_dim;
+    int mask;
+    uint16_t* const* out;
+};
+
+// The forward launch behind dk_nf4_linear_fwd, dk_nf4_glu_fwd and dk_nf4_linear_rope_fwd. h != NULL:
+// GLU mode (two groups of one shape, plain narrow statistics; gate/up outputs optional).
+// no_split: a single pass (no workspace). rope != NULL: at least two splits, the RoPE epilogue in
+// the split-K reduction (the small-M kernels are not used).
 static int linear_fwd_impl(const std::string& name, const uint16_t* x, int64_t m, int64_t k,
                            int64_t ldx, const dk_linear_fwd_group* groups, int ngroups, int lora_rank,
                            void* workspace, int64_t workspace_bytes_, void* stream, uint16_t* h,
-                           int64_t ldh, bool no_split) {
+                           int64_t ldh, bool no_split, const RopeSpec* rope = nullptr) {
     const bool glu = h != nullptr;
     if (ngroups < 1 || ngroups > kMaxGroups || groups == nullptr)
         return fail(name + ": need 1..4 groups");
@@ -503,8 +516,15 @@ static int linear_fwd_impl(const std::string& name, const uint16_t* x, int64_t m
         nested = G.w.nested;
         // one statistics slot per row block and step needs 64-wide steps inside one block
         if (G.w.blocksize < 64 || k % 64 != 0) a.wide_stats = 1;
-        if ((G.y == nullptr && !glu) || (G.y != nullptr && (!aligned(G.y, 16) || G.ldy < G.w.n || (G.ldy % 8) != 0)))
+        const bool roped = rope != nullptr && ((rope->mask >> g) & 1);
+        if (roped) {
+            if (rope->out == nullptr || rope->out[g] == nullptr || !aligned(rope->out[g], 16) ||
+                G.w.n % rope->head_dim != 0)
+                return fail(name + ": a rotated group needs a 16-byte aligned head-major output and n % head_dim == 0");
+        } else if ((G.y == nullptr && !glu) ||
+                   (G.y != nullptr && (!aligned(G.y, 16) || G.ldy < G.w.n || (G.ldy % 8) != 0))) {
             return fail(name + ": y must be 16-byte aligned with ldy >= n, ldy % 8 == 0");
+        }
         if (G.lora_u != nullptr && (lora_rank == 0 || G.lora_b == nullptr))
             return fail(name + ": LoRA needs lora_rank > 0 and lora_b");
         if (G.lora_u != nullptr && (!aligned(G.lora_u, 16) || !aligned(G.lora_b, 16)))
@@ -532,7 +552,7 @@ static int linear_fwd_impl(const std::string& name, const uint16_t* x, int64_t m
     if ((m - 1) * ldx + k >= INT32_MAX / 2) return fail(name + ": x too large");
     bool any_lora = false;
     for (int g = 0; g < ngroups; ++g) any_lora = any_lora || groups[g].lora_u != nullptr;
-    if (small_m_forward(m, glu, any_lora)) {
+    if (rope == nullptr && small_m_forward(m, glu, any_lora)) {
         // few token rows, no LoRA terms: one pass over the packed weights
         a.x = reinterpret_cast<const _Float16*>(x);
         a.ldx = ldx;
@@ -576,7 +596,8 @@ static int linear_fwd_impl(const std::string& name, const uint16_t* x, int64_t m
     }
     bool fwd8_ok = k % 64 == 0;
     for (int g = 0; g < ngroups; ++g) fwd8_ok = fwd8_ok && k % groups[g].w.blocksize == 0;
-    const GemmPlan p = plan_fwd(m, k, ns, ngroups, glu, fwd8_ok, no_split);
+    const GemmPlan p = plan_fwd(m, k, ns, ngroups, glu, fwd8_ok, no_split, rope != nullptr ? 2 : 1);
+    if (rope != nullptr && p.splits < 2) return fail(name + ": the RoPE epilogue needs k >= 128 (two contraction steps)");
     const int64_t need = workspace_bytes(p);
     if (need > 0 && (workspace == nullptr || workspace_bytes_ < need || !aligned(workspace, 256)))
         return fail(name + ": workspace too small (need " + std::to_string(need) + " bytes)");
@@ -614,11 +635,40 @@ static int linear_fwd_impl(const std::string& name, const uint16_t* x, int64_t m
     r.out_fp32 = 0;
     for (int g = 0; g < ngroups; ++g)
         r.o[g] = ReduceOut{groups[g].y, groups[g].ldy, a.g[g].bias, a.g[g].col_begin, (int32_t)ns[g]};
+    if (rope != nullptr) {
+        r.rope_mask = rope->mask;
+        r.head_dim = rope->head_dim;
+        r.cos = rope->cos;
+        r.sin = rope->sin;
+        for (int g = 0; g < ngroups; ++g)
+            if ((rope->mask >> g) & 1) r.rope_out[g] = reinterpret_cast<_Float16*>(rope->out[g]);
+    }
     return check_hip(launch_splitk_reduce(r, st), "dk_nf4_linear_fwd split-K reduction");
 }
 
 
 extern "C" {
+
+int64_t dk_nf4_linear_rope_fwd_workspace(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
+    if (ngroups < 1 || ngroups > kMaxGroups || ns == nullptr || m <= 0 || k <= 0) return 0;
+    return std::max(workspace_bytes(plan_fwd(m, k, ns, ngroups, false, true, false, 2)),
+                    workspace_bytes(plan_fwd(m, k, ns, ngroups, false, false, false, 2)));
+}
+
+int dk_nf4_linear_rope_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
+                           const dk_linear_fwd_group* groups, int ngroups, int lora_rank, const float* cos,
+                           const float* sin, int head_dim, int rope_mask, uint16_t* const* rope_out,
+                           void* workspace, int64_t workspace_bytes_, void* stream) {
+    g_error.clear();
+    const char* who = "dk_nf4_linear_rope_fwd";
+    if (head_dim <= 0 || head_dim % 16 != 0) return fail(std::string(who) + ": head_dim must be a positive multiple of 16");
+    if (rope_mask <= 0 || rope_mask >= (1 << ngroups)) return fail(std::string(who) + ": rope_mask must name some of the groups");
+    if (cos == nullptr || sin == nullptr) return fail(std::string(who) + ": cos and sin are required");
+    const RopeSpec rope{cos, sin, head_dim, rope_mask, rope_out};
+    return linear_fwd_impl(who, x, m, k, ldx, groups, ngroups, lora_rank, workspace, workspace_bytes_, stream,
+                           nullptr, 0, false, &rope);
+}
+
 
 int dk_nf4_linear_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
                       const dk_linear_fwd_group* groups, int ngroups, int lora_rank, void* workspace,

@@ -115,6 +115,15 @@ struct ReduceArgs {
     int32_t splits, m, ncols, nout;
     int32_t out_fp32;
     ReduceOut o[kMaxGroups];
+    // RoPE epilogue of the groups whose bit is set in rope_mask (fp16 out only): the group's
+    // output, rounded to fp16, is rotated with cos / sin (fp32 [m, head_dim]) as
+    // x cos + rotate_half(x) sin in fp32 and stored head-major to rope_out[g]
+    // [n_g / head_dim, m, head_dim] instead of o[g].out
+    int32_t rope_mask;
+    int32_t head_dim;
+    const float* cos;
+    const float* sin;
+    _Float16* rope_out[kMaxGroups];
 };
 
 // Launch plans (tile size, split-K factor) chosen by the host.

@@ -304,6 +304,80 @@ class QKVProjection(torch.autograd.Function):
         return (grad_x, None, *adapter_grads)
 
 
+class QKVRopeProjection(torch.autograd.Function):
+    """The attention inputs of a Qwen2 layer in one fused launch each way: q, k, v = x16 . W^T + b
+    (+ LoRA terms, like QKVProjection), with q and k rotated (RoPE) and stored head-major in the
+    launch's epilogue -- the projections and FusedQKRope's forward (solution/attn.py:27-66,
+    396-418) without a token-major q or k in memory. Returns (q [1, H, T, D], k [1, HK, T, D],
+    v [T, HK*D]). Backward: the RoPE transpose (the same kernel as FusedQKRope's backward,
+    solution/attn.py:69-86), then one fused launch for dX with the LoRA terms.
+
+    projections: (q, k, v) dicts as for QKVProjection; cos, sin fp32 [T, D]."""
+
+    @staticmethod
+    def forward(ctx, x16, projections, cos, sin, n_heads, n_kv_heads, *adapters):
+        from .rope import rope_qk_backward  # noqa: F401 (imported for the backward)
+
+        x2 = x16.reshape(-1, x16.shape[-1]).contiguous()
+        head_dim = cos.shape[-1]
+        items, saved, rank = [], [], 0
+        for p in projections:
+            it = dict(packed=p["packed"], qs=p["qs"], bias=p.get("bias"))
+            if p.get("lora_a") is not None:
+                a16 = p["lora_a"].to(torch.float16).contiguous()
+                b16 = p["lora_b"].to(torch.float16).contiguous()
+                u = lora_down(x2, a16)
+                it.update(lora_u=u, lora_b=b16, lora_scale=p["scaling"])
+                rank = a16.shape[0]
+                saved.append((u, a16, b16))
+            else:
+                saved.append(None)
+            items.append(it)
+        q, k, v = _nf4.linear_rope_forward(x2, items, cos, sin, head_dim, 3, lora_rank=rank)
+        ctx.projections, ctx.saved_lora, ctx.rank = projections, saved, rank
+        ctx.save_for_backward(x2, cos, sin)
+        ctx.x_shape = x16.shape
+        return q.unsqueeze(0), k.unsqueeze(0), v
+
+    @staticmethod
+    def backward(ctx, grad_q, grad_k, grad_v):
+        from .rope import rope_qk_backward
+
+        x2, cos, sin = ctx.saved_tensors
+        m, kdim = x2.shape
+        n_q, n_k = (int(p["qs"].shape[0]) for p in ctx.projections[:2])
+        head_dim = cos.shape[-1]
+        if grad_q is None:
+            grad_q = torch.zeros((n_q // head_dim, m, head_dim), dtype=torch.float16, device=x2.device)
+        if grad_k is None:
+            grad_k = torch.zeros((n_k // head_dim, m, head_dim), dtype=torch.float16, device=x2.device)
+        dq, dk = rope_qk_backward(grad_q, grad_k, cos, sin)
+        items, adapter_grads = [], []
+        for p, sv, g in zip(ctx.projections, ctx.saved_lora, (dq, dk, grad_v)):
+            if g is None:
+                g = torch.zeros((m, int(p["qs"].shape[0])), dtype=torch.float16, device=x2.device)
+            g16 = g.to(torch.float16).reshape(m, -1).contiguous()
+            it = dict(packed=p["packed"], qs=p["qs"], dy=g16)
+            if sv is not None:
+                u, a16, b16 = sv
+                gu, da, db = lora_grads(g16, u, x2, b16, p["scaling"])
+                it.update(lora_gu=gu, lora_a=a16)
+                adapter_grads += [da.to(p["lora_a"].dtype), db.to(p["lora_b"].dtype)]
+            items.append(it)
+        grad_x = _nf4.linear_backward(items, m, kdim, lora_rank=ctx.rank).reshape(ctx.x_shape)
+        return (grad_x, None, None, None, None, None, *adapter_grads)
+
+
+def qkv_rope_projection(x16, projections, cos, sin, n_heads, n_kv_heads):
+    """q [1, H, T, D], k [1, HK, T, D] (rotated, head-major) and v [T, HK*D] of x16 in one fused
+    launch each way (QKVRopeProjection). LoRA terms of one rank the kernels take (16 or 32)."""
+    adapters = []
+    for p in projections:
+        if p.get("lora_a") is not None:
+            adapters += [p["lora_a"], p["lora_b"]]
+    return QKVRopeProjection.apply(x16, projections, cos, sin, n_heads, n_kv_heads, *adapters)
+
+
 FUSED_RANKS = (16, 32)  # LoRA ranks the GEMM kernels' rank-16 MFMA slices take
 
 

@@ -160,6 +160,48 @@ def linear_forward(x16, items, lora_rank=0):
     return outs
 
 
+_ROPE_NEED = {}
+
+
+def linear_rope_forward(x16, items, cos, sin, head_dim, rope_mask, lora_rank=0):
+    """linear_forward with RoPE in the epilogue (dk_nf4_linear_rope_fwd): item g with bit g set in
+    rope_mask comes back rotated and head-major [n_g / head_dim, M, head_dim] fp16, the others
+    token-major [M, n_g]. cos / sin: fp32 [M, head_dim]."""
+    assert 1 <= len(items) <= _lib.MAX_GROUPS
+    dev = x16.device
+    x2 = _rows(x16)
+    m, k = x2.shape
+    groups = (LinearFwdGroup * len(items))()
+    keep, outs, ns = [x2], [], []
+    rope_ptrs = (ctypes.c_void_p * len(items))()
+    for g, it in enumerate(items):
+        qs = it["qs"]
+        n = int(qs.shape[0])
+        _fwd_group(groups[g], it, dev, keep)
+        if (rope_mask >> g) & 1:
+            out = torch.empty((n // head_dim, m, head_dim), dtype=torch.float16, device=dev)
+            rope_ptrs[g] = out.data_ptr()
+            groups[g].y, groups[g].ldy = None, n
+        else:
+            out = torch.empty((m, n), dtype=torch.float16, device=dev)
+            groups[g].y, groups[g].ldy = out.data_ptr(), n
+        outs.append(out)
+        ns.append(n)
+    key = (m, k, tuple(ns))
+    need = _ROPE_NEED.get(key)
+    if need is None:
+        arr = (ctypes.c_int64 * len(ns))(*ns)
+        need = int(lib().dk_nf4_linear_rope_fwd_workspace(m, k, arr, len(ns)))
+        _ROPE_NEED[key] = need
+    ws, ws_bytes = _lib.WORKSPACE.get(need, dev)
+    c = cos.reshape(m, head_dim).to(torch.float32).contiguous()
+    s = sin.reshape(m, head_dim).to(torch.float32).contiguous()
+    check(lib().dk_nf4_linear_rope_fwd(ptr(x2), m, k, x2.stride(0), groups, len(items), int(lora_rank), ptr(c),
+                                       ptr(s), int(head_dim), int(rope_mask), rope_ptrs, ptr(ws), ws_bytes,
+                                       stream_of(dev)))
+    return outs
+
+
 def launch_plan(backward, m, k, ns, glu=False, lora=False, no_split=False, blocksize=64):
     """The plan dk_nf4_linear_fwd / dk_nf4_linear_bwd choose for these shapes (dk_nf4_linear_plan):
     dict(rows_blocks, waves, splits, kernel). glu: the fused GLU forward or the SwiGLU epilogue of

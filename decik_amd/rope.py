@@ -64,4 +64,5 @@ class FusedQKRope(torch.autograd.Function):
     def backward(ctx, grad_q, grad_k):
         cos, sin = ctx.saved_tensors
         dq, dk = rope_qk_backward(grad_q, grad_k, cos, sin)
-        return dq, dq.clone(), dk, None, None, None, None
+        # q_lora may be absent (None) when the LoRA term is already in q_base
+        return dq, dq.clone() if ctx.needs_input_grad[1] else None, dk, None, None, None, None

@@ -21,6 +21,8 @@
  *                                               (solution/nf4.py:99-104); the summed input
  *                                               gradients of RecomputedMLP (solution/mlp.py:106-109)
  *                                               and of the LoRA branch (solution/attn.py:257)
+ *   dk_nf4_linear_rope_fwd                    <- the q/k/v projections + FusedQKRope's forward
+ *                                               (solution/attn.py:27-66, 396-418)
  *   dk_nf4_glu_fwd                            <- gate and up projections + _swiglu_fwd of the
  *                                               Qwen2 MLP forward (solution/mlp.py:69-71)
  *   dk_nf4_linear_bwd_swiglu                  <- matmul(g16, w_down) + _swiglu_bwd of the MLP
@@ -122,6 +124,22 @@ int64_t dk_nf4_linear_fwd_workspace(int64_t m, int64_t k, const int64_t* ns, int
 int dk_nf4_linear_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
                       const dk_linear_fwd_group* groups, int ngroups, int lora_rank,
                       void* workspace, int64_t workspace_bytes, void* stream);
+
+/* dk_nf4_linear_fwd with RoPE and the head-major store of the attention inputs in its epilogue
+ * (the q/k projections followed by skc_rope_fwd_kernel / FusedQKRope, solution/attn.py:27-66,
+ * 396-418): for each group g whose bit is set in rope_mask, the projection output, rounded to fp16,
+ * is rotated per token as x cos + rotate_half(x) sin in fp32 (the reference's order, no fused
+ * multiply-add) and stored fp16 head-major to rope_out[g] [n_g / head_dim, m, head_dim]; its
+ * groups[g].y is not used. Other groups are stored as by dk_nf4_linear_fwd. cos, sin: fp32
+ * [m, head_dim]; head_dim % 16 == 0; n_g % head_dim == 0. The contraction is always split (the
+ * rotation runs in the split-K reduction), so k >= 128 and a workspace of
+ * dk_nf4_linear_rope_fwd_workspace bytes is needed. The q/k/v projection of a Qwen2 layer is one
+ * call: groups q, k, v with rope_mask 3. */
+int64_t dk_nf4_linear_rope_fwd_workspace(int64_t m, int64_t k, const int64_t* ns, int ngroups);
+int dk_nf4_linear_rope_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
+                           const dk_linear_fwd_group* groups, int ngroups, int lora_rank, const float* cos,
+                           const float* sin, int head_dim, int rope_mask, uint16_t* const* rope_out,
+                           void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Gate and up projections and SwiGLU in one launch: groups[0] = gate, groups[1] = up (one shape
  * [n, k]; bias and LoRA as in dk_nf4_linear_fwd), h = fp16(silu(gate) * up) [m, n] (row stride

@@ -86,11 +86,11 @@ def test_noalloc_input_gradient_matches_allocating_entry(device):
         assert torch.equal(a, b), f"m={m}: the static-scratch entry differs from the allocating one"
         ref = _oracle([(gate[2], dg.cpu().numpy()), (up[2], du.cpu().numpy())], m, np.arange(1536))
         assert_close(b, ref, what=f"noalloc m={m}")
-    # Qwen2.5-7B gate/up at M = 830: the allocating plan's partials exceed the scratch
+    # Qwen2.5-7B gate/up input gradient at the first token count whose allocating plan's
+    # partials exceed the scratch (1660 with the present cost tables: five splits, 113 MiB)
     gate7 = make_weight((18944, 3584), seed=305, device=device)
     up7 = make_weight((18944, 3584), seed=306, device=device)
-    m = 830
-    assert _workspace_need(m, 3584, [18944, 18944]) > scratch
+    m = next(t for t in (830, 1660, 3000, 8192) if _workspace_need(t, 3584, [18944, 18944]) > scratch)
     dg = randn16((m, 18944), seed=307, device=device, std=1e-2)
     du = randn16((m, 18944), seed=308, device=device, std=1e-2)
     items = [(gate7[0], gate7[1], dg), (up7[0], up7[1], du)]
