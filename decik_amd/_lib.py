@@ -39,7 +39,8 @@ class LinearFwdGroup(ctypes.Structure):
 
 class LinearBwdGroup(ctypes.Structure):
     _fields_ = [("w", NF4Weight), ("dy", c_vp), ("lddy", c_i64), ("lora_gu", c_vp),
-                ("lora_a", c_vp)]
+                ("lora_a", c_vp), ("lora_keep", c_vp), ("lora_keep_scale", ctypes.c_float),
+                ("reserved", c_i32)]
 
 
 EXPORTS = {
@@ -66,6 +67,9 @@ EXPORTS = {
     "dk_nf4_linear_bwd_swiglu": ([ctypes.POINTER(LinearBwdGroup), c_i64, c_i64, c_i32, c_vp, c_vp, c_i64,
                                   c_vp, c_vp, c_i64, c_vp], c_i32),
     "dk_lora_down": ([c_vp, c_i64, c_i64, c_i64, c_vp, c_i32, c_vp, c_vp], c_i32),
+    "dk_lora_down_dropout": ([c_vp, c_i32, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp], c_i32),
+    "dk_lora_bwd_dropout": ([c_vp, c_i64, c_vp, c_vp, c_i32, c_i64, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i32,
+                             c_f32, c_vp, c_vp, c_vp, c_vp], c_i32),
     "dk_lora_bwd": ([c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_i32, c_f32, c_vp,
                      c_vp, c_vp, c_vp], c_i32),
     "dk_lora_keep_pack": ([c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp], c_i32),

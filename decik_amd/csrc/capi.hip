@@ -756,12 +756,19 @@ static int linear_bwd_impl(const std::string& name, const dk_linear_bwd_group* g
             return fail(name + ": LoRA needs lora_rank > 0, lora_a and 16-byte aligned gu");
         if (G.lora_gu != nullptr && (m * lora_rank * 2 >= INT32_MAX || k * lora_rank * 2 >= INT32_MAX))
             return fail(name + ": LoRA operands larger than 2^31 bytes");
+        if (G.lora_keep != nullptr && (G.lora_gu == nullptr || (k % 8) != 0 || m * (k / 8) >= INT32_MAX / 2 ||
+                                       !(G.lora_keep_scale >= 0.0f)))
+            return fail(name + ": lora_keep needs a LoRA term, k % 8 == 0, fewer than 2^30 bytes and a scale >= 0");
+        if (G.lora_keep != nullptr && sw != nullptr)
+            return fail(name + ": the SwiGLU epilogue takes no dropout-masked LoRA term");
         if (G.w.blocksize < 64 || k % 64 != 0) a.wide_stats = 1;
         a.g[g].dy = reinterpret_cast<const _Float16*>(G.dy);
         a.g[g].lddy = (int32_t)G.lddy;
         a.g[g].dy_bytes = m > 0 ? (uint32_t)(((m - 1) * G.lddy + G.w.n) * 2) : 0;
         a.g[g].lora_gu = reinterpret_cast<const _Float16*>(G.lora_gu);
         a.g[g].lora_a = reinterpret_cast<const _Float16*>(G.lora_a);
+        a.g[g].lora_keep = G.lora_keep;
+        a.g[g].lora_keep_scale = G.lora_keep_scale;
         a.g[g].step_begin = step;
         a.g[g].nsteps = (int)((G.w.n + kBwdBC - 1) / kBwdBC);
         step += a.g[g].nsteps;
@@ -890,45 +897,82 @@ int dk_nf4_linear_bwd_swiglu(const dk_linear_bwd_group* group, int64_t m, int64_
                            stream, &sw);
 }
 
+}  // extern "C"
+
+// dk_lora_down / dk_lora_down_dropout: x fp16 or fp32 (x32), keep null or packed dropout bits
+static int lora_down_impl(const std::string& who, const void* x, bool x32, int64_t m, int64_t k, int64_t ldx,
+                          const uint8_t* keep, const float* keep_scale, const uint16_t* a, int rank, uint16_t* u,
+                          void* stream) {
+    if (rank != 16 && rank != 32) return fail(who + ": rank must be 16 or 32");
+    if (m < 0 || k <= 0 || (k % 8) != 0 || ldx < k || (ldx % 8) != 0)
+        return fail(who + ": k and ldx must be multiples of 8");
+    if (x == nullptr || a == nullptr || u == nullptr || !aligned(x, 16) || !aligned(a, 16))
+        return fail(who + ": x and a must be 16-byte aligned");
+    if (keep != nullptr && keep_scale == nullptr) return fail(who + ": keep bits need keep_scale");
+    // 32-bit byte offsets (with a 32-row margin for the tile past the last row)
+    if ((m + 32) * ldx * (x32 ? 4 : 2) >= INT32_MAX || k * rank * 2 >= INT32_MAX || (m + 32) * (k / 8) >= INT32_MAX)
+        return fail(who + ": tensors too large");
+    return check_hip(launch_lora_down(x, x32, m, k, ldx, keep, keep_scale, reinterpret_cast<const _Float16*>(a),
+                                      rank, reinterpret_cast<_Float16*>(u), static_cast<hipStream_t>(stream)),
+                     (who + " launch").c_str());
+}
+
+static int lora_bwd_impl(const std::string& who, const uint16_t* dy, int64_t lddy, const uint16_t* u, const void* x,
+                         bool x32, int64_t ldx, const uint8_t* keep, const float* keep_scale, const uint16_t* b,
+                         int64_t m, int64_t n, int64_t k, int rank, float scale, uint16_t* gu, float* da, float* db,
+                         void* stream) {
+    if (rank != 16 && rank != 32) return fail(who + ": rank must be 16 or 32");
+    if (m < 0 || n <= 0 || k <= 0 || lddy < n || ldx < k)
+        return fail(who + ": bad shapes");
+    if (dy == nullptr || u == nullptr || x == nullptr || b == nullptr || gu == nullptr)
+        return fail(who + ": null pointer");
+    if (!aligned(u, 16) || !aligned(b, 16) || !aligned(gu, 16) || !aligned(dy, 16) || !aligned(x, x32 ? 4 : 2))
+        return fail(who + ": dy, u, b, gu must be 16-byte aligned (x aligned to its element)");
+    if ((n % 8) != 0 || (lddy % 8) != 0) return fail(who + ": n and lddy must be multiples of 8");
+    if (keep != nullptr && (keep_scale == nullptr || (k % 8) != 0))
+        return fail(who + ": keep bits need keep_scale and k % 8 == 0");
+    // 32-bit byte offsets (with a 32-row margin for the tile past the last row)
+    if ((m + 32) * lddy * 2 >= INT32_MAX || (m + 32) * ldx * (x32 ? 4 : 2) >= INT32_MAX ||
+        (m + 32) * rank * 2 >= INT32_MAX || n * rank * 2 >= INT32_MAX || (m + 32) * (k / 8) >= INT32_MAX)
+        return fail(who + ": tensors too large");
+    return check_hip(launch_lora_bwd(reinterpret_cast<const _Float16*>(dy), lddy,
+                                     reinterpret_cast<const _Float16*>(u), x, x32, ldx, keep, keep_scale,
+                                     reinterpret_cast<const _Float16*>(b), m, n, k, rank, scale,
+                                     reinterpret_cast<_Float16*>(gu), da, db,
+                                     static_cast<hipStream_t>(stream)),
+                     (who + " launch").c_str());
+}
+
+extern "C" {
+
 int dk_lora_down(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const uint16_t* a, int rank,
                  uint16_t* u, void* stream) {
     g_error.clear();
-    if (rank != 16 && rank != 32) return fail("dk_lora_down: rank must be 16 or 32");
-    if (m < 0 || k <= 0 || (k % 8) != 0 || ldx < k || (ldx % 8) != 0)
-        return fail("dk_lora_down: k and ldx must be multiples of 8");
-    if (x == nullptr || a == nullptr || u == nullptr || !aligned(x, 16) || !aligned(a, 16))
-        return fail("dk_lora_down: x and a must be 16-byte aligned");
-    // 32-bit byte offsets (with a 32-row margin for the tile past the last row)
-    if ((m + 32) * ldx * 2 >= INT32_MAX || k * rank * 2 >= INT32_MAX) return fail("dk_lora_down: tensors too large");
-    return check_hip(launch_lora_down(reinterpret_cast<const _Float16*>(x), m, k, ldx,
-                                      reinterpret_cast<const _Float16*>(a), rank,
-                                      reinterpret_cast<_Float16*>(u), static_cast<hipStream_t>(stream)),
-                     "dk_lora_down launch");
+    return lora_down_impl("dk_lora_down", x, false, m, k, ldx, nullptr, nullptr, a, rank, u, stream);
+}
+
+int dk_lora_down_dropout(const void* x, int x_fp32, int64_t m, int64_t k, int64_t ldx, const uint8_t* keep_bits,
+                         const float* keep_scale, const uint16_t* a, int rank, uint16_t* u, void* stream) {
+    g_error.clear();
+    return lora_down_impl("dk_lora_down_dropout", x, x_fp32 != 0, m, k, ldx, keep_bits, keep_scale, a, rank, u,
+                          stream);
 }
 
 int dk_lora_bwd(const uint16_t* dy, int64_t lddy, const uint16_t* u, const uint16_t* x, int64_t ldx,
                 const uint16_t* b, int64_t m, int64_t n, int64_t k, int rank, float scale, uint16_t* gu,
                 float* da, float* db, void* stream) {
     g_error.clear();
-    if (rank != 16 && rank != 32) return fail("dk_lora_bwd: rank must be 16 or 32");
-    if (m < 0 || n <= 0 || k <= 0 || lddy < n || ldx < k)
-        return fail("dk_lora_bwd: bad shapes");
-    if (dy == nullptr || u == nullptr || x == nullptr || b == nullptr || gu == nullptr)
-        return fail("dk_lora_bwd: null pointer");
-    if (!aligned(u, 16) || !aligned(b, 16) || !aligned(gu, 16) || !aligned(dy, 16))
-        return fail("dk_lora_bwd: dy, u, b, gu must be 16-byte aligned");
-    if ((n % 8) != 0 || (lddy % 8) != 0) return fail("dk_lora_bwd: n and lddy must be multiples of 8");
-    // 32-bit byte offsets (with a 32-row margin for the tile past the last row)
-    if ((m + 32) * lddy * 2 >= INT32_MAX || (m + 32) * ldx * 2 >= INT32_MAX || (m + 32) * rank * 2 >= INT32_MAX ||
-        n * rank * 2 >= INT32_MAX)
-        return fail("dk_lora_bwd: tensors too large");
-    return check_hip(launch_lora_bwd(reinterpret_cast<const _Float16*>(dy), lddy,
-                                     reinterpret_cast<const _Float16*>(u),
-                                     reinterpret_cast<const _Float16*>(x), ldx,
-                                     reinterpret_cast<const _Float16*>(b), m, n, k, rank, scale,
-                                     reinterpret_cast<_Float16*>(gu), da, db,
-                                     static_cast<hipStream_t>(stream)),
-                     "dk_lora_bwd launch");
+    return lora_bwd_impl("dk_lora_bwd", dy, lddy, u, x, false, ldx, nullptr, nullptr, b, m, n, k, rank, scale, gu,
+                         da, db, stream);
+}
+
+int dk_lora_bwd_dropout(const uint16_t* dy, int64_t lddy, const uint16_t* u, const void* x, int x_fp32,
+                        int64_t ldx, const uint8_t* keep_bits, const float* keep_scale, const uint16_t* b,
+                        int64_t m, int64_t n, int64_t k, int rank, float scale, uint16_t* gu, float* da,
+                        float* db, void* stream) {
+    g_error.clear();
+    return lora_bwd_impl("dk_lora_bwd_dropout", dy, lddy, u, x, x_fp32 != 0, ldx, keep_bits, keep_scale, b, m, n,
+                         k, rank, scale, gu, da, db, stream);
 }
 
 int dk_lora_keep_pack(const uint8_t* keep_q, const uint8_t* keep_v, uint8_t* bits_q, uint8_t* bits_v,

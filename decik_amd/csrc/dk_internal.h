@@ -75,6 +75,8 @@ struct BwdGroupDev {
     uint32_t dy_bytes;
     const _Float16* lora_gu;
     const _Float16* lora_a;
+    const uint8_t* lora_keep;  // dropout keep bits of the LoRA branch's input [m, k / 8], or null
+    float lora_keep_scale;     // 1 / (1 - p)
     int32_t step_begin;  // first contraction step of this group
     int32_t nsteps;
 };
@@ -160,11 +162,14 @@ hipError_t launch_bwd8(const BwdArgs& a, int mb, int grid, hipStream_t s);
 hipError_t launch_splitk_reduce(const ReduceArgs& a, hipStream_t s);
 
 // LoRA and SwiGLU helpers.
-hipError_t launch_lora_down(const _Float16* x, int64_t m, int64_t k, int64_t ldx, const _Float16* a,
-                            int rank, _Float16* u, hipStream_t s);
-hipError_t launch_lora_bwd(const _Float16* dy, int64_t lddy, const _Float16* u, const _Float16* x,
-                           int64_t ldx, const _Float16* b, int64_t m, int64_t n, int64_t k, int rank,
-                           float scale, _Float16* gu, float* da, float* db, hipStream_t s);
+// x: fp16 or fp32 (x32) [m, ldx]; keep: packed dropout bits [m, k / 8] with keep_scale a device
+// fp32 scalar, or null (no dropout)
+hipError_t launch_lora_down(const void* x, bool x32, int64_t m, int64_t k, int64_t ldx, const uint8_t* keep,
+                            const float* keep_scale, const _Float16* a, int rank, _Float16* u, hipStream_t s);
+hipError_t launch_lora_bwd(const _Float16* dy, int64_t lddy, const _Float16* u, const void* x, bool x32,
+                           int64_t ldx, const uint8_t* keep, const float* keep_scale, const _Float16* b,
+                           int64_t m, int64_t n, int64_t k, int rank, float scale, _Float16* gu, float* da,
+                           float* db, hipStream_t s);
 hipError_t launch_lora_keep_pack(const uint8_t* kq, const uint8_t* kv, uint8_t* bq, uint8_t* bv,
                                  int64_t nbytes, hipStream_t s);
 hipError_t launch_lora_dropout_inputs(const void* x, bool x32, const uint8_t* bq, const uint8_t* bv,

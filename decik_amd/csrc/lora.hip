@@ -13,6 +13,12 @@
 // order, so the summation order is fixed (no atomics) and every call gives the same bits.
 // GU and dB are one launch (both read dY); dA, which needs GU, is a second one.
 //
+// X, as lora_down and lora_da read it, is the branch's input: fp16 or fp32 storage, optionally
+// through dropout (LoRAPairFromNorm's packed path, solution/attn.py:153-165, 219-223, 241-243):
+// fp16(x * (keep * scale)) with keep a packed bit ([m, k / 8] bytes, bit j % 8 of byte j / 8)
+// and scale = 1 / (1 - p) a device scalar, in fp32 and in that order, as skc_lora_inputs_kernel
+// rounds it; fp32 without dropout is fp16(x). The dropped-out input is never stored.
+//
 // MFMA operand layout (16x16x32, lane l, i = l % 16, g = l / 16): A operand A[i][8 g + e],
 // B operand B[8 g + e][i], result D[4 g + r][i], e = 0..7, r = 0..3. Operands whose 8 contraction
 // values are contiguous in memory are one 16-byte load; the others (the token-contracted products
@@ -55,16 +61,107 @@ __device__ __forceinline__ float tile_sum(const float* red, int t) {
     return s;
 }
 
+// The branch input X (see above): descriptors and the keep scale.
+struct XInput {
+    rsrc_t x, keep;
+    float scale;
+    int ldx, kbytes;  // row strides: x in elements, keep in bytes (k / 8)
+};
+
+template <bool X32, bool KEEP>
+__device__ __forceinline__ XInput x_input(const void* x, int m, int k, int ldx, const uint8_t* keep,
+                                          const float* keep_scale) {
+    XInput in;
+    in.x = make_rsrc(x, (uint32_t)(((int64_t)(m - 1) * ldx + k) * (X32 ? 4 : 2)));
+    in.keep = make_rsrc(keep, KEEP ? (uint32_t)m * (uint32_t)(k >> 3) : 0u);
+    in.scale = KEEP ? *keep_scale : 0.0f;
+    in.ldx = ldx;
+    in.kbytes = k >> 3;
+    return in;
+}
+
+// x * (keep * scale) for the 8 values of one keep byte's bits sh(e) (dropout), then fp16
+template <bool KEEP>
+__device__ __forceinline__ half8_t drop_round(const float (&xf)[8], const uint32_t (&bits)[8], float scale) {
+    half8_t o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        if constexpr (KEEP) {
+            float v = xf[e] * ((float)(bits[e] & 1u) * scale);
+            // the product is rounded to fp32 and then to fp16, as the reference rounds it: the
+            // empty asm keeps the compiler from folding multiply and conversion into one
+            // v_fma_mix (a single rounding, which differs at fp16 ties)
+            asm("" : "+v"(v));
+            o[e] = (_Float16)v;
+        } else
+
+            o[e] = (_Float16)xf[e];
+    }
+    return o;
+}
+
+// X[row, kk .. kk + 7] (kk % 8 == 0); zeros unless ok
+template <bool X32, bool KEEP>
+__device__ __forceinline__ half8_t x_row8(const XInput& in, int row, int kk, bool ok) {
+    if constexpr (!X32 && !KEEP)
+        return __builtin_bit_cast(half8_t, bload128(in.x, off_if(ok, (uint32_t)(row * in.ldx + kk) * 2u)));
+    float xf[8];
+    if constexpr (X32) {
+        const uint32_t o = (uint32_t)(row * in.ldx + kk) * 4u;
+        const float4_t lo = __builtin_bit_cast(float4_t, bload128(in.x, off_if(ok, o)));
+        const float4_t hi = __builtin_bit_cast(float4_t, bload128(in.x, off_if(ok, o + 16u)));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            xf[e] = lo[e];
+            xf[e + 4] = hi[e];
+        }
+    } else {
+        const half8_t h = __builtin_bit_cast(half8_t, bload128(in.x, off_if(ok, (uint32_t)(row * in.ldx + kk) * 2u)));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xf[e] = (float)h[e];
+    }
+    uint32_t bits[8];
+    if constexpr (KEEP) {
+        const uint32_t byte = bload8(in.keep, off_if(ok, (uint32_t)(row * in.kbytes + (kk >> 3))));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) bits[e] = byte >> e;
+    }
+    return drop_round<KEEP>(xf, bits, in.scale);
+}
+
+// X[mm + e, col] for e < valid (zeros past it, or everywhere unless ok0)
+template <bool X32, bool KEEP>
+__device__ __forceinline__ half8_t x_col8(const XInput& in, int mm, int col, bool ok0, int valid) {
+    if constexpr (!X32 && !KEEP)
+        return gather8(in.x, (uint32_t)(mm * in.ldx + col) * 2u, 2u * (uint32_t)in.ldx, ok0, valid);
+    float xf[8];
+    uint32_t bits[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const bool ok = ok0 && e < valid;
+        const uint32_t o = (uint32_t)((mm + e) * in.ldx + col);
+        if constexpr (X32)
+            xf[e] = bloadf(in.x, off_if(ok, o * 4u));
+        else
+            xf[e] = (float)__builtin_bit_cast(_Float16, (uint16_t)bload16(in.x, off_if(ok, o * 2u)));
+        if constexpr (KEEP)
+            bits[e] = bload8(in.keep, off_if(ok, (uint32_t)((mm + e) * in.kbytes + (col >> 3)))) >> (col & 7);
+    }
+    return drop_round<KEEP>(xf, bits, in.scale);
+}
+
 // U[m, t] = fp16(sum_k X[m, k] A[t, k]): A operand X (16 tokens), B operand A^T (rows of A).
-template <int R>
-__global__ __launch_bounds__(kLoraThreads) void lora_down_kernel(const _Float16* __restrict__ x, int m, int k,
-                                                                 int ldx, const _Float16* __restrict__ a,
+template <int R, bool X32, bool KEEP>
+__global__ __launch_bounds__(kLoraThreads) void lora_down_kernel(const void* __restrict__ x, int m, int k,
+                                                                 int ldx, const uint8_t* __restrict__ keep,
+                                                                 const float* __restrict__ keep_scale,
+                                                                 const _Float16* __restrict__ a,
                                                                  _Float16* __restrict__ u) {
     __shared__ float red[kLoraWaves * 16 * R];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int i = lane & 15, g = lane >> 4;
     const int m0 = blockIdx.x * 16;
-    const rsrc_t xr = make_rsrc(x, (uint32_t)(((int64_t)(m - 1) * ldx + k) * 2));
+    const XInput xin = x_input<X32, KEEP>(x, m, k, ldx, keep, keep_scale);
     const rsrc_t ar = make_rsrc(a, (uint32_t)R * (uint32_t)k * 2u);
     const bool rok = m0 + i < m;
     float4_t acc[R / 16];
@@ -77,7 +174,7 @@ __global__ __launch_bounds__(kLoraThreads) void lora_down_kernel(const _Float16*
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
             const int kk = 32 * (kc + q * kLoraWaves) + 8 * g;  // k % 8 == 0: wholly inside or past the end
-            xa[q] = __builtin_bit_cast(half8_t, bload128(xr, off_if(rok && kk < k, (uint32_t)((m0 + i) * ldx + kk) * 2u)));
+            xa[q] = x_row8<X32, KEEP>(xin, m0 + i, kk, rok && kk < k);
 #pragma unroll
             for (int h = 0; h < R / 16; ++h)
                 ab[q][h] = __builtin_bit_cast(half8_t, bload128(ar, off_if(kk < k, (uint32_t)((16 * h + i) * k + kk) * 2u)));
@@ -169,16 +266,18 @@ __global__ __launch_bounds__(kLoraThreads) void lora_gu_db_kernel(const _Float16
 
 // dA[t, k] = sum_m GU[m, t] X[m, k]: work-group = 16 columns k (all R rows t); A operand GU^T,
 // B operand X, both gathered along the token dimension.
-template <int R>
+template <int R, bool X32, bool KEEP>
 __global__ __launch_bounds__(kLoraThreads) void lora_da_kernel(const _Float16* __restrict__ gu,
-                                                               const _Float16* __restrict__ x, int ldx, int m,
+                                                               const void* __restrict__ x, int ldx,
+                                                               const uint8_t* __restrict__ keep,
+                                                               const float* __restrict__ keep_scale, int m,
                                                                int k, float* __restrict__ da) {
     __shared__ float red[kLoraWaves * 16 * R];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int i = lane & 15, g = lane >> 4;
     const int k0 = blockIdx.x * 16;
     const rsrc_t gr = make_rsrc(gu, (uint32_t)m * (uint32_t)R * 2u);
-    const rsrc_t xr = make_rsrc(x, (uint32_t)(((int64_t)(m - 1) * ldx + k) * 2));
+    const XInput xin = x_input<X32, KEEP>(x, m, k, ldx, keep, keep_scale);
     const bool cok = k0 + i < k;
     // acc[h]: D[t = 16 h + 4 g + r][k0 + i]
     float4_t acc[R / 16];
@@ -191,7 +290,7 @@ __global__ __launch_bounds__(kLoraThreads) void lora_da_kernel(const _Float16* _
         for (int q = 0; q < 2; ++q) {
             const int mm = min(32 * (c + q * kLoraWaves) + 8 * g, m);  // rows past m: zeros
             const int valid = m - mm;
-            xb[q] = gather8(xr, (uint32_t)(mm * ldx + k0 + i) * 2u, 2u * (uint32_t)ldx, cok, valid);
+            xb[q] = x_col8<X32, KEEP>(xin, mm, k0 + i, cok, valid);
 #pragma unroll
             for (int h = 0; h < R / 16; ++h)
                 ga[q][h] = gather8(gr, (uint32_t)(mm * R + 16 * h + i) * 2u, 2u * R, true, valid);
@@ -216,39 +315,54 @@ __global__ __launch_bounds__(kLoraThreads) void lora_da_kernel(const _Float16* _
     }
 }
 
-#define DK_RANK_CASES(X) X(16) X(32)
+#define DK_XIN_CASES(X, R)                                                                             \
+    X(R, false, false) X(R, false, true) X(R, true, false) X(R, true, true)
 
-hipError_t launch_lora_down(const _Float16* x, int64_t m, int64_t k, int64_t ldx, const _Float16* a,
-                            int rank, _Float16* u, hipStream_t s) {
+hipError_t launch_lora_down(const void* x, bool x32, int64_t m, int64_t k, int64_t ldx, const uint8_t* keep,
+                            const float* keep_scale, const _Float16* a, int rank, _Float16* u, hipStream_t s) {
     if (m == 0) return hipSuccess;
     const dim3 grid((unsigned)((m + 15) / 16));
-#define X(R)                                                                                           \
-    if (rank == R) {                                                                                   \
-        hipLaunchKernelGGL((lora_down_kernel<R>), grid, dim3(kLoraThreads), 0, s, x, (int)m, (int)k,   \
-                           (int)ldx, a, u);                                                            \
+    const bool kp = keep != nullptr;
+#define X(R, X32, KEEP)                                                                                \
+    if (rank == R && x32 == X32 && kp == KEEP) {                                                       \
+        hipLaunchKernelGGL((lora_down_kernel<R, X32, KEEP>), grid, dim3(kLoraThreads), 0, s, x, (int)m, \
+                           (int)k, (int)ldx, keep, keep_scale, a, u);                                  \
         return hipGetLastError();                                                                      \
     }
-    DK_RANK_CASES(X)
+    DK_XIN_CASES(X, 16)
+    DK_XIN_CASES(X, 32)
 #undef X
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_lora_bwd(const _Float16* dy, int64_t lddy, const _Float16* u, const _Float16* x,
-                           int64_t ldx, const _Float16* b, int64_t m, int64_t n, int64_t k, int rank,
-                           float scale, _Float16* gu, float* da, float* db, hipStream_t s) {
+hipError_t launch_lora_bwd(const _Float16* dy, int64_t lddy, const _Float16* u, const void* x, bool x32,
+                           int64_t ldx, const uint8_t* keep, const float* keep_scale, const _Float16* b,
+                           int64_t m, int64_t n, int64_t k, int rank, float scale, _Float16* gu, float* da,
+                           float* db, hipStream_t s) {
     if (m == 0) return hipSuccess;
     const int m_tiles = (int)((m + 15) / 16);
     const int n_tiles = db != nullptr ? (int)((n + 15) / 16) : 0;
+    const bool kp = keep != nullptr;
+    hipError_t e = hipErrorInvalidValue;
 #define X(R)                                                                                           \
     if (rank == R) {                                                                                   \
         hipLaunchKernelGGL((lora_gu_db_kernel<R>), dim3(m_tiles + n_tiles), dim3(kLoraThreads), 0, s,  \
                            dy, (int)lddy, u, b, (int)m, (int)n, scale, m_tiles, gu, db);               \
-        if (da != nullptr)                                                                             \
-            hipLaunchKernelGGL((lora_da_kernel<R>), dim3((unsigned)((k + 15) / 16)), dim3(kLoraThreads), \
-                               0, s, gu, x, (int)ldx, (int)m, (int)k, da);                             \
+        e = hipGetLastError();                                                                         \
+    }
+    X(16)
+    X(32)
+#undef X
+    if (e != hipSuccess || da == nullptr) return e;
+    const dim3 grid((unsigned)((k + 15) / 16));
+#define X(R, X32, KEEP)                                                                                \
+    if (rank == R && x32 == X32 && kp == KEEP) {                                                       \
+        hipLaunchKernelGGL((lora_da_kernel<R, X32, KEEP>), grid, dim3(kLoraThreads), 0, s, gu, x,      \
+                           (int)ldx, keep, keep_scale, (int)m, (int)k, da);                            \
         return hipGetLastError();                                                                      \
     }
-    DK_RANK_CASES(X)
+    DK_XIN_CASES(X, 16)
+    DK_XIN_CASES(X, 32)
 #undef X
     return hipErrorInvalidValue;
 }

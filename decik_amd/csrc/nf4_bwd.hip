@@ -98,7 +98,7 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void nf4_bwd_kernel(const Bw
         const int R = split == 0 ? sgpr(a.lora_rank) : 0;
         for (int gg = 0; gg < a.ngroups; ++gg) {
             const BwdGroupDev& G = a.g[gg];
-            if (G.lora_gu == nullptr || R == 0) continue;
+            if (G.lora_gu == nullptr || G.lora_keep != nullptr || R == 0) continue;  // dropout: epilogue
             const rsrc_t ars = make_rsrc(G.lora_a, (uint32_t)R * (uint32_t)K * 2u);
             const rsrc_t grs = make_rsrc(G.lora_gu, (uint32_t)M * (uint32_t)R * 2u);
             for (int t0 = 0; t0 < R; t0 += 16) {
@@ -382,6 +382,55 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void nf4_bwd_kernel(const Bw
 
     // ---- epilogue: lane (l32, g) holds columns kw0 + 32 g + c, c = 2 r + cb, of token rows
     // m0 + 32 i + l32 (acc[i * 2 + cb][r]).
+    // LoRA input-gradient terms of branches whose input went through dropout (split 0): per token
+    // block, P = GU_g . A_g on its own, rounded to fp16, times keep and the keep scale in fp32,
+    // then added. Lane value (cb, r) of token block i is column kw0 + 32 g + 2 r + cb: bit 2 r + cb
+    // of the four keep bytes at column (kw0 + 32 g) / 8 of the token's row.
+    if (split == 0) {
+        const int R = sgpr(a.lora_rank);
+        const bool kok = kw0 + 32 * g < K;  // k % 32 == 0: the lane's 32 columns all in or out
+        for (int gg = 0; gg < a.ngroups; ++gg) {
+            const BwdGroupDev& G = a.g[gg];
+            if (G.lora_keep == nullptr || G.lora_gu == nullptr || R == 0) continue;
+            const rsrc_t ars = make_rsrc(G.lora_a, (uint32_t)R * (uint32_t)K * 2u);
+            const rsrc_t grs = make_rsrc(G.lora_gu, (uint32_t)M * (uint32_t)R * 2u);
+            const rsrc_t krs = make_rsrc(G.lora_keep, (uint32_t)M * (uint32_t)(K >> 3));
+            const float ks = G.lora_keep_scale;
+            half8_t al[2][2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+#pragma unroll
+                    for (int cb = 0; cb < 2; ++cb) {
+                        const int col = kw0 + 2 * beta + cb;
+                        al[h][cb][e] = __builtin_bit_cast(
+                            _Float16, (uint16_t)bload16(ars, off_if(col < K && 16 * h < R,
+                                                                    (uint32_t)((16 * h + 8 * g + e) * K + col) * 2u)));
+                    }
+#pragma unroll
+            for (int i = 0; i < MB; ++i) {
+                const int m = m0 + 32 * i + l32;
+                float16_t p[2] = {};
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const half8_t gu = __builtin_bit_cast(
+                        half8_t, bload128(grs, off_if(m < M && 16 * h < R, (uint32_t)(m * R + 16 * h + 8 * g) * 2u)));
+#pragma unroll
+                    for (int cb = 0; cb < 2; ++cb) p[cb] = mfma32x32x16(al[h][cb], gu, p[cb]);  // zeros past the rank
+                }
+                const uint32_t bits = __builtin_bit_cast(
+                    uint32_t, bloadf(krs, off_if(m < M && kok, (uint32_t)m * (uint32_t)(K >> 3) +
+                                                                 (uint32_t)((kw0 + 32 * g) >> 3))));
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        acc[i * 2 + cb][r] = acc[i * 2 + cb][r] +
+                                             ((float)(_Float16)p[cb][r] * (float)((bits >> (2 * r + cb)) & 1u)) * ks;
+            }
+        }
+    }
     const int kc = kw0 + 32 * g;
     if (a.splits > 1) {
         float* slab = a.partials + (int64_t)split * M * K;

@@ -144,7 +144,7 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
         const int R = split == 0 ? sgpr(a.lora_rank) : 0;
         for (int gg = 0; gg < a.ngroups; ++gg) {
             const BwdGroupDev& G = a.g[gg];
-            if (G.lora_gu == nullptr || R == 0) continue;
+            if (G.lora_gu == nullptr || G.lora_keep != nullptr || R == 0) continue;  // dropout: epilogue
             const rsrc_t ars = make_rsrc(G.lora_a, (uint32_t)R * (uint32_t)K * 2u);
             const rsrc_t grs = make_rsrc(G.lora_gu, (uint32_t)M * (uint32_t)R * 2u);
             for (int t0 = 0; t0 < R; t0 += 16) {
@@ -457,6 +457,45 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
                 }
             }
             return;
+        }
+    }
+    // LoRA input-gradient terms of branches whose input went through dropout (split 0): per token
+    // block, P = GU_g . A_g on its own, rounded to fp16 (the branch's fp16 input gradient), times
+    // keep and the keep scale in fp32, then added to the block's dX. Lane value r of token block i
+    // is column kw0 + 16 g + r: bit r of the two keep bytes at column (kw0 + 16 g) / 8 of the row.
+    if (split == 0) {
+        const int R = sgpr(a.lora_rank);
+        for (int gg = 0; gg < a.ngroups; ++gg) {
+            const BwdGroupDev& G = a.g[gg];
+            if (G.lora_keep == nullptr || G.lora_gu == nullptr || R == 0) continue;
+            const rsrc_t ars = make_rsrc(G.lora_a, (uint32_t)R * (uint32_t)K * 2u);
+            const rsrc_t grs = make_rsrc(G.lora_gu, (uint32_t)M * (uint32_t)R * 2u);
+            const rsrc_t krs = make_rsrc(G.lora_keep, (uint32_t)M * (uint32_t)(K >> 3));
+            const float ks = G.lora_keep_scale;
+            half8_t al[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    al[h][e] = __builtin_bit_cast(
+                        _Float16, (uint16_t)bload16(ars, off_if(cok && 16 * h < R,
+                                                                (uint32_t)((16 * h + 8 * g + e) * K + kw0 + c) * 2u)));
+#pragma unroll
+            for (int i = 0; i < MB; ++i) {
+                const int m = m0 + 32 * i + l32;
+                float16_t p{};
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const half8_t gu = __builtin_bit_cast(
+                        half8_t, bload128(grs, off_if(m < M && 16 * h < R, (uint32_t)(m * R + 16 * h + 8 * g) * 2u)));
+                    p = mfma32x32x16(al[h], gu, p);  // zeros past the rank
+                }
+                const uint32_t bits = bload16(krs, off_if(m < M && cok, (uint32_t)m * (uint32_t)(K >> 3) +
+                                                                       (uint32_t)((kw0 + 16 * g) >> 3)));
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    acc[i][r] = acc[i][r] + ((float)(_Float16)p[r] * (float)((bits >> r) & 1u)) * ks;
+            }
         }
     }
     const bool out32 = a.splits > 1 || a.dx_fp32;

@@ -8,9 +8,12 @@ Here the base projection and the LoRA term are one launch in each direction: the
 epilogue adds s * U.B^T (an extra rank-r MFMA per output tile) before the single fp16 rounding,
 and the backward GEMM's epilogue adds GU.A to dX. U and GU come from small HIP kernels
 (dk_lora_down, dk_lora_bwd), which also produce dA and dB in fp32. With dropout (p > 0) the
-branch runs beside the projection as LoRAPairFromNorm does (LoRAPair below): packed keep-masks,
-dropped-out fp16 inputs, and the input gradient through the masks (dk_lora_keep_pack,
-dk_lora_dropout_inputs, dk_lora_up, dk_lora_input_grad).
+fused q/k/v launches (QKVProjection, QKVRopeProjection) take the packed keep-masks: U and dA
+rebuild fp16(x * (keep * scale)) in registers (dk_lora_down_dropout, dk_lora_bwd_dropout) and the
+backward GEMM masks each branch's input gradient in its epilogue, so no dropped-out input or
+per-branch input gradient is ever stored. LoRAPair / LoRAPairFromNorm keep the reference's
+separate branch (packed keep-masks, dropped-out fp16 inputs, the input gradient through the
+masks: dk_lora_keep_pack, dk_lora_dropout_inputs, dk_lora_up, dk_lora_input_grad).
 """
 
 import torch
@@ -19,20 +22,41 @@ from . import nf4 as _nf4
 from ._lib import check, lib, ptr, stream_of
 
 
-def lora_down(x16, a16):
-    """U = fp16(X . A^T): X fp16 [M, K], A fp16 [r, K] -> [M, r]."""
-    x2 = x16.reshape(-1, x16.shape[-1])
+def _plain(x, keep_bits):
+    return keep_bits is None and x.dtype == torch.float16
+
+
+def _keep_args(x2, keep_bits, keep_scale):
+    if keep_bits is None:
+        return None, None
+    m, k = x2.shape
+    assert keep_bits.dtype == torch.uint8 and keep_bits.is_contiguous() and keep_bits.numel() == m * (k // 8)
+    return keep_bits, keep_scale.to(torch.float32).reshape(1).contiguous()
+
+
+def lora_down(x, a16, keep_bits=None, keep_scale=None):
+    """U = fp16(X . A^T) [M, r] for A fp16 [r, K]. X = x for fp16 x [M, K]; for fp32 x, or with a
+    dropout mask (keep_bits: packed keep bits [M, K / 8] from pack_keep, keep_scale: fp32 device
+    scalar 1 / (1 - p)), X = fp16(x * (keep * scale)) is built inside the kernel
+    (dk_lora_down_dropout), as skc_lora_inputs_kernel rounds it (solution/attn.py:153-165)."""
+    x2 = x.reshape(-1, x.shape[-1])
     m, k = x2.shape
     r = a16.shape[0]
-    u = torch.empty((m, r), dtype=torch.float16, device=x16.device)
-    check(lib().dk_lora_down(ptr(x2), m, k, x2.stride(0), ptr(a16), r, ptr(u), stream_of(x16.device)))
+    u = torch.empty((m, r), dtype=torch.float16, device=x.device)
+    if _plain(x, keep_bits):
+        check(lib().dk_lora_down(ptr(x2), m, k, x2.stride(0), ptr(a16), r, ptr(u), stream_of(x.device)))
+        return u
+    bits, sc = _keep_args(x2, keep_bits, keep_scale)
+    check(lib().dk_lora_down_dropout(ptr(x2), 1 if x2.dtype == torch.float32 else 0, m, k, x2.stride(0),
+                                     ptr(bits), ptr(sc), ptr(a16), r, ptr(u), stream_of(x.device)))
     return u
 
 
-def lora_grads(dy16, u16, x16, b16, scaling, want_da=True, want_db=True):
-    """(GU fp16 [M, r], dA fp32 [r, K], dB fp32 [N, r]) for out = s * (U . B^T), U = X . A^T."""
+def lora_grads(dy16, u16, x, b16, scaling, want_da=True, want_db=True, keep_bits=None, keep_scale=None):
+    """(GU fp16 [M, r], dA fp32 [r, K], dB fp32 [N, r]) for out = s * (U . B^T), U = X . A^T, with X
+    from x (and the dropout mask) as lora_down builds it."""
     dy2 = dy16.reshape(-1, dy16.shape[-1])
-    x2 = x16.reshape(-1, x16.shape[-1])
+    x2 = x.reshape(-1, x.shape[-1])
     m, n = dy2.shape
     k = x2.shape[1]
     r = u16.shape[1]
@@ -40,8 +64,15 @@ def lora_grads(dy16, u16, x16, b16, scaling, want_da=True, want_db=True):
     gu = torch.empty((m, r), dtype=torch.float16, device=dev)
     da = torch.empty((r, k), dtype=torch.float32, device=dev) if want_da else None
     db = torch.empty((n, r), dtype=torch.float32, device=dev) if want_db else None
-    check(lib().dk_lora_bwd(ptr(dy2), dy2.stride(0), ptr(u16), ptr(x2), x2.stride(0), ptr(b16), m, n, k,
-                            r, float(scaling), ptr(gu), ptr(da), ptr(db), stream_of(dev)))
+    if _plain(x, keep_bits):
+        check(lib().dk_lora_bwd(ptr(dy2), dy2.stride(0), ptr(u16), ptr(x2), x2.stride(0), ptr(b16), m, n, k,
+                                r, float(scaling), ptr(gu), ptr(da), ptr(db), stream_of(dev)))
+        return gu, da, db
+    bits, sc = _keep_args(x2, keep_bits, keep_scale)
+    check(lib().dk_lora_bwd_dropout(ptr(dy2), dy2.stride(0), ptr(u16), ptr(x2),
+                                    1 if x2.dtype == torch.float32 else 0, x2.stride(0), ptr(bits), ptr(sc),
+                                    ptr(b16), m, n, k, r, float(scaling), ptr(gu), ptr(da), ptr(db),
+                                    stream_of(dev)))
     return gu, da, db
 
 
@@ -250,101 +281,123 @@ class NF4LoRALinear(torch.autograd.Function):
         return grad_x, None, None, None, da, db, None
 
 
-class QKVProjection(torch.autograd.Function):
-    """q, k, v = x16 . W_{q,k,v}^T + b_{q,k,v} (+ LoRA on any of them) in one fused forward launch
-    and one fused backward launch for dX = sum of the three input gradients (+ LoRA terms), the
-    call order of solution/attn.py:396-407 without the dropout draws.
+def _qkv_inputs(x):
+    """(x rows [T, W] as given, fp16 rows for the base GEMM)."""
+    x2 = x.reshape(-1, x.shape[-1]).contiguous()
+    return x2, (x2 if x2.dtype == torch.float16 else x2.to(torch.float16))
 
-    projections: tuple of 3 dicts {packed, qs, bias, lora_a, lora_b, scaling} (lora_* may be
-    None); the adapter tensors are passed again as flat arguments so autograd sees them."""
+
+def _qkv_forward_items(x2, x16, projections):
+    """Forward launch items of q, k, v: U of each LoRA term from the branch input (x16, or x with
+    its dropout mask), all of one rank. Returns (items, saved LoRA state per projection, rank)."""
+    ranks = {int(p["lora_a"].shape[0]) for p in projections if p.get("lora_a") is not None}
+    if len(ranks) > 1:
+        # one launch runs one rank (its LoRA slices and the U / B row strides)
+        raise ValueError(f"QKV projection: LoRA ranks differ within one launch: {sorted(ranks)}")
+    items, saved, rank = [], [], 0
+    for p in projections:
+        it = dict(packed=p["packed"], qs=p["qs"], bias=p.get("bias"))
+        if p.get("lora_a") is not None:
+            a16 = p["lora_a"].to(torch.float16).contiguous()
+            b16 = p["lora_b"].to(torch.float16).contiguous()
+            if p.get("keep_bits") is not None:
+                u = lora_down(x2, a16, p["keep_bits"], p["keep_scale"])
+            else:
+                u = lora_down(x16, a16)
+            it.update(lora_u=u, lora_b=b16, lora_scale=p["scaling"])
+            rank = a16.shape[0]
+            saved.append((u, a16, b16))
+        else:
+            saved.append(None)
+        items.append(it)
+    return items, saved, rank
+
+
+def _qkv_backward(x2, x16, projections, saved, grads, rank):
+    """dX of the three projections and their LoRA terms in one launch (dX in x's dtype), and the
+    adapter gradients. A branch with dropout: dA from the rebuilt dropped-out input, its input
+    gradient masked in the GEMM's epilogue with 1 / (1 - p) (skc_lora_input_grad_kernel's
+    scale, solution/attn.py:262-266)."""
+    m, k = x2.shape
+    items, adapter_grads = [], []
+    for p, sv, g in zip(projections, saved, grads):
+        if g is None:
+            g = torch.zeros((m, int(p["qs"].shape[0])), dtype=torch.float16, device=x2.device)
+        g16 = g.to(torch.float16).reshape(m, -1).contiguous()
+        it = dict(packed=p["packed"], qs=p["qs"], dy=g16)
+        if sv is not None:
+            u, a16, b16 = sv
+            if p.get("keep_bits") is not None:
+                gu, da, db = lora_grads(g16, u, x2, b16, p["scaling"], keep_bits=p["keep_bits"],
+                                        keep_scale=p["keep_scale"])
+                it.update(lora_keep=p["keep_bits"], lora_keep_scale=1.0 / (1.0 - float(p["p"])))
+            else:
+                gu, da, db = lora_grads(g16, u, x16, b16, p["scaling"])
+            it.update(lora_gu=gu, lora_a=a16)
+            adapter_grads += [da.to(p["lora_a"].dtype), db.to(p["lora_b"].dtype)]
+        items.append(it)
+    grad_x = _nf4.linear_backward(items, m, k, dx_fp32=x2.dtype == torch.float32, lora_rank=rank)
+    return grad_x, adapter_grads
+
+
+class QKVProjection(torch.autograd.Function):
+    """q, k, v = x . W_{q,k,v}^T + b_{q,k,v} (+ LoRA on any of them) in one fused forward launch
+    and one fused backward launch for dX = sum of the three input gradients (+ LoRA terms), the
+    call order of solution/attn.py:396-407.
+
+    x: fp16, or fp32 (the norm output the reference's attention receives; the base projections
+    take fp16(x), :398-401, and dX comes back fp32). projections: tuple of 3 dicts {packed, qs,
+    bias, lora_a, lora_b, scaling} (lora_* may be None), and for a LoRA branch with dropout
+    keep_bits (pack_keep's packed mask [T, W / 8]), keep_scale (fp32 device scalar 1 / (1 - p))
+    and p: the branch input is fp16(x * (keep * scale)), built inside the U kernel and again
+    for dA, and its input gradient is masked in the backward GEMM's epilogue (LoRAPairFromNorm's
+    packed path, solution/attn.py:153-180, 206-273, without the dropped-out inputs in memory).
+    The adapter tensors are passed again as flat arguments so autograd sees them."""
 
     @staticmethod
-    def forward(ctx, x16, projections, *adapters):
-        x2 = x16.reshape(-1, x16.shape[-1]).contiguous()
-        items, saved, rank = [], [], 0
-        ranks = {int(p["lora_a"].shape[0]) for p in projections if p.get("lora_a") is not None}
-        if len(ranks) > 1:
-            # one launch runs one rank (its LoRA slices and the U / B row strides)
-            raise ValueError(f"QKVProjection: LoRA ranks differ within one launch: {sorted(ranks)}")
-        for p in projections:
-            it = dict(packed=p["packed"], qs=p["qs"], bias=p.get("bias"))
-            if p.get("lora_a") is not None:
-                a16 = p["lora_a"].to(torch.float16).contiguous()
-                b16 = p["lora_b"].to(torch.float16).contiguous()
-                u = lora_down(x2, a16)
-                it.update(lora_u=u, lora_b=b16, lora_scale=p["scaling"])
-                rank = a16.shape[0]
-                saved.append((u, a16, b16))
-            else:
-                saved.append(None)
-            items.append(it)
-        outs = _nf4.linear_forward(x2, items, lora_rank=rank)
+    def forward(ctx, x, projections, *adapters):
+        x2, x16 = _qkv_inputs(x)
+        items, saved, rank = _qkv_forward_items(x2, x16, projections)
+        outs = _nf4.linear_forward(x16, items, lora_rank=rank)
         ctx.projections, ctx.saved_lora, ctx.rank = projections, saved, rank
-        ctx.save_for_backward(x2)
-        ctx.x_shape = x16.shape
-        return tuple(o.reshape(*x16.shape[:-1], o.shape[-1]) for o in outs)
+        ctx.save_for_backward(x2, x16)
+        ctx.x_shape = x.shape
+        return tuple(o.reshape(*x.shape[:-1], o.shape[-1]) for o in outs)
 
     @staticmethod
     def backward(ctx, *grads):
-        (x2,) = ctx.saved_tensors
-        m, k = x2.shape
-        items, adapter_grads = [], []
-        for p, sv, g in zip(ctx.projections, ctx.saved_lora, grads):
-            if g is None:
-                g = torch.zeros((m, int(p["qs"].shape[0])), dtype=torch.float16, device=x2.device)
-            g16 = g.to(torch.float16).reshape(m, -1).contiguous()
-            it = dict(packed=p["packed"], qs=p["qs"], dy=g16)
-            if sv is not None:
-                u, a16, b16 = sv
-                gu, da, db = lora_grads(g16, u, x2, b16, p["scaling"])
-                it.update(lora_gu=gu, lora_a=a16)
-                adapter_grads += [da.to(p["lora_a"].dtype), db.to(p["lora_b"].dtype)]
-            items.append(it)
-        grad_x = _nf4.linear_backward(items, m, k, lora_rank=ctx.rank).reshape(ctx.x_shape)
-        return (grad_x, None, *adapter_grads)
+        x2, x16 = ctx.saved_tensors
+        grad_x, adapter_grads = _qkv_backward(x2, x16, ctx.projections, ctx.saved_lora, grads, ctx.rank)
+        return (grad_x.reshape(ctx.x_shape), None, *adapter_grads)
 
 
 class QKVRopeProjection(torch.autograd.Function):
-    """The attention inputs of a Qwen2 layer in one fused launch each way: q, k, v = x16 . W^T + b
-    (+ LoRA terms, like QKVProjection), with q and k rotated (RoPE) and stored head-major in the
-    launch's epilogue -- the projections and FusedQKRope's forward (solution/attn.py:27-66,
-    396-418) without a token-major q or k in memory. Returns (q [1, H, T, D], k [1, HK, T, D],
-    v [T, HK*D]). Backward: the RoPE transpose (the same kernel as FusedQKRope's backward,
-    solution/attn.py:69-86), then one fused launch for dX with the LoRA terms.
+    """The attention inputs of a Qwen2 layer in one fused launch each way: q, k, v = x . W^T + b
+    (+ LoRA terms, with or without dropout, like QKVProjection), with q and k rotated (RoPE) and
+    stored head-major in the launch's epilogue -- the projections and FusedQKRope's forward
+    (solution/attn.py:27-66, 396-418) without a token-major q or k in memory. Returns (q [1, H, T,
+    D], k [1, HK, T, D], v [T, HK*D]). Backward: the RoPE transpose (the same kernel as
+    FusedQKRope's backward, solution/attn.py:69-86), then one fused launch for dX with the LoRA
+    terms.
 
     projections: (q, k, v) dicts as for QKVProjection; cos, sin fp32 [T, D]."""
 
     @staticmethod
-    def forward(ctx, x16, projections, cos, sin, n_heads, n_kv_heads, *adapters):
-        from .rope import rope_qk_backward  # noqa: F401 (imported for the backward)
-
-        x2 = x16.reshape(-1, x16.shape[-1]).contiguous()
-        head_dim = cos.shape[-1]
-        items, saved, rank = [], [], 0
-        for p in projections:
-            it = dict(packed=p["packed"], qs=p["qs"], bias=p.get("bias"))
-            if p.get("lora_a") is not None:
-                a16 = p["lora_a"].to(torch.float16).contiguous()
-                b16 = p["lora_b"].to(torch.float16).contiguous()
-                u = lora_down(x2, a16)
-                it.update(lora_u=u, lora_b=b16, lora_scale=p["scaling"])
-                rank = a16.shape[0]
-                saved.append((u, a16, b16))
-            else:
-                saved.append(None)
-            items.append(it)
-        q, k, v = _nf4.linear_rope_forward(x2, items, cos, sin, head_dim, 3, lora_rank=rank)
+    def forward(ctx, x, projections, cos, sin, n_heads, n_kv_heads, *adapters):
+        x2, x16 = _qkv_inputs(x)
+        items, saved, rank = _qkv_forward_items(x2, x16, projections)
+        q, k, v = _nf4.linear_rope_forward(x16, items, cos, sin, cos.shape[-1], 3, lora_rank=rank)
         ctx.projections, ctx.saved_lora, ctx.rank = projections, saved, rank
-        ctx.save_for_backward(x2, cos, sin)
-        ctx.x_shape = x16.shape
+        ctx.save_for_backward(x2, x16, cos, sin)
+        ctx.x_shape = x.shape
         return q.unsqueeze(0), k.unsqueeze(0), v
 
     @staticmethod
     def backward(ctx, grad_q, grad_k, grad_v):
         from .rope import rope_qk_backward
 
-        x2, cos, sin = ctx.saved_tensors
-        m, kdim = x2.shape
+        x2, x16, cos, sin = ctx.saved_tensors
+        m = x2.shape[0]
         n_q, n_k = (int(p["qs"].shape[0]) for p in ctx.projections[:2])
         head_dim = cos.shape[-1]
         if grad_q is None:
@@ -352,30 +405,20 @@ class QKVRopeProjection(torch.autograd.Function):
         if grad_k is None:
             grad_k = torch.zeros((n_k // head_dim, m, head_dim), dtype=torch.float16, device=x2.device)
         dq, dk = rope_qk_backward(grad_q, grad_k, cos, sin)
-        items, adapter_grads = [], []
-        for p, sv, g in zip(ctx.projections, ctx.saved_lora, (dq, dk, grad_v)):
-            if g is None:
-                g = torch.zeros((m, int(p["qs"].shape[0])), dtype=torch.float16, device=x2.device)
-            g16 = g.to(torch.float16).reshape(m, -1).contiguous()
-            it = dict(packed=p["packed"], qs=p["qs"], dy=g16)
-            if sv is not None:
-                u, a16, b16 = sv
-                gu, da, db = lora_grads(g16, u, x2, b16, p["scaling"])
-                it.update(lora_gu=gu, lora_a=a16)
-                adapter_grads += [da.to(p["lora_a"].dtype), db.to(p["lora_b"].dtype)]
-            items.append(it)
-        grad_x = _nf4.linear_backward(items, m, kdim, lora_rank=ctx.rank).reshape(ctx.x_shape)
-        return (grad_x, None, None, None, None, None, *adapter_grads)
+        grad_x, adapter_grads = _qkv_backward(x2, x16, ctx.projections, ctx.saved_lora, (dq, dk, grad_v),
+                                              ctx.rank)
+        return (grad_x.reshape(ctx.x_shape), None, None, None, None, None, *adapter_grads)
 
 
-def qkv_rope_projection(x16, projections, cos, sin, n_heads, n_kv_heads):
-    """q [1, H, T, D], k [1, HK, T, D] (rotated, head-major) and v [T, HK*D] of x16 in one fused
-    launch each way (QKVRopeProjection). LoRA terms of one rank the kernels take (16 or 32)."""
+def qkv_rope_projection(x, projections, cos, sin, n_heads, n_kv_heads):
+    """q [1, H, T, D], k [1, HK, T, D] (rotated, head-major) and v [T, HK*D] of x (fp16 or fp32)
+    in one fused launch each way (QKVRopeProjection). LoRA terms of one rank the kernels take (16
+    or 32), with or without dropout masks."""
     adapters = []
     for p in projections:
         if p.get("lora_a") is not None:
             adapters += [p["lora_a"], p["lora_b"]]
-    return QKVRopeProjection.apply(x16, projections, cos, sin, n_heads, n_kv_heads, *adapters)
+    return QKVRopeProjection.apply(x, projections, cos, sin, n_heads, n_kv_heads, *adapters)
 
 
 FUSED_RANKS = (16, 32)  # LoRA ranks the GEMM kernels' rank-16 MFMA slices take
@@ -395,14 +438,18 @@ def _project_one(x16, p):
     return (base.float() + lora.float()).to(torch.float16)
 
 
-def qkv_projection(x16, projections):
-    """q, k, v (+ LoRA) of x16 in one fused launch each way when every LoRA term has one rank the
-    kernels take (16 or 32); otherwise each projection runs on its own."""
+def qkv_projection(x, projections):
+    """q, k, v (+ LoRA, with or without dropout masks) of x (fp16 or fp32) in one fused launch each
+    way when every LoRA term has one rank the kernels take (16 or 32); otherwise each projection
+    runs on its own (no dropout masks there)."""
     ranks = {int(p["lora_a"].shape[0]) for p in projections if p.get("lora_a") is not None}
     if len(ranks) > 1 or not ranks <= set(FUSED_RANKS):
+        if any(p.get("keep_bits") is not None for p in projections):
+            raise ValueError("qkv_projection: dropout masks need one LoRA rank of 16 or 32")
+        x16 = x if x.dtype == torch.float16 else x.to(torch.float16)
         return tuple(_project_one(x16, p) for p in projections)
     adapters = []
     for p in projections:
         if p.get("lora_a") is not None:
             adapters += [p["lora_a"], p["lora_b"]]
-    return QKVProjection.apply(x16, projections, *adapters)
+    return QKVProjection.apply(x, projections, *adapters)

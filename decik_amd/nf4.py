@@ -217,7 +217,8 @@ def linear_backward(items, m, k, dx=None, dx_fp32=False, lora_rank=0):
     """Fused input gradient dX [m, k] = sum_i dY_i . W_i (+ GU_i . A_i), one fp32 accumulation.
 
     items: list of dicts with keys packed, qs, dy (fp16 [m, N_i]) and optional lora_gu
-    (fp16 [m, r]), lora_a (fp16 [r, k])."""
+    (fp16 [m, r]), lora_a (fp16 [r, k]); with lora_keep (packed dropout keep bits [m, k / 8],
+    uint8) and lora_keep_scale (1 / (1 - p)) the LoRA term is fp16(GU . A) * keep * scale."""
     assert 1 <= len(items) <= _lib.MAX_GROUPS
     dev = items[0]["dy"].device
     if dx is None:
@@ -235,7 +236,12 @@ def linear_backward(items, m, k, dx=None, dx_fp32=False, lora_rank=0):
         gu, a = it.get("lora_gu"), it.get("lora_a")
         groups[g].lora_gu = None if gu is None else gu.data_ptr()
         groups[g].lora_a = None if a is None else a.data_ptr()
-        keep += [dy, gu, a]
+        bits = it.get("lora_keep")
+        if bits is not None:
+            assert bits.dtype == torch.uint8 and bits.is_contiguous() and bits.numel() == m * (k // 8)
+            groups[g].lora_keep = bits.data_ptr()
+            groups[g].lora_keep_scale = float(it["lora_keep_scale"])
+        keep += [dy, gu, a, bits]
         ns.append(int(qs.shape[0]))
     need = _workspace_need(False, m, k, ns)
     ws, ws_bytes = _lib.WORKSPACE.get(need, dev)
@@ -298,7 +304,10 @@ def linear_backward_swiglu(item, gate, up, out=None, lora_rank=0):
     groups[0].w = w
     groups[0].dy = dy.data_ptr()
     groups[0].lddy = dy.stride(0)
-    gu, a = item.get("lora_gu"), item.get("lora_a")
+    gu, a, bits = item.get("lora_gu"), item.get("lora_a"), item.get("lora_keep")
+    if bits is not None:  # the C entry rejects it (no masked LoRA term in the SwiGLU epilogue)
+        groups[0].lora_keep = bits.data_ptr()
+        groups[0].lora_keep_scale = float(item["lora_keep_scale"])
     groups[0].lora_gu = None if gu is None else gu.data_ptr()
     groups[0].lora_a = None if a is None else a.data_ptr()
     keep += [dy, gu, a]

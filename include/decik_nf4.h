@@ -29,6 +29,9 @@
  *                                               backward (solution/mlp.py:95, 104)
  *   dk_lora_down / dk_lora_bwd                <- the rank-r products of LoRAPairFromNorm
  *                                               (solution/attn.py:225-227, 251-257)
+ *   dk_lora_down_dropout / dk_lora_bwd_dropout <- the same with skc_lora_inputs_kernel fused in
+ *     + dk_linear_bwd_group.lora_keep            and skc_lora_input_grad_kernel in the input-
+ *                                               gradient GEMM (solution/attn.py:153-180, 206-273)
  *   dk_lora_keep_pack                         <- skc_keep_pack_kernel / pack_keep
  *                                               (solution/attn.py:129-144, 195-203)
  *   dk_lora_dropout_inputs                    <- skc_lora_inputs_kernel / _lora_inputs
@@ -86,13 +89,20 @@ typedef struct dk_linear_fwd_group {
 
 /* One weight of a backward launch. Its contribution to dX[r, j] is
  *   sum_c dY[r, c] W[c, j] + sum_t GU[r, t] A[t, j]
- * (GU = lora_scale * dY.B from dk_lora_bwd, fp16 [m, rank]; A fp16 [rank, k]). */
+ * (GU = lora_scale * dY.B from dk_lora_bwd, fp16 [m, rank]; A fp16 [rank, k]). With lora_keep
+ * (the LoRA branch's input went through dropout, LoRAPairFromNorm's packed masks,
+ * solution/attn.py:168-180, 251-266) the LoRA part is instead
+ *   (fp16(sum_t GU[r, t] A[t, j]) * keep[r, j]) * lora_keep_scale     (fp32)
+ * with keep[r, j] = bit j % 8 of byte r * (k / 8) + j / 8 of lora_keep (dk_lora_keep_pack). */
 typedef struct dk_linear_bwd_group {
     dk_nf4_weight w;
     const uint16_t* dy;      /* fp16 [m, n], row stride lddy              */
     int64_t lddy;
     const uint16_t* lora_gu; /* fp16 [m, rank] or NULL                    */
     const uint16_t* lora_a;  /* fp16 [rank, k]                            */
+    const uint8_t* lora_keep; /* packed keep bits [m, k / 8] or NULL      */
+    float lora_keep_scale;   /* 1 / (1 - p)                               */
+    int32_t reserved;
 } dk_linear_bwd_group;
 
 /* Standalone dequantization: out = fp16 [n, k], bit-identical to the reference kernel
@@ -198,6 +208,22 @@ int dk_lora_down(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const uin
 int dk_lora_bwd(const uint16_t* dy, int64_t lddy, const uint16_t* u, const uint16_t* x,
                 int64_t ldx, const uint16_t* b, int64_t m, int64_t n, int64_t k, int rank,
                 float scale, uint16_t* gu, float* da, float* db, void* stream);
+
+/* dk_lora_down and dk_lora_bwd with the branch's input X given as the norm output the reference
+ * feeds LoRAPairFromNorm (solution/attn.py:153-165, 219-228, 241-257): x fp16 (x_fp32 = 0) or
+ * fp32 [m, k] (row stride ldx, 16-byte aligned), and optionally through dropout: X = fp16(x *
+ * (keep * keep_scale)) in fp32 (skc_lora_inputs_kernel's rounding), keep[r, j] = bit j % 8 of
+ * byte r * (k / 8) + j / 8 of keep_bits (dk_lora_keep_pack), keep_scale a device fp32 scalar
+ * (1 / (1 - p)). keep_bits NULL: X = fp16(x). The dropped-out input is rebuilt in registers and
+ * never stored; the backward GEMM applies the same mask to the branch's input gradient
+ * (dk_linear_bwd_group.lora_keep). */
+int dk_lora_down_dropout(const void* x, int x_fp32, int64_t m, int64_t k, int64_t ldx,
+                         const uint8_t* keep_bits, const float* keep_scale, const uint16_t* a, int rank,
+                         uint16_t* u, void* stream);
+int dk_lora_bwd_dropout(const uint16_t* dy, int64_t lddy, const uint16_t* u, const void* x, int x_fp32,
+                        int64_t ldx, const uint8_t* keep_bits, const float* keep_scale, const uint16_t* b,
+                        int64_t m, int64_t n, int64_t k, int rank, float scale, uint16_t* gu, float* da,
+                        float* db, void* stream);
 
 /* LoRA dropout (the packed-mask path of LoRAPairFromNorm). Masks are bool bytes (0/1), rows x width
  * row-major, width % 8 == 0; bits are [rows, width / 8]. */
