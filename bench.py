@@ -397,6 +397,164 @@ def cpu_baseline(sample_steps=3):
                        f"{sec * 1e3:.0f} ms/step")
 
 
+# ---- config C3: attention projections with LoRA on q and v, one layer fwd + bwd ------------------
+
+C3_LENGTHS = (100, 200, 130, 32, 150, 60, 90, 68)  # 8 packed sequences, 830 tokens
+N_HEADS, N_KV_HEADS, HEAD_DIM = 12, 2, 128
+LORA_P = 0.05  # the real run's lora_dropout
+
+
+def attn_weight_sets(min_bytes=512 << 20):
+    """Layers of q/k/v/o weights the C3 bench rotates through: more than `min_bytes` in all."""
+    per_set = 2 * nf4_bytes(HIDDEN, HIDDEN) + 2 * nf4_bytes(256, HIDDEN)
+    return max(4, -(-min_bytes // per_set) + 1)
+
+
+def rope_tables(lengths, d, base=1000000.0):
+    """cos / sin [T, D] fp32 of packed sequences (positions restart per sequence), Qwen2's rotary
+    embedding (inv_freq = base^(-2i/D), emb = [f, f])."""
+    import numpy as np
+
+    pos = np.concatenate([np.arange(n) for n in lengths]).astype(np.float32)
+    inv = (1.0 / (base ** (np.arange(0, d, 2, dtype=np.float32) / d))).astype(np.float32)
+    f = pos[:, None] * inv[None, :]
+    emb = np.concatenate([f, f], axis=1)
+    return np.cos(emb).astype(np.float32), np.sin(emb).astype(np.float32)
+
+
+def count_kernels(fn):
+    """(kernels launched, their summed duration in us) for one call of fn, from torch.profiler's
+    device events; (None, None) if the profiler is unavailable. The summed duration is the GPU
+    time of the call without the gaps between launches (the host's share of an eager step)."""
+    import torch
+
+    try:
+        from torch.profiler import ProfilerActivity, profile
+
+        torch.cuda.synchronize()
+        with profile(activities=[ProfilerActivity.CUDA]) as prof:
+            fn()
+            torch.cuda.synchronize()
+        ev = [e for e in prof.events() if e.device_type == torch.autograd.DeviceType.CUDA]
+        busy = sum(float(getattr(e, "device_time", None) or e.cuda_time) for e in ev)
+        return len(ev), busy
+    except Exception:  # noqa: BLE001 - a missing profiler only drops the count
+        return None, None
+
+
+def bench_c3(steps, warmup, device):
+    """Config C3: the attention projections of one Qwen2.5-1.5B layer at 830 packed tokens, forward
+    and backward: q [1536, 1536], k / v [256, 1536] with biases, LoRA r=16 (alpha 32, dropout
+    p = 0.05, fp32 adapters) on q and v, RoPE on q and k (12 and 2 heads of 128), o [1536, 1536];
+    the fp32 norm output x and the attention output are fixed synthetic inputs, the gradients of
+    q, k, v and o fixed synthetic tensors (solution/attn.py:396-418, 206-273, 27-126).
+
+    fused: pack_keep, QKVRopeProjection (U of q and v from x and the keep bits; q/k/v + biases +
+    LoRA + RoPE in one launch and its reduction; backward: the RoPE transpose, GU/dB and dA per
+    branch, one dX launch with the masked LoRA terms), and o.
+    reference_order: the reference's sequence of operations on this package's kernels: three
+    base projections on their own fp16 casts of x, LoRAPairFromNorm's packed path (dropped-out
+    inputs, U, up-projection, scaling, per branch), v = fp16(v_base + v_lora) in fp32, FusedQKRope,
+    o, and autograd's backward of all that.
+    Both rotate over enough layers' weights (more than 512 MB) that repeats miss the Infinity Cache."""
+    import torch
+
+    from decik_amd import lora, nf4
+    from decik_amd.rope import FusedQKRope
+
+    n_sets = attn_weight_sets()
+    layers = make_layers(n_sets, ("q", "k", "v", "o"), device, base_seed=40_000)
+    bound = 1.0 / (HIDDEN ** 0.5)
+    for li, L in enumerate(layers):
+        for j, name in enumerate(("q", "k", "v")):
+            L[name + "_bias"] = seeded_fp16((L[name][1].shape[0],), 41_000 + 3 * li + j, 0.1, device)
+        g = torch.Generator(device="cpu").manual_seed(42_000 + li)
+        for name, n in (("q", 1536), ("v", 256)):
+            a = ((torch.rand((LORA_R, HIDDEN), generator=g) * 2 - 1) * bound).to(device).requires_grad_(True)
+            b = (torch.randn((n, LORA_R), generator=g) * 1e-3).to(device).requires_grad_(True)
+            L[name + "_lora"] = (a, b)
+    gen = torch.Generator(device="cpu").manual_seed(43_000)
+    x = torch.randn((M, HIDDEN), generator=gen).to(device).requires_grad_(True)  # fp32 norm output
+    attn = seeded_fp16((M, HIDDEN), 43_001, 1.0, device).requires_grad_(True)
+    keep_q = (torch.rand((M, HIDDEN), generator=gen) >= LORA_P).to(device)
+    keep_v = (torch.rand((M, HIDDEN), generator=gen) >= LORA_P).to(device)
+    scale = torch.tensor(1.0 / (1.0 - LORA_P), dtype=torch.float32, device=device)
+    c, s_ = rope_tables(C3_LENGTHS, HEAD_DIM)
+    cos, sin = torch.from_numpy(c).to(device), torch.from_numpy(s_).to(device)
+    gq = seeded_fp16((1, N_HEADS, M, HEAD_DIM), 43_002, 1e-2, device)
+    gk = seeded_fp16((1, N_KV_HEADS, M, HEAD_DIM), 43_003, 1e-2, device)
+    gv = seeded_fp16((M, N_KV_HEADS * HEAD_DIM), 43_004, 1e-2, device)
+    go = seeded_fp16((M, HIDDEN), 43_005, 1e-2, device)
+    sc = LORA_ALPHA / LORA_R
+
+    def fused(L):
+        bq, bv = lora.pack_keep(keep_q, keep_v)
+        (aq, bq_w), (av, bv_w) = L["q_lora"], L["v_lora"]
+        projs = (dict(packed=L["q"][0], qs=L["q"][1], bias=L["q_bias"], lora_a=aq, lora_b=bq_w, scaling=sc,
+                      keep_bits=bq, keep_scale=scale, p=LORA_P),
+                 dict(packed=L["k"][0], qs=L["k"][1], bias=L["k_bias"]),
+                 dict(packed=L["v"][0], qs=L["v"][1], bias=L["v_bias"], lora_a=av, lora_b=bv_w, scaling=sc,
+                      keep_bits=bv, keep_scale=scale, p=LORA_P))
+        q, k, v = lora.qkv_rope_projection(x, projs, cos, sin, N_HEADS, N_KV_HEADS)
+        o = nf4.NF4Linear.apply(attn, L["o"][0], None, L["o"][1])
+        torch.autograd.backward([q, k, v, o], [gq, gk, gv, go])
+
+    def reference_order(L):
+        (aq, bq_w), (av, bv_w) = L["q_lora"], L["v_lora"]
+        q_base = nf4.NF4Linear.apply(x.to(torch.float16), L["q"][0], L["q_bias"], L["q"][1])
+        k = nf4.NF4Linear.apply(x.to(torch.float16), L["k"][0], L["k_bias"], L["k"][1])
+        v_base = nf4.NF4Linear.apply(x.to(torch.float16), L["v"][0], L["v_bias"], L["v"][1])
+        bq, bv = lora.pack_keep(keep_q, keep_v)
+        q_lora, v_lora = lora.LoRAPairFromNorm.apply(x, None, None, None, None, bq, scale, None, bv, scale,
+                                                     aq, bq_w, av, bv_w, sc, sc, LORA_P, LORA_P, True)
+        v = (v_base.float() + v_lora.float()).to(torch.float16)
+        q, k = FusedQKRope.apply(q_base, q_lora.to(torch.float16), k, cos, sin, N_HEADS, N_KV_HEADS)
+        o = nf4.NF4Linear.apply(attn, L["o"][0], None, L["o"][1])
+        torch.autograd.backward([q, k, v, o], [gq, gk, gv, go])
+
+    def clear():
+        x.grad = attn.grad = None
+        for L in layers:
+            for a, b in (L["q_lora"], L["v_lora"]):
+                a.grad = b.grad = None
+
+    res = {}
+    for name, fn in (("fused", fused), ("reference_order", reference_order)):
+        for i in range(n_sets):  # fills every weight's block-scale cache
+            fn(layers[i])
+            clear()
+        for i in range(warmup):
+            fn(layers[i % n_sets])
+            clear()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(steps):
+            fn(layers[i % n_sets])
+            clear()
+        b.record()
+        torch.cuda.synchronize()
+        launches, busy = count_kernels(lambda fn=fn: (fn(layers[-1]), clear()))
+        res[name] = dict(ms=a.elapsed_time(b) / steps, launches=launches, busy_us=busy)
+    gemm = 2 * sum(gemm_flops(n, k) for name, n, k in QWEN15_SHAPES if name in ("q", "k", "v", "o"))
+    lora_f = sum(2 * M * LORA_R * (HIDDEN + n) + 2 * M * LORA_R * (2 * HIDDEN + 2 * n) for n in (1536, 256))
+    out = dict(workload="Qwen2.5-1.5B attention projections, one layer fwd+bwd, M=830 (8 packed sequences): "
+                        "q [1536,1536], k/v [256,1536] + biases, LoRA r=16 alpha 32 dropout 0.05 on q/v "
+                        "(fp32 x and adapters), RoPE 12/2 heads x 128, o [1536,1536]; NF4 bs 64 double quant; "
+                        f"{n_sets} layers of weights rotated",
+               step_gflops=round((gemm + lora_f) / 1e9, 2))
+    for name, r in res.items():
+        out[name] = dict(ms=round(r["ms"], 4), tflops=round((gemm + lora_f) / (r["ms"] * 1e-3) / 1e12, 1),
+                         launches=r["launches"],
+                         gpu_busy_ms=None if r["busy_us"] is None else round(r["busy_us"] / 1e3, 4))
+    out["speedup"] = round(res["reference_order"]["ms"] / res["fused"]["ms"], 3)
+    if res["fused"]["busy_us"] and res["reference_order"]["busy_us"]:
+        out["gpu_busy_speedup"] = round(res["reference_order"]["busy_us"] / res["fused"]["busy_us"], 3)
+    out["note"] = ("ms: eager steps back to back (HIP events), bound by the host's Python and launch "
+                   "overhead at this size; gpu_busy_ms: the kernels' summed durations in one profiled step")
+    return out
+
+
 # ---- config C4: the full Qwen2.5-1.5B frozen-linear stack, one training step ------------------
 
 LORA_R, LORA_ALPHA = 16, 32
@@ -516,6 +674,7 @@ def bench_c4(steps, warmup, device, n_layers=28):
         b.record()
         torch.cuda.synchronize()
         res[name] = a.elapsed_time(b) / steps
+    launches, busy = count_kernels(step)
     base, lora_f = stack_flops(n_layers)
     return dict(
         workload=f"Qwen2.5-1.5B {n_layers} layers x {{q,k,v,o,gate,up,down}} NF4 (bs 64, double quant) + "
@@ -527,7 +686,10 @@ def bench_c4(steps, warmup, device, n_layers=28):
         tflops=round((base + lora_f) / (res["step"] * 1e-3) / 1e12, 1),
         gemm_tflops=round(base / (res["gemm_only"] * 1e-3) / 1e12, 1),
         frac=round(base / (res["gemm_only"] * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4),
-        step_gflops=round((base + lora_f) / 1e9, 1), launches_per_step=14 * n_layers)
+        step_gflops=round((base + lora_f) / 1e9, 1), launches_per_step=launches,
+        gpu_busy_ms=None if busy is None else round(busy / 1e3, 4),
+        note="ms_per_step: steps back to back (HIP events); gpu_busy_ms: the kernels' summed durations in "
+             "one profiled step (the gap to ms_per_step is host launch overhead)")
 
 
 # ---- config C5: the Qwen2.5-7B sweep -----------------------------------------------------------
@@ -613,7 +775,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-dequant", action="store_true")
     ap.add_argument("--skip-configs", action="store_true",
-                    help="skip the 28-layer stack step (C4) and the Qwen2.5-7B sweep (C5)")
+                    help="skip the attention-projection step (C3), the 28-layer stack step (C4) and "
+                         "the Qwen2.5-7B sweep (C5)")
+    ap.add_argument("--configs", default="c3,c4,c5",
+                    help="comma-separated subset of c3, c4, c5 to run besides the headline MLP step")
     ap.add_argument("--only", default=None,
                     choices=["fwd_gate_up", "fwd_down", "bwd_down", "bwd_gate_up"],
                     help="time only this launch kind (for counter runs); prints its roofline only")
@@ -651,11 +816,17 @@ def main():
         del src, dst
     with no_gc():
         deq = None if (args.skip_dequant or args.only) else bench_dequant(max(args.steps, 10), args.warmup, device)
-    c4 = c5 = None
-    if not (args.skip_configs or args.only):
+    c3 = c4 = c5 = None
+    configs = set() if (args.skip_configs or args.only) else {c.strip() for c in args.configs.split(",") if c.strip()}
+    if "c3" in configs:
+        with no_gc():
+            c3 = bench_c3(max(args.steps, 10), args.warmup, device)
+        torch.cuda.empty_cache()
+    if "c4" in configs:
         with no_gc():
             c4 = bench_c4(max(2, min(args.steps, 5)), 1, device)
         torch.cuda.empty_cache()
+    if "c5" in configs:
         with no_gc():
             c5 = bench_c5(device)
         torch.cuda.empty_cache()
@@ -707,6 +878,8 @@ def main():
                                              frac=round(deq["gbs"] / HBM_PEAK_GBS, 4),
                                              measured_ceiling=round(mixed_ceiling(peaks, deq["read"], deq["write"]), 1),
                                              frac_of_measured=round(deq["gbs"] / mixed_ceiling(peaks, deq["read"], deq["write"]), 4)))
+    if c3 is not None:
+        line["c3_attention_step"] = c3
     if c4 is not None:
         line["c4_stack_step"] = c4
     if c5 is not None:

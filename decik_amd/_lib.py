@@ -113,8 +113,18 @@ def check(rc):
         raise DecikError(lib().dk_last_error().decode())
 
 
+_raw_stream = torch._C._cuda_getCurrentRawStream
+
+
+def raw_stream(device):
+    """The current HIP stream of `device` as an integer handle (what torch.cuda.current_stream(
+    device).cuda_stream returns, without building a Stream object on every call)."""
+    idx = device.index
+    return _raw_stream(torch.cuda.current_device() if idx is None else idx)
+
+
 def stream_of(device):
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    return ctypes.c_void_p(raw_stream(device))
 
 
 def ptr(t):
@@ -200,6 +210,40 @@ class ScaleCache:
 SCALES = ScaleCache()
 
 
+class DescCache:
+    """The NF4Weight descriptor the fused GEMMs take for a (packed, QuantState) pair -- with the
+    cached block scales for a nested weight -- built once and reused while the packed tensor and
+    the statistics are unchanged (the check costs a few attribute reads, building the descriptor
+    several times that)."""
+
+    def __init__(self):
+        self._d = {}
+        self._lock = threading.Lock()
+
+    def get(self, packed, qs, device):
+        scales = SCALES.get(packed, qs, device) if qs.nested else None
+        key = id(qs)
+        ver = (packed.data_ptr(), device.index, id(scales),
+               _version_key(qs) if qs.nested else ((qs.absmax.data_ptr(), qs.absmax._version),
+                                                    int(qs.blocksize), tuple(int(v) for v in qs.shape)))
+        with self._lock:
+            ent = self._d.get(key)
+        if ent is not None and ent[0] == ver and ent[3]() is qs:
+            return ent[1], ent[2]
+        w, keep = weight_desc(packed, qs, device, scales)
+
+        def drop(_ref, key=key):
+            with self._lock:
+                self._d.pop(key, None)
+
+        with self._lock:
+            self._d[key] = (ver, w, keep, weakref.ref(qs, drop))
+        return w, keep
+
+
+DESCS = DescCache()
+
+
 class Workspace:
     """Split-K workspaces (fp32 partial slabs), one per (device, stream), grown on demand."""
 
@@ -210,7 +254,7 @@ class Workspace:
     def get(self, nbytes, device):
         if nbytes <= 0:
             return None, 0
-        key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+        key = (device.index, raw_stream(device))
         with self._lock:
             buf = self._bufs.get(key)
             if buf is None or buf.numel() < nbytes:
