@@ -338,7 +338,7 @@ bool small_m_forward(int64_t m, bool glu, bool lora) {
     return forced == nullptr || *forced == 0;
 }
 bool gemv_requested(int64_t m, int64_t k) {
-    if (m > kGemvMaxM) return false;
+    if (m > kGemvMaxM || !gemv_fits(k)) return false;
     const char* v = std::getenv("DECIK_SMALL_M");
     if (v != nullptr && std::string(v) == "gemv") return true;
     if (v != nullptr && std::string(v) == "skinny") return false;

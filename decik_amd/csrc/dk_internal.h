@@ -146,7 +146,10 @@ struct GemmPlan {
 hipError_t launch_fwd(const FwdArgs& a, int mb, int grid, hipStream_t s);
 // GEMV for launches of at most kGemvMaxM token rows (no LoRA terms, no GLU epilogue, no split)
 constexpr int kGemvMaxM = 2;  // measured: the MFMA kernels are faster from 3 token rows on 7B shapes
-hipError_t launch_gemv(const FwdArgs& a, hipStream_t s);
+// a: the groups' tile_begin fields become their first work-group. gemv_fits: the GEMV takes
+// this contraction length.
+hipError_t launch_gemv(FwdArgs& a, hipStream_t s);
+bool gemv_fits(int64_t k);
 // Forward launches of few token rows (no LoRA terms, no GLU epilogue): nf4_skinny_kernel. A
 // work-group owns 64 weight rows; a.splits work-groups share them along the contraction, each
 // covering a.ksteps_per_split 128-wide super-steps; g[].tile_begin = each group's first 64-row

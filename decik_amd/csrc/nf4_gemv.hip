@@ -1,164 +1,252 @@
-// Fused NF4 dequant x fp16 product for launches with few token rows (m <= kGemvMaxM): the same
-// Y = X.W^T + bias as nf4_fwd_kernel (solution/nf4.py:93-96) for the small-M regime (one token
-// when decoding, a handful in a short batch), where the product is bound by reading the packed
-// weight once. The MFMA kernels pad such launches to 32-token tiles and dequantize every weight
-// for one useful multiply-add; here each weight is dequantized once and used for every token in
-// fp32 dot products.
+// Fused NF4 dequant x fp16 product for launches with one or two token rows: the same
+// Y = X.W^T + bias as nf4_fwd_kernel (solution/nf4.py:93-96) in the decoding regime, where the
+// call is bound by streaming the packed weight from HBM once. The MFMA kernels pad such launches
+// to 32-token tiles and dequantize every weight for one useful multiply-add; here each weight is
+// dequantized once and used for every token in fp32 dot products (v_dot2_f32_f16).
 //
-// Each wave owns RW consecutive weight rows (four waves per work-group): lane l takes 16-byte
-// chunks l, l + 64, ... of each row (32 weights of one block each; every load instruction reads
-// 1 KB contiguous of one row), dequantizes them to the reference's fp16 bits through a byte-pair
-// code book (one 8-byte LDS read per packed byte), and accumulates v_dot2_f32_f16 products with
-// the matching 32 values of every token row of X (fp32 accumulation). One X fragment serves the
-// RW rows: with RW = 4, X (read from the caches) costs a quarter of what it costs with a row per
-// wave, where it was read four times for every packed byte (7B gate at one token: 23 -> 18 us).
-// Launches with few rows (long ones: 7B down) keep RW = 1 for enough waves to cover the memory
-// latency. A butterfly reduction over the wave's lanes finishes each dot product; lanes 0..RW-1
-// add the bias, round once to fp16 and store.
+// The kernel is organised around keeping as much of the weight in flight as HBM needs:
+// - A work-group (four waves) owns `rows` consecutive weight rows of one group. Their packed
+//   bytes are contiguous ([n, k / 2] row-major), so the work-group streams one contiguous range
+//   of 16-byte chunks (32 weights of one block each: blocks are powers of two >= 32 and
+//   k % 32 == 0): thread t takes chunks t, t + 256, ..., so every load instruction reads 4 KB
+//   contiguous, and all of a thread's chunk loads (and their block scales) are issued before
+//   any is used -- the whole weight of a 7B projection is in flight at once.
+// - X (m x k fp16) is copied to LDS by the work-group while the weight loads are in flight, in
+//   a transposed order: 16-byte piece e of the 64-byte k-range p of a chunk goes to slot
+//   e * (k / 32) + p, so the lanes of a wave (consecutive chunks, consecutive p) read
+//   consecutive 16-byte slots -- no LDS bank conflicts -- where the natural order would put 64
+//   bytes between neighbouring lanes.
+// - Each chunk's dot products (fp32) go to an LDS slot; a wave then sums each row's slots in a
+//   fixed order (lane l: slots l, l + 64, ...; then a butterfly across the lanes), adds the bias,
+//   rounds once to fp16 and stores. The summation order depends only on k: every call gives the
+//   same bits.
+// - Dequantization as in the other kernels: byte-pair code book in LDS (one 8-byte read per
+//   packed byte), fp32 multiply by the block scale, one fp16 rounding: the reference's bits.
 #include "dk_internal.h"
 
 namespace dk {
 
 constexpr int kGemvThreads = 256;  // four waves
+constexpr int kGemvMaxChunks = 8;  // chunks (16-byte loads) per thread
 
-template <int MT, bool NESTED, int kGemvRows>
-__global__ __launch_bounds__(kGemvThreads) void nf4_gemv_kernel(const FwdArgs a) {
-    // byte-pair code books: entry 256 g + b holds (code_g[b >> 4], code_g[b & 15]), the two
-    // weights of packed byte b
-    __shared__ float2_t lut2[256 * kMaxGroups];
-    for (int gg = 0; gg < a.ngroups; ++gg) {
-        const float* code = a.g[gg].w.code;
-        lut2[256 * gg + threadIdx.x] = float2_t{code[threadIdx.x >> 4], code[threadIdx.x & 15]};
-    }
-    __syncthreads();
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+// LDS bytes of a launch: code book, X of the token rows, the chunk partial sums
+static size_t gemv_smem_bytes(int mt, int k, int chunks) {
+    // dynamic part: nested code2 table (256 floats), X, sums (the code book is static)
+    return 256 * sizeof(float) + (size_t)mt * k * 2 + (size_t)mt * chunks * sizeof(float);
+}
 
-    // this wave's first row among the launch's rows (groups back to back, col_begin = first row;
-    // groups have n % 8 == 0, so a wave's rows lie in one group)
-    const int row0 = (blockIdx.x * (kGemvThreads / 64) + wave) * kGemvRows;
-    if (row0 >= a.ncols) return;
+template <int MT, bool NESTED, int CPT>
+__global__ __launch_bounds__(kGemvThreads) void nf4_gemv_kernel(const FwdArgs a, const int rows_per_wg) {
+    // byte-pair code book (static: its address is a constant the LDS reads take as an offset)
+    __shared__ float2_t lut2[256];
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    float* c2 = (float*)smem;                        // nested: code2 table
+    _Float16* xs = (_Float16*)(smem + 256 * 4);      // [MT][k], transposed 16-byte pieces
+    const int K = a.k, M = a.m;
+    float* part = (float*)(xs + MT * K);             // [MT][rows * cpr]
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS bases stay scalar
     int gi = 0;
 #pragma unroll
-    for (int i = 1; i < kMaxGroups; ++i)
-        if (i < a.ngroups && row0 >= a.g[i].col_begin) gi = i;
+    for (int q = 1; q < kMaxGroups; ++q)
+        if (q < a.ngroups && (int)blockIdx.x >= a.g[q].tile_begin) gi = q;
     const FwdGroupDev& G = a.g[gi];
     const NF4Dev& W = G.w;
-    const int n0 = row0 - G.col_begin;
-    const int K = a.k, M = a.m;
-    const int64_t rowb = (int64_t)(K >> 1);  // packed bytes per row
-    const char* book = (const char*)(lut2 + 256 * gi);
-    const float offset = NESTED ? *W.offset : 0.0f;
+    const int N = (int)W.n;
+    const int n0 = ((int)blockIdx.x - G.tile_begin) * rows_per_wg;
+    const int rows = min(rows_per_wg, N - n0);
+    const int cpr = K >> 5;                 // chunks per row
+    const int nch = rows * cpr;             // chunks of this work-group
+    const uint32_t c0 = (uint32_t)n0 * (uint32_t)cpr;  // first chunk (flat over the weight)
 
-    float acc[kGemvRows][MT];
-#pragma unroll
-    for (int r = 0; r < kGemvRows; ++r)
-#pragma unroll
-        for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
-    // chunk c = 16 packed bytes = 32 weights of one block (k % 32 == 0, blocks >= 32, aligned)
-    for (int c = lane; c < (K >> 5); c += 64) {
-        u32x4_t p[kGemvRows];
-#pragma unroll
-        for (int r = 0; r < kGemvRows; ++r) p[r] = *(const u32x4_t*)(W.packed + (int64_t)(n0 + r) * rowb + 16 * c);
-        float s[kGemvRows];
-#pragma unroll
-        for (int r = 0; r < kGemvRows; ++r) {
-            const int64_t blk = ((int64_t)(n0 + r) * K + 32 * c) >> W.bs_shift;
-            if constexpr (NESTED) {
-                s[r] = W.code2[W.absmax8[blk]] * W.absmax2[blk >> W.bs2_shift];
-                s[r] = s[r] + offset;
-            } else {
-                s[r] = W.absmaxf[blk];
-            }
-        }
-        // the 32 X values of this chunk for every token row (elements copied to scalars:
-        // hipcc compiles __builtin_bit_cast of a vector element v[j] as element 0 whatever j is)
-        uint32_t xs[MT][16];
-#pragma unroll
+    // Load order (vector memory operations complete in order): the code-book entries of this
+    // thread, X of every token row straight into LDS (no registers), then the thread's chunk loads
+    // and block scales, all issued before any is used; waiting until only the chunk loads are
+    // outstanding then covers the code book and X.
+    const float b_hi = W.code[tid >> 4], b_lo = W.code[tid & 15];
+    const float c2v = NESTED ? W.code2[tid] : 0.0f;
+    const float offset = NESTED ? *W.offset : 0.0f;
+    {
+        const uint32_t xbytes = (uint32_t)K * 2u;
         for (int m = 0; m < MT; ++m) {
-            if (m < M) {
-                const u32x4_t* xp = (const u32x4_t*)(a.x + (int64_t)m * a.ldx + 32 * c);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const u32x4_t xv = xp[e];
-                    xs[m][4 * e + 0] = xv[0];
-                    xs[m][4 * e + 1] = xv[1];
-                    xs[m][4 * e + 2] = xv[2];
-                    xs[m][4 * e + 3] = xv[3];
-                }
-            } else {
-#pragma unroll
-                for (int q = 0; q < 16; ++q) xs[m][q] = 0u;
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < kGemvRows; ++r) {
-            // the reference's fp16 bits of the row's 32 weights: pair q of dword e = weights
-            // 8 e + 2 q, + 1
-            const uint32_t pw[4] = {p[r][0], p[r][1], p[r][2], p[r][3]};
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const float2_t cv = *(const float2_t*)(book + (((pw[e] >> (8 * q)) & 0xFFu) << 3));
-                    const uint32_t w2 = pack_half2(cv.x * s[r], cv.y * s[r]);
-#pragma unroll
-                    for (int m = 0; m < MT; ++m)
-                        acc[r][m] = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, w2),
-                                                           __builtin_bit_cast(half2_t, xs[m][4 * e + q]), acc[r][m],
-                                                           false);
+            const rsrc_t xr = make_rsrc(a.x + (int64_t)min(m, M - 1) * a.ldx, m < M ? xbytes : 0u);
+            for (uint32_t o = 1024u * (uint32_t)wave; o < xbytes; o += 4096u)
+                if (o + 16u * (uint32_t)lane < xbytes) {  // rows past m: zeros (descriptor of size 0)
+                    // slot s = e * cpr + p holds piece e of k-range p: source bytes 16 (4 p + e)
+                    const uint32_t sl = (o >> 4) + (uint32_t)lane, e = sl / (uint32_t)cpr;
+                    const uint32_t src = (4u * (sl - e * (uint32_t)cpr) + e) * 16u;
+                    bload128_lds(xr, (uint8_t*)xs + (size_t)m * xbytes + o, src);
                 }
         }
     }
+    asm volatile("" ::: "memory");  // the chunk loads stay behind the X loads (the wait below counts on it)
+    const rsrc_t wrs = make_rsrc(W.packed, W.packed_bytes);
+    const rsrc_t ars = make_rsrc(NESTED ? (const void*)W.absmax8 : (const void*)W.absmaxf, W.absmax_bytes);
+    const rsrc_t a2rs = make_rsrc(W.absmax2, NESTED ? W.absmax2_bytes : 0u);
+    const uint32_t bs_shift = W.bs_shift, bs2_shift = W.bs2_shift;
+    u32x4_t p[CPT];
+    float s[CPT];
+    uint32_t q8[CPT];
 #pragma unroll
-    for (int r = 0; r < kGemvRows; ++r)
+    for (int i = 0; i < CPT; ++i) {
+        const int c = tid + kGemvThreads * i;
+        const bool ok = c < nch;
+        const uint32_t ch = c0 + (uint32_t)c;
+        p[i] = bload128(wrs, off_if(ok, ch * 16u));
+        const uint32_t blk = (ch * 32u) >> bs_shift;
+        if constexpr (NESTED) {
+            q8[i] = bload8(ars, off_if(ok, blk));
+            s[i] = bloadf(a2rs, off_if(ok, (blk >> bs2_shift) * 4u));
+        } else {
+            s[i] = bloadf(ars, off_if(ok, blk * 4u));
+        }
+    }
+
+    // code book and nested code2 table; the barrier (without the release fence of
+    // __syncthreads, which would wait for the chunk loads too) then publishes every wave's share
+    // of them and of X
+    wait_vmcnt<(NESTED ? 3 : 2) * CPT>();
+    lut2[tid] = float2_t{b_hi, b_lo};
+    if constexpr (NESTED) c2[tid] = c2v;
+    lds_barrier();
+
+    // k-range p (chunk within its row) of the thread's chunk i: advanced by 256 chunks a step
+    int pk = tid % cpr;
+    const int dp = kGemvThreads % cpr;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+        const int c = tid + kGemvThreads * i;
+        float sc = s[i];
+        if constexpr (NESTED) sc = c2[q8[i]] * sc + offset;  // two roundings (no contraction)
+        const int pc = c < nch ? pk : 0;
+        pk += dp;
+        if (pk >= cpr) pk -= cpr;
+        // the 32 X values of this chunk for every token row: dword j of piece e holds
+        // X[32 p + 8 e + 2 j] and X[32 p + 8 e + 2 j + 1]
+        u32x4_t xv[MT][4];
 #pragma unroll
         for (int m = 0; m < MT; ++m)
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) acc[r][m] += __shfl_xor(acc[r][m], o, 64);
-    if (lane < kGemvRows) {
-        // lane r stores row n0 + r (the butterfly left every lane with every total)
+            for (int e = 0; e < 4; ++e) xv[m][e] = *(const u32x4_t*)(xs + m * K + (e * cpr + pc) * 8);
+        float acc[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t w = p[i][e];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                // packed byte 4 e + q: weights 32 p + 8 e + 2 q (high nibble) and + 1
+                const float2_t cv = *(const float2_t*)((const char*)lut2 + (((w >> (8 * q)) & 0xFFu) << 3));
+                const half2_t w2 = __builtin_bit_cast(half2_t, pack_half2(cv.x * sc, cv.y * sc));
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    // elements copied to a scalar first: hipcc compiles __builtin_bit_cast of a
+                    // vector element v[j] as element 0 whatever j is
+                    const uint32_t xq = xv[m][e][q];
+                    acc[m] = __builtin_amdgcn_fdot2(w2, __builtin_bit_cast(half2_t, xq), acc[m], false);
+                }
+            }
+        }
+        // the chunk's sums go to LDS at once (kept in registers to the end, the compiler sinks
+        // their arithmetic below everything and holds every chunk's operands meanwhile)
+        if (c < nch)
+#pragma unroll
+            for (int m = 0; m < MT; ++m) part[m * nch + c] = acc[m];
+    }
+    lds_barrier();
+
+    // each row's sum in a fixed order: lane l adds slots l, l + 64, ... of the row, then a butterfly
+    for (int r = wave; r < rows; r += kGemvThreads / 64) {
         float v[MT];
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-            v[m] = acc[0][m];
+            v[m] = 0.0f;
+            for (int j = lane; j < cpr; j += 64) v[m] += part[m * nch + r * cpr + j];
 #pragma unroll
-            for (int r = 1; r < kGemvRows; ++r)
-                if (lane == r) v[m] = acc[r][m];
+            for (int o = 32; o > 0; o >>= 1) v[m] += __shfl_xor(v[m], o, 64);
         }
-        const int n = n0 + lane;
-        const float b = G.bias != nullptr ? (float)G.bias[n] : 0.0f;
+        if (lane == 0) {
+            const int n = n0 + r;
+            const float b = G.bias != nullptr ? (float)G.bias[n] : 0.0f;
 #pragma unroll
-        for (int m = 0; m < MT; ++m)
-            if (m < M) G.y[(int64_t)m * G.ldy + n] = to_half(v[m] + b);
+            for (int m = 0; m < MT; ++m)
+                if (m < M) G.y[(int64_t)m * G.ldy + n] = to_half(v[m] + b);
+        }
     }
 }
 
-template <int MT, int RW>
-static hipError_t launch_gemv_rw(const FwdArgs& a, hipStream_t s) {
-    const int rows_per_wg = (kGemvThreads / 64) * RW;
-    const int grid = (a.ncols + rows_per_wg - 1) / rows_per_wg;
-    if (a.nested)
-        hipLaunchKernelGGL((nf4_gemv_kernel<MT, true, RW>), dim3(grid), dim3(kGemvThreads), 0, s, a);
-    else
-        hipLaunchKernelGGL((nf4_gemv_kernel<MT, false, RW>), dim3(grid), dim3(kGemvThreads), 0, s, a);
+// Work-group shape of a launch: `cpt` chunk loads per thread and `rows` rows per work-group
+// (rows * cpr <= 256 cpt). The fewest loads per thread whose rows fill at least 95% of them
+// (more, smaller work-groups measured faster: 7B gate at one token 15.1 us with 7 loads, 13.3
+// with 5), else the best fill.
+struct GemvShape {
+    int cpt, rows;
+};
+
+static GemvShape gemv_shape(int k) {
+    const int cpr = k >> 5;
+    GemvShape best{0, 0};
+    double best_fill = -1.0;
+    for (int cpt = 4; cpt <= kGemvMaxChunks; ++cpt) {
+        const int rows = kGemvThreads * cpt / cpr;
+        if (rows < 1) continue;
+        const double fill = (double)rows * cpr / (kGemvThreads * cpt);
+        if (fill >= 0.95) return GemvShape{cpt, rows};
+        if (fill > best_fill + 1e-9) {
+            best_fill = fill;
+            best = GemvShape{cpt, rows};
+        }
+    }
+    return best;
+}
+
+// Whether the GEMV takes a launch of contraction k (a row must fit one work-group's loads, X of
+// two token rows and the sums must fit LDS).
+bool gemv_fits(int64_t k) {
+    if (k <= 0 || k % 32 != 0 || k > kGemvThreads * kGemvMaxChunks * 32) return false;
+    const GemvShape sh = gemv_shape((int)k);
+    return sh.rows >= 1 && gemv_smem_bytes(kGemvMaxM, (int)k, sh.rows * (int)(k >> 5)) <= 158 * 1024;
+}
+
+template <int MT, bool NESTED, int CPT>
+static hipError_t launch_gemv_t(const FwdArgs& a, int rows, int grid, hipStream_t s) {
+    const size_t lds = gemv_smem_bytes(MT, a.k, rows * (a.k >> 5));
+    const hipError_t e = allow_dynamic_lds((const void*)nf4_gemv_kernel<MT, NESTED, CPT>, lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((nf4_gemv_kernel<MT, NESTED, CPT>), dim3(grid), dim3(kGemvThreads), lds, s, a, rows);
     return hipGetLastError();
 }
 
-// four rows per wave while that still gives four waves per SIMD on a 256-CU device
-template <int MT>
-static hipError_t launch_gemv_t(const FwdArgs& a, hipStream_t s) {
-    return a.ncols >= 4 * 4 * 1024 ? launch_gemv_rw<MT, 4>(a, s) : launch_gemv_rw<MT, 1>(a, s);
+template <int MT, bool NESTED>
+static hipError_t launch_gemv_cpt(const FwdArgs& a, int cpt, int rows, int grid, hipStream_t s) {
+    switch (cpt) {
+        case 4: return launch_gemv_t<MT, NESTED, 4>(a, rows, grid, s);
+        case 5: return launch_gemv_t<MT, NESTED, 5>(a, rows, grid, s);
+        case 6: return launch_gemv_t<MT, NESTED, 6>(a, rows, grid, s);
+        case 7: return launch_gemv_t<MT, NESTED, 7>(a, rows, grid, s);
+        case 8: return launch_gemv_t<MT, NESTED, 8>(a, rows, grid, s);
+        default: return hipErrorInvalidValue;
+    }
 }
 
-hipError_t launch_gemv(const FwdArgs& a, hipStream_t s) {
-    if (a.m < 1 || a.m > kGemvMaxM || a.glu) return hipErrorInvalidValue;
+// a: the groups' tile_begin fields are overwritten with their first work-group
+hipError_t launch_gemv(FwdArgs& a, hipStream_t s) {
+    if (a.m < 1 || a.m > kGemvMaxM || a.glu || !gemv_fits(a.k)) return hipErrorInvalidValue;
     for (int g = 0; g < a.ngroups; ++g)
         if (a.g[g].lora_u != nullptr) return hipErrorInvalidValue;
-    if (a.m == 1) return launch_gemv_t<1>(a, s);
-    if (a.m == 2) return launch_gemv_t<2>(a, s);
-    if (a.m <= 4) return launch_gemv_t<4>(a, s);
-    return launch_gemv_t<8>(a, s);
+    const GemvShape sh = gemv_shape(a.k);
+    int grid = 0;
+    for (int g = 0; g < a.ngroups; ++g) {
+        a.g[g].tile_begin = grid;
+        grid += (int)((a.g[g].w.n + sh.rows - 1) / sh.rows);
+    }
+    if (a.m == 1)
+        return a.nested ? launch_gemv_cpt<1, true>(a, sh.cpt, sh.rows, grid, s)
+                        : launch_gemv_cpt<1, false>(a, sh.cpt, sh.rows, grid, s);
+    return a.nested ? launch_gemv_cpt<2, true>(a, sh.cpt, sh.rows, grid, s)
+                    : launch_gemv_cpt<2, false>(a, sh.cpt, sh.rows, grid, s);
 }
 
 }  // namespace dk

@@ -194,9 +194,10 @@ def test_skinny_split_k(m, raw, device, monkeypatch, skinny):
 @pytest.mark.parametrize("m", [1, 2])
 @pytest.mark.parametrize("nested,blocksize", CASES)
 def test_gemv_small_m(m, nested, blocksize, device, raw_statistics, gemv):
-    """The GEMV kernel (forward launches of at most 2 token rows without LoRA terms, when asked
-    for): three weights in one launch (q/k/v-like, with bias), statistics read raw, k = 1056 (a
-    row of 33 16-byte chunks: lane 0 takes two)."""
+    """The GEMV kernel (forward launches of at most 2 token rows without LoRA terms): three
+    weights in one launch (q/k/v-like, with bias; each weight's last work-group holds fewer
+    rows), statistics read raw, k = 1056 (rows of 33 16-byte chunks: a work-group's chunk range
+    and its X pieces wrap across rows at odd positions)."""
     from decik_amd.nf4 import launch_plan, linear_forward
 
     assert launch_plan(False, m, 1056, [320, 64, 64])["kernel"] == "nf4_gemv_kernel"
@@ -215,9 +216,9 @@ def test_gemv_small_m(m, nested, blocksize, device, raw_statistics, gemv):
 
 @pytest.mark.parametrize("m", [1, 2])
 def test_gemv_short_k_no_bias(m, device, gemv):
-    """GEMV edges: k = 64 (two 16-byte chunks per row: lanes 2-63 hold no weights), two weights
-    of 72 and 8 rows, no bias. Weight rows must be a multiple of 8: a 67-row weight is rejected
-    with that message before anything runs."""
+    """GEMV edges: k = 64 (two 16-byte chunks per row: a work-group takes hundreds of rows), two
+    weights of 72 and 8 rows, no bias. Weight rows must be a multiple of 8: a 67-row weight is
+    rejected with that message before anything runs."""
     from decik_amd import _lib
     from decik_amd.nf4 import launch_plan, linear_forward
 
@@ -233,6 +234,28 @@ def test_gemv_short_k_no_bias(m, device, gemv):
         refs.append(O.linear_ref(x.cpu().numpy(), w16))
     for y, ref in zip(linear_forward(x, items), refs):
         assert_close(y, ref, what=f"gemv short k m={m}")
+
+
+@pytest.mark.parametrize("m", [1, 2])
+def test_gemv_long_k(m, device, monkeypatch):
+    """A long contraction (k = 18944, the 7B down projection's: 592 chunks a row, three rows a
+    work-group, X staged whole in LDS; two token rows are sent to the GEMV on purpose, the
+    planner would take the small-M MFMA kernel): 40 rows against the oracle, and the same bits on
+    a second call (the row sums run in a fixed order)."""
+    import torch
+
+    from decik_amd.nf4 import launch_plan, linear_forward
+
+    monkeypatch.setenv("DECIK_SMALL_M", "gemv")
+    k = 18944
+    assert launch_plan(False, m, k, [40])["kernel"] == "nf4_gemv_kernel"
+    packed, qs, w16 = make_weight((40, k), seed=150, device=device)
+    x = randn16((m, k), seed=151 + m, device=device)
+    b = randn16((40,), seed=153, device=device, std=0.1)
+    (y,) = linear_forward(x, [dict(packed=packed, qs=qs, bias=b)])
+    assert_close(y, O.linear_ref(x.cpu().numpy(), w16, b.cpu().numpy()), what=f"gemv long k m={m}")
+    (y2,) = linear_forward(x, [dict(packed=packed, qs=qs, bias=b)])
+    assert torch.equal(y, y2)
 
 
 def test_gemv_not_used_with_lora_or_forced_plan(device, monkeypatch):
