@@ -703,42 +703,74 @@ def fused_bytes(n, k, m):
     return nf4_bytes(n, k) + 2 * m * (n + k)
 
 
-def bench_c5(device, reps=7, flush_bytes=512 << 20):
+def bench_c5(device, reps=3, min_bytes=512 << 20):
     """Each 7B projection shape at every M: forward Y = X.W^T (the GEMV kernel at M = 1, the
     small-M kernel at M = 8, the MFMA kernels above) and, for M >= 64, the input gradient
-    dX = dY.W. Before every timed call a sum over a 512 MiB buffer evicts the caches (L2 and the
-    256 MB Infinity Cache) by reading -- a fill would leave dirty lines whose write-back the timed
-    call would pay for (about 3 us on the large shapes) -- so the weight comes from HBM; the call
-    is bracketed by HIP events on its stream (the flush also covers the host's enqueue time).
-    Median of `reps`."""
+    dX = dY.W. Enough copies of the weight to total more than 512 MB of NF4 data are called back
+    to back, so every call reads its weight from HBM (the 256 MB Infinity Cache cannot hold the
+    set) while X / dY stay cached, as they would between consecutive layers. The calls are
+    captured once in a HIP graph and the graph is replayed: what is timed is the GPU's work (the
+    host's per-call Python and launch cost would otherwise bound the small shapes). Each replay's
+    last output is checked against the same call run eagerly; a shape whose capture fails or
+    differs is timed eagerly instead (`timing` says which). Per-call time = replay time / copies,
+    median of `reps` replays."""
     import torch
 
     from decik_amd import nf4
     from decik_amd.quant import quantize_nf4
 
-    flush = torch.ones(flush_bytes // 4, dtype=torch.float32, device=device)
-    sink = torch.empty(1, dtype=torch.float32, device=device)
     rows = []
     for si, (name, n, k) in enumerate(QWEN7_SHAPES):
-        packed, qs = quantize_nf4(seeded_fp16((n, k), 30_000 + si, 0.02, device), blocksize=64,
-                                  compress_statistics=True)
+        copies = max(2, min(600, -(-min_bytes // nf4_bytes(n, k))))
+        base = seeded_fp16((n, k), 30_000 + si, 0.02, device)
+        ws = []
+        for c in range(copies):
+            # distinct weights (a sign flip of a seeded pattern per copy) so no two calls share lines
+            ws.append(quantize_nf4(base if c % 2 == 0 else -base, blocksize=64, compress_statistics=True))
+        del base
         for m in C5_M:
             x = seeded_fp16((m, k), 31_000 + m, 1.0, device)
             dy = seeded_fp16((m, n), 32_000 + m, 1e-2, device)
-            calls = {"fwd": lambda: nf4.linear_forward(x, [dict(packed=packed, qs=qs)])}
+            kinds = {"fwd": lambda p, q: nf4.linear_forward(x, [dict(packed=p, qs=q)])[0]}
             if m >= 64:
-                calls["bwd"] = lambda: nf4.linear_backward([dict(packed=packed, qs=qs, dy=dy)], m, k)
-            for d, fn in calls.items():
-                fn()
+                kinds["bwd"] = lambda p, q: nf4.linear_backward([dict(packed=p, qs=q, dy=dy)], m, k)
+            for d, call in kinds.items():
+                for p, q in ws:  # fills every block-scale cache and the workspace
+                    call(p, q)
+                torch.cuda.synchronize()
+                ref = call(*ws[-1]).clone()
+                timing = "graph"
+                try:
+                    g = torch.cuda.CUDAGraph()
+                    side = torch.cuda.Stream()
+                    side.wait_stream(torch.cuda.current_stream())
+                    with torch.cuda.stream(side):
+                        call(*ws[0])  # warm-up on the capture stream
+                    torch.cuda.current_stream().wait_stream(side)
+                    torch.cuda.synchronize()
+                    outs = []
+                    with torch.cuda.graph(g):
+                        for p, q in ws:
+                            outs.append(call(p, q))
+                    g.replay()
+                    torch.cuda.synchronize()
+                    if not torch.equal(outs[-1], ref):
+                        raise RuntimeError("graph replay differs from the eager call")
+                    run = g.replay
+                except Exception:  # noqa: BLE001 - timed eagerly instead
+                    timing, g, outs = "eager", None, None
+                    run = lambda: [call(p, q) for p, q in ws]  # noqa: E731
                 times = []
                 for _ in range(reps):
-                    torch.sum(flush, dim=0, out=sink[0])
                     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                     a.record()
-                    fn()
+                    run()
                     b.record()
                     torch.cuda.synchronize()
-                    times.append(a.elapsed_time(b))
+                    times.append(a.elapsed_time(b) / copies)
+                if outs is not None and not torch.equal(outs[-1], ref):
+                    raise RuntimeError(f"C5 {name} m={m} {d}: a graph replay differs from the eager call")
+                del g, outs
                 ms = statistics.median(times)
                 fl = gemm_flops(n, k, m)
                 by = fused_bytes(n, k, m)
@@ -747,11 +779,13 @@ def bench_c5(device, reps=7, flush_bytes=512 << 20):
                                  gbs=round(by / (ms * 1e-3) / 1e9, 1), hbm_frac=round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                                  tflops=round(fl / (ms * 1e-3) / 1e12, 2),
                                  mfma_frac=round(fl / (ms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4),
-                                 kernel=plan["kernel"], splits=plan["splits"]))
-        del packed, qs
-    del flush
-    return dict(workload="Qwen2.5-7B projections (NF4 bs 64, double quant), one call per shape and M, "
-                         "caches flushed before each call", rows=rows)
+                                 kernel=plan["kernel"], splits=plan["splits"], copies=copies, timing=timing))
+            torch.cuda.empty_cache()
+        del ws
+        torch.cuda.empty_cache()
+    return dict(workload="Qwen2.5-7B projections (NF4 bs 64, double quant, cached fp32 block scales), each shape "
+                         "and M: back-to-back calls over weight copies totalling > 512 MB (weights from HBM), "
+                         "replayed from a HIP graph", rows=rows)
 
 
 def load_traffic(kind):
@@ -767,6 +801,19 @@ def load_traffic(kind):
         return None
 
 
+def copy_probe(device):
+    """The fp32 -> fp16 conversion of 128 Mi values three times: one elementwise kernel of known
+    traffic (512 MiB read, 256 MiB written) that scales rocprofv3's FETCH_SIZE / WRITE_SIZE."""
+    import torch
+
+    src = torch.ones(128 << 20, dtype=torch.float32, device=device)
+    dst = torch.empty(128 << 20, dtype=torch.float16, device=device)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -780,8 +827,9 @@ def main():
     ap.add_argument("--configs", default="c3,c4,c5",
                     help="comma-separated subset of c3, c4, c5 to run besides the headline MLP step")
     ap.add_argument("--only", default=None,
-                    choices=["fwd_gate_up", "fwd_down", "bwd_down", "bwd_gate_up"],
-                    help="time only this launch kind (for counter runs); prints its roofline only")
+                    choices=["fwd_gate_up", "fwd_down", "bwd_down", "bwd_gate_up", "dequant"],
+                    help="time only this launch kind, or the standalone dequantization (for counter runs); "
+                         "prints its roofline only")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also convert 128 Mi fp32 values to fp16 three times: one elementwise "
                          "kernel of known traffic (512 MiB read, 256 MiB written), to scale "
@@ -805,15 +853,18 @@ def main():
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
 
+    if args.only == "dequant":
+        if args.copy_probe:
+            copy_probe(device)
+        with no_gc():
+            deq = bench_dequant(max(args.steps, 10), args.warmup, device)
+        print(json.dumps(dict(only="dequant", gbs=round(deq["gbs"], 1), ms=round(deq["ms"], 4), bytes=deq["bytes"],
+                              frac=round(deq["gbs"] / HBM_PEAK_GBS, 4))))
+        return
     with no_gc():
         mlp = bench_mlp(args.steps, args.warmup, device, only=args.only)
     if args.copy_probe:
-        src = torch.ones(128 << 20, dtype=torch.float32, device=device)
-        dst = torch.empty(128 << 20, dtype=torch.float16, device=device)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+        copy_probe(device)
     with no_gc():
         deq = None if (args.skip_dequant or args.only) else bench_dequant(max(args.steps, 10), args.warmup, device)
     c3 = c4 = c5 = None
