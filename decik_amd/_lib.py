@@ -220,8 +220,14 @@ class DescCache:
         self._d = {}
         self._lock = threading.Lock()
 
-    def get(self, packed, qs, device):
-        scales = SCALES.get(packed, qs, device) if qs.nested else None
+    def get(self, packed, qs, device, scales_of=None):
+        """(NF4Weight, tensors to keep alive). scales_of(packed, qs, device) gives the block
+        scales to describe the weight with (None: its own statistics); default: the cached
+        scales of a nested weight."""
+        if scales_of is None:
+            scales = SCALES.get(packed, qs, device) if qs.nested else None
+        else:
+            scales = scales_of(packed, qs, device)
         key = id(qs)
         ver = (packed.data_ptr(), device.index, id(scales),
                _version_key(qs) if qs.nested else ((qs.absmax.data_ptr(), qs.absmax._version),

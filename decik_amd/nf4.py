@@ -138,7 +138,7 @@ def linear_forward(x16, items, lora_rank=0):
         out = it.get("out")
         if out is None:
             out = torch.empty((m, n), dtype=torch.float16, device=dev)
-        w, kp = _lib.DESCS.get(it["packed"], qs, dev)
+        w, kp = _lib.DESCS.get(it["packed"], qs, dev, _scales)
         keep += kp
         groups[g].w = w
         bias = it.get("bias")
@@ -227,7 +227,7 @@ def linear_backward(items, m, k, dx=None, dx_fp32=False, lora_rank=0):
     keep, ns = [dx], []
     for g, it in enumerate(items):
         qs = it["qs"]
-        w, kp = _lib.DESCS.get(it["packed"], qs, dev)
+        w, kp = _lib.DESCS.get(it["packed"], qs, dev, _scales)
         keep += kp
         dy = _rows(it["dy"])
         groups[g].w = w
@@ -253,7 +253,7 @@ def linear_backward(items, m, k, dx=None, dx_fp32=False, lora_rank=0):
 
 def _fwd_group(g, it, dev, keep):
     qs = it["qs"]
-    w, kp = _lib.DESCS.get(it["packed"], qs, dev)
+    w, kp = _lib.DESCS.get(it["packed"], qs, dev, _scales)
     keep += kp
     g.w = w
     bias = it.get("bias")
@@ -299,7 +299,7 @@ def linear_backward_swiglu(item, gate, up, out=None, lora_rank=0):
     assert gate.is_contiguous() and up.is_contiguous() and dgate.is_contiguous() and dup.is_contiguous()
     groups = (LinearBwdGroup * 1)()
     qs = item["qs"]
-    w, kp = _lib.DESCS.get(item["packed"], qs, dev)
+    w, kp = _lib.DESCS.get(item["packed"], qs, dev, _scales)
     keep = list(kp)
     dy = _rows(item["dy"])
     groups[0].w = w

@@ -206,3 +206,29 @@ def test_no_bit_cast_of_vector_elements():
             if mt.group(1) in vec_vars:
                 bad.append(f"{os.path.basename(path)}: {mt.group(0)}")
     assert not bad, bad
+
+
+def test_descriptor_cache_follows_the_scales_hook():
+    """DESCS keys a cached NF4Weight on the scales it was built with: describing a nested weight
+    by its raw statistics (a hook returning None, as the raw-statistics tests and the bench's
+    uncached timing do) and then by block scales gives two different descriptors, each reused
+    while nothing changes; an in-place change of the statistics rebuilds it."""
+    import torch
+
+    from decik_amd import _lib
+    from decik_amd.quant import quantize_nf4
+
+    w16 = (torch.randn(64, 128, generator=torch.Generator().manual_seed(5)) * 0.02).half()
+    packed, qs = quantize_nf4(w16, blocksize=64, compress_statistics=True)
+    cpu = torch.device("cpu")
+    cache = _lib.DescCache()
+    raw, _ = cache.get(packed, qs, cpu, lambda p, q, d: None)
+    assert raw.nested == 1 and raw.absmax == qs.absmax.data_ptr()
+    scales = torch.ones(128 * 64 // 64, dtype=torch.float32)
+    cooked, keep = cache.get(packed, qs, cpu, lambda p, q, d: scales)
+    assert cooked.nested == 0 and cooked.absmax == scales.data_ptr() and any(t is scales for t in keep)
+    again, _ = cache.get(packed, qs, cpu, lambda p, q, d: scales)
+    assert again is cooked  # reused
+    qs.absmax.add_(0)  # bumps the version counter
+    rebuilt, _ = cache.get(packed, qs, cpu, lambda p, q, d: scales)
+    assert rebuilt is not cooked and rebuilt.absmax == scales.data_ptr()
