@@ -166,13 +166,27 @@ def weight_desc(packed, qs, device, scales=None):
     return w, keep
 
 
+def _stats(qs):
+    """The statistics tensors (and scalars) a QuantState's block scales are computed from."""
+    if qs.nested:
+        s2 = qs.state2
+        return (qs.absmax, s2.absmax, s2.code, qs.offset)
+    return (qs.absmax,)
+
+
 def _version_key(qs):
-    """What the block scales of a nested QuantState depend on: storage and in-place version of
-    each statistics tensor, the offset and the block sizes."""
-    def tk(t):
-        return (t.data_ptr(), t._version) if torch.is_tensor(t) else (float(t),)
-    return (tk(qs.absmax), tk(qs.state2.absmax), tk(qs.state2.code), tk(qs.offset),
-            int(qs.blocksize), int(qs.state2.blocksize), tuple(int(s) for s in qs.shape))
+    """What the block scales of a nested QuantState depend on: identity and in-place version of
+    each statistics tensor (the cache entry keeps the tensors alive, so an identity is never
+    reused while it is compared), the offset and the block sizes."""
+    key = [int(qs.blocksize), tuple(qs.shape)]
+    for t in _stats(qs):
+        if isinstance(t, torch.Tensor):
+            key += (id(t), t._version)
+        else:
+            key.append(float(t))
+    if qs.nested:
+        key.append(int(qs.state2.blocksize))
+    return tuple(key)
 
 
 class ScaleCache:
@@ -203,7 +217,7 @@ class ScaleCache:
                 self._d.pop(key, None)
 
         with self._lock:
-            self._d[key] = (ver, scales, weakref.ref(qs, drop))
+            self._d[key] = (ver, scales, weakref.ref(qs, drop), _stats(qs))
         return scales
 
 
@@ -212,9 +226,12 @@ SCALES = ScaleCache()
 
 class DescCache:
     """The NF4Weight descriptor the fused GEMMs take for a (packed, QuantState) pair -- with the
-    cached block scales for a nested weight -- built once and reused while the packed tensor and
-    the statistics are unchanged (the check costs a few attribute reads, building the descriptor
-    several times that)."""
+    cached block scales for a nested weight -- built once and reused while it stays valid: the
+    same packed tensor, statistics tensors and scales (compared by identity; the entry keeps them
+    alive, so an identity is not reused meanwhile). An in-place change of the statistics leaves
+    the descriptor's pointers valid; the scales cache notices it and hands out new scales, which
+    rebuilds the descriptor. The check costs a few attribute reads, building the descriptor
+    several times that."""
 
     def __init__(self):
         self._d = {}
@@ -229,9 +246,8 @@ class DescCache:
         else:
             scales = scales_of(packed, qs, device)
         key = id(qs)
-        ver = (packed.data_ptr(), device.index, id(scales),
-               _version_key(qs) if qs.nested else ((qs.absmax.data_ptr(), qs.absmax._version),
-                                                    int(qs.blocksize), tuple(int(v) for v in qs.shape)))
+        ver = (id(packed), packed.data_ptr(), device.index, id(scales), id(qs.code), int(qs.blocksize),
+               tuple(id(t) if isinstance(t, torch.Tensor) else float(t) for t in _stats(qs)))
         with self._lock:
             ent = self._d.get(key)
         if ent is not None and ent[0] == ver and ent[3]() is qs:
@@ -243,7 +259,7 @@ class DescCache:
                 self._d.pop(key, None)
 
         with self._lock:
-            self._d[key] = (ver, w, keep, weakref.ref(qs, drop))
+            self._d[key] = (ver, w, keep + [qs.code, scales, *_stats(qs)], weakref.ref(qs, drop))
         return w, keep
 
 

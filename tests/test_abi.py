@@ -212,7 +212,8 @@ def test_descriptor_cache_follows_the_scales_hook():
     """DESCS keys a cached NF4Weight on the scales it was built with: describing a nested weight
     by its raw statistics (a hook returning None, as the raw-statistics tests and the bench's
     uncached timing do) and then by block scales gives two different descriptors, each reused
-    while nothing changes; an in-place change of the statistics rebuilds it."""
+    while nothing changes; new scales (what the scales cache hands out after an in-place change
+    of the statistics) or a replaced statistics tensor rebuild it."""
     import torch
 
     from decik_amd import _lib
@@ -229,6 +230,30 @@ def test_descriptor_cache_follows_the_scales_hook():
     assert cooked.nested == 0 and cooked.absmax == scales.data_ptr() and any(t is scales for t in keep)
     again, _ = cache.get(packed, qs, cpu, lambda p, q, d: scales)
     assert again is cooked  # reused
-    qs.absmax.add_(0)  # bumps the version counter
-    rebuilt, _ = cache.get(packed, qs, cpu, lambda p, q, d: scales)
-    assert rebuilt is not cooked and rebuilt.absmax == scales.data_ptr()
+    qs.absmax.add_(0)  # in place: the descriptor's pointers stay valid
+    assert cache.get(packed, qs, cpu, lambda p, q, d: scales)[0] is cooked
+    scales2 = scales.clone()
+    rebuilt, _ = cache.get(packed, qs, cpu, lambda p, q, d: scales2)
+    assert rebuilt is not cooked and rebuilt.absmax == scales2.data_ptr()
+    qs.absmax = qs.absmax.clone()  # a replaced statistics tensor
+    raw2, _ = cache.get(packed, qs, cpu, lambda p, q, d: None)
+    assert raw2.absmax == qs.absmax.data_ptr()
+
+
+def test_scale_cache_version_key_tracks_statistics():
+    """The block-scale cache's key changes with an in-place write to any statistics tensor and
+    with a replaced tensor, and not otherwise."""
+    import torch
+
+    from decik_amd import _lib
+    from decik_amd.quant import quantize_nf4
+
+    w16 = (torch.randn(32, 256, generator=torch.Generator().manual_seed(6)) * 0.02).half()
+    _, qs = quantize_nf4(w16, blocksize=64, compress_statistics=True)
+    k0 = _lib._version_key(qs)
+    assert _lib._version_key(qs) == k0
+    qs.state2.absmax.mul_(1)
+    k1 = _lib._version_key(qs)
+    assert k1 != k0
+    qs.absmax = qs.absmax.clone()
+    assert _lib._version_key(qs) != k1
