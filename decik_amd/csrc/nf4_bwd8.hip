@@ -11,20 +11,23 @@
 // per lane and weight row -- and all 32*MB tokens, so each dequantized weight feeds MB MFMAs.
 //
 // A operand (A = W^T): lane l (l32 = l % 32, g = l / 32) serves A row l32 = output column
-// c = arow_to_n(l32) of the wave's 32 (packed byte c / 2; high nibble for even c). Its eight
-// contraction slots of slice j are the weight rows 32 g + 8 j + e of the 64-row step; dY's B
-// operand uses the same order. Lane l ends with the 16 consecutive columns 16 g + r of token row
-// l32 of every 32-token block.
+// c = l32 ^ 1 of the wave's 32. Its eight contraction slots of slice j are the weight rows
+// 32 g + 8 j + e of the 64-row step; dY's B operand uses the same order.
 //
-// Per wave and step: the wave's 16 packed bytes of each of the 64 rows (four 256-byte DMA loads,
-// stored as 16-row groups of [dword column][16 rows], so a lane reads its 8 rows of one dword
-// column with two 16-byte loads) and one block statistic per row (32 aligned columns of a row
-// always lie in one block: k % 32 == 0 and blocks are powers of two >= 32). The dY tile (32*MB x
-// 64 fp16) is shared by the work-group through a ring three steps deep, as in nf4_bwd_kernel.
-// Row scales of step t + 1 are computed during slice 2 of step t, one row per lane, and read back
-// through a per-wave LDS table. The loop is software-pipelined one slice ahead, as in the forward
-// kernels: stage A (packed dwords and row scales of the next slice) after the slice's first MFMA,
-// stage B (byte gather, code-book addresses and reads) after the third, stage C (scaling and fp16
+// Per wave and step: the wave's 16 packed bytes of each of the 64 rows (one 16-byte DMA load per
+// lane, stored as rows of 16 bytes) and one block statistic per row (32 aligned columns of a row
+// always lie in one block: k % 32 == 0 and blocks are powers of two >= 32). The weights reach the
+// MFMA layout through the LDS transpose read ds_read_b64_tr_b4: in each group of 16 lanes, lane r
+// reads 8 bytes (16 columns) of row 32 g + 8 j + r and lane i gets back nibble i of the 16 rows,
+// i.e. column i ^ 1 (bitsandbytes keeps the first of two columns in the high nibble) for slices j
+// and j + 1, one nibble per row in row order. A byte of that dword holds two rows of the lane's
+// column, so one byte-pair code-book entry (one 8-byte LDS read, its address one SDWA shift)
+// gives both codes; each is scaled by its own row's scale. The dY tile (32*MB x 64 fp16) is
+// shared by the work-group through a ring three steps deep, as in nf4_bwd_kernel. Row scales of
+// step t + 1 are computed during slice 2 of step t, one row per lane, and read back through a
+// per-wave LDS table. The loop is software-pipelined one slice ahead, as in the forward kernels:
+// stage A (transposed read every other slice, row scales of the next slice) after the slice's
+// first MFMA, stage B (code-book addresses and reads) after the third, stage C (scaling and fp16
 // packing) after the last but one, and each dY fragment refilled right after its MFMA read it.
 //
 // Epilogue: each token block's 32 x 256 tile goes through LDS (the rings, after a barrier) and
@@ -34,6 +37,27 @@
 #include "gemm_common.h"
 
 namespace dk {
+
+// LDS transpose read (gfx950 ds_read_b64_tr_b4): the 16 lanes of each lane group read 8 bytes each
+// (row r = lane r's 16 nibbles, low nibble first); lane i of the group receives nibble i of rows
+// 0..15, in order (row e at bits 4 e of the 64-bit result).
+__device__ __forceinline__ u32x2_t lds_tr4(const uint8_t* p) {
+    typedef int v2i __attribute__((ext_vector_type(2)));
+    const v2i r = __builtin_amdgcn_ds_read_tr4_b64_v2i32((__attribute__((address_space(3))) v2i*)p);
+    return u32x2_t{(uint32_t)r[0], (uint32_t)r[1]};
+}
+
+// 8 x byte e of w (the byte-pair code-book offset) in one SDWA instruction
+__device__ __forceinline__ uint32_t byte_x8(uint32_t w, int e) {
+    uint32_t r;
+    switch (e) {
+        case 0: asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0" : "=v"(r) : "v"(w)); break;
+        case 1: asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1" : "=v"(r) : "v"(w)); break;
+        case 2: asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2" : "=v"(r) : "v"(w)); break;
+        default: asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3" : "=v"(r) : "v"(w)); break;
+    }
+    return r;
+}
 
 constexpr int kB8Waves = 8;
 constexpr int kB8Threads = 64 * kB8Waves;
@@ -56,20 +80,22 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
     constexpr int DBUF = BM * 128;                             // bytes of one dY ring buffer
     constexpr int DCH = BM * 8;                                // its 16-byte chunks
     constexpr int DPT = (DCH + kB8Threads - 1) / kB8Threads;   // dY loads per thread and step
-    constexpr int NL = DPT + 4 + (NESTED ? 2 : 1);             // loads per thread and step
+    constexpr int NL = DPT + 1 + (NESTED ? 2 : 1);             // loads per thread and step
     static_assert(DCH % 64 == 0, "a wave's dY load is wholly inside or past the tile");
     // epilogue staging area: the dY ring, the weight rings and the scale tables (contiguous)
     constexpr int STAGE = 3 * DBUF + kB8Waves * (3 * kB8WSlot + kB8ScaleBytes);
     static_assert(2 * 32 * (kB8BN * 4 + 16) <= STAGE, "epilogue staging fits the rings");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    __shared__ float luts[16 * kMaxGroups];  // code books, group g at byte 64 g
+    // byte-pair code book of the current group: entry x = (code[x & 15], code[x >> 4]), the
+    // weights of the two rows whose nibbles share byte x of a transposed dword
+    __shared__ float2_t lutT[256];
     uint8_t* dummy = smem + kB8Tables;
     uint8_t* dring = dummy + kB8Dummy;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS bases stay scalar
     const int l32 = lane & 31, g = lane >> 5;
-    const int c = arow_to_n(l32);      // this lane's output column within the wave's 32
+    const int c = l32 ^ 1;             // this lane's output column within the wave's 32
     const int xsw = (l32 >> 1) & 7;    // LDS swizzle of this lane's dY rows
 
     const int L = xcd_logical_id();
@@ -86,20 +112,15 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
     const int cs0 = split * a.csteps_per_split;
     const int cs1 = min(a.csteps, cs0 + a.csteps_per_split);
 
-    for (int gg = 0; gg < a.ngroups; ++gg) {
-        if (tid < 16) luts[16 * gg + tid] = a.g[gg].w.code[tid];
-        if (NESTED && tid < 256) ((float*)smem)[256 * gg + tid] = a.g[gg].w.code2[tid];
+    if constexpr (NESTED) {
+        for (int gg = 0; gg < a.ngroups; ++gg)
+            if (tid < 256) ((float*)smem)[256 * gg + tid] = a.g[gg].w.code2[tid];
     }
-    // v_perm selector that gathers byte (c / 2) % 4 of two dwords into the low two bytes
-    const uint32_t bb = (uint32_t)((c >> 1) & 3);
-    const uint32_t bsel = bb | ((bb + 4u) << 8) | 0x0C0C0000u;
-    // rotation (right) that moves this lane's nibble of every byte to bits 2..5, i.e. to the
-    // code-book byte address 4 * nibble: 2 for the high nibble, 30 (left by 2) for the low one
-    const uint32_t nrot = (c & 1) ? 30u : 2u;
     uint8_t* wring = dring + 3 * DBUF + wave * (3 * kB8WSlot);
     float* stab = (float*)(dring + 3 * DBUF + kB8Waves * 3 * kB8WSlot + wave * kB8ScaleBytes);
-    // this lane's packed reads: 16-row group 2 g + j / 2, dword column c / 8, rows 8 (j % 2) ..
-    const int pkl = 512 * g + 64 * (c >> 3);
+    // this lane's transposed reads (slices j, j + 1 for even j): row 32 g + 8 j + (lane % 16) of
+    // the step, bytes 8 (l32 / 16) .. of the wave's 16
+    const int pkl = 16 * (32 * g + (lane & 15)) + 8 * ((lane >> 4) & 1);
 
     float16_t acc[MB];  // token block i
 #pragma unroll
@@ -185,7 +206,12 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
         const uint32_t bs_shift = sgpr((uint32_t)G.w.bs_shift), bs2_shift = sgpr((uint32_t)G.w.bs2_shift);
         const float offset = NESTED ? *G.w.offset : 0.0f;
         const float* c2 = (const float*)smem + 256 * gi;
-        const uint32_t gbase4 = (uint32_t)(64 * gi) * 0x01010101u;  // this group's code book
+        {
+            // the previous group's readers are past the barrier that ended its loop; this
+            // group's prologue barrier publishes the new book
+            const float* book = G.w.code;
+            if (tid < 256) lutT[tid] = float2_t{book[tid & 15], book[tid >> 4]};
+        }
 
         // Loads use per-lane offsets fixed for the group (bit 31 set where the lane's data lies
         // outside the tile or the weight: it reads zeros) against buffer descriptors whose base
@@ -212,11 +238,9 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
             // loads h < DPT - 1 never pass the tile (folded at compile time: no scalar select)
             return ((h + 1) * kB8Threads <= DCH || wq0 < DCH) ? dring + rd + wq0 * 16 : dummy;
         };
-        // packed bytes: DMA instruction d fetches rows 16 d .. 16 d + 15, the wave's 4 dwords of
-        // each; lane l -> (dword column l / 16, row l % 16) lands at byte 256 d + 4 l
-        const int prr = lane & 15;
-        const uint32_t po = off_if(cok, (uint32_t)prr * (uint32_t)(K >> 1) + (uint32_t)(kw0 >> 1) + 4u * (uint32_t)(lane >> 4));
-        const uint32_t prow16 = 16u * (uint32_t)(K >> 1);  // bytes of 16 weight rows
+        // packed bytes: lane l fetches the wave's 16 bytes of row l of the step, landing at
+        // byte 16 l of the slot (rows of 16 bytes, the layout the transposed reads take)
+        const uint32_t po = off_if(cok, (uint32_t)lane * (uint32_t)(K >> 1) + (uint32_t)(kw0 >> 1));
         // statistics: lane = weight row of the step
         const uint32_t blk0 = ((uint32_t)lane * (uint32_t)K + (uint32_t)kw0) >> bs_shift;
         const uint32_t so = off_if(cok, NESTED ? blk0 : blk0 * 4u);
@@ -231,8 +255,7 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
             if (!tail) {
 #pragma unroll
                 for (int h = 0; h < DPT; ++h) bload128_lds(drs, dy_dst(rd, h), dyo[h]);
-#pragma unroll
-                for (int d = 0; d < 4; ++d) bload32_lds(wrs, slot + 256 * d, po + (uint32_t)d * prow16);
+                bload128_lds(wrs, slot, po);
             } else {
                 // rows and dY columns past N read zeros. The empty volatile asm keeps this a
                 // branch taken only on a group's last, partial step: merged with the plain loads
@@ -241,9 +264,7 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
 #pragma unroll
                 for (int h = 0; h < DPT; ++h)
                     bload128_lds(drs, dy_dst(rd, h), off_if(n0 + 8 * dy_col(h) < N, dyo[h]));
-#pragma unroll
-                for (int d = 0; d < 4; ++d)
-                    bload32_lds(wrs, slot + 256 * d, off_if(n0 + 16 * d + prr < N, po + (uint32_t)d * prow16));
+                bload128_lds(wrs, slot, off_if(n0 + lane < N, po));
             }
             const uint32_t kb = ((uint32_t)n0 * (uint32_t)K) >> bs_shift;  // blocks before this step
             const bool rok = !tail || n0 + lane < N;
@@ -295,22 +316,22 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
         scales_3(t0, 0);
 
         half8_t xf[MB], w, wn;
-        u32x4_t d0, d1;  // next slice: packed dwords of rows r0 .. r0 + 3 and r0 + 4 .. r0 + 7
+        u32x2_t tr;      // the last transposed read: this lane's nibbles of two slices
+        uint32_t d0;     // next slice: this lane's nibbles of its 8 rows (row e at bits 4 e)
         float4_t s0, s1; // ... their row scales
         float v[8];      // ... their code-book values
-        u32x4_t e0, e1;  // two-slice pipeline: the packed dwords and scales of the slice after
+        uint32_t e0;     // two-slice pipeline: the nibbles and scales of the slice after
         float4_t t0s, t1s;
         auto stage_A = [&](int rw, int sidx, int j) __attribute__((always_inline)) {
-            const uint8_t* pk = wring + rw + pkl + 256 * (j >> 1) + 32 * (j & 1);
+            if ((j & 1) == 0) tr = lds_tr4(wring + rw + pkl + 128 * j);
+            const uint32_t dj = (j & 1) ? tr[1] : tr[0];
             const float* sc = stab + 64 * sidx + 32 * g + 8 * j;
             if constexpr (P2) {
-                e0 = *(const u32x4_t*)pk;
-                e1 = *(const u32x4_t*)(pk + 16);
+                e0 = dj;
                 t0s = *(const float4_t*)sc;
                 t1s = *(const float4_t*)(sc + 4);
             } else {
-                d0 = *(const u32x4_t*)pk;
-                d1 = *(const u32x4_t*)(pk + 16);
+                d0 = dj;
                 s0 = *(const float4_t*)sc;
                 s1 = *(const float4_t*)(sc + 4);
             }
@@ -319,22 +340,17 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
         auto advance = [&]() __attribute__((always_inline)) {
             if constexpr (P2) {
                 d0 = e0;
-                d1 = e1;
                 s0 = t0s;
                 s1 = t1s;
             }
         };
         auto stage_B = [&]() __attribute__((always_inline)) {
-            // this lane's byte of rows r0 .. r0 + 3 and r0 + 4 .. r0 + 7, gathered into two dwords
-            const uint32_t rb0 = __builtin_amdgcn_perm(d0[1], d0[0], bsel) | (__builtin_amdgcn_perm(d0[3], d0[2], bsel) << 16);
-            const uint32_t rb1 = __builtin_amdgcn_perm(d1[1], d1[0], bsel) | (__builtin_amdgcn_perm(d1[3], d1[2], bsel) << 16);
-            uint32_t a0 = (__builtin_amdgcn_alignbit(rb0, rb0, nrot) & 0x3C3C3C3Cu) | gbase4;
-            uint32_t a1 = (__builtin_amdgcn_alignbit(rb1, rb1, nrot) & 0x3C3C3C3Cu) | gbase4;
-            asm("" : "+v"(a0), "+v"(a1));  // one v_bfe per lookup (see nib_addrs)
+            // byte b of d0 holds rows 2 b (low nibble) and 2 b + 1: one code-book pair each
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                v[e] = lut_at(luts, a0, e);
-                v[e + 4] = lut_at(luts, a1, e);
+            for (int b = 0; b < 4; ++b) {
+                const float2_t cv = *(const float2_t*)((const char*)lutT + byte_x8(d0, b));
+                v[2 * b] = cv.x;
+                v[2 * b + 1] = cv.y;
             }
         };
         auto stage_C = [&]() __attribute__((always_inline)) -> half8_t {
@@ -412,9 +428,21 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
     }
     lds_barrier();  // the rings become the staging area (also when no group had steps here)
 
-    // ---- epilogue. Lane (l32, g) holds, for token block i, token row m0 + 32 i + l32 and the 16
-    // consecutive columns colw + r of the tile (acc[i][r]).
-    const int colw = 32 * wave + 16 * g;
+    // ---- epilogue. Lane (l32, g) holds, for token block i, token row m0 + 32 i + l32 and, in
+    // acc[i][4 a + b], column colw + 8 a + (b ^ 1) of the tile (D row 8 a + 4 g + b is A row, i.e.
+    // output column, (8 a + 4 g + b) ^ 1): four runs of 4 columns, 8 apart, pairs swapped.
+    const int colw = 32 * wave + 4 * g;
+    // stage a lane's 16 values of one token block as fp16 / fp32 at their columns of an LDS row
+    auto stage_half = [&](uint8_t* lp, const float16_t& v) __attribute__((always_inline)) {
+#pragma unroll
+        for (int a4 = 0; a4 < 4; ++a4)
+            *(u32x2_t*)(lp + 16 * a4) = u32x2_t{pack_half2(v[4 * a4 + 1], v[4 * a4]), pack_half2(v[4 * a4 + 3], v[4 * a4 + 2])};
+    };
+    auto stage_float = [&](uint8_t* lp, const float16_t& v) __attribute__((always_inline)) {
+#pragma unroll
+        for (int a4 = 0; a4 < 4; ++a4)
+            *(float4_t*)(lp + 32 * a4) = float4_t{v[4 * a4 + 1], v[4 * a4], v[4 * a4 + 3], v[4 * a4 + 2]};
+    };
     if constexpr (MB <= 4) {
         if (a.swiglu) {
             // dgate / dup from G = fp16(dY . W) and the gate / up chunks fetched at the start
@@ -424,11 +452,7 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
                 // G = fp16(dY . W) through LDS as 32 x 256 fp16 rows
                 uint8_t* buf = dring + (i & 1) * 32 * RB;
                 uint8_t* lp = buf + l32 * RB + colw * 2;
-                uint32_t o[8];
-#pragma unroll
-                for (int r = 0; r < 16; r += 2) o[r >> 1] = pack_half2(acc[i][r], acc[i][r + 1]);
-                *(u32x4_t*)lp = u32x4_t{o[0], o[1], o[2], o[3]};
-                *(u32x4_t*)(lp + 16) = u32x4_t{o[4], o[5], o[6], o[7]};
+                stage_half(lp, acc[i]);
                 lds_barrier();
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
@@ -490,11 +514,14 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
                         half8_t, bload128(grs, off_if(m < M && 16 * h < R, (uint32_t)(m * R + 16 * h + 8 * g) * 2u)));
                     p = mfma32x32x16(al[h], gu, p);  // zeros past the rank
                 }
-                const uint32_t bits = bload16(krs, off_if(m < M && cok, (uint32_t)m * (uint32_t)(K >> 3) +
-                                                                       (uint32_t)((kw0 + 16 * g) >> 3)));
+                // the wave's 32 keep bits of the row (k % 32 == 0: 4-byte aligned)
+                const uint32_t bits = __builtin_bit_cast(
+                    uint32_t, bloadf(krs, off_if(m < M && cok, (uint32_t)m * (uint32_t)(K >> 3) + (uint32_t)(kw0 >> 3))));
 #pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    acc[i][r] = acc[i][r] + ((float)(_Float16)p[r] * (float)((bits >> r) & 1u)) * ks;
+                for (int r = 0; r < 16; ++r) {
+                    const int col = 8 * (r >> 2) + 4 * g + ((r & 3) ^ 1);  // of the wave's 32
+                    acc[i][r] = acc[i][r] + ((float)(_Float16)p[r] * (float)((bits >> col) & 1u)) * ks;
+                }
             }
         }
     }
@@ -509,8 +536,7 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
         for (int i = 0; i < MB; ++i) {
             uint8_t* buf = dring + (i & 1) * 32 * RB;
             uint8_t* lp = buf + l32 * RB + colw * 4;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) *(float4_t*)(lp + 16 * q) = chunk4(acc[i], q);
+            stage_float(lp, acc[i]);
             lds_barrier();
 #pragma unroll
             for (int h = 0; h < 4; ++h) {
@@ -530,11 +556,7 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
         for (int i = 0; i < MB; ++i) {
             uint8_t* buf = dring + (i & 1) * 32 * RB;
             uint8_t* lp = buf + l32 * RB + colw * 2;
-            uint32_t o[8];
-#pragma unroll
-            for (int r = 0; r < 16; r += 2) o[r >> 1] = pack_half2(acc[i][r], acc[i][r + 1]);
-            *(u32x4_t*)lp = u32x4_t{o[0], o[1], o[2], o[3]};
-            *(u32x4_t*)(lp + 16) = u32x4_t{o[4], o[5], o[6], o[7]};
+            stage_half(lp, acc[i]);
             lds_barrier();
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
