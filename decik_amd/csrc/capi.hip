@@ -177,6 +177,14 @@ const VariantCost* choose_plan(const VariantCost* vs, int nv, int64_t m, int64_t
     return pick;
 }
 
+// Work-group order of the eight-wave kernels. Consecutive logical work-groups run on one XCD
+// and share its L2: with token tiles fastest an XCD reads the weight columns of its tiles once
+// and every token row, with column tiles fastest the reverse. Column tiles go first when there
+// are many token tiles and the activations (2 bytes per token and contraction index) outweigh
+// the packed weights (half a byte per output column and contraction index): measured on MI355X,
+// 3-6% faster at M = 8192 for the 7B projections, 3% slower at M = 830 for the 1.5B MLP.
+bool cols_first(int m_tiles, int64_t m, int64_t out_cols) { return m_tiles >= 8 && 4 * m > out_cols; }
+
 // Split-K workspace: the fp32 partial slabs (splits x m x ncols), nothing else. Contents need not
 // be initialised and are dead after the call.
 int64_t workspace_bytes(const GemmPlan& p) { return p.splits > 1 ? p.partial_floats * 4 : 0; }
@@ -618,6 +626,7 @@ static int linear_fwd_impl(const std::string& name, const uint16_t* x, int64_t m
     a.glu = glu ? 1 : 0;
     a.h = reinterpret_cast<_Float16*>(h);
     a.ldh = ldh;
+    a.cols_first = cols_first(p.m_tiles, m, ncols) ? 1 : 0;
     if (need > 0) a.partials = static_cast<float*>(workspace);
     const int64_t wgs = (int64_t)p.m_tiles * p.n_tiles * p.splits;
     if (wgs > INT32_MAX / 2 || ncols > INT32_MAX / 2) return fail(name + ": problem too large");
@@ -792,6 +801,7 @@ static int linear_bwd_impl(const std::string& name, const dk_linear_bwd_group* g
     a.csteps_per_split = p.steps_per_split;
     a.dx_fp32 = dx_fp32 ? 1 : 0;
     a.nested = nested;
+    a.cols_first = cols_first(p.m_tiles, m, k) ? 1 : 0;
     if (sw != nullptr) {
         a.swiglu = 1;
         a.gate = reinterpret_cast<const _Float16*>(sw->gate);

@@ -65,6 +65,8 @@ struct FwdArgs {
     int32_t glu;
     _Float16* h;
     int64_t ldh;
+    // work-group order of nf4_fwd8_kernel: column tiles fastest (1) or token tiles fastest (0)
+    int32_t cols_first;
     FwdGroupDev g[kMaxGroups];
 };
 
@@ -100,6 +102,8 @@ struct BwdArgs {
     _Float16* dgate;
     _Float16* dup;
     int64_t ldd;
+    // work-group order of nf4_bwd8_kernel: column tiles fastest (1) or token tiles fastest (0)
+    int32_t cols_first;
     BwdGroupDev g[kMaxGroups];
 };
 

@@ -64,7 +64,7 @@ constexpr int kB8Threads = 64 * kB8Waves;
 constexpr int kB8BN = 32 * kB8Waves;          // output columns per tile
 constexpr int kB8Tables = kMaxGroups * 1024;  // code2 tables (nested statistics), 1 KB per group
 constexpr int kB8Dummy = 1024;                // target of the dY loads of waves past the tile
-// Per-wave ring slot of one step: 1 KB packed bytes (4 x [4 dword columns][16 rows]), then one
+// Per-wave ring slot of one step: 1 KB packed bytes (64 rows of 16 bytes), then one
 // statistics dword slot per row (codes or fp32 absmax at +1024, absmax2 at +1280).
 constexpr int kB8WSlot = 1536;
 constexpr int kB8ScaleBytes = 2 * 64 * 4;  // per wave: row-scale tables of two steps
@@ -100,10 +100,12 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
 
     const int L = xcd_logical_id();
     if (L >= a.m_tiles * a.k_tiles * a.splits) return;
-    const int m_tile = L % a.m_tiles;
-    const int rest = L / a.m_tiles;
-    const int k_tile = rest % a.k_tiles;
-    const int split = rest / a.k_tiles;
+    // consecutive logical ids share an XCD's L2: token tiles fastest share the weight columns,
+    // column tiles fastest share the dY rows (chosen by the host for large token counts)
+    const int mk = L % (a.m_tiles * a.k_tiles);
+    const int split = L / (a.m_tiles * a.k_tiles);
+    const int m_tile = a.cols_first ? mk / a.k_tiles : mk % a.m_tiles;
+    const int k_tile = a.cols_first ? mk % a.k_tiles : mk / a.m_tiles;
     const int M = sgpr(a.m), K = sgpr(a.k);
     const int m0 = m_tile * BM;
     const int tile_k0 = k_tile * kB8BN;

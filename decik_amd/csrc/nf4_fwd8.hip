@@ -68,10 +68,12 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
 
     const int L = xcd_logical_id();
     if (L >= a.m_tiles * a.n_tiles * a.splits) return;
-    const int m_tile = L % a.m_tiles;
-    const int rest = L / a.m_tiles;
-    const int n_tile = rest % a.n_tiles;
-    const int split = rest / a.n_tiles;
+    // consecutive logical ids share an XCD's L2: token tiles fastest share the weight columns,
+    // column tiles fastest share the token rows (chosen by the host for large token counts)
+    const int mn = L % (a.m_tiles * a.n_tiles);
+    const int split = L / (a.m_tiles * a.n_tiles);
+    const int m_tile = a.cols_first ? mn / a.n_tiles : mn % a.m_tiles;
+    const int n_tile = a.cols_first ? mn % a.n_tiles : mn / a.m_tiles;
 
     int gi = 0;  // the weight of this tile (normal mode)
 #pragma unroll

@@ -272,3 +272,24 @@ def test_gemv_not_used_with_lora_or_forced_plan(device, monkeypatch):
     ref = O.linear_ref(x.cpu().numpy(), w16)
     assert_close(y0, ref, what="gemv")
     assert_close(y1, ref, what="mfma at m=2")
+
+
+@pytest.mark.parametrize("fwd_plan,bwd_plan", [("8,1,8", "8,1,8,256"), ("8,2,8", "8,3,8,256")])
+def test_column_tiles_first_order(fwd_plan, bwd_plan, device, monkeypatch):
+    """2048 token rows on 256-token tiles (eight token tiles, activations heavier than the packed
+    weights): the eight-wave kernels take their tiles column tiles first, also with split-K.
+    Every output row and column against the oracle, forward and input gradient."""
+    from decik_amd.nf4 import launch_plan, linear_backward, linear_forward
+
+    m, n, k = 2048, 2048, 512
+    monkeypatch.setenv("DECIK_FWD_PLAN", fwd_plan)
+    monkeypatch.setenv("DECIK_BWD_PLAN", bwd_plan)
+    assert launch_plan(False, m, k, [n])["kernel"] == "nf4_fwd8_kernel"
+    assert launch_plan(True, m, k, [n])["kernel"] == "nf4_bwd8_kernel"
+    packed, qs, w16 = make_weight((n, k), seed=180, device=device)
+    x = randn16((m, k), seed=181, device=device)
+    dy = randn16((m, n), seed=182, device=device, std=1e-2)
+    (y,) = linear_forward(x, [dict(packed=packed, qs=qs)])
+    assert_close(y, O.linear_ref(x.cpu().numpy(), w16), what=f"fwd columns first {fwd_plan}")
+    dx = linear_backward([dict(packed=packed, qs=qs, dy=dy)], m, k)
+    assert_close(dx, O.linear_dx_ref(dy.cpu().numpy(), w16), what=f"bwd columns first {bwd_plan}")
