@@ -47,18 +47,6 @@ __device__ __forceinline__ u32x2_t lds_tr4(const uint8_t* p) {
     return u32x2_t{(uint32_t)r[0], (uint32_t)r[1]};
 }
 
-// 8 x byte e of w (the byte-pair code-book offset) in one SDWA instruction
-__device__ __forceinline__ uint32_t byte_x8(uint32_t w, int e) {
-    uint32_t r;
-    switch (e) {
-        case 0: asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0" : "=v"(r) : "v"(w)); break;
-        case 1: asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1" : "=v"(r) : "v"(w)); break;
-        case 2: asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2" : "=v"(r) : "v"(w)); break;
-        default: asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3" : "=v"(r) : "v"(w)); break;
-    }
-    return r;
-}
-
 constexpr int kB8Waves = 8;
 constexpr int kB8Threads = 64 * kB8Waves;
 constexpr int kB8BN = 32 * kB8Waves;          // output columns per tile

@@ -155,6 +155,18 @@ __device__ __forceinline__ void nib_addrs(uint32_t w, uint32_t gbase4, uint32_t&
     asm("" : "+v"(hi), "+v"(lo));
 }
 
+// 8 x byte e of w (the byte-pair code-book offset) in one SDWA instruction
+__device__ __forceinline__ uint32_t byte_x8(uint32_t w, int e) {
+    uint32_t r;
+    switch (e) {
+        case 0: asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0" : "=v"(r) : "v"(w)); break;
+        case 1: asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1" : "=v"(r) : "v"(w)); break;
+        case 2: asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2" : "=v"(r) : "v"(w)); break;
+        default: asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3" : "=v"(r) : "v"(w)); break;
+    }
+    return r;
+}
+
 __device__ __forceinline__ float lut_at(const float* lut, uint32_t addrs, int byte) {
     return *(const float*)((const char*)lut + __builtin_amdgcn_ubfe(addrs, 8 * byte, 8));
 }
