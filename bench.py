@@ -526,16 +526,22 @@ def bench_c3(steps, warmup, device):
         for i in range(warmup):
             fn(layers[i % n_sets])
             clear()
-        torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        for i in range(steps):
-            fn(layers[i % n_sets])
-            clear()
-        b.record()
-        torch.cuda.synchronize()
+        # five timed blocks of `steps` steps: the eager step is bound by the host, whose speed
+        # drifts between blocks; the median is reported, the spread beside it
+        blocks = []
+        for _ in range(5):
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for i in range(steps):
+                fn(layers[i % n_sets])
+                clear()
+            b.record()
+            torch.cuda.synchronize()
+            blocks.append(a.elapsed_time(b) / steps)
         launches, busy = count_kernels(lambda fn=fn: (fn(layers[-1]), clear()))
-        res[name] = dict(ms=a.elapsed_time(b) / steps, launches=launches, busy_us=busy)
+        res[name] = dict(ms=statistics.median(blocks), spread=(min(blocks), max(blocks)), launches=launches,
+                         busy_us=busy)
     gemm = 2 * sum(gemm_flops(n, k) for name, n, k in QWEN15_SHAPES if name in ("q", "k", "v", "o"))
     lora_f = sum(2 * M * LORA_R * (HIDDEN + n) + 2 * M * LORA_R * (2 * HIDDEN + 2 * n) for n in (1536, 256))
     out = dict(workload="Qwen2.5-1.5B attention projections, one layer fwd+bwd, M=830 (8 packed sequences): "
@@ -544,14 +550,16 @@ def bench_c3(steps, warmup, device):
                         f"{n_sets} layers of weights rotated",
                step_gflops=round((gemm + lora_f) / 1e9, 2))
     for name, r in res.items():
-        out[name] = dict(ms=round(r["ms"], 4), tflops=round((gemm + lora_f) / (r["ms"] * 1e-3) / 1e12, 1),
+        out[name] = dict(ms=round(r["ms"], 4), ms_range=[round(v, 4) for v in r["spread"]],
+                         tflops=round((gemm + lora_f) / (r["ms"] * 1e-3) / 1e12, 1),
                          launches=r["launches"],
                          gpu_busy_ms=None if r["busy_us"] is None else round(r["busy_us"] / 1e3, 4))
     out["speedup"] = round(res["reference_order"]["ms"] / res["fused"]["ms"], 3)
     if res["fused"]["busy_us"] and res["reference_order"]["busy_us"]:
         out["gpu_busy_speedup"] = round(res["reference_order"]["busy_us"] / res["fused"]["busy_us"], 3)
     out["note"] = ("ms: eager steps back to back (HIP events), bound by the host's Python and launch "
-                   "overhead at this size; gpu_busy_ms: the kernels' summed durations in one profiled step")
+                   "overhead at this size: median of five blocks of steps (ms_range: the fastest and "
+                   "slowest block); gpu_busy_ms: the kernels' summed durations in one profiled step")
     return out
 
 
