@@ -124,6 +124,7 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
     constexpr int qB = MB >= 7 ? 2 : 1, qC = MB >= 7 ? MB - 2 : MB - 1;
     constexpr int qS1 = 1, qS2 = MB >= 7 ? 3 : 2, qS3 = MB >= 7 ? 5 : 3;  // next step's row scales
     static_assert(qS3 < MB && qB < qC, "stages inside the slice");
+    static_assert(MB <= 4 || DPT + 1 < MB, "a step's load parts fit one slice's MFMA gaps");
 
     // SwiGLU mode: this thread's two 16-byte chunks (row ch / 32, columns 8 (ch % 32) ..) of
     // every token block's gate and up tiles, requested as the kernel starts so that their reads
@@ -235,26 +236,37 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
         const uint32_t blk0 = ((uint32_t)lane * (uint32_t)K + (uint32_t)kw0) >> bs_shift;
         const uint32_t so = off_if(cok, NESTED ? blk0 : blk0 * 4u);
 
-        auto load_step = [&](int t, int rd, int rw, bool live) __attribute__((always_inline)) {
+        // Part p of load_step (p < DPT: dY chunk p; DPT: the packed weights; DPT + 1: their
+        // statistics), so that the main loop issues a step's loads one per MFMA gap: issued in one
+        // burst after the barrier they held up the matrix pipe (7.7% of the 7B q/o input gradient
+        // at M = 8192).
+        auto load_part = [&](int p, int t, int rd, int rw, bool live) __attribute__((always_inline)) {
             const int n0 = (t - sb) * kBwdBC;
             const bool tail = n0 + kBwdBC > N;  // uniform
-            const rsrc_t drs = make_rsrc(gdy + n0, live ? dy_bytes - 2u * (uint32_t)n0 : 0u);
+            if (p < DPT) {
+                const rsrc_t drs = make_rsrc(gdy + n0, live ? dy_bytes - 2u * (uint32_t)n0 : 0u);
+                if (!tail) {
+                    bload128_lds(drs, dy_dst(rd, p), dyo[p]);
+                } else {
+                    // rows and dY columns past N read zeros. The empty volatile asm keeps this a
+                    // branch taken only on a group's last, partial step: merged with the plain
+                    // loads, the per-lane checks became selects on every step (~8% of the loop).
+                    asm volatile("");
+                    bload128_lds(drs, dy_dst(rd, p), off_if(n0 + 8 * dy_col(p) < N, dyo[p]));
+                }
+                return;
+            }
             uint8_t* slot = wring + rw;
-            const uint32_t pskip = (uint32_t)n0 * (uint32_t)(K >> 1);
-            const rsrc_t wrs = make_rsrc(gpk + pskip, live ? pk_bytes - pskip : 0u);
-            if (!tail) {
-#pragma unroll
-                for (int h = 0; h < DPT; ++h) bload128_lds(drs, dy_dst(rd, h), dyo[h]);
-                bload128_lds(wrs, slot, po);
-            } else {
-                // rows and dY columns past N read zeros. The empty volatile asm keeps this a
-                // branch taken only on a group's last, partial step: merged with the plain loads
-                // above, the per-lane checks became selects on every step (~8% of the loop).
-                asm volatile("");
-#pragma unroll
-                for (int h = 0; h < DPT; ++h)
-                    bload128_lds(drs, dy_dst(rd, h), off_if(n0 + 8 * dy_col(h) < N, dyo[h]));
-                bload128_lds(wrs, slot, off_if(n0 + lane < N, po));
+            if (p == DPT) {
+                const uint32_t pskip = (uint32_t)n0 * (uint32_t)(K >> 1);
+                const rsrc_t wrs = make_rsrc(gpk + pskip, live ? pk_bytes - pskip : 0u);
+                if (!tail) {
+                    bload128_lds(wrs, slot, po);
+                } else {
+                    asm volatile("");
+                    bload128_lds(wrs, slot, off_if(n0 + lane < N, po));
+                }
+                return;
             }
             const uint32_t kb = ((uint32_t)n0 * (uint32_t)K) >> bs_shift;  // blocks before this step
             const bool rok = !tail || n0 + lane < N;
@@ -267,6 +279,11 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
                 const rsrc_t ars = make_rsrc(gamf + kb, live ? am_bytes - 4u * kb : 0u);
                 bload32_lds(ars, slot + 1024, off_if(rok, so));
             }
+        };
+        // every load of step t (the prologue)
+        auto load_step = [&](int t, int rd, int rw, bool live) __attribute__((always_inline)) {
+#pragma unroll
+            for (int p = 0; p < DPT + 2; ++p) load_part(p, t, rd, rw, live);
         };
 
         // Row scale of step t (lane = row) from this wave's statistics in slot rw, into table
@@ -377,9 +394,16 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
                     if (j == 3 && q == 0) {
                         // every wave's loads of step t+1 have landed (each waited in slice 1 or 2)
                         // and every wave is past step t's slots: refill them with step t+3
-                        // (zeros past the segment's end). Past the last step the reads below
-                        // see stale slots and their values go unused.
+                        // (zeros past the segment's end), one part after each of this slice's
+                        // MFMAs. Past the last step the reads below see stale slots and their
+                        // values go unused.
                         lds_barrier();
+                    }
+                    if constexpr (MB > 4) {
+                        if (j == 3 && q <= DPT + 1) load_part(q, t + 3, rd0, rw0, t + 3 < t1);
+                    } else if (j == 3 && q == 0) {
+                        // four MFMAs a slice leave no room to spread them (measured: the burst is
+                        // 1.3% faster for the down-projection input gradient at MB = 4)
                         load_step(t + 3, rd0, rw0, t + 3 < t1);
                     }
                     // refill the dY fragment the MFMA above has read (slice j + 1)

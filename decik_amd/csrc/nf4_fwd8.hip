@@ -51,6 +51,7 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
     constexpr int NL = XPT + 1 + (NESTED ? 2 : 1);               // loads per thread and step
     static_assert(XCH % 64 == 0, "a wave's X load is wholly inside or past the tile");
     static_assert(2 * 32 * (256 * 4 + 16) <= 3 * XBUF, "epilogue staging fits the X ring");
+    static_assert(XPT + 1 < MB, "a step's load parts fit one slice's MFMA gaps");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     // byte-pair code books (gate, up in GLU mode; the same book otherwise): entry 256 b + byte
     // holds (code_b[byte >> 4], code_b[byte & 15]), the two weights of one packed byte
@@ -150,16 +151,23 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
     const float* const gam2 = NESTED ? sgpr(W.absmax2) : nullptr;
     const uint32_t am2_bytes = NESTED ? sgpr(W.absmax2_bytes) : 0u;
     uint8_t* wring = xs + 3 * XBUF + wave * (3 * wslot_bytes);
-    auto load_step = [&](int t, int rx, int rw, bool live) __attribute__((always_inline)) {
+    // Part p of step t's loads (p < XPT: X chunk p; XPT: the packed weights; XPT + 1: their
+    // statistics), so that the main loop issues a step's loads one per MFMA gap: issued in one
+    // burst after the barrier they held up the matrix pipe.
+    auto load_part = [&](int p, int t, int rx, int rw, bool live) __attribute__((always_inline)) {
         const uint32_t k0 = (uint32_t)t * kFwdBK;
-        const rsrc_t xrs = make_rsrc(gx + 2u * k0, live ? x_bytes - 2u * k0 : 0u);
-#pragma unroll
-        for (int h = 0; h < XPT; ++h)
-            // loads h < XPT - 1 never pass the tile (folded at compile time: no scalar select)
-            bload128_lds(xrs, ((h + 1) * kF8Threads <= XCH || xdst[h] >= 0) ? xs + rx + xdst[h] : dummy, xo[h]);
+        if (p < XPT) {
+            const rsrc_t xrs = make_rsrc(gx + 2u * k0, live ? x_bytes - 2u * k0 : 0u);
+            // loads p < XPT - 1 never pass the tile (folded at compile time: no scalar select)
+            bload128_lds(xrs, ((p + 1) * kF8Threads <= XCH || xdst[p] >= 0) ? xs + rx + xdst[p] : dummy, xo[p]);
+            return;
+        }
         uint8_t* slot = wring + rw;
-        const rsrc_t wrs = make_rsrc(gpk + k0 / 2u, live ? pk_bytes - k0 / 2u : 0u);
-        bload128_lds(wrs, slot, wo);
+        if (p == XPT) {
+            const rsrc_t wrs = make_rsrc(gpk + k0 / 2u, live ? pk_bytes - k0 / 2u : 0u);
+            bload128_lds(wrs, slot, wo);
+            return;
+        }
         const uint32_t kb = k0 >> bs_shift;  // blocks of a row before this step
         if constexpr (NESTED) {
             const rsrc_t ars = make_rsrc(gam8 + kb, live ? am_bytes - kb : 0u);
@@ -170,6 +178,11 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
             const rsrc_t ars = make_rsrc(gamf + kb, live ? am_bytes - 4u * kb : 0u);
             bload32_lds(ars, slot + 1024, so);
         }
+    };
+    // every load of step t (the prologue)
+    auto load_step = [&](int t, int rx, int rw, bool live) __attribute__((always_inline)) {
+#pragma unroll
+        for (int p = 0; p < XPT + 2; ++p) load_part(p, t, rx, rw, live);
     };
     // fp32 scale of this lane's row at step t (0 outside the weight)
     auto scale_of = [&](const uint8_t* slot) __attribute__((always_inline)) -> float {
@@ -260,8 +273,9 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
                     wait_vmcnt<NL>();
                     fetch_step(rw1);
                     lds_barrier();
-                    load_step(t + 3, rx0, rw0, t + 3 < ks1);
                 }
+                // step t+3's loads, one part after each of slice 3's MFMAs
+                if (j == 3 && q <= XPT + 1) load_part(q, t + 3, rx0, rw0, t + 3 < ks1);
                 // refill the X fragment the MFMA above has read (slice j + 1)
                 xf[q] = xfrag(xs + (j < 3 ? rx0 : rx1), q, jn);
                 if (q == (j < 3 ? qA : qA + 1)) {
