@@ -18,7 +18,8 @@
 // software-pipelined one slice ahead: between the MFMAs of slice j the wave refills each X
 // fragment register right after its MFMA has read it and unpacks slice j + 1 in three stages
 // (code-book addresses, code-book reads, scaling and fp16 packing). Slice 3 holds the step
-// boundary (own-slot fetch, wait, barrier, refill of the freed ring slots).
+// boundary (own-slot fetch, wait, barrier) and the refill of the freed ring slots, one load
+// after each of its MFMAs.
 //
 // Epilogue: each token block's 32 x 256 output tile goes through LDS (the X ring, after a
 // barrier) and leaves as whole 512-byte rows; GLU tiles pair the gate wave (0..3) and up wave
