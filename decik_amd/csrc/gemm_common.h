@@ -49,6 +49,31 @@ __device__ __forceinline__ float16_t join4(float4_t a, float4_t b, float4_t c, f
     return __builtin_shufflevector(ab, cd, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
 }
 
+// Ring refills spread over a step. A step's loads are split into parts, issued in the order
+// packed weights, their statistics, then the activation chunks (the weights come from HBM, the
+// activation tiles mostly from L2, so the weights get the longest flight). Issue index i goes
+// after MFMA (i / 4) * (MB / 2) of one slice: for i % 4 == 0, slice 3 of the step three before
+// (once that step's barrier has freed the ring slots), otherwise slice i % 4 - 1 of the step two
+// before; each slice then issues at most two loads, and the eight waves' loads no longer meet
+// in one slice.
+__host__ __device__ constexpr int spread_slice(int i) { return i % 4 == 0 ? 3 : i % 4 - 1; }
+// the part of issue index i, for a step of `chunks` activation chunks (parts 0 .. chunks - 1),
+// the packed weights (part chunks) and their statistics (part chunks + 1)
+__host__ __device__ constexpr int spread_part(int i, int chunks) {
+    return i == 0 ? chunks : (i == 1 ? chunks + 1 : i - 2);
+}
+// loads of one step issued by the time the parts after MFMA 0 of slice `slice` (of the step two
+// before) are out, counting the slice-3 parts of the step before that first (slice < 0: those
+// only); the statistics part is `stats_loads` loads
+__host__ __device__ constexpr int spread_loads(int parts, int stats_loads, int slice) {
+    int n = 0;
+    for (int i = 0; i < parts; ++i) {
+        const int s = spread_slice(i);
+        if (s == 3 || s < slice || (s == slice && i < 4)) n += i == 1 ? stats_loads : 1;
+    }
+    return n;
+}
+
 template <typename V>
 struct AccChunks;
 template <>

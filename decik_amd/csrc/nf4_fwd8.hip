@@ -18,8 +18,9 @@
 // software-pipelined one slice ahead: between the MFMAs of slice j the wave refills each X
 // fragment register right after its MFMA has read it and unpacks slice j + 1 in three stages
 // (code-book addresses, code-book reads, scaling and fp16 packing). Slice 3 holds the step
-// boundary (own-slot fetch, wait, barrier) and the refill of the freed ring slots, one load
-// after each of its MFMAs.
+// boundary (own-slot fetch, wait, barrier); the refill of the freed ring slots starts there and
+// continues through slices 0-2 of the next step, at most two loads per slice (spread_part), so
+// that the eight waves' loads do not queue up in one slice.
 //
 // Epilogue: each token block's 32 x 256 output tile goes through LDS (the X ring, after a
 // barrier) and leaves as whole 512-byte rows; GLU tiles pair the gate wave (0..3) and up wave
@@ -52,7 +53,9 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
     constexpr int NL = XPT + 1 + (NESTED ? 2 : 1);               // loads per thread and step
     static_assert(XCH % 64 == 0, "a wave's X load is wholly inside or past the tile");
     static_assert(2 * 32 * (256 * 4 + 16) <= 3 * XBUF, "epilogue staging fits the X ring");
-    static_assert(XPT + 1 < MB, "a step's load parts fit one slice's MFMA gaps");
+    constexpr int NP = XPT + 2;                                  // load parts per step
+    static_assert(NP <= 8 && MB >= 2, "at most two load parts per slice");
+    constexpr int L3 = spread_loads(NP, NESTED ? 2 : 1, -1);     // loads issued in slice 3
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     // byte-pair code books (gate, up in GLU mode; the same book otherwise): entry 256 b + byte
     // holds (code_b[byte >> 4], code_b[byte & 15]), the two weights of one packed byte
@@ -227,12 +230,13 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
 
     // Ring buffers: step t uses X buffer rx0 (byte offset in the X ring) and weight slot rw0;
     // step t + 1 uses rx1 / rw1; step t + 3 reuses step t's.
-    int rx0 = 0, rw0 = 0, rx1 = XBUF, rw1 = wslot_bytes;
-    // Prologue: three steps in flight; wait for the first.
+    int rx0 = 0, rw0 = 0, rx1 = XBUF, rw1 = wslot_bytes, rx2 = 2 * XBUF, rw2 = 2 * wslot_bytes;
+    // Prologue: two steps and the slice-3 parts of the third in flight; wait for the first.
     load_step(ks0, 0, 0, true);
     load_step(ks0 + 1, XBUF, wslot_bytes, ks0 + 1 < ks1);
-    load_step(ks0 + 2, 2 * XBUF, 2 * wslot_bytes, ks0 + 2 < ks1);
-    wait_vmcnt<2 * NL>();
+#pragma unroll
+    for (int i = 0; i < NP; i += 4) load_part(spread_part(i, XPT), ks0 + 2, rx2, rw2, ks0 + 2 < ks1);
+    wait_vmcnt<NL + L3>();
     lds_barrier();
 
     u32x4_t p;  // packed weights of the current step (slice j: dword j)
@@ -275,8 +279,16 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
                     fetch_step(rw1);
                     lds_barrier();
                 }
-                // step t+3's loads, one part after each of slice 3's MFMAs
-                if (j == 3 && q <= XPT + 1) load_part(q, t + 3, rx0, rw0, t + 3 < ks1);
+                // ring refills: slice 3 starts step t+3 in the slots step t has freed, slices 0-2
+                // continue step t+2
+#pragma unroll
+                for (int r = 0; r < 2; ++r) {
+                    const int i = 4 * r + (j == 3 ? 0 : j + 1);
+                    if (i < NP && q == r * (MB / 2)) {
+                        if (j == 3) load_part(spread_part(i, XPT), t + 3, rx0, rw0, t + 3 < ks1);
+                        else load_part(spread_part(i, XPT), t + 2, rx2, rw2, t + 2 < ks1);
+                    }
+                }
                 // refill the X fragment the MFMA above has read (slice j + 1)
                 xf[q] = xfrag(xs + (j < 3 ? rx0 : rx1), q, jn);
                 if (q == (j < 3 ? qA : qA + 1)) {
@@ -302,10 +314,13 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
             w = wn;
         }
         // rotate the rings: step t + 1's buffers become the current ones
+        const int rxo = rx0, rwo = rw0;
         rx0 = rx1;
         rw0 = rw1;
-        rx1 = rx1 == 2 * XBUF ? 0 : rx1 + XBUF;
-        rw1 = rw1 == 2 * wslot_bytes ? 0 : rw1 + wslot_bytes;
+        rx1 = rx2;
+        rw1 = rw2;
+        rx2 = rxo;
+        rw2 = rwo;
     }
     wait_vmcnt<0>();
     lds_barrier();  // every wave is done with the X ring: it becomes the staging area
