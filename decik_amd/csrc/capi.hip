@@ -226,6 +226,8 @@ void finish_plan(GemmPlan& p, int64_t m, int64_t ncols) {
 constexpr VariantCost kFwdVariants[] = {{1, 4, kFwdBN, 3, 2.35, 0.65},
                                        {2, 4, kFwdBN, 2, 2.23, 0.65},
                                        {4, 4, kFwdBN, 2, 3.10, 0.65},
+                                       {2, 8, kFwdBN, 1, 1.00, 0.80},
+                                       {4, 8, kFwdBN, 1, 1.40, 0.80},
                                        {7, 8, kFwdBN, 1, 2.00, 0.90},
                                        {8, 8, kFwdBN, 1, 2.25, 0.90},
                                        {9, 8, kFwdBN, 1, 2.45, 0.90}};

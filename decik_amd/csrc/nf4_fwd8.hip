@@ -9,7 +9,10 @@
 // of 32*MB tokens (MB = 7, 8 or 9: 224, 256 or 288 tokens) x 256 weight rows; each wave owns 32 weight
 // rows and all 32*MB tokens, so each dequantized weight feeds MB MFMAs (~3 VALU per MFMA), and
 // the X tile, staged once per step for all eight waves, is read by each wave at one 16-byte
-// fragment per MFMA.
+// fragment per MFMA. MB = 2 and 4 (64 and 128 tokens) serve launches with few token rows: there
+// the four-wave kernel's tiles leave a single wave per SIMD (one work-group per CU), which then
+// waits on its own code-book reads; two waves per SIMD on the same tiles hide them (7B gate
+// projection at 64 tokens: 40.2 -> 30.8 us per call).
 //
 // Per wave and 64-wide step: one 16-byte packed load per lane (row arow_to_n(l32), k half
 // g = lane / 32) and the row's block statistics, through a per-wave LDS ring three steps deep;
@@ -40,8 +43,17 @@ constexpr int kF8Dummy = 1024;   // target of the X loads of waves past the tile
 // wide: slot lane holds the block of the lane's row and k half.
 constexpr int kF8WSlot = 1536;
 
+// Epilogue staging: two 32-token blocks of fp32 partial sums (rows 1040 bytes apart), the
+// largest of the epilogues; it reuses the X ring, which is sized to hold it.
+constexpr int kF8Stage = 2 * 32 * (256 * 4 + 16);
+
+// bytes of the X ring region: three step buffers, or the epilogue staging if that is larger
+__host__ __device__ constexpr int fwd8_xring_bytes(int mb) {
+    return 3 * 32 * mb * 128 > kF8Stage ? 3 * 32 * mb * 128 : kF8Stage;
+}
+
 __host__ __device__ constexpr size_t fwd8_smem_bytes(int mb) {
-    return kF8Header + kF8Dummy + 3 * (size_t)(32 * mb * 128) + kF8Waves * 3 * (size_t)kF8WSlot;
+    return kF8Header + kF8Dummy + (size_t)fwd8_xring_bytes(mb) + kF8Waves * 3 * (size_t)kF8WSlot;
 }
 
 template <int MB, bool NESTED>
@@ -52,7 +64,7 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
     constexpr int XPT = (XCH + kF8Threads - 1) / kF8Threads;     // X loads per thread and step
     constexpr int NL = XPT + 1 + (NESTED ? 2 : 1);               // loads per thread and step
     static_assert(XCH % 64 == 0, "a wave's X load is wholly inside or past the tile");
-    static_assert(2 * 32 * (256 * 4 + 16) <= 3 * XBUF, "epilogue staging fits the X ring");
+    static_assert(kF8Stage <= fwd8_xring_bytes(MB), "epilogue staging fits the X ring");
     constexpr int NP = XPT + 2;                                  // load parts per step
     static_assert(NP <= 8 && MB >= 2, "at most two load parts per slice");
     constexpr int L3 = spread_loads(NP, NESTED ? 2 : 1, -1);     // loads issued in slice 3
@@ -154,7 +166,7 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
     const uint32_t am_bytes = sgpr(W.absmax_bytes);
     const float* const gam2 = NESTED ? sgpr(W.absmax2) : nullptr;
     const uint32_t am2_bytes = NESTED ? sgpr(W.absmax2_bytes) : 0u;
-    uint8_t* wring = xs + 3 * XBUF + wave * (3 * wslot_bytes);
+    uint8_t* wring = xs + fwd8_xring_bytes(MB) + wave * (3 * wslot_bytes);
     // Part p of step t's loads (p < XPT: X chunk p; XPT: the packed weights; XPT + 1: their
     // statistics), so that the main loop issues a step's loads one per MFMA gap: issued in one
     // burst after the barrier they held up the matrix pipe.
@@ -261,8 +273,14 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
         }
         w = __builtin_bit_cast(half8_t, o);
     }
-    // stage positions (MFMA index after which a stage runs)
-    constexpr int qA = 0, qB = 1, qC = MB - 3;
+    // stage positions (MFMA index after which a stage runs). With seven or more MFMAs a slice the
+    // stages take separate gaps, and in slice 3, whose first gap holds the step boundary, the
+    // address and code-book stages move one gap later; with fewer (MB = 2, 4) the code-book reads
+    // follow the addresses in the first gap of every slice and the scaling takes the last gap
+    // that leaves them time to land.
+    constexpr bool SMALL = MB < 7;
+    constexpr int qA = 0, qB = SMALL ? 0 : 1, qC = SMALL ? (MB > 2 ? MB - 2 : 1) : MB - 3;
+    constexpr int q3 = SMALL ? 0 : 1;  // slice 3's shift of stages A and B
     for (int t = ks0; t < ks1; ++t) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -291,11 +309,11 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
                 }
                 // refill the X fragment the MFMA above has read (slice j + 1)
                 xf[q] = xfrag(xs + (j < 3 ? rx0 : rx1), q, jn);
-                if (q == (j < 3 ? qA : qA + 1)) {
+                if (q == (j < 3 ? qA : qA + q3)) {
 #pragma unroll
                     for (int e = 0; e < 4; ++e) pa[e] = pair_addr(p[jn], e);
                 }
-                if (q == (j < 3 ? qB : qB + 1)) {
+                if (q == (j < 3 ? qB : qB + q3)) {
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const float2_t cv = pair_at(pa[e]);
@@ -428,7 +446,7 @@ static hipError_t launch_fwd8_t(const FwdArgs& a, int grid, hipStream_t s) {
 hipError_t launch_fwd8(const FwdArgs& a, int mb, int grid, hipStream_t s) {
 #define X(T) \
     if (mb == T) return a.nested ? launch_fwd8_t<T, true>(a, grid, s) : launch_fwd8_t<T, false>(a, grid, s);
-    X(7) X(8) X(9)
+    X(2) X(4) X(7) X(8) X(9)
 #undef X
     return hipErrorInvalidValue;
 }

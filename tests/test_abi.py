@@ -158,6 +158,11 @@ def test_launch_plans():
             os.environ["DECIK_SMALL_M"] = old_sm
     glu = launch_plan(False, 830, 1536, [8960, 8960], glu=True)
     assert glu["splits"] == 1 and glu["kernel"] == "nf4_fwd8_kernel"
+    # 64 and 128 token rows: the eight-wave forward kernel on 64- / 128-token tiles (two waves
+    # per SIMD where the four-wave kernel's tiles left one)
+    assert launch_plan(False, 64, 3584, [18944]) == dict(rows_blocks=2, waves=8, splits=3, kernel="nf4_fwd8_kernel")
+    assert launch_plan(False, 128, 3584, [18944]) == dict(rows_blocks=4, waves=8, splits=3, kernel="nf4_fwd8_kernel")
+    assert launch_plan(False, 64, 3584, [18944, 18944], glu=True)["rows_blocks"] == 2
     # k % blocksize != 0: the eight-wave forward kernel may not run
     assert launch_plan(False, 830, 1536, [8960], blocksize=1024)["kernel"] == "nf4_fwd_kernel"
     assert launch_plan(True, 830, 1536, [8960, 8960], no_split=True)["splits"] == 1

@@ -24,7 +24,7 @@ def _two_books(device, n1, n2, k, nested=True):
     return (p1, q1, w1), (p2, q2, w2)
 
 
-@pytest.mark.parametrize("plan", ["1,1,4", "2,2,4", "7,1,8", "8,2,8"])
+@pytest.mark.parametrize("plan", ["1,1,4", "2,2,4", "2,2,8", "4,1,8", "7,1,8", "8,2,8"])
 def test_grouped_forward(plan, device, monkeypatch):
     from decik_amd.nf4 import linear_forward
 
@@ -37,7 +37,7 @@ def test_grouped_forward(plan, device, monkeypatch):
     assert_close(y2, O.linear_ref(xn, w2), what=f"second book, plan {plan}")
 
 
-@pytest.mark.parametrize("plan", ["9,1,8", "2,1"])
+@pytest.mark.parametrize("plan", ["9,1,8", "2,1,8", "2,1"])
 def test_glu_forward(plan, device, monkeypatch):
     from decik_amd.nf4 import glu_forward
 

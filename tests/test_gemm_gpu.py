@@ -80,7 +80,7 @@ def test_backward_fp32_output(device):
     assert torch.equal(dx32.to(torch.float16), dx16)
 
 
-@pytest.mark.parametrize("plan", ["2,1", "4,1", "1,3"])
+@pytest.mark.parametrize("plan", ["2,1", "4,1", "1,3", "2,2,8", "4,1,8"])
 def test_grouped_forward_equals_separate(plan, device, monkeypatch):
     """q, k, v sharing X in one launch = three launches with the same plan (bit for bit: the
     same tile shape and contraction splits give the same fp32 summation order), and each output

@@ -26,7 +26,7 @@ def _separate_glu(x, gate_it, up_it):
     return g, u, swiglu_fwd(g, u)
 
 
-@pytest.mark.parametrize("plan", ["4,1", "2,1", "1,1", "9,1,8"])
+@pytest.mark.parametrize("plan", ["4,1", "2,1", "1,1", "2,1,8", "4,1,8", "9,1,8"])
 @pytest.mark.parametrize("m,n,k", GLU_SHAPES)
 def test_glu_forward_equals_separate(m, n, k, plan, device, monkeypatch):
     from decik_amd.nf4 import glu_forward

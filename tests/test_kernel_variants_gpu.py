@@ -5,6 +5,7 @@ fp32 block scales: nested double-quant statistics read by the kernels themselves
 kernel. Plans are forced so that each kernel and its split-K path run (solution/nf4.py:93-104;
 the summed input gradient of solution/mlp.py:106-109)."""
 import pytest
+import torch
 
 from helpers import O, assert_close, make_weight, randn16
 
@@ -21,7 +22,7 @@ def raw_statistics(monkeypatch):
     monkeypatch.setattr(nf4, "_scales", lambda packed, qs, device: None)
 
 
-@pytest.mark.parametrize("plan", ["4,1,4", "2,3,4", "7,2,8", "8,1,8", "9,2,8"])
+@pytest.mark.parametrize("plan", ["4,1,4", "2,3,4", "2,3,8", "4,1,8", "7,2,8", "8,1,8", "9,2,8"])
 @pytest.mark.parametrize("nested,blocksize", CASES)
 def test_forward_variants(nested, blocksize, plan, device, monkeypatch, raw_statistics):
     from decik_amd.nf4 import linear_forward
@@ -293,3 +294,45 @@ def test_column_tiles_first_order(fwd_plan, bwd_plan, device, monkeypatch):
     assert_close(y, O.linear_ref(x.cpu().numpy(), w16), what=f"fwd columns first {fwd_plan}")
     dx = linear_backward([dict(packed=packed, qs=qs, dy=dy)], m, k)
     assert_close(dx, O.linear_dx_ref(dy.cpu().numpy(), w16), what=f"bwd columns first {bwd_plan}")
+
+
+@pytest.mark.parametrize("plan", ["2,1,8", "2,3,8", "4,1,8", "4,2,8"])
+@pytest.mark.parametrize("m", [33, 64, 130])
+def test_small_tile_forward(plan, m, device, monkeypatch):
+    """The eight-wave forward kernel on 64- and 128-token tiles (MB = 2, 4): partial token tiles
+    (33, 130 rows), two weights with a partial column tile (320 and 200 rows), bias, LoRA terms
+    on the first weight only, split-K; then its GLU mode at the same sizes against the separate
+    launches of the same tiles, unsplit. The first part reads raw nested statistics (blocks of 128 and 64), the GLU part
+    cached block scales."""
+    from decik_amd import nf4
+    from decik_amd.lora import lora_down
+    from decik_amd.nf4 import glu_forward, launch_plan, linear_forward
+    from decik_amd.swiglu import swiglu_fwd
+
+    monkeypatch.setenv("DECIK_FWD_PLAN", plan)
+    k, r = 1024, 16
+    assert launch_plan(False, m, k, [320, 200])["kernel"] == "nf4_fwd8_kernel"
+    p1, q1, w1 = make_weight((320, k), seed=190, device=device, nested=True, blocksize=128)
+    p2, q2, w2 = make_weight((200, k), seed=191, device=device)
+    x = randn16((m, k), seed=192 + m, device=device)
+    b1 = randn16((320,), seed=193, device=device, std=0.1)
+    b2 = randn16((200,), seed=194, device=device, std=0.1)
+    a = randn16((r, k), seed=195, device=device, std=0.05)
+    lb = randn16((320, r), seed=196, device=device, std=0.05)
+    u = lora_down(x, a)
+    items = [dict(packed=p1, qs=q1, bias=b1, lora_u=u, lora_b=lb, lora_scale=2.0), dict(packed=p2, qs=q2, bias=b2)]
+    raw = nf4._scales
+    monkeypatch.setattr(nf4, "_scales", lambda packed, qs, device: None)
+    y1, y2 = linear_forward(x, items, lora_rank=r)
+    xn = x.cpu().numpy()
+    lora = O.lora_fwd_ref(xn, a.cpu().numpy(), lb.cpu().numpy(), 2.0)[1]
+    assert_close(y1, O.linear_ref(xn, w1, b1.cpu().numpy()) + lora, what=f"first weight, plan {plan}, m={m}")
+    assert_close(y2, O.linear_ref(xn, w2, b2.cpu().numpy()), what=f"second weight, plan {plan}, m={m}")
+    monkeypatch.setattr(nf4, "_scales", raw)
+    # the GLU launch never splits: the separate launches it must equal run unsplit too
+    monkeypatch.setenv("DECIK_FWD_PLAN", plan.split(",")[0] + ",1,8")
+    p3, q3, _ = make_weight((200, k), seed=197, device=device)
+    gi, ui = dict(packed=p2, qs=q2, bias=b2), dict(packed=p3, qs=q3)
+    g, up, h = glu_forward(x, gi, ui)
+    g2, u2 = linear_forward(x, [gi, ui])
+    assert torch.equal(g, g2) and torch.equal(up, u2) and torch.equal(h, swiglu_fwd(g2, u2))
