@@ -237,11 +237,12 @@ constexpr int kNumFwdVariants = sizeof(kFwdVariants) / sizeof(kFwdVariants[0]);
 constexpr VariantCost kBwdVariants[] = {{2, 4, 256, 2, 2.55, 0.90},
                                        {2, 8, 512, 1, 2.60, 1.0},
                                        {4, 8, 512, 1, 3.40, 1.0},
+                                       {2, 8, 256, 1, 1.00, 1.0},
                                        {4, 8, 256, 1, 1.75, 0.90},
                                        {7, 8, 256, 1, 2.10, 0.90},
                                        {8, 8, 256, 1, 2.25, 0.90}};
 constexpr int kNumBwdVariants = sizeof(kBwdVariants) / sizeof(kBwdVariants[0]);
-constexpr int kNumBwdSwigluVariants = 4;  // nf4_bwd_kernel's and nf4_bwd8_kernel<4>
+constexpr int kNumBwdSwigluVariants = 5;  // nf4_bwd_kernel's, nf4_bwd8_kernel<2> and <4>
 static_assert(kBwdVariants[kNumBwdSwigluVariants - 1].bn == 256 && kBwdVariants[kNumBwdSwigluVariants - 1].rows_blocks == 4 &&
               kBwdVariants[kNumBwdSwigluVariants].rows_blocks > 4, "SwiGLU-capable variants first");
 

@@ -9,6 +9,8 @@
 // Here a work-group is 8 waves (two per SIMD, one work-group per CU) on a tile of 32*MB tokens
 // (MB = 4, 7 or 8) x 256 output columns; each wave owns 32 columns -- one A operand, one nibble
 // per lane and weight row -- and all 32*MB tokens, so each dequantized weight feeds MB MFMAs.
+// MB = 2 (64 tokens) serves launches with few token rows, which on 128-token tiles would spend
+// half their MFMAs on padding (7B gate/up input gradient at 64 tokens: 45 -> 40 us).
 //
 // A operand (A = W^T): lane l (l32 = l % 32, g = l / 32) serves A row l32 = output column
 // c = l32 ^ 1 of the wave's 32. Its eight contraction slots of slice j are the weight rows
@@ -32,7 +34,7 @@
 //
 // Epilogue: each token block's 32 x 256 tile goes through LDS (the rings, after a barrier) and
 // leaves as whole rows: split-K partial slabs (reduced by splitk_reduce_kernel), dX in fp32 or
-// fp16, or (SwiGLU mode, MB = 4) dgate / dup from the tile rounded to fp16 and the matching gate
+// fp16, or (SwiGLU mode, MB <= 4) dgate / dup from the tile rounded to fp16 and the matching gate
 // and up tiles, which every thread fetches for all its token blocks as the kernel starts.
 #include "gemm_common.h"
 
@@ -57,8 +59,17 @@ constexpr int kB8Dummy = 1024;                // target of the dY loads of waves
 constexpr int kB8WSlot = 1536;
 constexpr int kB8ScaleBytes = 2 * 64 * 4;  // per wave: row-scale tables of two steps
 
+// Epilogue staging: two 32-token blocks of fp32 tiles (rows 1040 bytes apart), in the dY ring
+// and the weight rings and scale tables behind it; the dY ring region is sized so that it fits.
+constexpr int kB8Stage = 2 * 32 * (kB8BN * 4 + 16);
+__host__ __device__ constexpr int bwd8_dring_bytes(int mb) {
+    return 3 * 32 * mb * 128 + kB8Waves * (3 * kB8WSlot + kB8ScaleBytes) >= kB8Stage
+               ? 3 * 32 * mb * 128
+               : kB8Stage - kB8Waves * (3 * kB8WSlot + kB8ScaleBytes);
+}
+
 __host__ __device__ constexpr size_t bwd8_smem_bytes(int mb) {
-    return kB8Tables + kB8Dummy + 3 * (size_t)(32 * mb * 128) +
+    return kB8Tables + kB8Dummy + (size_t)bwd8_dring_bytes(mb) +
            kB8Waves * (3 * (size_t)kB8WSlot + kB8ScaleBytes);
 }
 
@@ -71,7 +82,8 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
     constexpr int NL = DPT + 1 + (NESTED ? 2 : 1);             // loads per thread and step
     static_assert(DCH % 64 == 0, "a wave's dY load is wholly inside or past the tile");
     // epilogue staging area: the dY ring, the weight rings and the scale tables (contiguous)
-    constexpr int STAGE = 3 * DBUF + kB8Waves * (3 * kB8WSlot + kB8ScaleBytes);
+    constexpr int DRING = bwd8_dring_bytes(MB);                // bytes of the dY ring region
+    constexpr int STAGE = DRING + kB8Waves * (3 * kB8WSlot + kB8ScaleBytes);
     static_assert(2 * 32 * (kB8BN * 4 + 16) <= STAGE, "epilogue staging fits the rings");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     // byte-pair code book of the current group: entry x = (code[x & 15], code[x >> 4]), the
@@ -106,8 +118,8 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
         for (int gg = 0; gg < a.ngroups; ++gg)
             if (tid < 256) ((float*)smem)[256 * gg + tid] = a.g[gg].w.code2[tid];
     }
-    uint8_t* wring = dring + 3 * DBUF + wave * (3 * kB8WSlot);
-    float* stab = (float*)(dring + 3 * DBUF + kB8Waves * 3 * kB8WSlot + wave * kB8ScaleBytes);
+    uint8_t* wring = dring + DRING + wave * (3 * kB8WSlot);
+    float* stab = (float*)(dring + DRING + kB8Waves * 3 * kB8WSlot + wave * kB8ScaleBytes);
     // this lane's transposed reads (slices j, j + 1 for even j): row 32 g + 8 j + (lane % 16) of
     // the step, bytes 8 (l32 / 16) .. of the wave's 16
     const int pkl = 16 * (32 * g + (lane & 15)) + 8 * ((lane >> 4) & 1);
@@ -118,11 +130,14 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
 
     // stage positions (MFMA index after which a stage runs). With few MFMAs per slice (P2) the
     // packed dwords and row scales are read two slices ahead (LA = 2), so the next step's row
-    // scales are made in slice 1 (JW) instead of slice 2.
+    // scales are made in slice 1 (JW) instead of slice 2. With two MFMAs a slice (MB = 2) the
+    // code-book reads follow stage A in the first gap and the scaling takes the second; the row
+    // scales take both gaps of slice 1.
     constexpr bool P2 = MB <= 4;
     constexpr int LA = P2 ? 2 : 1, JW = P2 ? 1 : 2;
-    constexpr int qB = MB >= 7 ? 2 : 1, qC = MB >= 7 ? MB - 2 : MB - 1;
-    constexpr int qS1 = 1, qS2 = MB >= 7 ? 3 : 2, qS3 = MB >= 7 ? 5 : 3;  // next step's row scales
+    constexpr int qB = MB >= 7 ? 2 : (MB >= 4 ? 1 : 0), qC = MB >= 7 ? MB - 2 : MB - 1;
+    // next step's row scales
+    constexpr int qS1 = MB >= 4 ? 1 : 0, qS2 = MB >= 7 ? 3 : (MB >= 4 ? 2 : 1), qS3 = MB >= 7 ? 5 : (MB >= 4 ? 3 : 1);
     static_assert(qS3 < MB && qB < qC, "stages inside the slice");
     static_assert(MB <= 4 || DPT + 1 < MB, "a step's load parts fit one slice's MFMA gaps");
 
@@ -596,7 +611,7 @@ hipError_t launch_bwd8(const BwdArgs& a, int mb, int grid, hipStream_t s) {
     if (a.swiglu && (mb > 4 || a.splits > 1)) return hipErrorInvalidValue;  // SwiGLU: MB <= 4, no split
 #define X(T) \
     if (mb == T) return a.nested ? launch_bwd8_t<T, true>(a, grid, s) : launch_bwd8_t<T, false>(a, grid, s);
-    X(4) X(7) X(8)
+    X(2) X(4) X(7) X(8)
 #undef X
     return hipErrorInvalidValue;
 }
