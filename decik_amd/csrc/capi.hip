@@ -325,9 +325,11 @@ GemmPlan plan_skinny(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
         ncols += ns[g];
     }
     p.steps = (int)((k + kSkinnyStep - 1) / kSkinnyStep);
+    // split the contraction while the work-groups still fit one per CU and every split keeps at
+    // least one super-step per wave
     p.splits = 1;
-    while (p.splits < 32 && rgroups * p.splits < 2 * num_cus() &&
-           (p.steps + p.splits) / (p.splits + 1) >= 2 * kSkinnyWaves)
+    while (p.splits < 32 && rgroups * (p.splits + 1) <= num_cus() &&
+           (p.steps + p.splits) / (p.splits + 1) >= kSkinnyWaves)
         ++p.splits;
     p.n_tiles = (int)rgroups;
     p.m_tiles = 1;
