@@ -178,14 +178,14 @@ __global__ __launch_bounds__(kGemvThreads) void nf4_gemv_kernel(const FwdArgs a,
 }
 
 // Work-group shape of a launch: `cpt` chunk loads per thread and `rows` rows per work-group
-// (rows * cpr <= 256 cpt). The fewest loads per thread whose rows fill at least 95% of them
-// (more, smaller work-groups measured faster: 7B gate at one token 15.1 us with 7 loads, 13.3
-// with 5), else the best fill.
+// (rows * cpr <= 256 cpt).
 struct GemvShape {
     int cpt, rows;
 };
 
-static GemvShape gemv_shape(int k) {
+// The fewest loads per thread whose rows fill at least 95% of them, else the best fill (4 to 8
+// loads per thread): the shape that bounds the LDS a launch of contraction k needs.
+static GemvShape gemv_shape_bound(int k) {
     const int cpr = k >> 5;
     GemvShape best{0, 0};
     double best_fill = -1.0;
@@ -206,8 +206,41 @@ static GemvShape gemv_shape(int k) {
 // two token rows and the sums must fit LDS).
 bool gemv_fits(int64_t k) {
     if (k <= 0 || k % 32 != 0 || k > kGemvThreads * kGemvMaxChunks * 32) return false;
-    const GemvShape sh = gemv_shape((int)k);
+    const GemvShape sh = gemv_shape_bound((int)k);
     return sh.rows >= 1 && gemv_smem_bytes(kGemvMaxM, (int)k, sh.rows * (int)(k >> 5)) <= 158 * 1024;
+}
+
+// The shape of a launch of `nrows` weight rows and mt token rows. Every work-group stages X
+// (2 k mt bytes) next to its rows' packed bytes (k / 2 per row), and fewer loads per thread
+// mean more, lighter work-groups in flight. Among the load counts whose rows fill at least 75%
+// of the loads: the fewest with at least 4 mt rows (X traffic at most the weight's), unless that
+// leaves fewer than 1024 work-groups -- then the fewest of all, for parallelism. Graph-replayed
+// on MI355X at one token (us, against the previous 4-8-load rule): 7B gate 17.0 -> 15.3, k/v
+// 5.5 -> 3.7, q/o 7.6 -> 6.3; Qwen2.5-1.5B gate 8.4 -> 6.7, down 8.9 -> 7.1, q/o 6.4 -> 4.3,
+// k/v 6.0 -> 3.7. The row sums keep their order whatever the shape: the same bits.
+static GemvShape gemv_shape(int k, int64_t nrows, int mt) {
+    const int cpr = k >> 5;
+    GemvShape fewest{0, 0}, most{0, 0};
+    double most_fill = -1.0;
+    for (int cpt = 1; cpt <= kGemvMaxChunks; ++cpt) {
+        const int rows = kGemvThreads * cpt / cpr;
+        if (rows < 1) continue;
+        const double fill = (double)rows * cpr / (kGemvThreads * cpt);
+        if (fill < 0.75) continue;
+        if (fewest.cpt == 0) fewest = GemvShape{cpt, rows};
+        if (rows >= 4 * mt) {
+            most = GemvShape{cpt, rows};
+            break;
+        }
+        if (rows > most.rows || (rows == most.rows && fill > most_fill + 1e-9)) {
+            most = GemvShape{cpt, rows};
+            most_fill = fill;
+        }
+    }
+    if (most.cpt == 0) return gemv_shape_bound(k);
+    const GemvShape pick = (nrows + most.rows - 1) / most.rows >= 1024 ? most : fewest;
+    if (gemv_smem_bytes(mt, k, pick.rows * cpr) > 158 * 1024) return gemv_shape_bound(k);
+    return pick;
 }
 
 template <int MT, bool NESTED, int CPT>
@@ -222,6 +255,9 @@ static hipError_t launch_gemv_t(const FwdArgs& a, int rows, int grid, hipStream_
 template <int MT, bool NESTED>
 static hipError_t launch_gemv_cpt(const FwdArgs& a, int cpt, int rows, int grid, hipStream_t s) {
     switch (cpt) {
+        case 1: return launch_gemv_t<MT, NESTED, 1>(a, rows, grid, s);
+        case 2: return launch_gemv_t<MT, NESTED, 2>(a, rows, grid, s);
+        case 3: return launch_gemv_t<MT, NESTED, 3>(a, rows, grid, s);
         case 4: return launch_gemv_t<MT, NESTED, 4>(a, rows, grid, s);
         case 5: return launch_gemv_t<MT, NESTED, 5>(a, rows, grid, s);
         case 6: return launch_gemv_t<MT, NESTED, 6>(a, rows, grid, s);
@@ -236,7 +272,9 @@ hipError_t launch_gemv(FwdArgs& a, hipStream_t s) {
     if (a.m < 1 || a.m > kGemvMaxM || a.glu || !gemv_fits(a.k)) return hipErrorInvalidValue;
     for (int g = 0; g < a.ngroups; ++g)
         if (a.g[g].lora_u != nullptr) return hipErrorInvalidValue;
-    const GemvShape sh = gemv_shape(a.k);
+    int64_t nrows = 0;
+    for (int g = 0; g < a.ngroups; ++g) nrows += a.g[g].w.n;
+    const GemvShape sh = gemv_shape(a.k, nrows, a.m);
     int grid = 0;
     for (int g = 0; g < a.ngroups; ++g) {
         a.g[g].tile_begin = grid;
