@@ -442,6 +442,45 @@ def count_kernels(fn):
         return None, None
 
 
+def graph_steps(step_grads, layers, reps=3):
+    """Per-step GPU time of step_grads(L) (a forward and torch.autograd.grad of it, returning the
+    gradients) over every layer in `layers`, captured once in a HIP graph and replayed `reps`
+    times: the host's Python and launch cost, which bounds the eager step, drops out. After every
+    replay the last step's gradients are compared with the same step run eagerly, bit for bit.
+    Returns (ms per step, median of the replays) or (None, reason) when capture fails or a replay
+    differs."""
+    import torch
+
+    ref = [t.clone() for t in step_grads(layers[-1])]
+    torch.cuda.synchronize()
+    try:
+        g = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step_grads(layers[0])  # warm-up on the capture stream
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        outs = []
+        with torch.cuda.graph(g):
+            for L in layers:
+                outs.append(step_grads(L))
+        times = []
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            g.replay()
+            b.record()
+            torch.cuda.synchronize()
+            if not all(torch.equal(o, r) for o, r in zip(outs[-1], ref)):
+                return None, "a replay differs from the eager step"
+            times.append(a.elapsed_time(b) / len(layers))
+        del g, outs
+        return statistics.median(times), None
+    except Exception as e:  # noqa: BLE001 - reported instead of a graph time
+        return None, f"capture failed: {type(e).__name__}: {str(e)[:100]}"
+
+
 def bench_c3(steps, warmup, device):
     """Config C3: the attention projections of one Qwen2.5-1.5B layer at 830 packed tokens, forward
     and backward: q [1536, 1536], k / v [256, 1536] with biases, LoRA r=16 (alpha 32, dropout
@@ -497,7 +536,7 @@ def bench_c3(steps, warmup, device):
                       keep_bits=bv, keep_scale=scale, p=LORA_P))
         q, k, v = lora.qkv_rope_projection(x, projs, cos, sin, N_HEADS, N_KV_HEADS)
         o = nf4.NF4Linear.apply(attn, L["o"][0], None, L["o"][1])
-        torch.autograd.backward([q, k, v, o], [gq, gk, gv, go])
+        return [q, k, v, o]
 
     def reference_order(L):
         (aq, bq_w), (av, bv_w) = L["q_lora"], L["v_lora"]
@@ -510,7 +549,21 @@ def bench_c3(steps, warmup, device):
         v = (v_base.float() + v_lora.float()).to(torch.float16)
         q, k = FusedQKRope.apply(q_base, q_lora.to(torch.float16), k, cos, sin, N_HEADS, N_KV_HEADS)
         o = nf4.NF4Linear.apply(attn, L["o"][0], None, L["o"][1])
-        torch.autograd.backward([q, k, v, o], [gq, gk, gv, go])
+        return [q, k, v, o]
+
+    def step(forward):
+        """forward + backward with the gradients accumulated into .grad (the eager step)"""
+        def run(L):
+            torch.autograd.backward(forward(L), [gq, gk, gv, go])
+        return run
+
+    def step_grads(forward):
+        """forward + backward returning the gradients of x, the attention output and the four
+        adapters (graph capture: no accumulation into .grad)"""
+        def run(L):
+            (aq, bq_w), (av, bv_w) = L["q_lora"], L["v_lora"]
+            return torch.autograd.grad(forward(L), [x, attn, aq, bq_w, av, bv_w], [gq, gk, gv, go])
+        return run
 
     def clear():
         x.grad = attn.grad = None
@@ -519,7 +572,8 @@ def bench_c3(steps, warmup, device):
                 a.grad = b.grad = None
 
     res = {}
-    for name, fn in (("fused", fused), ("reference_order", reference_order)):
+    for name, forward in (("fused", fused), ("reference_order", reference_order)):
+        fn = step(forward)
         for i in range(n_sets):  # fills every weight's block-scale cache
             fn(layers[i])
             clear()
@@ -540,8 +594,9 @@ def bench_c3(steps, warmup, device):
             torch.cuda.synchronize()
             blocks.append(a.elapsed_time(b) / steps)
         launches, busy = count_kernels(lambda fn=fn: (fn(layers[-1]), clear()))
+        graph_ms, graph_note = graph_steps(step_grads(forward), layers)
         res[name] = dict(ms=statistics.median(blocks), spread=(min(blocks), max(blocks)), launches=launches,
-                         busy_us=busy)
+                         busy_us=busy, graph_ms=graph_ms, graph_note=graph_note)
     gemm = 2 * sum(gemm_flops(n, k) for name, n, k in QWEN15_SHAPES if name in ("q", "k", "v", "o"))
     lora_f = sum(2 * M * LORA_R * (HIDDEN + n) + 2 * M * LORA_R * (2 * HIDDEN + 2 * n) for n in (1536, 256))
     out = dict(workload="Qwen2.5-1.5B attention projections, one layer fwd+bwd, M=830 (8 packed sequences): "
@@ -553,13 +608,23 @@ def bench_c3(steps, warmup, device):
         out[name] = dict(ms=round(r["ms"], 4), ms_range=[round(v, 4) for v in r["spread"]],
                          tflops=round((gemm + lora_f) / (r["ms"] * 1e-3) / 1e12, 1),
                          launches=r["launches"],
-                         gpu_busy_ms=None if r["busy_us"] is None else round(r["busy_us"] / 1e3, 4))
+                         gpu_busy_ms=None if r["busy_us"] is None else round(r["busy_us"] / 1e3, 4),
+                         graph_ms=None if r["graph_ms"] is None else round(r["graph_ms"], 4),
+                         graph_tflops=None if r["graph_ms"] is None else
+                         round((gemm + lora_f) / (r["graph_ms"] * 1e-3) / 1e12, 1))
+        if r["graph_note"]:
+            out[name]["graph_note"] = r["graph_note"]
     out["speedup"] = round(res["reference_order"]["ms"] / res["fused"]["ms"], 3)
+    if res["fused"]["graph_ms"] and res["reference_order"]["graph_ms"]:
+        out["graph_speedup"] = round(res["reference_order"]["graph_ms"] / res["fused"]["graph_ms"], 3)
     if res["fused"]["busy_us"] and res["reference_order"]["busy_us"]:
         out["gpu_busy_speedup"] = round(res["reference_order"]["busy_us"] / res["fused"]["busy_us"], 3)
     out["note"] = ("ms: eager steps back to back (HIP events), bound by the host's Python and launch "
                    "overhead at this size: median of five blocks of steps (ms_range: the fastest and "
-                   "slowest block); gpu_busy_ms: the kernels' summed durations in one profiled step")
+                   "slowest block); gpu_busy_ms: the kernels' summed durations in one profiled step; "
+                   "graph_ms: the same step over every layer's weights captured once in a HIP graph "
+                   "(forward + torch.autograd.grad) and replayed, median of three replays, each "
+                   "replay's last gradients equal to the eager step's bit for bit")
     return out
 
 
