@@ -13,7 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libdecik_nf4.so")
-SOURCES = ["capi.hip", "nf4_dequant.hip", "nf4_fwd.hip", "nf4_fwd8.hip", "nf4_gemv.hip", "nf4_skinny.hip", "nf4_bwd.hip", "nf4_bwd8.hip", "splitk.hip", "lora.hip", "lora_dropout.hip", "rope.hip", "swiglu.hip", "probe.hip"]
+SOURCES = ["capi.hip", "nf4_dequant.hip", "nf4_fwd.hip", "nf4_fwd8.hip", "nf4_gemv.hip", "nf4_skinny.hip", "nf4_bwd8.hip", "splitk.hip", "lora.hip", "lora_dropout.hip", "rope.hip", "swiglu.hip", "probe.hip"]
 ARCH = os.environ.get("DECIK_ARCH", "gfx950")
 
 FLAGS = [

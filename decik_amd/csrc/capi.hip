@@ -232,22 +232,16 @@ constexpr VariantCost kFwdVariants[] = {{1, 4, kFwdBN, 3, 2.35, 0.65},
                                        {8, 8, kFwdBN, 1, 2.25, 0.90},
                                        {9, 8, kFwdBN, 1, 2.45, 0.90}};
 constexpr int kNumFwdVariants = sizeof(kFwdVariants) / sizeof(kFwdVariants[0]);
-// waves 8 with 256 columns: nf4_bwd8_kernel (eight waves of 32 output columns), listed after
-// nf4_bwd_kernel's; its SwiGLU epilogue exists for rows_blocks 4 only, which comes first.
-constexpr VariantCost kBwdVariants[] = {{2, 4, 256, 2, 2.55, 0.90},
-                                       {2, 8, 512, 1, 2.60, 1.0},
-                                       {4, 8, 512, 1, 3.40, 1.0},
-                                       {2, 8, 256, 1, 1.00, 1.0},
+// nf4_bwd8_kernel: eight waves of 32 output columns (256-column tiles); its SwiGLU epilogue
+// exists for rows_blocks <= 4, which come first.
+constexpr VariantCost kBwdVariants[] = {{2, 8, 256, 1, 1.00, 1.0},
                                        {4, 8, 256, 1, 1.75, 0.90},
                                        {7, 8, 256, 1, 2.10, 0.90},
                                        {8, 8, 256, 1, 2.25, 0.90}};
 constexpr int kNumBwdVariants = sizeof(kBwdVariants) / sizeof(kBwdVariants[0]);
-constexpr int kNumBwdSwigluVariants = 5;  // nf4_bwd_kernel's, nf4_bwd8_kernel<2> and <4>
-static_assert(kBwdVariants[kNumBwdSwigluVariants - 1].bn == 256 && kBwdVariants[kNumBwdSwigluVariants - 1].rows_blocks == 4 &&
+constexpr int kNumBwdSwigluVariants = 2;  // rows_blocks 2 and 4
+static_assert(kBwdVariants[kNumBwdSwigluVariants - 1].rows_blocks == 4 &&
               kBwdVariants[kNumBwdSwigluVariants].rows_blocks > 4, "SwiGLU-capable variants first");
-
-// nf4_bwd8_kernel variants: eight waves, 256-column tiles
-constexpr bool is_bwd8(const VariantCost& v) { return v.waves == 8 && v.bn == 256; }
 
 // The eight-wave variants come last: nf4_fwd8_kernel advances its load descriptors by whole
 // steps, so it needs k % 64 == 0 and blocks that do not straddle rows (k % blocksize == 0).
@@ -306,7 +300,6 @@ GemmPlan plan_bwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool swi
                         no_split ? 1 : 32, max_partial_bytes);
     p.mt = v->rows_blocks;
     p.waves = v->waves;
-    p.bwd8 = is_bwd8(*v);
     p.n_tiles = (int)((k + v->bn - 1) / v->bn);
     p.m_tiles = (int)((m + kRowUnit * p.mt - 1) / (kRowUnit * p.mt));
     finish_plan(p, m, k);
@@ -455,7 +448,7 @@ int dk_nf4_linear_plan(int backward, int64_t m, int64_t k, const int64_t* ns, in
     int kernel;
     if (backward) {
         p = plan_bwd(m, k, ns, ngroups, glu, single);
-        kernel = p.bwd8 ? 3 : 2;
+        kernel = 3;  // nf4_bwd8_kernel
     } else if (small_m_forward(m, glu, lora) && gemv_requested(m, k)) {
         p = GemmPlan{};
         p.waves = 4;
@@ -820,8 +813,7 @@ static int linear_bwd_impl(const std::string& name, const dk_linear_bwd_group* g
     const int64_t wgs = (int64_t)p.m_tiles * p.n_tiles * p.splits;
     if (wgs > INT32_MAX / 2) return fail(name + ": problem too large");
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    const hipError_t le = p.bwd8 ? launch_bwd8(a, p.mt, pad8((int)wgs), st)
-                                 : launch_bwd(a, p.mt, p.waves, pad8((int)wgs), st);
+    const hipError_t le = launch_bwd8(a, p.mt, pad8((int)wgs), st);
     if (check_hip(le, "dk_nf4_linear_bwd launch")) return 1;
     if (p.splits <= 1) return 0;
     ReduceArgs r{};

@@ -136,11 +136,9 @@ struct ReduceArgs {
 struct GemmPlan {
     int mt;        // 32-row token blocks per tile
     int waves;     // waves per work-group (forward: 4 = nf4_fwd_kernel, 8 = nf4_fwd8_kernel;
-                   // backward: nf4_bwd_kernel's 4 or 8 waves of 64 output columns, or
-                   // nf4_bwd8_kernel's 8 of 32)
-    bool bwd8;     // backward: nf4_bwd8_kernel
+                   // backward: nf4_bwd8_kernel's 8 of 32 output columns)
     int m_tiles;
-    int n_tiles;   // output column tiles (fwd: weight rows / 256; bwd: k / 512)
+    int n_tiles;   // output column tiles (fwd: weight rows / 256; bwd: k / 256)
     int steps;     // main-loop steps over the whole contraction
     int splits;
     int steps_per_split;
@@ -162,9 +160,8 @@ constexpr int kSkinnyMaxM = 32;
 hipError_t launch_skinny(const FwdArgs& a, int grid, hipStream_t s);
 // 8-wave forward kernel (32 weight rows x 32*mb tokens per wave), mb = 8 or 9
 hipError_t launch_fwd8(const FwdArgs& a, int mb, int grid, hipStream_t s);
-hipError_t launch_bwd(const BwdArgs& a, int mb, int waves, int grid, hipStream_t s);
-// 8-wave input-gradient kernel (32 output columns x 32*mb tokens per wave), mb = 4, 7 or 8; the
-// SwiGLU epilogue with mb = 4 only
+// 8-wave input-gradient kernel (32 output columns x 32*mb tokens per wave), mb = 2, 4, 7 or 8;
+// the SwiGLU epilogue with mb <= 4
 hipError_t launch_bwd8(const BwdArgs& a, int mb, int grid, hipStream_t s);
 hipError_t launch_splitk_reduce(const ReduceArgs& a, hipStream_t s);
 

@@ -124,18 +124,18 @@ def test_workspace_sizes():
 
 def test_launch_plans():
     """dk_nf4_linear_plan (host-only): the eight-wave input-gradient kernel serves the MLP's
-    gate/up input gradient at M = 830; SwiGLU-epilogue launches never split and use that kernel
-    only with 4 token blocks; the fused GLU forward never splits; forced plans apply only where
+    gate/up input gradient at M = 830; SwiGLU-epilogue launches never split and use at most 4
+    token blocks; the fused GLU forward never splits; forced plans apply only where
     their kernel may run; bad arguments are reported."""
     from decik_amd import _lib
     from decik_amd.nf4 import launch_plan
 
     gu = launch_plan(True, 830, 1536, [8960, 8960])
     assert gu["kernel"] == "nf4_bwd8_kernel" and gu["splits"] > 1
-    # the SwiGLU epilogue: never split, and in the eight-wave kernel only with 4 token blocks
+    # the SwiGLU epilogue: never split, and only with at most 4 token blocks
     sw = launch_plan(True, 830, 8960, [1536], glu=True)
     assert sw["splits"] == 1
-    assert sw["kernel"] == "nf4_bwd_kernel" or sw["rows_blocks"] == 4
+    assert sw["kernel"] == "nf4_bwd8_kernel" and sw["rows_blocks"] <= 4
     # at most 32 token rows, no LoRA, no GLU epilogue: the small-M kernel, split along the
     # contraction only where the rows cannot fill the GPU
     for m in (1, 2):
@@ -176,11 +176,13 @@ def test_launch_plans():
         # variants that spilled registers are not offered: a forced plan naming one is ignored
         os.environ["DECIK_BWD_PLAN"] = "9,3,8"
         assert launch_plan(True, 830, 1536, [8960])["rows_blocks"] != 9
-        os.environ["DECIK_BWD_PLAN"] = "4,2,8"
-        assert launch_plan(True, 830, 1536, [8960])["kernel"] == "nf4_bwd_kernel"
         os.environ["DECIK_BWD_PLAN"] = "4,2,8,256"
         assert launch_plan(True, 830, 1536, [8960]) == dict(rows_blocks=4, waves=8, splits=2,
                                                              kernel="nf4_bwd8_kernel")
+        # the retired four-wave input-gradient variants are not offered: a forced plan naming one
+        # is ignored
+        os.environ["DECIK_BWD_PLAN"] = "2,1,4"
+        assert launch_plan(True, 830, 1536, [8960])["kernel"] == "nf4_bwd8_kernel"
     finally:
         if old is None:
             os.environ.pop("DECIK_BWD_PLAN", None)

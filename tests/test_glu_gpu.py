@@ -110,7 +110,7 @@ def test_glu_forward_nested_descriptor_takes_two_launches(device, monkeypatch):
 BWD_SHAPES = [(830, 1536, 8960), (64, 264, 256), (17, 96, 128)]  # (M, N, K): W [N, K], dY [M, N]
 
 
-@pytest.mark.parametrize("plan", ["2,1,8", "2,1,4", "4,1,8", "2,1,8,256", "4,1,8,256"])
+@pytest.mark.parametrize("plan", ["2,1,8", "4,1,8"])
 @pytest.mark.parametrize("m,n,k", BWD_SHAPES)
 def test_bwd_swiglu_equals_separate(m, n, k, plan, device, monkeypatch):
     from decik_amd.nf4 import linear_backward, linear_backward_swiglu
