@@ -282,9 +282,9 @@ def bench_dequant(iters, warmup, device, n_layers=8):
 
 def measured_peaks(device):
     """This device's ceilings as measured here: HBM read, write and copy rates of dk_probe_hbm (the
-    dequantization kernel's access pattern: 16-byte lanes, four chunks in flight per thread; stores
-    non-temporal or plain, whichever is faster) over 1 GiB buffers (past the 256 MB Infinity
-    Cache), median of 7; and the
+    dequantization kernel's access pattern: 16-byte lanes; the best of 4, 8 or 16 chunks in flight
+    per thread, non-temporal or plain loads and stores) over 1 GiB buffers (past the 256 MB
+    Infinity Cache), median of 7; and the
     dense fp16 MFMA rate of a register-only loop of v_mfma_f32_32x32x16_f16 (dk_probe_mfma_f16,
     1024 work-groups of 8 waves)."""
     import torch
@@ -298,8 +298,12 @@ def measured_peaks(device):
     dst = torch.empty_like(src)
     sums = torch.zeros(nbytes // 16384 + 1, dtype=torch.float32, device=device)
     rates = {}
-    # write and copy: the better of non-temporal and plain stores (mode + 4)
-    for name, modes, moved in (("read", (0,), nbytes), ("write", (1, 5), nbytes), ("copy", (2, 6), 2 * nbytes)):
+    # the best of the probe's variants: chunks per thread (+ 16, + 32), plain loads (+ 8) and
+    # plain stores (+ 4)
+    var = [u + l for u in (0, 16, 32) for l in (0, 8)]
+    for name, modes, moved in (("read", tuple(v for v in var), nbytes),
+                               ("write", tuple(v + s + 1 for v in (0, 16, 32) for s in (0, 4)), nbytes),
+                               ("copy", tuple(v + s + 2 for v in var for s in (0, 4)), 2 * nbytes)):
         best = 0.0
         for mode in modes:
             times = []
@@ -994,14 +998,20 @@ def main():
                                  for k, v in mlp["uncached_ms"].items()},
     )
     if deq is not None:
+        probe = mixed_ceiling(peaks, deq["read"], deq["write"])
+        roof = dict(bound="hbm", achieved=round(deq["gbs"], 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                    frac=round(deq["gbs"] / HBM_PEAK_GBS, 4), probe_mix_gbs=round(probe, 1))
+        if deq["gbs"] <= probe:
+            roof["frac_of_measured"] = round(deq["gbs"] / probe, 4)
+        else:
+            # the streaming probes do not reach this kernel's own rate: no measured ceiling is claimed
+            roof["note"] = ("the dequantization runs above dk_probe_hbm's rates for its read/write mix "
+                            "(every probe variant, 64 MB to 1 GiB buffers): no measured ceiling is "
+                            "claimed, frac is against the published peak")
         line["dequant"] = dict(value=round(deq["gbs"], 1), unit="GB/s", ms=round(deq["ms"], 4),
                                bytes=deq["bytes"], launches=deq["launches"],
                                workload="all 7 Qwen2.5-1.5B projections x 8 layers per iteration",
-                               roofline=dict(bound="hbm", achieved=round(deq["gbs"], 1),
-                                             peak=HBM_PEAK_GBS, unit="GB/s",
-                                             frac=round(deq["gbs"] / HBM_PEAK_GBS, 4),
-                                             measured_ceiling=round(mixed_ceiling(peaks, deq["read"], deq["write"]), 1),
-                                             frac_of_measured=round(deq["gbs"] / mixed_ceiling(peaks, deq["read"], deq["write"]), 4)))
+                               roofline=roof)
     if c3 is not None:
         line["c3_attention_step"] = c3
     if c4 is not None:

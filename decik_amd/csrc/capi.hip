@@ -1134,7 +1134,7 @@ int dk_swiglu_bwd(const uint16_t* grad, const uint16_t* gate, const uint16_t* up
 int dk_probe_hbm(const void* src, void* dst, int64_t bytes, int mode, float* sums, void* stream) {
     g_error.clear();
     const int kind = mode & 3;
-    if (bytes <= 0 || (bytes % 16) != 0 || mode < 0 || (mode & ~7) != 0 || kind > 2 || bytes / 16 / 1024 >= INT32_MAX ||
+    if (bytes <= 0 || (bytes % 16) != 0 || mode < 0 || (mode & ~63) != 0 || ((mode >> 4) & 3) == 3 || kind > 2 || bytes / 16 / 1024 >= INT32_MAX ||
         (kind != 1 && (src == nullptr || !aligned(src, 16))) || (kind != 0 && (dst == nullptr || !aligned(dst, 16))) ||
         (kind == 0 && sums == nullptr))
         return fail("dk_probe_hbm: bad arguments");

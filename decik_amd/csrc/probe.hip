@@ -44,16 +44,19 @@ hipError_t launch_mfma_peak(int64_t work_groups, int iters, float* out, hipStrea
     return hipGetLastError();
 }
 
-// HBM streaming rate with the access pattern of the dequantization kernel: each thread handles 4
-// 16-byte chunks 4 KB apart (every load or store instruction covers 1 KB contiguous per wave),
-// issues all its loads first, and stores non-temporally (mode bit 4: plain stores). mode 0: read
-// only (one float per work-group is written, so the loads stay); mode 1: write only (fill);
-// mode 2: copy.
-constexpr int kHbmThreads = 256, kHbmUnits = 4;
+// HBM streaming rate with the access pattern of the dequantization kernel: each thread handles
+// UNITS 16-byte chunks 4 KB apart (every load or store instruction covers 1 KB contiguous per
+// wave) and issues all its loads first. mode bits 0-1: 0 read only (one float per work-group is
+// written, so the loads stay), 1 write only (fill), 2 copy; bit 2: plain instead of
+// non-temporal stores; bit 3: plain instead of non-temporal loads; bits 4-5: 4, 8 or 16 chunks
+// per thread. The caller takes the best of the variants as the device's ceiling.
+constexpr int kHbmThreads = 256;
 
+template <int UNITS>
 __global__ __launch_bounds__(kHbmThreads) void hbm_probe_kernel(const u32x4_t* __restrict__ src, u32x4_t* __restrict__ dst,
                                                                 int64_t chunks, int mode, float* __restrict__ sums) {
-    const bool plain = (mode & 4) != 0;
+    constexpr int kHbmUnits = UNITS;
+    const bool plain = (mode & 4) != 0, plain_loads = (mode & 8) != 0;
     mode &= 3;
     const int64_t base = (int64_t)blockIdx.x * kHbmThreads * kHbmUnits + threadIdx.x;
     u32x4_t v[kHbmUnits];
@@ -61,7 +64,8 @@ __global__ __launch_bounds__(kHbmThreads) void hbm_probe_kernel(const u32x4_t* _
 #pragma unroll
         for (int u = 0; u < kHbmUnits; ++u) {
             const int64_t c = base + (int64_t)u * kHbmThreads;
-            v[u] = c < chunks ? __builtin_nontemporal_load(src + c) : u32x4_t{0u, 0u, 0u, 0u};
+            v[u] = c >= chunks ? u32x4_t{0u, 0u, 0u, 0u}
+                               : (plain_loads ? src[c] : __builtin_nontemporal_load(src + c));
         }
     } else {
 #pragma unroll
@@ -84,13 +88,23 @@ __global__ __launch_bounds__(kHbmThreads) void hbm_probe_kernel(const u32x4_t* _
     }
 }
 
-hipError_t launch_hbm_probe(const void* src, void* dst, int64_t bytes, int mode, float* sums, hipStream_t s) {
+template <int UNITS>
+static hipError_t launch_hbm_probe_t(const void* src, void* dst, int64_t bytes, int mode, float* sums, hipStream_t s) {
     const int64_t chunks = bytes / 16;
-    const int64_t per_wg = (int64_t)kHbmThreads * kHbmUnits;
+    const int64_t per_wg = (int64_t)kHbmThreads * UNITS;
     const int64_t grid = (chunks + per_wg - 1) / per_wg;
-    hipLaunchKernelGGL(hbm_probe_kernel, dim3((unsigned)grid), dim3(kHbmThreads), 0, s, (const u32x4_t*)src,
-                       (u32x4_t*)dst, chunks, mode, sums);
+    hipLaunchKernelGGL(hbm_probe_kernel<UNITS>, dim3((unsigned)grid), dim3(kHbmThreads), 0, s, (const u32x4_t*)src,
+                       (u32x4_t*)dst, chunks, mode & 15, sums);
     return hipGetLastError();
+}
+
+hipError_t launch_hbm_probe(const void* src, void* dst, int64_t bytes, int mode, float* sums, hipStream_t s) {
+    switch ((mode >> 4) & 3) {
+        case 0: return launch_hbm_probe_t<4>(src, dst, bytes, mode, sums, s);
+        case 1: return launch_hbm_probe_t<8>(src, dst, bytes, mode, sums, s);
+        case 2: return launch_hbm_probe_t<16>(src, dst, bytes, mode, sums, s);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace dk

@@ -297,11 +297,11 @@ int dk_nf4_linear_plan(int backward, int64_t m, int64_t k, const int64_t* ns, in
 int dk_probe_mfma_f16(int64_t work_groups, int32_t iters, float* out, void* stream);
 
 /* Diagnostic, no counterpart in the reference: this device's HBM streaming rate, with the access
- * pattern of the dequantization kernel (16-byte lanes, four chunks in flight per thread,
- * non-temporal stores). mode 0: read `bytes` of src (sums: one float per 16 KB of src, written
- * only to keep the loads, in practice never); 1: write `bytes` of dst; 2: copy src to dst; + 4:
- * plain instead of non-temporal stores. bytes % 16 == 0, src and dst 16-byte aligned. Allocates
- * nothing. */
+ * pattern of the dequantization kernel (16-byte lanes, every chunk of a thread in flight at
+ * once). mode 0: read `bytes` of src (sums: one float per 16 KB of src, written only to keep the
+ * loads, in practice never); 1: write `bytes` of dst; 2: copy src to dst; + 4: plain instead of
+ * non-temporal stores; + 8: plain instead of non-temporal loads; + 16 / + 32: 8 / 16 chunks per
+ * thread instead of 4. bytes % 16 == 0, src and dst 16-byte aligned. Allocates nothing. */
 int dk_probe_hbm(const void* src, void* dst, int64_t bytes, int mode, float* sums, void* stream);
 
 /* Description of the last error on the calling thread ("" if none). */

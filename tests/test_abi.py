@@ -68,6 +68,10 @@ def test_argument_errors_are_reported():
     assert rc != 0 and b"1..4 groups" in L.dk_last_error()
     rc = L.dk_lora_down(ctypes.c_void_p(16), 8, 64, 64, ctypes.c_void_p(16), 8, ctypes.c_void_p(16), None)
     assert rc != 0 and b"rank" in L.dk_last_error()
+    rc = L.dk_probe_hbm(ctypes.c_void_p(16), ctypes.c_void_p(16), 1024, 2 + 64, ctypes.c_void_p(16), None)
+    assert rc != 0 and b"bad arguments" in L.dk_last_error()  # no such probe variant
+    rc = L.dk_probe_hbm(ctypes.c_void_p(16), ctypes.c_void_p(16), 1024, 2 + 48, ctypes.c_void_p(16), None)
+    assert rc != 0 and b"bad arguments" in L.dk_last_error()
     w = _lib.NF4Weight()
     w.n, w.k, w.blocksize = 8, 64, 64
     rc = L.dk_nf4_dequant(ctypes.byref(w), None, None)
