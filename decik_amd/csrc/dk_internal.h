@@ -7,7 +7,7 @@ namespace dk {
 
 constexpr int kDequantThreads = 256;
 constexpr int kMaxDequantBatch = 24;  // weights per launch (kernel arguments stay < 4 KB)
-constexpr int kDequantUnits = 4;  // packed dwords per thread
+constexpr int kDequantUnits = 8;  // packed dwords per thread
 
 struct DequantArgs {
     NF4Dev w[kMaxDequantBatch];
