@@ -451,7 +451,9 @@ int dk_nf4_linear_plan(int backward, int64_t m, int64_t k, const int64_t* ns, in
         kernel = 3;  // nf4_bwd8_kernel
     } else if (small_m_forward(m, glu, lora) && gemv_requested(m, k)) {
         p = GemmPlan{};
-        p.waves = 4;
+        int64_t nrows = 0;
+        for (int g = 0; g < ngroups; ++g) nrows += ns[g];
+        p.waves = gemv_waves(m, k, nrows);
         p.splits = 1;
         kernel = 4;  // nf4_gemv_kernel
     } else if (small_m_forward(m, glu, lora)) {

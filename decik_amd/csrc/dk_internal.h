@@ -152,6 +152,8 @@ constexpr int kGemvMaxM = 2;  // measured: the MFMA kernels are faster from 3 to
 // this contraction length.
 hipError_t launch_gemv(FwdArgs& a, hipStream_t s);
 bool gemv_fits(int64_t k);
+// waves per work-group of a GEMV launch (k must fit: gemv_fits)
+int gemv_waves(int64_t m, int64_t k, int64_t nrows);
 // Forward launches of few token rows (no LoRA terms, no GLU epilogue): nf4_skinny_kernel. A
 // work-group owns 64 weight rows; a.splits work-groups share them along the contraction, each
 // covering a.ksteps_per_split 128-wide super-steps; g[].tile_begin = each group's first 64-row

@@ -58,9 +58,6 @@ __global__ __launch_bounds__(kDequantThreads) void nf4_dequant_kernel(const Dequ
     const rsrc_t prs = make_rsrc(w.packed + base, span);
     const uint32_t bs_shift = sgpr((uint32_t)w.bs_shift);
     const int64_t blk0 = (2 * base) >> bs_shift;  // first block of the work-group
-    const int64_t nblk = (2 * nbytes + w.blocksize - 1) >> bs_shift;
-    const int64_t blk_left = nblk - blk0;
-    const uint32_t blk_span = (uint32_t)(blk_left < (int64_t)INT32_MAX ? blk_left : INT32_MAX);
     // The work-group's block scales, once per block: thread i computes block blk0 + i (and
     // blk0 + i + 256, ...) into an LDS table, so each unit reads its scale from LDS instead of
     // issuing two global loads of its own. Order: statistics loads, then the packed loads, then

@@ -5,12 +5,13 @@
 // dequantized once and used for every token in fp32 dot products (v_dot2_f32_f16).
 //
 // The kernel is organised around keeping as much of the weight in flight as HBM needs:
-// - A work-group (four waves) owns `rows` consecutive weight rows of one group. Their packed
-//   bytes are contiguous ([n, k / 2] row-major), so the work-group streams one contiguous range
-//   of 16-byte chunks (32 weights of one block each: blocks are powers of two >= 32 and
-//   k % 32 == 0): thread t takes chunks t, t + 256, ..., so every load instruction reads 4 KB
-//   contiguous, and all of a thread's chunk loads (and their block scales) are issued before
-//   any is used -- the whole weight of a 7B projection is in flight at once.
+// - A work-group (four waves; eight where X of long rows would limit a CU to 12 waves) owns
+//   `rows` consecutive weight rows of one group. Their packed bytes are contiguous ([n, k / 2]
+//   row-major), so the work-group streams one contiguous range of 16-byte chunks (32 weights of
+//   one block each: blocks are powers of two >= 32 and k % 32 == 0): thread t of T takes chunks
+//   t, t + T, ..., so every load instruction reads 4 KB contiguous, and all of a thread's chunk
+//   loads (and their block scales) are issued before any is used -- the whole weight of a 7B
+//   projection is in flight at once.
 // - X (m x k fp16) is copied to LDS by the work-group while the weight loads are in flight, in
 //   a transposed order: 16-byte piece e of the 64-byte k-range p of a chunk goes to slot
 //   e * (k / 32) + p, so the lanes of a wave (consecutive chunks, consecutive p) read
@@ -28,6 +29,7 @@ namespace dk {
 
 constexpr int kGemvThreads = 256;  // four waves
 constexpr int kGemvMaxChunks = 8;  // chunks (16-byte loads) per thread
+constexpr size_t kGemvWideLds = 40 * 1024;  // LDS per work-group past which it takes eight waves
 
 // LDS bytes of a launch: code book, X of the token rows, the chunk partial sums
 static size_t gemv_smem_bytes(int mt, int k, int chunks) {
@@ -35,8 +37,8 @@ static size_t gemv_smem_bytes(int mt, int k, int chunks) {
     return 256 * sizeof(float) + (size_t)mt * k * 2 + (size_t)mt * chunks * sizeof(float);
 }
 
-template <int MT, bool NESTED, int CPT>
-__global__ __launch_bounds__(kGemvThreads) void nf4_gemv_kernel(const FwdArgs a, const int rows_per_wg) {
+template <int MT, bool NESTED, int CPT, int TH>
+__global__ __launch_bounds__(TH) void nf4_gemv_kernel(const FwdArgs a, const int rows_per_wg) {
     // byte-pair code book (static: its address is a constant the LDS reads take as an offset)
     __shared__ float2_t lut2[256];
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -64,14 +66,14 @@ __global__ __launch_bounds__(kGemvThreads) void nf4_gemv_kernel(const FwdArgs a,
     // thread, X of every token row straight into LDS (no registers), then the thread's chunk loads
     // and block scales, all issued before any is used; waiting until only the chunk loads are
     // outstanding then covers the code book and X.
-    const float b_hi = W.code[tid >> 4], b_lo = W.code[tid & 15];
-    const float c2v = NESTED ? W.code2[tid] : 0.0f;
+    const float b_hi = W.code[(tid & 255) >> 4], b_lo = W.code[tid & 15];
+    const float c2v = NESTED ? W.code2[tid & 255] : 0.0f;
     const float offset = NESTED ? *W.offset : 0.0f;
     {
         const uint32_t xbytes = (uint32_t)K * 2u;
         for (int m = 0; m < MT; ++m) {
             const rsrc_t xr = make_rsrc(a.x + (int64_t)min(m, M - 1) * a.ldx, m < M ? xbytes : 0u);
-            for (uint32_t o = 1024u * (uint32_t)wave; o < xbytes; o += 4096u)
+            for (uint32_t o = 1024u * (uint32_t)wave; o < xbytes; o += 1024u * (TH / 64))
                 if (o + 16u * (uint32_t)lane < xbytes) {  // rows past m: zeros (descriptor of size 0)
                     // slot s = e * cpr + p holds piece e of k-range p: source bytes 16 (4 p + e)
                     const uint32_t sl = (o >> 4) + (uint32_t)lane, e = sl / (uint32_t)cpr;
@@ -90,7 +92,7 @@ __global__ __launch_bounds__(kGemvThreads) void nf4_gemv_kernel(const FwdArgs a,
     uint32_t q8[CPT];
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-        const int c = tid + kGemvThreads * i;
+        const int c = tid + TH * i;
         const bool ok = c < nch;
         const uint32_t ch = c0 + (uint32_t)c;
         p[i] = bload128(wrs, off_if(ok, ch * 16u));
@@ -107,16 +109,18 @@ __global__ __launch_bounds__(kGemvThreads) void nf4_gemv_kernel(const FwdArgs a,
     // __syncthreads, which would wait for the chunk loads too) then publishes every wave's share
     // of them and of X
     wait_vmcnt<(NESTED ? 3 : 2) * CPT>();
-    lut2[tid] = float2_t{b_hi, b_lo};
-    if constexpr (NESTED) c2[tid] = c2v;
+    if (tid < 256) {
+        lut2[tid] = float2_t{b_hi, b_lo};
+        if constexpr (NESTED) c2[tid] = c2v;
+    }
     lds_barrier();
 
     // k-range p (chunk within its row) of the thread's chunk i: advanced by 256 chunks a step
     int pk = tid % cpr;
-    const int dp = kGemvThreads % cpr;
+    const int dp = TH % cpr;
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-        const int c = tid + kGemvThreads * i;
+        const int c = tid + TH * i;
         float sc = s[i];
         if constexpr (NESTED) sc = c2[q8[i]] * sc + offset;  // two roundings (no contraction)
         const int pc = c < nch ? pk : 0;
@@ -158,7 +162,7 @@ __global__ __launch_bounds__(kGemvThreads) void nf4_gemv_kernel(const FwdArgs a,
     lds_barrier();
 
     // each row's sum in a fixed order: lane l adds slots l, l + 64, ... of the row, then a butterfly
-    for (int r = wave; r < rows; r += kGemvThreads / 64) {
+    for (int r = wave; r < rows; r += TH / 64) {
         float v[MT];
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
@@ -177,10 +181,10 @@ __global__ __launch_bounds__(kGemvThreads) void nf4_gemv_kernel(const FwdArgs a,
     }
 }
 
-// Work-group shape of a launch: `cpt` chunk loads per thread and `rows` rows per work-group
-// (rows * cpr <= 256 cpt).
+// Work-group shape of a launch: `threads` per work-group, `cpt` chunk loads per thread and
+// `rows` rows per work-group (rows * cpr <= threads * cpt).
 struct GemvShape {
-    int cpt, rows;
+    int cpt, rows, threads = kGemvThreads;
 };
 
 // The fewest loads per thread whose rows fill at least 95% of them, else the best fill (4 to 8
@@ -240,31 +244,56 @@ static GemvShape gemv_shape(int k, int64_t nrows, int mt) {
     if (most.cpt == 0) return gemv_shape_bound(k);
     const GemvShape pick = (nrows + most.rows - 1) / most.rows >= 1024 ? most : fewest;
     if (gemv_smem_bytes(mt, k, pick.rows * cpr) > 158 * 1024) return gemv_shape_bound(k);
+    if (gemv_smem_bytes(mt, k, pick.rows * cpr) > kGemvWideLds) {
+        // X of long rows limits the work-groups a CU holds (three four-wave work-groups, 12 waves,
+        // from 40 KB): eight-wave work-groups with at least 4 loads per thread and 85% fill double
+        // the waves per CU for the same LDS. Graph-replayed at one token: 7B down ([3584, 18944])
+        // 19.3-21.2 -> 17.5-18.1 us; the shorter-row shapes gained nothing (their work-groups
+        // already fill the CU's waves).
+        for (int cpt = 4; cpt <= kGemvMaxChunks; ++cpt) {
+            const int rows = 2 * kGemvThreads * cpt / cpr;
+            if (rows < 1 || (double)rows * cpr < 0.85 * 2 * kGemvThreads * cpt) continue;
+            if (gemv_smem_bytes(mt, k, rows * cpr) <= 158 * 1024) return GemvShape{cpt, rows, 2 * kGemvThreads};
+            break;
+        }
+    }
     return pick;
 }
 
-template <int MT, bool NESTED, int CPT>
-static hipError_t launch_gemv_t(const FwdArgs& a, int rows, int grid, hipStream_t s) {
+template <int MT, bool NESTED, int CPT, int TH>
+static hipError_t launch_gemv_th(const FwdArgs& a, int rows, int grid, hipStream_t s) {
     const size_t lds = gemv_smem_bytes(MT, a.k, rows * (a.k >> 5));
-    const hipError_t e = allow_dynamic_lds((const void*)nf4_gemv_kernel<MT, NESTED, CPT>, lds);
+    const hipError_t e = allow_dynamic_lds((const void*)nf4_gemv_kernel<MT, NESTED, CPT, TH>, lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((nf4_gemv_kernel<MT, NESTED, CPT>), dim3(grid), dim3(kGemvThreads), lds, s, a, rows);
+    hipLaunchKernelGGL((nf4_gemv_kernel<MT, NESTED, CPT, TH>), dim3(grid), dim3(TH), lds, s, a, rows);
     return hipGetLastError();
 }
 
+template <int MT, bool NESTED, int CPT>
+static hipError_t launch_gemv_t(const FwdArgs& a, const GemvShape& sh, int grid, hipStream_t s) {
+    if constexpr (CPT >= 4)  // eight-wave shapes take at least 4 loads per thread
+        if (sh.threads == 2 * kGemvThreads) return launch_gemv_th<MT, NESTED, CPT, 2 * kGemvThreads>(a, sh.rows, grid, s);
+    if (sh.threads != kGemvThreads) return hipErrorInvalidValue;
+    return launch_gemv_th<MT, NESTED, CPT, kGemvThreads>(a, sh.rows, grid, s);
+}
+
 template <int MT, bool NESTED>
-static hipError_t launch_gemv_cpt(const FwdArgs& a, int cpt, int rows, int grid, hipStream_t s) {
-    switch (cpt) {
-        case 1: return launch_gemv_t<MT, NESTED, 1>(a, rows, grid, s);
-        case 2: return launch_gemv_t<MT, NESTED, 2>(a, rows, grid, s);
-        case 3: return launch_gemv_t<MT, NESTED, 3>(a, rows, grid, s);
-        case 4: return launch_gemv_t<MT, NESTED, 4>(a, rows, grid, s);
-        case 5: return launch_gemv_t<MT, NESTED, 5>(a, rows, grid, s);
-        case 6: return launch_gemv_t<MT, NESTED, 6>(a, rows, grid, s);
-        case 7: return launch_gemv_t<MT, NESTED, 7>(a, rows, grid, s);
-        case 8: return launch_gemv_t<MT, NESTED, 8>(a, rows, grid, s);
+static hipError_t launch_gemv_cpt(const FwdArgs& a, const GemvShape& sh, int grid, hipStream_t s) {
+    switch (sh.cpt) {
+        case 1: return launch_gemv_t<MT, NESTED, 1>(a, sh, grid, s);
+        case 2: return launch_gemv_t<MT, NESTED, 2>(a, sh, grid, s);
+        case 3: return launch_gemv_t<MT, NESTED, 3>(a, sh, grid, s);
+        case 4: return launch_gemv_t<MT, NESTED, 4>(a, sh, grid, s);
+        case 5: return launch_gemv_t<MT, NESTED, 5>(a, sh, grid, s);
+        case 6: return launch_gemv_t<MT, NESTED, 6>(a, sh, grid, s);
+        case 7: return launch_gemv_t<MT, NESTED, 7>(a, sh, grid, s);
+        case 8: return launch_gemv_t<MT, NESTED, 8>(a, sh, grid, s);
         default: return hipErrorInvalidValue;
     }
+}
+
+int gemv_waves(int64_t m, int64_t k, int64_t nrows) {
+    return gemv_shape((int)k, nrows, (int)m).threads / 64;
 }
 
 // a: the groups' tile_begin fields are overwritten with their first work-group
@@ -281,10 +310,10 @@ hipError_t launch_gemv(FwdArgs& a, hipStream_t s) {
         grid += (int)((a.g[g].w.n + sh.rows - 1) / sh.rows);
     }
     if (a.m == 1)
-        return a.nested ? launch_gemv_cpt<1, true>(a, sh.cpt, sh.rows, grid, s)
-                        : launch_gemv_cpt<1, false>(a, sh.cpt, sh.rows, grid, s);
-    return a.nested ? launch_gemv_cpt<2, true>(a, sh.cpt, sh.rows, grid, s)
-                    : launch_gemv_cpt<2, false>(a, sh.cpt, sh.rows, grid, s);
+        return a.nested ? launch_gemv_cpt<1, true>(a, sh, grid, s)
+                        : launch_gemv_cpt<1, false>(a, sh, grid, s);
+    return a.nested ? launch_gemv_cpt<2, true>(a, sh, grid, s)
+                    : launch_gemv_cpt<2, false>(a, sh, grid, s);
 }
 
 }  // namespace dk

@@ -144,6 +144,10 @@ def test_launch_plans():
     # contraction only where the rows cannot fill the GPU
     for m in (1, 2):
         assert launch_plan(False, m, 3584, [18944])["kernel"] == "nf4_gemv_kernel"
+    # GEMV work-groups: four waves, eight where X of long rows fills the LDS (7B down at one token)
+    assert launch_plan(False, 1, 3584, [18944])["waves"] == 4
+    assert launch_plan(False, 1, 18944, [3584])["waves"] == 8
+    assert launch_plan(False, 1, 8960, [1536])["waves"] == 4
     for m in (3, 8, 32):
         assert launch_plan(False, m, 3584, [18944])["kernel"] == "nf4_skinny_kernel"
     assert launch_plan(False, 8, 3584, [18944])["splits"] == 1

@@ -240,16 +240,17 @@ def test_gemv_short_k_no_bias(m, device, gemv):
 @pytest.mark.parametrize("m", [1, 2])
 def test_gemv_long_k(m, device, monkeypatch):
     """A long contraction (k = 18944, the 7B down projection's: 592 chunks a row, three rows a
-    work-group, X staged whole in LDS; two token rows are sent to the GEMV on purpose, the
-    planner would take the small-M MFMA kernel): 40 rows against the oracle, and the same bits on
-    a second call (the row sums run in a fixed order)."""
+    work-group of eight waves, X staged whole in LDS; two token rows are sent to the GEMV on
+    purpose, the planner would take the small-M MFMA kernel): 40 rows against the oracle, and the
+    same bits on a second call (the row sums run in a fixed order)."""
     import torch
 
     from decik_amd.nf4 import launch_plan, linear_forward
 
     monkeypatch.setenv("DECIK_SMALL_M", "gemv")
     k = 18944
-    assert launch_plan(False, m, k, [40])["kernel"] == "nf4_gemv_kernel"
+    plan = launch_plan(False, m, k, [40])
+    assert plan["kernel"] == "nf4_gemv_kernel" and plan["waves"] == 8
     packed, qs, w16 = make_weight((40, k), seed=150, device=device)
     x = randn16((m, k), seed=151 + m, device=device)
     b = randn16((40,), seed=153, device=device, std=0.1)
