@@ -57,3 +57,86 @@ def test_random_input_gradient(m, n, k, nested, bs, seed, plan, device, monkeypa
     dx = linear_backward([dict(packed=packed, qs=qs, dy=dy)], m, k_in, dx_fp32=True)
     assert_close(dx, O.linear_dx_ref(dy.cpu().numpy(), w16), max_rel=1e-4, mean_rel=1e-5,
                  what=f"bwd m={m} n={n} k={k_in} nested={nested} bs={bs} plan={plan}")
+
+
+# Few token rows (the decoding regime: GEMV at 1-2 rows, the small-M kernel at 3-32, split along
+# the contraction where the rows cannot fill the GPU), with contractions up to 20480 so that X of
+# long rows takes the GEMV's eight-wave work-groups.
+_RNG_S = np.random.default_rng(20261203)
+SMALL = []
+for _i in range(12):
+    m = [1, 2, int(_RNG_S.integers(3, 33))][_i % 3]
+    n = 8 * int(_RNG_S.integers(1, 400))
+    k = 64 * int(_RNG_S.integers(1, 321))
+    nested, bs = [(True, 64), (True, 128), (True, 256), (False, 32)][int(_RNG_S.integers(0, 4))]
+    if k % bs:
+        k = bs * max(1, k // bs)
+    SMALL.append((m, n, k, nested, bs, 8000 + _i))
+# shapes whose X fills the GEMV's LDS (eight-wave work-groups), the 7B down projection among them
+SMALL += [(1, 3584, 18944, True, 64, 8100), (1, 200, 20480, False, 32, 8101), (2, 304, 8192, True, 64, 8102),
+          (1, 136, 16384, True, 128, 8103)]
+
+
+@pytest.mark.parametrize("m,n,k,nested,bs,seed", SMALL)
+def test_random_small_m_forward(m, n, k, nested, bs, seed, device):
+    import torch
+
+    from decik_amd.nf4 import launch_plan, linear_forward
+
+    kernel = launch_plan(False, m, k, [n], blocksize=bs)["kernel"]
+    assert kernel == ("nf4_gemv_kernel" if m <= 2 and (m == 1 or k <= 8192) else "nf4_skinny_kernel")
+    packed, qs, w16 = make_weight((n, k), seed=seed, device=device, nested=nested, blocksize=bs)
+    x = randn16((m, k), seed=seed + 1, device=device)
+    b = randn16((n,), seed=seed + 2, device=device, std=0.1)
+    (y,) = linear_forward(x, [dict(packed=packed, qs=qs, bias=b)])
+    assert_close(y, O.linear_ref(x.cpu().numpy(), w16, b.cpu().numpy()),
+                 what=f"small-m fwd m={m} n={n} k={k} nested={nested} bs={bs} kernel={kernel}")
+    (y2,) = linear_forward(x, [dict(packed=packed, qs=qs, bias=b)])
+    assert torch.equal(y, y2)
+
+
+# The MLP's fused launches (solution/mlp.py:69-71, 95-104) at seeded random shapes with the
+# planner's own plans: gate/up + SwiGLU forward, and the down-projection input gradient with the
+# SwiGLU backward in its epilogue (contractions with k % 64 == 32 included).
+_RNG_G = np.random.default_rng(20261204)
+GLU = []
+for _i in range(8):
+    GLU.append((int(_RNG_G.integers(1, 701)), 8 * int(_RNG_G.integers(1, 200)),
+                64 * int(_RNG_G.integers(1, 40)), 8200 + 10 * _i))
+
+
+@pytest.mark.parametrize("m,n,k,seed", GLU)
+def test_random_glu_forward(m, n, k, seed, device):
+    import torch
+
+    from decik_amd.nf4 import glu_forward
+    from decik_amd.swiglu import swiglu_fwd
+
+    pg, qg, wg = make_weight((n, k), seed=seed, device=device)
+    pu, qu, wu = make_weight((n, k), seed=seed + 1, device=device)
+    x = randn16((m, k), seed=seed + 2, device=device)
+    bg = randn16((n,), seed=seed + 3, device=device, std=0.1)
+    bu = randn16((n,), seed=seed + 4, device=device, std=0.1)
+    g, u, h = glu_forward(x, dict(packed=pg, qs=qg, bias=bg), dict(packed=pu, qs=qu, bias=bu))
+    xn = x.cpu().numpy()
+    assert_close(g, O.linear_ref(xn, wg, bg.cpu().numpy()), what=f"gate m={m} n={n} k={k}")
+    assert_close(u, O.linear_ref(xn, wu, bu.cpu().numpy()), what=f"up m={m} n={n} k={k}")
+    assert torch.equal(h, swiglu_fwd(g, u))
+
+
+@pytest.mark.parametrize("m,n,k,seed", GLU)
+def test_random_bwd_swiglu(m, n, k, seed, device):
+    import torch
+
+    from decik_amd.nf4 import linear_backward_swiglu
+
+    k_in = k - 32 if k > 64 and (seed // 10) % 2 else k  # W [n, k_in]: the down projection
+    packed, qs, w16 = make_weight((n, k_in), seed=seed + 5, device=device)
+    dy = randn16((m, n), seed=seed + 6, device=device, std=1e-2)
+    gate = randn16((m, k_in), seed=seed + 7, device=device)
+    up = randn16((m, k_in), seed=seed + 8, device=device)
+    dg, du = linear_backward_swiglu(dict(packed=packed, qs=qs, dy=dy), gate, up)
+    dh = torch.from_numpy(O.linear_dx_ref(dy.cpu().numpy(), w16)).half().numpy()
+    dg_ref, du_ref = O.swiglu_bwd_ref(dh, gate.cpu().numpy(), up.cpu().numpy())
+    assert_close(dg, dg_ref, what=f"dgate m={m} n={n} k={k_in}")
+    assert_close(du, du_ref, what=f"dup m={m} n={n} k={k_in}")
