@@ -125,11 +125,20 @@ struct VariantCost {
 
 constexpr double kPartialUsPerMB = 0.36;  // split-K: partial slabs written, then read and summed
 constexpr double kReduceLaunchUs = 4.0;   // split-K: the reduction launch
+// Forward split-K with few outputs: the reduction is a few thousand threads, each adding its
+// outputs' splits in order, so every split lengthens a chain of dependent loads -- a cost per
+// split that the slab bytes miss. Graph-replayed forwards at 33-512 tokens (7B q/o, k/v, qkv;
+// 1.5B o, down; splits 2..28) fit 0.26 us per split; with it the plans of launches of at most
+// 300K outputs split 2-4x less and run 3-20% faster. Larger reductions fill the GPU (the term
+// made them pick smaller tiles and run up to 28% slower), and input-gradient launches with few
+// work-groups are slower unsplit than the model says, so neither takes the term.
+constexpr double kSplitUs = 0.26;
+constexpr int64_t kSmallReduceOutputs = 300000;
 constexpr int kRowUnit = 32;              // token rows per row block
 
 // col_tiles: output column tiles of the launch for this variant's tile width.
 double plan_time(const VariantCost& v, int64_t m, int64_t col_tiles, int64_t ncols, int steps,
-                 int splits) {
+                 int splits, bool split_chain) {
     const int64_t rows = (int64_t)kRowUnit * v.rows_blocks;
     const int64_t tiles = ((m + rows - 1) / rows) * col_tiles;
     const int64_t slots = (int64_t)num_cus() * v.per_cu;
@@ -145,6 +154,7 @@ double plan_time(const VariantCost& v, int64_t m, int64_t col_tiles, int64_t nco
         t += per * v.step_us * v.lone;
     }
     if (splits > 1) t += (double)splits * m * ncols * 4.0 * 1e-6 * kPartialUsPerMB + kReduceLaunchUs;
+    if (splits > 1 && split_chain && m * ncols <= kSmallReduceOutputs) t += splits * kSplitUs;
     return t;
 }
 
@@ -155,7 +165,8 @@ double plan_time(const VariantCost& v, int64_t m, int64_t col_tiles, int64_t nco
 template <typename ColTiles>
 const VariantCost* choose_plan(const VariantCost* vs, int nv, int64_t m, int64_t ncols, int steps,
                                ColTiles col_tiles_of, int* splits, int max_splits = 32,
-                               int64_t max_partial_bytes = INT64_MAX, int min_splits = 1) {
+                               int64_t max_partial_bytes = INT64_MAX, int min_splits = 1,
+                               bool split_chain = false) {
     double best = 1e300;
     const VariantCost* pick = &vs[0];
     *splits = 1;
@@ -166,7 +177,7 @@ const VariantCost* choose_plan(const VariantCost* vs, int nv, int64_t m, int64_t
             const int per = steps > 0 ? (steps + s - 1) / s : 0;
             if (steps > 0 && (steps + per - 1) / per != s) continue;  // s splits must all get work
             if (s > 1 && (double)s * m * ncols * 4.0 > (double)max_partial_bytes) continue;
-            const double t = plan_time(v, m, col_tiles_of(v), ncols, steps, s);
+            const double t = plan_time(v, m, col_tiles_of(v), ncols, steps, s, split_chain);
             if (t < best * 0.999) {
                 best = t;
                 pick = &v;
@@ -273,7 +284,7 @@ GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool glu
     if (v == nullptr) {
         const int64_t nt = p.n_tiles;
         v = choose_plan(kFwdVariants, nv, m, ncols, p.steps, [nt](const VariantCost&) { return nt; },
-                        &p.splits, (glu || no_split) ? 1 : 32, INT64_MAX, min_splits);
+                        &p.splits, (glu || no_split) ? 1 : 32, INT64_MAX, min_splits, true);
     }
     p.mt = v->rows_blocks;
     p.waves = v->waves;

@@ -144,6 +144,10 @@ def test_launch_plans():
     # contraction only where the rows cannot fill the GPU
     for m in (1, 2):
         assert launch_plan(False, m, 3584, [18944])["kernel"] == "nf4_gemv_kernel"
+    # forward split-K with few outputs: each split lengthens the reduction's chain of dependent
+    # loads, so these split less than the slab bytes alone would have them (7B k/v, q/o at 64 tokens)
+    assert launch_plan(False, 64, 3584, [512])["splits"] == 14
+    assert launch_plan(False, 64, 3584, [3584])["splits"] == 8
     # GEMV work-groups: four waves, eight where X of long rows fills the LDS (7B down at one token)
     assert launch_plan(False, 1, 3584, [18944])["waves"] == 4
     assert launch_plan(False, 1, 18944, [3584])["waves"] == 8
