@@ -10,6 +10,27 @@ namespace dk {
 
 constexpr int kReduceThreads = 256;
 
+// Sum of the split slabs at C (2 or 4) consecutive columns of one row, in split order: the
+// narrow form for reductions too small to fill the GPU at 8 columns a thread.
+template <int C>
+__device__ __forceinline__ void sum_splits_n(const ReduceArgs& a, const float* base, int col, float (&v)[C]) {
+    using vec_t = float __attribute__((ext_vector_type(C)));
+    constexpr int kBatch = 16;  // splits whose loads are in flight together
+#pragma unroll
+    for (int e = 0; e < C; ++e) v[e] = 0.0f;
+    for (int s0 = 0; s0 < a.splits; s0 += kBatch) {
+        vec_t l[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u)
+            if (s0 + u < a.splits) l[u] = *(const vec_t*)(base + (int64_t)(s0 + u) * a.slab + col);
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u)
+            if (s0 + u < a.splits)
+#pragma unroll
+                for (int e = 0; e < C; ++e) v[e] += l[u][e];
+    }
+}
+
 // Sum of the split slabs at 8 consecutive columns of one row, in split order.
 __device__ __forceinline__ void sum_splits(const ReduceArgs& a, const float* base, int col, float4_t& v0, float4_t& v1) {
     constexpr int kBatch = 16;  // splits whose loads are in flight together
@@ -126,9 +147,50 @@ __global__ __launch_bounds__(kReduceThreads) void splitk_reduce_kernel(const Red
     }
 }
 
+// The same sums with C columns a thread (no RoPE epilogue): each output adds its splits in the
+// same order as in splitk_reduce_kernel, so the bits are the same.
+template <int C>
+__global__ __launch_bounds__(kReduceThreads) void splitk_reduce_narrow_kernel(const ReduceArgs a) {
+    const int chunks = a.ncols / C;
+    const int64_t item = (int64_t)blockIdx.x * kReduceThreads + threadIdx.x;
+    if (item >= (int64_t)a.m * chunks) return;
+    const int row = (int)(item / chunks);
+    const int col = (int)(item - (int64_t)row * chunks) * C;
+    int g = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxGroups; ++i)
+        if (i < a.nout && col >= a.o[i].col_begin) g = i;
+    const ReduceOut& o = a.o[g];
+    const int oc = col - o.col_begin;  // groups start at multiples of 8: a chunk lies in one group
+    float v[C];
+    sum_splits_n<C>(a, a.partials + (int64_t)row * a.ncols, col, v);
+    if (o.bias != nullptr)
+#pragma unroll
+        for (int e = 0; e < C; ++e) v[e] += (float)o.bias[oc + e];
+    if (a.out_fp32) {
+        float* dst = (float*)o.out + (int64_t)row * o.ld + oc;
+#pragma unroll
+        for (int e = 0; e < C; ++e) dst[e] = v[e];
+    } else {
+        uint32_t* dst = (uint32_t*)((_Float16*)o.out + (int64_t)row * o.ld + oc);
+#pragma unroll
+        for (int e = 0; e < C; e += 2) dst[e >> 1] = pack_half2(v[e], v[e + 1]);
+    }
+}
+
+// Reductions of fewer chunks than this run the narrow kernel (a quarter of the columns a thread,
+// four times the threads): below it the eight-column kernel leaves most CUs idle.
+constexpr int64_t kNarrowReduceChunks = 256 * kReduceThreads;
+
 hipError_t launch_splitk_reduce(const ReduceArgs& a, hipStream_t s) {
     if (a.m <= 0 || a.ncols <= 0) return hipSuccess;
     const int64_t items = (int64_t)a.m * (a.ncols >> 3);
+    if (a.rope_mask == 0 && items < kNarrowReduceChunks) {
+        const int64_t n2 = items * 4;
+        hipLaunchKernelGGL(splitk_reduce_narrow_kernel<2>, dim3((unsigned)((n2 + kReduceThreads - 1) / kReduceThreads)),
+                           dim3(kReduceThreads), 0, s, a);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((items + kReduceThreads - 1) / kReduceThreads)),
                        dim3(kReduceThreads), 0, s, a);
     return hipGetLastError();
