@@ -329,12 +329,18 @@ GemmPlan plan_skinny(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
         ncols += ns[g];
     }
     p.steps = (int)((k + kSkinnyStep - 1) / kSkinnyStep);
-    // split the contraction while the work-groups still fit one per CU and every split keeps at
-    // least one super-step per wave
+    // split the contraction as far as the work-groups still fit one per CU and every split keeps
+    // at least two super-steps (all splits non-empty). Weights of few row groups (k/v) gain most
+    // from the extra work-groups pulling them: graph-replayed forced splits at 8 and 24 tokens,
+    // 7B k/v 10.4 / 12.4 us at 3 splits (the earlier rule: one super-step per wave, 8 a split)
+    // -> 8.4 / 9.7 at 12, 7B q/o 11.9 / 14.0 at 3 -> 11.2 / 13.2 at 4, 1.5B q/o and k/v 10%
+    // faster at 24 tokens with 6 splits than unsplit; the wide weights (7B gate, 1.5B gate) stay
+    // unsplit
     p.splits = 1;
-    while (p.splits < 32 && rgroups * (p.splits + 1) <= num_cus() &&
-           (p.steps + p.splits) / (p.splits + 1) >= kSkinnyWaves)
-        ++p.splits;
+    for (int s = 2; s <= 32 && s <= p.steps / 2 && rgroups * s <= num_cus(); ++s) {
+        const int per = (p.steps + s - 1) / s;
+        if ((p.steps + per - 1) / per == s) p.splits = s;
+    }
     p.n_tiles = (int)rgroups;
     p.m_tiles = 1;
     p.mt = m <= 16 ? 1 : 2;

@@ -156,6 +156,8 @@ def test_launch_plans():
         assert launch_plan(False, m, 3584, [18944])["kernel"] == "nf4_skinny_kernel"
     assert launch_plan(False, 8, 3584, [18944])["splits"] == 1
     assert launch_plan(False, 8, 18944, [3584])["splits"] > 1
+    # few row groups (7B k/v: 8 groups of 64 rows, 28 super-steps): split down to two super-steps
+    assert launch_plan(False, 8, 3584, [512])["splits"] == 14
     assert launch_plan(False, 33, 3584, [18944])["kernel"] != "nf4_skinny_kernel"
     assert launch_plan(False, 1, 3584, [18944], lora=True)["kernel"] not in ("nf4_skinny_kernel", "nf4_gemv_kernel")
     old_sm = os.environ.get("DECIK_SMALL_M")
