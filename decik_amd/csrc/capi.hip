@@ -365,8 +365,10 @@ bool gemv_requested(int64_t m, int64_t k) {
     const char* v = std::getenv("DECIK_SMALL_M");
     if (v != nullptr && std::string(v) == "gemv") return true;
     if (v != nullptr && std::string(v) == "skinny") return false;
-    // two rows of a long contraction (7B down): the skinny kernel's split is faster (24 vs 31 us)
-    return m == 1 || k <= 8192;
+    // two rows of a long contraction: the small-M kernel's split is faster for the 7B down
+    // projection (k = 18944: 23.7 vs 35.1 us graph-replayed), the GEMV for the 1.5B one (k = 8960:
+    // 8.6 vs 10.8 us)
+    return m == 1 || k <= 12288;
 }
 
 
