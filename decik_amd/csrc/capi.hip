@@ -355,10 +355,19 @@ GemmPlan plan_skinny(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
 // 18 us against 25, q/o 10 against 16), and at two rows on all but the long contraction of down;
 // from 3 rows on the skinny kernel wins (7B gate at 8 rows: 28 us against 39 for the MFMA
 // kernels). DECIK_SMALL_M = gemv / skinny forces one of them for launches both may take.
-bool small_m_forward(int64_t m, bool glu, bool lora) {
+// Past 16 rows (two 16-token blocks a work-group), weights of more 64-row groups than CUs go to
+// the MFMA kernels: the skinny kernel's second round then holds few work-groups (7B gate, 296
+// groups: 38.8 / 39.6 us at 24 / 32 rows against 34.2 / 34.9 on 64-token MFMA tiles).
+bool small_m_forward(int64_t m, bool glu, bool lora, const int64_t* ns, int ngroups) {
     if (glu || lora || m < 1 || m > kSkinnyMaxM) return false;
     const char* forced = std::getenv("DECIK_FWD_PLAN");
-    return forced == nullptr || *forced == 0;
+    if (forced != nullptr && *forced != 0) return false;
+    if (m > 16) {
+        int64_t rgroups = 0;
+        for (int g = 0; g < ngroups; ++g) rgroups += (ns[g] + kSkinnyRows - 1) / kSkinnyRows;
+        if (rgroups > num_cus()) return false;
+    }
+    return true;
 }
 bool gemv_requested(int64_t m, int64_t k) {
     if (m > kGemvMaxM || !gemv_fits(k)) return false;
@@ -449,7 +458,7 @@ int dk_nf4_block_scales(const dk_nf4_weight* w, float* scales, void* stream) {
 
 int64_t dk_nf4_linear_fwd_workspace(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
     if (ngroups < 1 || ngroups > kMaxGroups || ns == nullptr || m <= 0 || k <= 0) return 0;
-    if (small_m_forward(m, false, false)) return workspace_bytes(plan_skinny(m, k, ns, ngroups));
+    if (small_m_forward(m, false, false, ns, ngroups)) return workspace_bytes(plan_skinny(m, k, ns, ngroups));
     // the plan also depends on the block sizes (eight-wave kernel or not): cover both
     return std::max(workspace_bytes(plan_fwd(m, k, ns, ngroups, false, true)),
                     workspace_bytes(plan_fwd(m, k, ns, ngroups, false, false)));
@@ -468,14 +477,14 @@ int dk_nf4_linear_plan(int backward, int64_t m, int64_t k, const int64_t* ns, in
     if (backward) {
         p = plan_bwd(m, k, ns, ngroups, glu, single);
         kernel = 3;  // nf4_bwd8_kernel
-    } else if (small_m_forward(m, glu, lora) && gemv_requested(m, k)) {
+    } else if (small_m_forward(m, glu, lora, ns, ngroups) && gemv_requested(m, k)) {
         p = GemmPlan{};
         int64_t nrows = 0;
         for (int g = 0; g < ngroups; ++g) nrows += ns[g];
         p.waves = gemv_waves(m, k, nrows);
         p.splits = 1;
         kernel = 4;  // nf4_gemv_kernel
-    } else if (small_m_forward(m, glu, lora)) {
+    } else if (small_m_forward(m, glu, lora, ns, ngroups)) {
         p = plan_skinny(m, k, ns, ngroups);
         kernel = 5;  // nf4_skinny_kernel
     } else {
@@ -579,7 +588,7 @@ static int linear_fwd_impl(const std::string& name, const uint16_t* x, int64_t m
     if ((m - 1) * ldx + k >= INT32_MAX / 2) return fail(name + ": x too large");
     bool any_lora = false;
     for (int g = 0; g < ngroups; ++g) any_lora = any_lora || groups[g].lora_u != nullptr;
-    if (rope == nullptr && small_m_forward(m, glu, any_lora)) {
+    if (rope == nullptr && small_m_forward(m, glu, any_lora, ns, ngroups)) {
         // few token rows, no LoRA terms: one pass over the packed weights
         a.x = reinterpret_cast<const _Float16*>(x);
         a.ldx = ldx;

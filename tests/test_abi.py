@@ -152,8 +152,11 @@ def test_launch_plans():
     assert launch_plan(False, 1, 3584, [18944])["waves"] == 4
     assert launch_plan(False, 1, 18944, [3584])["waves"] == 8
     assert launch_plan(False, 1, 8960, [1536])["waves"] == 4
-    for m in (3, 8, 32):
+    for m in (3, 8, 16):
         assert launch_plan(False, m, 3584, [18944])["kernel"] == "nf4_skinny_kernel"
+    # past 16 rows, a weight of more 64-row groups than CUs (7B gate: 296) takes the MFMA kernel
+    assert launch_plan(False, 32, 3584, [18944])["kernel"] == "nf4_fwd8_kernel"
+    assert launch_plan(False, 32, 18944, [3584])["kernel"] == "nf4_skinny_kernel"
     assert launch_plan(False, 8, 3584, [18944])["splits"] == 1
     assert launch_plan(False, 8, 18944, [3584])["splits"] > 1
     # few row groups (7B k/v: 8 groups of 64 rows, 28 super-steps): split down to two super-steps

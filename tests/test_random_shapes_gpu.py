@@ -84,7 +84,10 @@ def test_random_small_m_forward(m, n, k, nested, bs, seed, device):
     from decik_amd.nf4 import launch_plan, linear_forward
 
     kernel = launch_plan(False, m, k, [n], blocksize=bs)["kernel"]
-    assert kernel == ("nf4_gemv_kernel" if m <= 2 and (m == 1 or k <= 12288) else "nf4_skinny_kernel")
+    if m <= 2 and (m == 1 or k <= 12288):
+        assert kernel == "nf4_gemv_kernel"
+    else:
+        assert kernel == ("nf4_fwd8_kernel" if m > 16 and (n + 63) // 64 > 256 else "nf4_skinny_kernel")
     packed, qs, w16 = make_weight((n, k), seed=seed, device=device, nested=nested, blocksize=bs)
     x = randn16((m, k), seed=seed + 1, device=device)
     b = randn16((n,), seed=seed + 2, device=device, std=0.1)
