@@ -458,10 +458,13 @@ int dk_nf4_block_scales(const dk_nf4_weight* w, float* scales, void* stream) {
 
 int64_t dk_nf4_linear_fwd_workspace(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
     if (ngroups < 1 || ngroups > kMaxGroups || ns == nullptr || m <= 0 || k <= 0) return 0;
-    if (small_m_forward(m, false, false, ns, ngroups)) return workspace_bytes(plan_skinny(m, k, ns, ngroups));
-    // the plan also depends on the block sizes (eight-wave kernel or not): cover both
-    return std::max(workspace_bytes(plan_fwd(m, k, ns, ngroups, false, true)),
-                    workspace_bytes(plan_fwd(m, k, ns, ngroups, false, false)));
+    // the plan also depends on the block sizes (eight-wave kernel or not) and, for few token rows,
+    // on LoRA terms (which keep such launches off the small-M kernel): cover every case
+    const int64_t tiled = std::max(workspace_bytes(plan_fwd(m, k, ns, ngroups, false, true)),
+                                   workspace_bytes(plan_fwd(m, k, ns, ngroups, false, false)));
+    if (small_m_forward(m, false, false, ns, ngroups))
+        return std::max(tiled, workspace_bytes(plan_skinny(m, k, ns, ngroups)));
+    return tiled;
 }
 
 int dk_nf4_linear_plan(int backward, int64_t m, int64_t k, const int64_t* ns, int ngroups, int flags,

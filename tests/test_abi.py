@@ -148,6 +148,11 @@ def test_launch_plans():
     # loads, so these split less than the slab bytes alone would have them (7B k/v, q/o at 64 tokens)
     assert launch_plan(False, 64, 3584, [512])["splits"] == 14
     assert launch_plan(False, 64, 3584, [3584])["splits"] == 8
+    # the forward workspace query covers launches of few rows with LoRA terms (tiled, split plans)
+    for m, k, ns in ((8, 3584, [18944]), (8, 1536, [8960]), (24, 3584, [3584])):
+        plan = launch_plan(False, m, k, ns, lora=True)
+        arr = (ctypes.c_int64 * len(ns))(*ns)
+        assert _lib.lib().dk_nf4_linear_fwd_workspace(m, k, arr, len(ns)) >= plan["splits"] * m * sum(ns) * 4
     # GEMV work-groups: four waves, eight where X of long rows fills the LDS (7B down at one token)
     assert launch_plan(False, 1, 3584, [18944])["waves"] == 4
     assert launch_plan(False, 1, 18944, [3584])["waves"] == 8

@@ -35,6 +35,24 @@ def test_lengths_sum():
     assert lens.sum() == 830 and lens.min() >= 32 and lens.max() <= 200
 
 
+@pytest.mark.parametrize("m,n,k", [(8, 8960, 1536), (24, 3584, 3584)])
+def test_nf4_lora_linear_few_rows(m, n, k, device):
+    """Few token rows with LoRA terms: such launches stay off the small-M kernel and run split
+    MFMA plans, whose workspace the size query must cover (it cannot see the LoRA terms)."""
+    from decik_amd.lora import NF4LoRALinear
+    from decik_amd.nf4 import launch_plan
+
+    assert launch_plan(False, m, k, [n], lora=True)["splits"] > 1
+    packed, qs, w16 = make_weight((n, k), seed=n + m, device=device)
+    bias = randn16((n,), seed=5, device=device, std=0.1)
+    a, b = adapters(n, k, seed=6, device=device)
+    x = randn16((m, k), seed=7, device=device)
+    y = NF4LoRALinear.apply(x, packed, bias, qs, a.float(), b.float(), 2.0)
+    xn = x.cpu().numpy()
+    _, lora = O.lora_fwd_ref(xn, a.cpu().numpy(), b.cpu().numpy(), 2.0)
+    assert_close(y, O.linear_ref(xn, w16, bias.cpu().numpy()) + lora, what=f"Y m={m} n={n}")
+
+
 @pytest.mark.parametrize("n", [1536, 256])
 def test_nf4_lora_linear(n, device):
     from decik_amd.lora import NF4LoRALinear
