@@ -121,9 +121,10 @@ int dk_nf4_dequant_batched(const dk_nf4_weight* ws, uint16_t* const* outs, int c
  * absmax2 chain), so a caller may compute it once per frozen weight and reuse it. */
 int dk_nf4_block_scales(const dk_nf4_weight* w, float* scales, void* stream);
 
-/* Bytes of workspace dk_nf4_linear_fwd needs for these shapes (0 if none): the fp32 partial
- * sums of a split contraction. Its contents need not be initialised and are dead after the
- * call. Calls that run concurrently (different streams) need different workspaces. */
+/* Bytes of workspace dk_nf4_linear_fwd needs for these shapes (0 if none), whatever the block
+ * sizes, statistics form and LoRA terms of the call: the fp32 partial sums of a split
+ * contraction. Its contents need not be initialised and are dead after the call. Calls that run
+ * concurrently (different streams) need different workspaces. */
 int64_t dk_nf4_linear_fwd_workspace(int64_t m, int64_t k, const int64_t* ns, int ngroups);
 
 /* Fused dequant x fp16 GEMM, forward, for up to DK_MAX_GROUPS weights that share X
