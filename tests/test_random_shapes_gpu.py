@@ -143,3 +143,30 @@ def test_random_bwd_swiglu(m, n, k, seed, device):
     dg_ref, du_ref = O.swiglu_bwd_ref(dh, gate.cpu().numpy(), up.cpu().numpy())
     assert_close(dg, dg_ref, what=f"dgate m={m} n={n} k={k_in}")
     assert_close(du, du_ref, what=f"dup m={m} n={n} k={k_in}")
+
+
+@pytest.mark.parametrize("dx", [False, True])
+def test_narrow_reduction_same_bits(dx, device, monkeypatch):
+    """The split-K reduction of small launches (two columns a thread) sums every output's splits
+    in the same order as the eight-column reduction of large ones: under one forced plan, the
+    first 64 token rows of a 512-row launch (eight-column reduction) equal a 64-row launch of the
+    same rows (two-column reduction) bit for bit, forward (fp16 out, bias) and input gradient
+    (fp32 out)."""
+    import torch
+
+    from decik_amd.nf4 import linear_backward, linear_forward
+
+    n, k = 2048, 1024
+    packed, qs, _ = make_weight((n, k), seed=8300, device=device)
+    if not dx:
+        monkeypatch.setenv("DECIK_FWD_PLAN", "2,4,8")
+        x = randn16((512, k), seed=8301, device=device)
+        b = randn16((n,), seed=8302, device=device, std=0.1)
+        (big,) = linear_forward(x, [dict(packed=packed, qs=qs, bias=b)])
+        (small,) = linear_forward(x[:64].contiguous(), [dict(packed=packed, qs=qs, bias=b)])
+    else:
+        monkeypatch.setenv("DECIK_BWD_PLAN", "2,4,8")
+        dy = randn16((512, n), seed=8303, device=device, std=1e-2)
+        big = linear_backward([dict(packed=packed, qs=qs, dy=dy)], 512, k, dx_fp32=True)
+        small = linear_backward([dict(packed=packed, qs=qs, dy=dy[:64].contiguous())], 64, k, dx_fp32=True)
+    assert torch.equal(big[:64], small)
