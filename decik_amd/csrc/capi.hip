@@ -173,7 +173,7 @@ const VariantCost* choose_plan(const VariantCost* vs, int nv, int64_t m, int64_t
     for (int i = 0; i < nv; ++i) {
         const VariantCost& v = vs[i];
         const int max_s = steps < max_splits ? steps : max_splits;
-        for (int s = min_splits < max_s ? min_splits : 1; s <= (max_s > 0 ? max_s : 1); ++s) {
+        for (int s = min_splits <= max_s ? min_splits : 1; s <= (max_s > 0 ? max_s : 1); ++s) {
             const int per = steps > 0 ? (steps + s - 1) / s : 0;
             if (steps > 0 && (steps + per - 1) / per != s) continue;  // s splits must all get work
             if (s > 1 && (double)s * m * ncols * 4.0 > (double)max_partial_bytes) continue;
@@ -317,11 +317,11 @@ GemmPlan plan_bwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool swi
     return p;
 }
 
-// nf4_skinny_kernel (forward, m <= kSkinnyMaxM): 64-row groups; contraction splits so that the
-// launch has at least two work-groups per CU, while every split keeps at least two 128-wide
-// super-steps per wave (16 per work-group).
+// nf4_skinny_kernel (forward, m <= kSkinnyMaxM): 64-row groups; contraction splits while the
+// launch still has at most one work-group per CU and every split keeps at least two 128-wide
+// super-steps per wave (16 per work-group). no_split: a single pass (no workspace).
 constexpr int kSkinnyRows = 64, kSkinnyStep = 128, kSkinnyWaves = 8;
-GemmPlan plan_skinny(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
+GemmPlan plan_skinny(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool no_split = false) {
     GemmPlan p{};
     int64_t rgroups = 0, ncols = 0;
     for (int g = 0; g < ngroups; ++g) {
@@ -337,7 +337,7 @@ GemmPlan plan_skinny(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
     // faster at 24 tokens with 6 splits than unsplit; the wide weights (7B gate, 1.5B gate) stay
     // unsplit
     p.splits = 1;
-    for (int s = 2; s <= 32 && s <= p.steps / 2 && rgroups * s <= num_cus(); ++s) {
+    for (int s = 2; !no_split && s <= 32 && s <= p.steps / 2 && rgroups * s <= num_cus(); ++s) {
         const int per = (p.steps + s - 1) / s;
         if ((p.steps + per - 1) / per == s) p.splits = s;
     }
@@ -488,7 +488,7 @@ int dk_nf4_linear_plan(int backward, int64_t m, int64_t k, const int64_t* ns, in
         p.splits = 1;
         kernel = 4;  // nf4_gemv_kernel
     } else if (small_m_forward(m, glu, lora, ns, ngroups)) {
-        p = plan_skinny(m, k, ns, ngroups);
+        p = plan_skinny(m, k, ns, ngroups, single);
         kernel = 5;  // nf4_skinny_kernel
     } else {
         p = plan_fwd(m, k, ns, ngroups, glu, k % 64 == 0 && k % blocksize == 0, single);
@@ -604,7 +604,7 @@ static int linear_fwd_impl(const std::string& name, const uint16_t* x, int64_t m
         if (ncols > INT32_MAX / 2) return fail(name + ": problem too large");
         const hipStream_t st = static_cast<hipStream_t>(stream);
         if (gemv_requested(m, k)) return check_hip(launch_gemv(a, st), "dk_nf4_linear_fwd GEMV launch");
-        const GemmPlan p = plan_skinny(m, k, ns, ngroups);
+        const GemmPlan p = plan_skinny(m, k, ns, ngroups, no_split);
         const int64_t need = workspace_bytes(p);
         if (need > 0 && (workspace == nullptr || workspace_bytes_ < need || !aligned(workspace, 256)))
             return fail(name + ": workspace too small (need " + std::to_string(need) + " bytes)");

@@ -125,123 +125,132 @@ def lora_up(gu16, a16):
     return out
 
 
-class LoRAPair(torch.autograd.Function):
-    """The q and v LoRA branches with dropout, lora_B(lora_A(dropout(x))) * scaling each, as
-    LoRAPairFromNorm computes them on its packed-mask path (solution/attn.py:206-273): the masks
-    are kept packed to bits and backward rebuilds the dropped-out inputs from x. (The reference
-    rebuilds x itself from the RMSNorm input; here x is saved.) x: [.., W] fp16 or fp32;
-    bits_*: packed keep-masks; scale_*: fp32 device scalars 1/(1-p); a_* [r, W], b_* [N, r]
-    adapter weights (used in fp16); returns (out_q, out_v) fp16."""
+class _QVDropout:
+    """Dropout of the q and v LoRA branch inputs, in either form the reference accepts
+    (solution/attn.py:206-273), as data for one implementation of the pair:
 
-    @staticmethod
-    def forward(ctx, x, bits_q, scale_q, bits_v, scale_v, a_q, b_q, a_v, b_v, scaling_q, scaling_v,
-                p_q, p_v):
-        inputs = lora_inputs(x, bits_q, bits_v, scale_q, scale_v)
-        outs, us = [], []
-        for x16, a, b, s in zip(inputs, (a_q, a_v), (b_q, b_v), (scaling_q, scaling_v)):
-            a16 = a.to(torch.float16).contiguous()
-            u = lora_down(x16, a16)
-            # fp16(u . B^T) (the rank-r up product), then * scaling in fp16 as torch scales
-            up = lora_up(u, b.to(torch.float16).t().contiguous())
-            outs.append(up * s)
-            us.append(u)
-        ctx.save_for_backward(x, bits_q, scale_q, bits_v, scale_v, us[0], us[1], a_q, b_q, a_v, b_v)
-        ctx.scalings, ctx.ps = (scaling_q, scaling_v), (p_q, p_v)
-        shape = x.shape[:-1]
-        return outs[0].reshape(*shape, -1), outs[1].reshape(*shape, -1)
+    packed: keep bits [T, W / 8] per branch (pack_keep) with fp32 device scalars 1 / (1 - p);
+        one HIP pass forms fp16(x * (keep * scale)) of both branches (dk_lora_dropout_inputs, the
+        same kernel forward and backward) and one the fp32 input gradient through both masks
+        (dk_lora_input_grad, (g * keep) * 1/(1 - p) per branch, q's plus v's).
+    elementwise: per branch an x-shaped fp32 tensor for the forward (the dropout output of ones)
+        and a mask with its kept value for the backward, or None for a branch without dropout;
+        plain torch ops on the GPU with the reference's operation order."""
 
-    @staticmethod
-    def backward(ctx, grad_q, grad_v):
-        x, bits_q, scale_q, bits_v, scale_v, u_q, u_v, a_q, b_q, a_v, b_v = ctx.saved_tensors
-        inputs = lora_inputs(x, bits_q, bits_v, scale_q, scale_v)
-        grads, input_grads = [], []
-        branches = ((grad_q, u_q, a_q, b_q, ctx.scalings[0]), (grad_v, u_v, a_v, b_v, ctx.scalings[1]))
-        for (grad, u, a, b, s), x16 in zip(branches, inputs):
-            if grad is None:
-                grad = torch.zeros(u.shape[:-1] + (b.shape[0],), dtype=torch.float16, device=u.device)
-            g16 = grad.to(torch.float16).reshape(-1, grad.shape[-1]).contiguous()
-            a16 = a.to(torch.float16).contiguous()
-            gu, da, db = lora_grads(g16, u, x16, b.to(torch.float16).contiguous(), s)
-            grads += [da.to(a.dtype), db.to(b.dtype)]
-            input_grads.append(lora_up(gu, a16))
-        grad_x = lora_input_grad(input_grads[0], input_grads[1], bits_q, bits_v,
-                                 1.0 / (1.0 - ctx.ps[0]), 1.0 / (1.0 - ctx.ps[1]))
-        return (grad_x.view(x.shape), None, None, None, None, grads[0], grads[1], grads[2], grads[3],
-                None, None, None, None)
+    def __init__(self, packed, fwd, bwd, p):
+        # fwd: (scaled_q, scaled_v); bwd: ((mask_q, scale_q), (mask_v, scale_v)); p: (p_q, p_v)
+        self.packed, self.fwd, self.bwd, self.p = packed, fwd, bwd, p
+
+    def inputs(self, x, forward):
+        """fp16 rows [T, W] of both branch inputs."""
+        if self.packed:
+            (bq, sq), (bv, sv) = self.bwd
+            return lora_inputs(x, bq, bv, sq, sv)
+        width = x.shape[-1]
+        out = []
+        for i in range(2):
+            if forward:
+                f = self.fwd[i]
+                v = x if f is None else x * f
+            else:
+                mask, kept = self.bwd[i]
+                v = x if mask is None else x * (mask * kept)
+            out.append(v.to(torch.float16).reshape(-1, width).contiguous())
+        return tuple(out)
+
+    def input_grad(self, gx16):
+        """fp32 [T, W] input gradient of x through both branches' dropout (gx16: the fp16 input
+        gradients of the q and v products)."""
+        if self.packed:
+            (bq, _), (bv, _) = self.bwd
+            return lora_input_grad(gx16[0], gx16[1], bq, bv, 1.0 / (1.0 - self.p[0]), 1.0 / (1.0 - self.p[1]))
+        total = None
+        for gx, (mask, _), p in zip(gx16, self.bwd, self.p):
+            term = gx.to(torch.float32)
+            if mask is not None:
+                term = term * mask.reshape(gx.shape) * (1.0 / (1.0 - p))
+            total = term if total is None else total + term
+        return total
 
 
-def _branch_input(x, scaled=None, mask=None, scale=None):
-    """fp16(x * dropout) of one branch on the reference's unpacked path (solution/attn.py:219-223,
-    240-243): the forward multiplies by `scaled` (the dropout output of ones, x-shaped), the
-    backward rebuilds it from the mask and its kept value; no dropout: fp16(x)."""
-    width = x.shape[-1]
-    if scaled is not None:
-        return (x * scaled).to(torch.float16).reshape(-1, width).contiguous()
-    if mask is not None:
-        return (x * (mask * scale)).to(torch.float16).reshape(-1, width).contiguous()
-    return x.to(torch.float16).reshape(-1, width).contiguous()
+def _qv_lora_forward(x, drop, adapters, scalings):
+    """(out_q, out_v, u_q, u_v): out = fp16(fp16(U . B^T) * s), U = fp16(X . A^T) per branch, with
+    X the branch's dropped-out fp16 input (solution/attn.py:224-228)."""
+    outs, us = [], []
+    for x16, (a, b), s in zip(drop.inputs(x, True), adapters, scalings):
+        u = lora_down(x16, a.to(torch.float16).contiguous())
+        outs.append(lora_up(u, b.to(torch.float16).t().contiguous()) * s)
+        us.append(u)
+    lead = x.shape[:-1]
+    return outs[0].reshape(*lead, -1), outs[1].reshape(*lead, -1), us[0], us[1]
+
+
+def _qv_lora_backward(x, drop, adapters, scalings, us, grads):
+    """(dX fp32 in x's shape, [dA_q, dB_q, dA_v, dB_v] in the adapters' dtypes). Per branch the
+    fused dk_lora_bwd gives GU = fp16(s * dY . B), dB = s * dY^T . U and dA = GU^T . X in fp32
+    (the products autograd forms, solution/attn.py:251-257); GU . A is the branch's input gradient
+    before its dropout. A branch that received no gradient contributes zeros, formed as the
+    reference forms them."""
+    xs = drop.inputs(x, False)
+    rows = xs[0].shape[0]
+    adapter_grads, input_grads = [], []
+    for x16, (a, b), s, u, g in zip(xs, adapters, scalings, us, grads):
+        a16 = a.to(torch.float16).contiguous()
+        b16 = b.to(torch.float16).contiguous()
+        if g is None:
+            g16 = torch.zeros((rows, b16.shape[0]), dtype=torch.float16, device=x.device)
+        else:
+            g16 = g.to(torch.float16).reshape(rows, -1).contiguous()
+        gu, da, db = lora_grads(g16, u, x16, b16, s)
+        adapter_grads += [da.to(a.dtype), db.to(b.dtype)]
+        input_grads.append(lora_up(gu, a16))
+    return drop.input_grad(input_grads).view(x.shape), adapter_grads
 
 
 class LoRAPairFromNorm(torch.autograd.Function):
-    """The reference's LoRAPairFromNorm.apply(x, h, norm_weight, eps, scaled_q, mask_q, scale_q,
-    scaled_v, mask_v, scale_v, a_q, b_q, a_v, b_v, scaling_q, scaling_v, p_q, p_v, packed)
-    (solution/attn.py:206-273): peft's q and v LoRA branches, lora_B(lora_A(dropout(x))) *
-    scaling, on this package's kernels.
+    """The q and v LoRA branches of a Qwen2 attention layer, lora_B(lora_A(dropout(x))) * scaling
+    each (peft under fp16 autocast, solution/attn.py:344-346), with the reference's argument list
+    apply(x, h, norm_weight, eps, scaled_q, mask_q, scale_q, scaled_v, mask_v, scale_v, a_q, b_q,
+    a_v, b_v, scaling_q, scaling_v, p_q, p_v, packed) (solution/attn.py:206-273).
 
-    packed=True: mask_q / mask_v are bit-packed keep-masks (pack_keep) and scale_q / scale_v fp32
-    device scalars; the dropped-out inputs and the input gradient through both masks are the HIP
-    kernels of LoRAPair (bit-exact restatements). packed=False: the reference's elementwise
-    torch ops on the GPU (`scaled_*` in the forward, mask * scale in the backward; a branch with
-    no dropout passes None). The reference rebuilds x in backward from the RMSNorm input h
-    (bit-identically, :240); the RMSNorm kernel is outside this package, so x is saved instead and
-    h, norm_weight and eps are accepted unused. Returns (out_q, out_v) fp16; gradients flow to x
-    (fp32) and the four adapter weights (their dtype)."""
+    packed=True: mask_* are pack_keep bits and scale_* fp32 device scalars 1 / (1 - p);
+    packed=False: scaled_* (forward) and mask_* * scale_* (backward) are x-shaped tensors, None
+    for a branch without dropout (see _QVDropout). x is saved and the dropped-out inputs formed
+    again in the backward; the reference rebuilds x from the RMSNorm input instead (:240), and the
+    norm is outside this package, so h, norm_weight and eps are accepted unused. Returns (out_q,
+    out_v) fp16; gradients reach x (fp32) and the four adapter weights (their dtype)."""
 
     @staticmethod
     def forward(ctx, x, h, norm_weight, eps, scaled_q, mask_q, scale_q, scaled_v, mask_v, scale_v,
                 a_q, b_q, a_v, b_v, scaling_q, scaling_v, p_q, p_v, packed):
-        if packed:
-            inputs = lora_inputs(x, mask_q, mask_v, scale_q, scale_v)
-        else:
-            inputs = (_branch_input(x, scaled_q), _branch_input(x, scaled_v))
-        outs, us = [], []
-        for x16, a, b, s in zip(inputs, (a_q, a_v), (b_q, b_v), (scaling_q, scaling_v)):
-            u = lora_down(x16, a.to(torch.float16).contiguous())
-            outs.append(lora_up(u, b.to(torch.float16).t().contiguous()) * s)
-            us.append(u)
-        ctx.save_for_backward(x, mask_q, scale_q, mask_v, scale_v, us[0], us[1], a_q, b_q, a_v, b_v)
-        ctx.scalings, ctx.ps, ctx.packed = (scaling_q, scaling_v), (p_q, p_v), packed
-        lead = x.shape[:-1]
-        return outs[0].reshape(*lead, -1), outs[1].reshape(*lead, -1)
+        drop = _QVDropout(bool(packed), (scaled_q, scaled_v), ((mask_q, scale_q), (mask_v, scale_v)),
+                          (p_q, p_v))
+        scalings = (scaling_q, scaling_v)
+        out_q, out_v, u_q, u_v = _qv_lora_forward(x, drop, ((a_q, b_q), (a_v, b_v)), scalings)
+        ctx.save_for_backward(x, u_q, u_v, a_q, b_q, a_v, b_v)
+        ctx.drop, ctx.scalings = drop, scalings
+        return out_q, out_v
 
     @staticmethod
     def backward(ctx, grad_q, grad_v):
-        x, mask_q, scale_q, mask_v, scale_v, u_q, u_v, a_q, b_q, a_v, b_v = ctx.saved_tensors
-        width = x.shape[-1]
-        if ctx.packed:
-            inputs = lora_inputs(x, mask_q, mask_v, scale_q, scale_v)
-        else:
-            inputs = (_branch_input(x, None, mask_q, scale_q), _branch_input(x, None, mask_v, scale_v))
-        grads, input_grads = [], []
-        branches = ((grad_q, u_q, a_q, b_q, ctx.scalings[0]), (grad_v, u_v, a_v, b_v, ctx.scalings[1]))
-        for (grad, u, a, b, s), x16 in zip(branches, inputs):
-            if grad is None:
-                grad = torch.zeros(u.shape[:-1] + (b.shape[0],), dtype=torch.float16, device=u.device)
-            g16 = grad.to(torch.float16).reshape(-1, grad.shape[-1]).contiguous()
-            gu, da, db = lora_grads(g16, u, x16, b.to(torch.float16).contiguous(), s)
-            grads += [da.to(a.dtype), db.to(b.dtype)]
-            input_grads.append(lora_up(gu, a.to(torch.float16).contiguous()))
-        if ctx.packed:
-            grad_x = lora_input_grad(input_grads[0], input_grads[1], mask_q, mask_v,
-                                     1.0 / (1.0 - ctx.ps[0]), 1.0 / (1.0 - ctx.ps[1]))
-        else:
-            grad_x = None
-            for gx16, m, p in zip(input_grads, (mask_q, mask_v), ctx.ps):
-                gx = gx16.to(torch.float32)
-                if m is not None:
-                    gx = gx * m.reshape(-1, width) * (1.0 / (1.0 - p))
-                grad_x = gx if grad_x is None else grad_x + gx
-        return ((grad_x.view(x.shape),) + (None,) * 9 + tuple(grads) + (None,) * 5)
+        x, u_q, u_v, a_q, b_q, a_v, b_v = ctx.saved_tensors
+        grad_x, adapter_grads = _qv_lora_backward(x, ctx.drop, ((a_q, b_q), (a_v, b_v)), ctx.scalings,
+                                                  (u_q, u_v), (grad_q, grad_v))
+        # gradients of x and the four adapters; the other 14 arguments take none
+        return (grad_x, *(None,) * 9, *adapter_grads, *(None,) * 5)
+
+
+class LoRAPair:
+    """Both LoRA branches with packed dropout masks: apply(x, bits_q, scale_q, bits_v, scale_v,
+    a_q, b_q, a_v, b_v, scaling_q, scaling_v, p_q, p_v) -> (out_q, out_v) fp16, i.e.
+    LoRAPairFromNorm on its packed path. x: [.., W] fp16 or fp32; bits_*: pack_keep masks;
+    scale_*: fp32 device scalars 1 / (1 - p); a_* [r, W], b_* [N, r] adapter weights (used in
+    fp16); gradients reach x (fp32) and the adapters."""
+
+    @staticmethod
+    def apply(x, bits_q, scale_q, bits_v, scale_v, a_q, b_q, a_v, b_v, scaling_q, scaling_v, p_q, p_v):
+        return LoRAPairFromNorm.apply(x, None, None, None, None, bits_q, scale_q, None, bits_v, scale_v,
+                                      a_q, b_q, a_v, b_v, scaling_q, scaling_v, p_q, p_v, True)
 
 
 class NF4LoRALinear(torch.autograd.Function):

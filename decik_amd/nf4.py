@@ -187,7 +187,7 @@ def linear_rope_forward(x16, items, cos, sin, head_dim, rope_mask, lora_rank=0):
             groups[g].y, groups[g].ldy = out.data_ptr(), n
         outs.append(out)
         ns.append(n)
-    key = (m, k, tuple(ns))
+    key = (m, k, tuple(ns), os.environ.get("DECIK_FWD_PLAN"))
     need = _ROPE_NEED.get(key)
     if need is None:
         arr = (ctypes.c_int64 * len(ns))(*ns)
