@@ -261,9 +261,11 @@ static_assert(kFwdVariants[kNumFwd4Variants - 1].waves == 4 && kFwdVariants[kNum
               "four-wave variants first");
 
 // glu: two weights of ns[0] rows, a tile takes 128 rows of each; never split (the epilogue
-// needs the finished sums). fwd8_ok: the eight-wave kernel may run (see above).
+// needs the finished sums). fwd8_ok: the eight-wave kernel may run (see above). fwd4_ok: the
+// four-wave kernel may run (not for GLU launches on nested statistics: its GLU waves mix the two
+// weights' rows and keep one code2 table).
 GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool glu, bool fwd8_ok,
-                  bool no_split = false, int min_splits = 1) {
+                  bool no_split = false, int min_splits = 1, bool fwd4_ok = true) {
     GemmPlan p{};
     p.steps = (int)((k + kFwdBK - 1) / kFwdBK);
     p.n_tiles = 0;
@@ -278,12 +280,13 @@ GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool glu
         }
     }
     const int nv = fwd8_ok ? kNumFwdVariants : kNumFwd4Variants;
-    const VariantCost* v = plan_override("DECIK_FWD_PLAN", kFwdVariants, nv, p.steps, &p.splits);
+    const int v0 = fwd4_ok || !fwd8_ok ? 0 : kNumFwd4Variants;  // the first variant offered
+    const VariantCost* v = plan_override("DECIK_FWD_PLAN", kFwdVariants + v0, nv - v0, p.steps, &p.splits);
     if (v != nullptr && (glu || no_split)) p.splits = 1;
     if (v != nullptr && p.splits < min_splits && p.steps >= min_splits) v = nullptr;
     if (v == nullptr) {
         const int64_t nt = p.n_tiles;
-        v = choose_plan(kFwdVariants, nv, m, ncols, p.steps, [nt](const VariantCost&) { return nt; },
+        v = choose_plan(kFwdVariants + v0, nv - v0, m, ncols, p.steps, [nt](const VariantCost&) { return nt; },
                         &p.splits, (glu || no_split) ? 1 : 32, INT64_MAX, min_splits, true);
     }
     p.mt = v->rows_blocks;
@@ -315,6 +318,58 @@ GemmPlan plan_bwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool swi
     p.m_tiles = (int)((m + kRowUnit * p.mt - 1) / (kRowUnit * p.mt));
     finish_plan(p, m, k);
     return p;
+}
+
+// Input-gradient launches whose tiles overrun whole rounds of resident work-groups by a partial
+// round (the 7B down projection at 830 tokens: 296 tiles of 224 x 256 for 256 CUs) leave most
+// CUs idle in that last round. The column tiles that fill whole rounds then run as one launch
+// (unsplit), and the remaining output columns as a second launch planned on its own -- usually
+// split over every CU, then reduced -- when the time model says two launches are faster.
+struct BwdParts {
+    GemmPlan a;      // the whole launch, or the first part: column tiles 0 .. a.n_tiles - 1
+    GemmPlan b;      // the second part (two only): column tiles kt_b .., k - 256 kt_b columns
+    int kt_b = 0;
+    bool two = false;
+};
+
+constexpr double kSecondLaunchUs = 3.0;  // a second GEMM launch and its gap
+constexpr double kTwoPartGain = 0.95;    // two launches only for an estimated gain of 5% or more
+
+const VariantCost* bwd_variant(int mt) {
+    for (int i = 0; i < kNumBwdVariants; ++i)
+        if (kBwdVariants[i].rows_blocks == mt) return &kBwdVariants[i];
+    return &kBwdVariants[0];
+}
+
+BwdParts plan_bwd_parts(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool swiglu,
+                        int64_t max_partial_bytes = INT64_MAX) {
+    BwdParts r;
+    r.a = plan_bwd(m, k, ns, ngroups, swiglu, false, max_partial_bytes);
+    const char* forced = std::getenv("DECIK_BWD_PLAN");
+    if (swiglu || (forced != nullptr && *forced != 0)) return r;
+    const int64_t slots = num_cus();  // one work-group per CU
+    const int64_t tiles = (int64_t)r.a.m_tiles * r.a.n_tiles;  // unsplit
+    if (tiles <= slots || tiles % slots == 0) return r;
+    const int kt_a = (int)((tiles / slots) * slots / r.a.m_tiles);  // whole column tiles of the full rounds
+    if (kt_a < 1 || kt_a >= r.a.n_tiles) return r;
+    const int64_t k_b = k - (int64_t)kt_a * 256;
+    const GemmPlan b = plan_bwd(m, k_b, ns, ngroups, false, false, max_partial_bytes);
+    const VariantCost* va = bwd_variant(r.a.mt);
+    const VariantCost* vb = bwd_variant(b.mt);
+    const double t_one = plan_time(*va, m, r.a.n_tiles, k, r.a.steps, r.a.splits, false);
+    const double t_two = plan_time(*va, m, kt_a, (int64_t)kt_a * 256, r.a.steps, 1, false) +
+                         plan_time(*vb, m, b.n_tiles, k_b, b.steps, b.splits, false) + kSecondLaunchUs;
+    if (t_two >= kTwoPartGain * t_one) return r;
+    no_split(r.a);
+    r.a.n_tiles = kt_a;
+    r.b = b;
+    r.kt_b = kt_a;
+    r.two = true;
+    return r;
+}
+
+int64_t workspace_bytes(const BwdParts& p) {
+    return std::max(workspace_bytes(p.a), p.two ? workspace_bytes(p.b) : (int64_t)0);
 }
 
 // nf4_skinny_kernel (forward, m <= kSkinnyMaxM): 64-row groups; contraction splits while the
@@ -491,7 +546,8 @@ int dk_nf4_linear_plan(int backward, int64_t m, int64_t k, const int64_t* ns, in
         p = plan_skinny(m, k, ns, ngroups, single);
         kernel = 5;  // nf4_skinny_kernel
     } else {
-        p = plan_fwd(m, k, ns, ngroups, glu, k % 64 == 0 && k % blocksize == 0, single);
+        p = plan_fwd(m, k, ns, ngroups, glu, k % 64 == 0 && k % blocksize == 0, single, 1,
+                     !(glu && (flags & DK_PLAN_NESTED) != 0));
         kernel = p.waves == 8 ? 1 : 0;
     }
     out[0] = p.mt;
@@ -503,7 +559,7 @@ int dk_nf4_linear_plan(int backward, int64_t m, int64_t k, const int64_t* ns, in
 
 int64_t dk_nf4_linear_bwd_workspace(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
     if (ngroups < 1 || ngroups > kMaxGroups || ns == nullptr || m <= 0 || k <= 0) return 0;
-    return workspace_bytes(plan_bwd(m, k, ns, ngroups, false));
+    return workspace_bytes(plan_bwd_parts(m, k, ns, ngroups, false));
 }
 
 }  // extern "C"
@@ -584,9 +640,9 @@ static int linear_fwd_impl(const std::string& name, const uint16_t* x, int64_t m
         ncols += G.w.n;
         ns[g] = G.w.n;
     }
-    if (glu && (ngroups != 2 || ns[0] != ns[1] || nested || a.wide_stats ||
-                groups[0].w.blocksize != groups[1].w.blocksize))
-        return fail(name + ": GLU mode needs two plain weights of one shape, blocksize >= 64, k % 64 == 0");
+    if (glu && (ngroups != 2 || ns[0] != ns[1] || groups[0].w.nested != groups[1].w.nested || a.wide_stats ||
+                groups[0].w.blocksize != groups[1].w.blocksize || k % 64 != 0))
+        return fail(name + ": GLU mode needs two weights of one shape and statistics kind, blocksize >= 64, k % 64 == 0");
     if (m == 0 || tile == 0) return 0;
     if ((m - 1) * ldx + k >= INT32_MAX / 2) return fail(name + ": x too large");
     bool any_lora = false;
@@ -635,7 +691,7 @@ static int linear_fwd_impl(const std::string& name, const uint16_t* x, int64_t m
     }
     bool fwd8_ok = k % 64 == 0;
     for (int g = 0; g < ngroups; ++g) fwd8_ok = fwd8_ok && k % groups[g].w.blocksize == 0;
-    const GemmPlan p = plan_fwd(m, k, ns, ngroups, glu, fwd8_ok, no_split, rope != nullptr ? 2 : 1);
+    const GemmPlan p = plan_fwd(m, k, ns, ngroups, glu, fwd8_ok, no_split, rope != nullptr ? 2 : 1, !(glu && nested));
     if (rope != nullptr && p.splits < 2) return fail(name + ": the RoPE epilogue needs k >= 128 (two contraction steps)");
     const int64_t need = workspace_bytes(p);
     if (need > 0 && (workspace == nullptr || workspace_bytes_ < need || !aligned(workspace, 256)))
@@ -729,7 +785,7 @@ int dk_nf4_glu_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
     const int64_t n = wg.n;
     if (!aligned(h, 16) || ldh < n || (ldh % 8) != 0)
         return fail("dk_nf4_glu_fwd: h must be 16-byte aligned with ldh >= n, ldh % 8 == 0");
-    const bool fused = !wg.nested && !wu.nested && wg.blocksize == wu.blocksize && wg.blocksize >= 64 &&
+    const bool fused = wg.nested == wu.nested && wg.blocksize == wu.blocksize && wg.blocksize >= 64 &&
                        k % 64 == 0;
     if (fused)
         return linear_fwd_impl("dk_nf4_glu_fwd", x, m, k, ldx, groups, 2, lora_rank, nullptr, 0, stream,
@@ -737,7 +793,7 @@ int dk_nf4_glu_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
     // other statistics: gate and up by the grouped launch (one pass), then the SwiGLU kernel
     if (groups[0].y == nullptr || groups[1].y == nullptr || groups[0].ldy != n || groups[1].ldy != n ||
         ldh != n)
-        return fail("dk_nf4_glu_fwd: nested or narrow-block weights need gate and up outputs, all rows contiguous");
+        return fail("dk_nf4_glu_fwd: narrow-block or mixed-statistics weights need gate and up outputs, all rows contiguous");
     if (linear_fwd_impl("dk_nf4_glu_fwd", x, m, k, ldx, groups, 2, lora_rank, nullptr, 0, stream, nullptr,
                         0, true))
         return 1;
@@ -758,6 +814,37 @@ struct SwigluBwdOut {
     uint16_t* dup;
     int64_t ldd;
 };
+
+// One input-gradient launch (plan p) over the output columns 256 kt0 .. 256 kt0 + cols - 1, then
+// its split-K reduction into the same columns of dX. `a` carries everything but the tiling.
+static int launch_bwd_part(BwdArgs a, const GemmPlan& p, int kt0, int64_t cols, void* workspace,
+                           hipStream_t st) {
+    a.m_tiles = p.m_tiles;
+    a.k_tiles = p.n_tiles;
+    a.k_tile0 = kt0;
+    a.pcols = (int32_t)cols;
+    a.splits = p.splits;
+    a.csteps = p.steps;
+    a.csteps_per_split = p.steps_per_split;
+    a.cols_first = cols_first(p.m_tiles, a.m, cols) ? 1 : 0;
+    a.partials = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
+    const int64_t wgs = (int64_t)p.m_tiles * p.n_tiles * p.splits;
+    if (wgs > INT32_MAX / 2) return fail("dk_nf4_linear_bwd: problem too large");
+    if (check_hip(launch_bwd8(a, p.mt, pad8((int)wgs), st), "dk_nf4_linear_bwd launch")) return 1;
+    if (p.splits <= 1) return 0;
+    const int64_t c0 = (int64_t)kt0 * 256;
+    ReduceArgs r{};
+    r.partials = a.partials;
+    r.slab = (int64_t)a.m * cols;
+    r.splits = p.splits;
+    r.m = a.m;
+    r.ncols = (int)cols;
+    r.nout = 1;
+    r.out_fp32 = a.dx_fp32;
+    void* out = static_cast<uint8_t*>(a.dx) + c0 * (a.dx_fp32 ? 4 : 2);
+    r.o[0] = ReduceOut{out, a.lddx, nullptr, 0, (int32_t)cols};
+    return check_hip(launch_splitk_reduce(r, st), "dk_nf4_linear_bwd split-K reduction");
+}
 
 // The input-gradient launch behind dk_nf4_linear_bwd and dk_nf4_linear_bwd_swiglu (sw != NULL:
 // no dX; the epilogue turns fp16(dY.W) into dgate / dup; never split).
@@ -815,8 +902,8 @@ static int linear_bwd_impl(const std::string& name, const dk_linear_bwd_group* g
         ns[g] = G.w.n;
     }
     if (m == 0) return 0;
-    const GemmPlan p = plan_bwd(m, k, ns, ngroups, sw != nullptr, false, max_partial_bytes);
-    const int64_t need = workspace_bytes(p);
+    const BwdParts parts = plan_bwd_parts(m, k, ns, ngroups, sw != nullptr, max_partial_bytes);
+    const int64_t need = workspace_bytes(parts);
     if (need > 0 && (workspace == nullptr || workspace_bytes_ < need || !aligned(workspace, 256)))
         return fail(name + ": workspace too small (need " + std::to_string(need) + " bytes)");
     a.dx = dx;
@@ -825,14 +912,8 @@ static int linear_bwd_impl(const std::string& name, const dk_linear_bwd_group* g
     a.k = (int)k;
     a.ngroups = ngroups;
     a.lora_rank = lora_rank;
-    a.m_tiles = p.m_tiles;
-    a.k_tiles = p.n_tiles;
-    a.splits = p.splits;
-    a.csteps = p.steps;
-    a.csteps_per_split = p.steps_per_split;
     a.dx_fp32 = dx_fp32 ? 1 : 0;
     a.nested = nested;
-    a.cols_first = cols_first(p.m_tiles, m, k) ? 1 : 0;
     if (sw != nullptr) {
         a.swiglu = 1;
         a.gate = reinterpret_cast<const _Float16*>(sw->gate);
@@ -842,23 +923,9 @@ static int linear_bwd_impl(const std::string& name, const dk_linear_bwd_group* g
         a.dup = reinterpret_cast<_Float16*>(sw->dup);
         a.ldd = sw->ldd;
     }
-    if (need > 0) a.partials = static_cast<float*>(workspace);
-    const int64_t wgs = (int64_t)p.m_tiles * p.n_tiles * p.splits;
-    if (wgs > INT32_MAX / 2) return fail(name + ": problem too large");
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    const hipError_t le = launch_bwd8(a, p.mt, pad8((int)wgs), st);
-    if (check_hip(le, "dk_nf4_linear_bwd launch")) return 1;
-    if (p.splits <= 1) return 0;
-    ReduceArgs r{};
-    r.partials = a.partials;
-    r.slab = m * k;
-    r.splits = p.splits;
-    r.m = (int)m;
-    r.ncols = (int)k;
-    r.nout = 1;
-    r.out_fp32 = dx_fp32 ? 1 : 0;
-    r.o[0] = ReduceOut{dx, lddx, nullptr, 0, (int32_t)k};
-    return check_hip(launch_splitk_reduce(r, st), "dk_nf4_linear_bwd split-K reduction");
+    if (launch_bwd_part(a, parts.a, 0, k, workspace, st)) return 1;
+    return parts.two ? launch_bwd_part(a, parts.b, parts.kt_b, k - (int64_t)parts.kt_b * 256, workspace, st) : 0;
 }
 
 extern "C" {

@@ -61,7 +61,8 @@ struct FwdArgs {
     int32_t ncols;       // columns of a partial slab (sum of the groups' n)
     float* partials;     // splits x m x ncols fp32 (splits > 1)
     // GLU mode: groups 0 (gate) and 1 (up) of one shape; a tile takes 128 rows of each and the
-    // epilogue also writes h = fp16(silu(gate) up) (no split-K; plain narrow statistics)
+    // epilogue also writes h = fp16(silu(gate) up) (no split-K; narrow statistics; nested ones on
+    // nf4_fwd8_kernel only)
     int32_t glu;
     _Float16* h;
     int64_t ldh;
@@ -104,6 +105,11 @@ struct BwdArgs {
     int64_t ldd;
     // work-group order of nf4_bwd8_kernel: column tiles fastest (1) or token tiles fastest (0)
     int32_t cols_first;
+    // the launch covers output column tiles k_tile0 .. k_tile0 + k_tiles - 1 (a remainder launch
+    // starts past the tiles of a first one); split-K partial slabs are pcols columns wide and
+    // start at column 256 k_tile0
+    int32_t k_tile0;
+    int32_t pcols;
     BwdGroupDev g[kMaxGroups];
 };
 

@@ -108,7 +108,7 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
     const int k_tile = a.cols_first ? mk % a.k_tiles : mk / a.m_tiles;
     const int M = sgpr(a.m), K = sgpr(a.k);
     const int m0 = m_tile * BM;
-    const int tile_k0 = k_tile * kB8BN;
+    const int tile_k0 = (a.k_tile0 + k_tile) * kB8BN;
     const int kw0 = tile_k0 + 32 * wave;  // the wave's first output column
     const bool cok = kw0 < K;             // k % 32 == 0: the wave's columns are all in or all out
     const int cs0 = split * a.csteps_per_split;
@@ -558,8 +558,10 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
     if (out32) {
         // 32 x 256 fp32 tiles (rows 1040 bytes apart) -> whole 1 KB rows of the split's partial
         // slab or of dX
-        float* dst = a.splits > 1 ? a.partials + (int64_t)split * M * K : (float*)a.dx;
-        const int64_t ld = a.splits > 1 ? (int64_t)K : a.lddx;
+        // (a slab holds the launch's pcols columns from column c0 = 256 k_tile0 on)
+        float* dst = a.splits > 1 ? a.partials + (int64_t)split * M * a.pcols : (float*)a.dx;
+        const int64_t ld = a.splits > 1 ? (int64_t)a.pcols : a.lddx;
+        const int c0 = a.splits > 1 ? a.k_tile0 * kB8BN : 0;
         constexpr int RB = kB8BN * 4 + 16;
 #pragma unroll
         for (int i = 0; i < MB; ++i) {
@@ -572,7 +574,7 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
                 const int ch = tid + kB8Threads * h, row = ch >> 6, cc = ch & 63;
                 const float4_t val = *(const float4_t*)(buf + row * RB + cc * 16);
                 const int m = m0 + 32 * i + row, col = tile_k0 + 4 * cc;
-                if (m < M && col < K) *(float4_t*)(dst + (int64_t)m * ld + col) = val;
+                if (m < M && col < K) *(float4_t*)(dst + (int64_t)m * ld + (col - c0)) = val;
             }
         }
         return;

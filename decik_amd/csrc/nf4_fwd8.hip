@@ -34,7 +34,7 @@ namespace dk {
 
 constexpr int kF8Waves = 8;
 constexpr int kF8Threads = 64 * kF8Waves;
-constexpr int kF8Header = 1024;  // code2 table
+constexpr int kF8Header = 2048;  // code2 tables (GLU: gate's, then up's)
 constexpr int kF8Dummy = 1024;   // target of the X loads of waves past the tile (zeros)
 
 // Per-wave ring slot of one step: 1 KB packed bytes (lane: 16 bytes), then 64 statistics dword
@@ -115,8 +115,12 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
         lut2[tid] = float2_t{book[(tid >> 4) & 15], book[tid & 15]};
     }
     if constexpr (NESTED) {
-        if (tid < 256) c2[tid] = W.code2[tid];
+        // GLU: threads 256..511 bring the up weight's table (the waves of each weight index
+        // their own)
+        if (glu) c2[tid] = a.g[tid >> 8].w.code2[tid & 255];
+        else if (tid < 256) c2[tid] = W.code2[tid];
     }
+    const float* const c2w = c2 + (glu ? 256 * (wave >> 2) : 0);  // this wave's weight's table
     const float offset = NESTED ? *W.offset : 0.0f;
     // byte offset of this wave's byte-pair code book in lut2
     const uint32_t book8 = (uint32_t)(glu ? 2048 * (wave >> 2) : 0);
@@ -207,7 +211,7 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
         if constexpr (NESTED) {
             const uint32_t q = slot[1024 + 4 * si];
             const float a2 = *(const float*)(slot + 1280 + 4 * si);
-            sc = c2[q] * a2 + offset;
+            sc = c2w[q] * a2 + offset;
         } else {
             sc = *(const float*)(slot + 1024 + 4 * si);
         }

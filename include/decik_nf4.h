@@ -155,9 +155,10 @@ int dk_nf4_linear_rope_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
 /* Gate and up projections and SwiGLU in one launch: groups[0] = gate, groups[1] = up (one shape
  * [n, k]; bias and LoRA as in dk_nf4_linear_fwd), h = fp16(silu(gate) * up) [m, n] (row stride
  * ldh) from the fp16-rounded gate and up -- the same bits as dk_nf4_linear_fwd followed by
- * dk_swiglu_fwd. groups[i].y may be NULL (not stored) for plain weights with blocksize >= 64 and
- * k % 64 == 0; other weights run as the grouped launch then the SwiGLU kernel and need both y,
- * with rows contiguous (ldy = ldh = n). No workspace. */
+ * dk_swiglu_fwd. One launch when gate and up have the same statistics kind (both plain or both
+ * nested, as bitsandbytes stores them), blocksize >= 64 and k % 64 == 0; then groups[i].y may be
+ * NULL (not stored). Other weights run as the grouped launch then the SwiGLU kernel and need both
+ * y, with rows contiguous (ldy = ldh = n). No workspace. */
 int dk_nf4_glu_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
                    const dk_linear_fwd_group* groups, int lora_rank, uint16_t* h, int64_t ldh,
                    void* stream);
@@ -276,7 +277,8 @@ int dk_swiglu_bwd(const uint16_t* grad, const uint16_t* gate, const uint16_t* up
  * (backward = 0) or dk_nf4_linear_bwd (backward = 1) chooses for these shapes, for reports and
  * tuning. flags: DK_PLAN_GLU (forward: the fused GLU mode of dk_nf4_glu_fwd; backward: the SwiGLU
  * epilogue of dk_nf4_linear_bwd_swiglu), DK_PLAN_LORA (some group has LoRA terms),
- * DK_PLAN_NO_SPLIT (a single pass). blocksize: the largest block size of the groups' weights.
+ * DK_PLAN_NO_SPLIT (a single pass), DK_PLAN_NESTED (with DK_PLAN_GLU, forward: the weights carry
+ * nested statistics). blocksize: the largest block size of the groups' weights.
  * out[0] = 32-token row blocks per tile, out[1] = waves per work-group, out[2] = contraction
  * splits, out[3] = kernel (0 nf4_fwd_kernel, 1 nf4_fwd8_kernel, 2 no longer returned (an
  * earlier input-gradient kernel), 3 nf4_bwd8_kernel, 4 nf4_gemv_kernel (forward launches of one
@@ -289,6 +291,7 @@ int dk_swiglu_bwd(const uint16_t* grad, const uint16_t* gate, const uint16_t* up
 #define DK_PLAN_GLU 1
 #define DK_PLAN_LORA 2
 #define DK_PLAN_NO_SPLIT 4
+#define DK_PLAN_NESTED 8
 int dk_nf4_linear_plan(int backward, int64_t m, int64_t k, const int64_t* ns, int ngroups, int flags,
                        int blocksize, int32_t* out);
 

@@ -202,3 +202,28 @@ def test_c5_qwen7b_shapes(shape, m, qwen7b_weights, device):
     assert_close(y[rows], O.linear_ref(x[rows].cpu().numpy(), w16), what=f"7B {shape} fwd m={m}")
     dx = linear_backward([dict(packed=packed, qs=qs, dy=dy)], m, k)
     assert_close(dx[rows], O.linear_dx_ref(dy[rows].cpu().numpy(), w16), what=f"7B {shape} dX m={m}")
+
+
+@pytest.mark.parametrize("dx_fp32", [False, True])
+def test_c5_down_input_gradient_two_launches(dx_fp32, qwen7b_weights, device, monkeypatch):
+    """The 7B down-projection input gradient at 830 tokens (296 tiles of 224 x 256 for 256 CUs)
+    runs as two launches: the 64 column tiles of the full round unsplit, then the last 2560
+    columns split over every CU and reduced. The first part gives the same bits as the one-launch
+    unsplit plan; every column meets the bar against the oracle."""
+    from decik_amd.nf4 import linear_backward
+
+    packed, qs, w16 = qwen7b_weights["down"]
+    n, k = (int(v) for v in qs.shape)
+    m = 830
+    dy = randn16((m, n), seed=731, device=device, std=1e-2)
+    item = [dict(packed=packed, qs=qs, dy=dy)]
+    dx = linear_backward(item, m, k, dx_fp32=dx_fp32)
+    monkeypatch.setenv("DECIK_BWD_PLAN", "7,1")
+    dx1 = linear_backward(item, m, k, dx_fp32=dx_fp32)
+    monkeypatch.delenv("DECIK_BWD_PLAN")
+    torch.cuda.synchronize()
+    assert torch.equal(dx[:, :16384], dx1[:, :16384])
+    rows = np.arange(0, m, 7)
+    ref = O.linear_dx_ref(dy[rows].cpu().numpy(), w16)
+    assert_close(dx[rows], ref, what="7B down dX, two launches")
+    assert_close(dx[rows][:, 16384:], ref[:, 16384:], what="7B down dX, remainder columns")

@@ -8,7 +8,7 @@ against the oracle (max|err| <= 1e-2 max|ref|, mean rel <= 1e-3)."""
 import pytest
 import torch
 
-from helpers import assert_close, make_weight, randn16
+from helpers import assert_close, make_weight, oracle_state, randn16
 from oracle import nf4 as O
 
 pytestmark = pytest.mark.gpu
@@ -71,36 +71,80 @@ def test_glu_forward_with_lora(device, monkeypatch):
     assert torch.equal(g, g2) and torch.equal(u, u2) and torch.equal(h, swiglu_fwd(g2, u2))
 
 
-def test_glu_forward_nested_descriptor_takes_two_launches(device, monkeypatch):
-    """The C entry with nested (double-quant) statistics runs the grouped launch and the SwiGLU
-    kernel; without gate/up outputs it refuses."""
-    from decik_amd._lib import LinearFwdGroup, lib, ptr, stream_of, weight_desc
+def _glu_groups(items, outs, n, device):
+    from decik_amd._lib import LinearFwdGroup, weight_desc
 
-    monkeypatch.setenv("DECIK_FWD_PLAN", "2,1")
-    m, n, k = 64, 256, 256
-    pg, qg, wg = make_weight((n, k), seed=71, device=device)
-    pu, qu, wu = make_weight((n, k), seed=72, device=device)
-    x = randn16((m, k), seed=73, device=device)
+    groups = (LinearFwdGroup * 2)()
+    keep = []
+    for i, ((p, q), y) in enumerate(zip(items, outs)):
+        w, kp = weight_desc(p, q, device)  # the statistics as stored: no cached scales
+        keep += kp
+        groups[i].w = w
+        groups[i].y = None if y is None else y.data_ptr()
+        groups[i].ldy = n
+    return groups, keep
+
+
+@pytest.mark.parametrize("m,n,k,plan", [(64, 256, 256, "2,1,8"), (830, 8960, 1536, None), (300, 384, 512, "4,1,8")])
+def test_glu_forward_nested_statistics_one_launch(m, n, k, plan, device, monkeypatch):
+    """Raw double-quant statistics (bitsandbytes' nested absmax, decoded in the kernel with each
+    weight's own code2 table) take the one-launch GLU forward: the same bits as the grouped launch
+    on the derived fp32 block scales followed by the SwiGLU kernel, with or without the gate/up
+    outputs."""
+    from decik_amd._lib import lib, ptr, stream_of
+    from decik_amd.nf4 import launch_plan
+
+    if plan is not None:
+        monkeypatch.setenv("DECIK_FWD_PLAN", plan)
+    pg, qg, wg = make_weight((n, k), seed=71 + n, device=device)
+    pu, qu, wu = make_weight((n, k), seed=72 + n, device=device)
+    # different code2 tables for the two weights, so a wave reading the other weight's table fails
+    qu.state2.code = qu.state2.code.flip(0).contiguous()
+    wu = O.dequant_nf4(oracle_state(pu, qu), nthreads=0)
+    x = randn16((m, k), seed=m + 73, device=device)
     g = torch.empty((m, n), dtype=torch.float16, device=device)
     u = torch.empty_like(g)
     h = torch.empty_like(g)
-    groups = (LinearFwdGroup * 2)()
-    keep = []
-    for i, (p, q, y) in enumerate([(pg, qg, g), (pu, qu, u)]):
-        w, kp = weight_desc(p, q, device)  # nested: no cached scales
-        keep += kp
-        assert w.nested == 1
-        groups[i].w = w
-        groups[i].y = y.data_ptr()
-        groups[i].ldy = n
+    groups, keep = _glu_groups([(pg, qg), (pu, qu)], [g, u], n, device)
+    assert groups[0].w.nested == 1 and groups[1].w.nested == 1
+    assert launch_plan(False, m, k, [n, n], glu=True, nested=True)["waves"] == 8
     rc = lib().dk_nf4_glu_fwd(ptr(x), m, k, k, groups, 0, ptr(h), n, stream_of(device))
     assert rc == 0, lib().dk_last_error()
     g2, u2, h2 = _separate_glu(x, dict(packed=pg, qs=qg), dict(packed=pu, qs=qu))
     torch.cuda.synchronize()
-    assert_close(g, O.linear_ref(x.cpu().numpy(), wg, None), what="nested gate")
+    assert torch.equal(g, g2) and torch.equal(u, u2) and torch.equal(h, h2)
+    xn = x.cpu().numpy()
+    assert_close(g, O.linear_ref(xn, wg, None), what="nested gate")
+    assert_close(u, O.linear_ref(xn, wu, None), what="nested up")
+    groups2, keep2 = _glu_groups([(pg, qg), (pu, qu)], [None, None], n, device)
+    h3 = torch.empty_like(h)
+    rc = lib().dk_nf4_glu_fwd(ptr(x), m, k, k, groups2, 0, ptr(h3), n, stream_of(device))
+    assert rc == 0, lib().dk_last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(h3, h)
+    del keep, keep2
+
+
+def test_glu_forward_narrow_blocks_take_two_launches(device):
+    """Weights of 32-element blocks run the grouped launch and the SwiGLU kernel; without gate/up
+    outputs the entry refuses."""
+    from decik_amd._lib import lib, ptr, stream_of
+
+    m, n, k = 64, 256, 256
+    pg, qg, wg = make_weight((n, k), seed=81, device=device, blocksize=32)
+    pu, qu, wu = make_weight((n, k), seed=82, device=device, blocksize=32)
+    x = randn16((m, k), seed=83, device=device)
+    g = torch.empty((m, n), dtype=torch.float16, device=device)
+    u = torch.empty_like(g)
+    h = torch.empty_like(g)
+    groups, keep = _glu_groups([(pg, qg), (pu, qu)], [g, u], n, device)
+    rc = lib().dk_nf4_glu_fwd(ptr(x), m, k, k, groups, 0, ptr(h), n, stream_of(device))
+    assert rc == 0, lib().dk_last_error()
+    torch.cuda.synchronize()
     from decik_amd.swiglu import swiglu_fwd
 
-    assert torch.equal(g, g2) and torch.equal(u, u2) and torch.equal(h, swiglu_fwd(g, u))
+    assert_close(g, O.linear_ref(x.cpu().numpy(), wg, None), what="narrow-block gate")
+    assert torch.equal(h, swiglu_fwd(g, u))
     groups[0].y = None
     rc = lib().dk_nf4_glu_fwd(ptr(x), m, k, k, groups, 0, ptr(h), n, stream_of(device))
     assert rc != 0 and b"gate and up outputs" in lib().dk_last_error()
