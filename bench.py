@@ -857,30 +857,47 @@ def bench_c5(device, reps=3, min_bytes=512 << 20):
                 fl = gemm_flops(n, k, m)
                 by = fused_bytes(n, k, m)
                 plan = nf4.launch_plan(d == "bwd", m, k, [n])
-                rows.append(dict(shape=name, n=n, k=k, m=m, dir=d, us=round(ms * 1e3, 2),
-                                 gbs=round(by / (ms * 1e-3) / 1e9, 1), hbm_frac=round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                                 tflops=round(fl / (ms * 1e-3) / 1e12, 2),
-                                 mfma_frac=round(fl / (ms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4),
-                                 kernel=plan["kernel"], splits=plan["splits"], copies=copies, timing=timing))
+                rows.append([name, m, d, round(ms * 1e3, 2), round(by / (ms * 1e-3) / 1e9, 1),
+                             round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), round(fl / (ms * 1e-3) / 1e12, 2),
+                             round(fl / (ms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4), plan["kernel"], plan["splits"],
+                             plan["launches"], copies, timing])
             torch.cuda.empty_cache()
         del ws
         torch.cuda.empty_cache()
     return dict(workload="Qwen2.5-7B projections (NF4 bs 64, double quant, cached fp32 block scales), each shape "
                          "and M: back-to-back calls over weight copies totalling > 512 MB (weights from HBM), "
-                         "replayed from a HIP graph", rows=rows)
+                         "replayed from a HIP graph",
+                shapes={name: [n, k] for name, n, k in QWEN7_SHAPES},
+                columns=["shape", "m", "dir", "us", "gbs", "hbm_frac", "tflops", "mfma_frac", "kernel", "splits",
+                         "gemm_launches", "copies", "timing"],
+                rows=rows)
+
+
+def mlp_plan(kind):
+    """The launch plan of MLP launch `kind` as the library's planner chooses it (host-only)."""
+    from decik_amd import nf4
+
+    args = {"fwd_gate_up": (False, HIDDEN, [INTER, INTER], True), "fwd_down": (False, INTER, [HIDDEN], False),
+            "bwd_down": (True, INTER, [HIDDEN], True), "bwd_gate_up": (True, HIDDEN, [INTER, INTER], False)}[kind]
+    return nf4.launch_plan(args[0], M, args[1], args[2], glu=args[3])
 
 
 def load_traffic(kind):
-    """HBM bytes per call of launch `kind`, from the committed rocprofv3 --pmc FETCH_SIZE /
-    WRITE_SIZE summary (profiles/traffic.json, made with `bench.py --only <kind>`), or None if
-    that summary covers another launch."""
+    """(HBM bytes per call of launch `kind`, None) from the committed rocprofv3 --pmc FETCH_SIZE /
+    WRITE_SIZE summary (profiles/traffic.json, made with `bench.py --only <kind>`), or (None, why)
+    if that summary covers another launch or was measured on another launch plan than the
+    planner's current one (a stale summary)."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:
             t = json.load(f)
-        return t["bytes_per_call"] if t["launch"] == kind else None
-    except (OSError, ValueError, KeyError, TypeError):
-        return None
+        if t["launch"] != kind:
+            return None, f"profiles/traffic.json covers {t['launch']}"
+        if t.get("plan") != mlp_plan(kind):
+            return None, f"profiles/traffic.json was measured on plan {t.get('plan')}, the planner now picks {mlp_plan(kind)}"
+        return t["bytes_per_call"], None
+    except (OSError, ValueError, KeyError, TypeError) as e:
+        return None, f"profiles/traffic.json unreadable ({type(e).__name__})"
 
 
 def copy_probe(device):
@@ -975,10 +992,13 @@ def main():
     ms = mlp["launch_ms"][dom]
     achieved = mlp["flops"][dom] / (ms * 1e-3) / 1e12
     kern = mlp["symbol"][dom] + (" + splitk_reduce_kernel" if split_launch(dom) else "")
+    traffic, traffic_note = load_traffic(dom)
     roofline = dict(kernel=kern, launch=dom, bound="mfma", achieved=round(achieved, 2),
                     peak=FP16_PEAK_TFLOPS, unit="TFLOP/s", frac=round(achieved / FP16_PEAK_TFLOPS, 4),
                     flops_per_launch=mlp["flops"][dom], avg_launch_ms=round(ms, 5),
-                    traffic=load_traffic(dom))
+                    traffic=traffic, plan=mlp_plan(dom))
+    if traffic_note is not None:
+        roofline["traffic_note"] = traffic_note
     if args.only is not None:
         print(json.dumps(dict(only=args.only, roofline=roofline)))
         return
@@ -1004,6 +1024,13 @@ def main():
         kernels_uncached_nested={k: dict(ms=round(v, 4), tflops=round(mlp["flops"][k] / (v * 1e-3) / 1e12, 1))
                                  for k, v in mlp["uncached_ms"].items()},
     )
+    if c3 is not None:
+        line["c3_attention_step"] = c3
+    if c4 is not None:
+        line["c4_stack_step"] = c4
+    if c5 is not None:
+        line["c5_qwen7b_sweep"] = c5
+    # the dequantization last but one: the end of the line is what a truncated log keeps
     if deq is not None:
         probe = mixed_ceiling(peaks, deq["read"], deq["write"])
         roof = dict(bound="hbm", achieved=round(deq["gbs"], 1), peak=HBM_PEAK_GBS, unit="GB/s",
@@ -1023,12 +1050,6 @@ def main():
                                cache_resident=dict(value=round(deq_cached["gbs"], 1), unit="GB/s",
                                                    workload="x 8 layers (187 MB packed, stays in the "
                                                             "Infinity Cache between iterations)"))
-    if c3 is not None:
-        line["c3_attention_step"] = c3
-    if c4 is not None:
-        line["c4_stack_step"] = c4
-    if c5 is not None:
-        line["c5_qwen7b_sweep"] = c5
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
     else:

@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libdecik_nf4.so")
 MAX_GROUPS = 4
 # dk_nf4_linear_plan flags and kernel ids (include/decik_nf4.h)
-PLAN_GLU, PLAN_LORA, PLAN_NO_SPLIT, PLAN_NESTED = 1, 2, 4, 8
+PLAN_GLU, PLAN_LORA, PLAN_NO_SPLIT, PLAN_NESTED, PLAN_PARTS = 1, 2, 4, 8, 16
 # dk_nf4_linear_plan's kernel ids (2, an earlier input-gradient kernel, is no longer returned)
 PLAN_KERNELS = ("nf4_fwd_kernel", "nf4_fwd8_kernel", "retired", "nf4_bwd8_kernel", "nf4_gemv_kernel",
                 "nf4_skinny_kernel")

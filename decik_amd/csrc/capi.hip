@@ -532,8 +532,18 @@ int dk_nf4_linear_plan(int backward, int64_t m, int64_t k, const int64_t* ns, in
     const bool single = (flags & DK_PLAN_NO_SPLIT) != 0;
     GemmPlan p;
     int kernel;
+    int launches = 1, splits_b = 0;
     if (backward) {
-        p = plan_bwd(m, k, ns, ngroups, glu, single);
+        if (single) {
+            p = plan_bwd(m, k, ns, ngroups, glu, true);
+        } else {
+            const BwdParts parts = plan_bwd_parts(m, k, ns, ngroups, glu);
+            p = parts.a;
+            if (parts.two) {
+                launches = 2;
+                splits_b = parts.b.splits;
+            }
+        }
         kernel = 3;  // nf4_bwd8_kernel
     } else if (small_m_forward(m, glu, lora, ns, ngroups) && gemv_requested(m, k)) {
         p = GemmPlan{};
@@ -554,6 +564,10 @@ int dk_nf4_linear_plan(int backward, int64_t m, int64_t k, const int64_t* ns, in
     out[1] = p.waves;
     out[2] = p.splits;
     out[3] = kernel;
+    if (flags & DK_PLAN_PARTS) {
+        out[4] = launches;
+        out[5] = splits_b;
+    }
     return 0;
 }
 

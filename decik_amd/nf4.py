@@ -204,15 +204,18 @@ def linear_rope_forward(x16, items, cos, sin, head_dim, rope_mask, lora_rank=0):
 
 def launch_plan(backward, m, k, ns, glu=False, lora=False, no_split=False, blocksize=64, nested=False):
     """The plan dk_nf4_linear_fwd / dk_nf4_linear_bwd choose for these shapes (dk_nf4_linear_plan):
-    dict(rows_blocks, waves, splits, kernel). glu: the fused GLU forward or the SwiGLU epilogue of
-    the backward; lora: some weight has LoRA terms; blocksize: the largest block size; nested: the
+    dict(rows_blocks, waves, splits, kernel, launches, splits_second) -- the first GEMM launch's
+    tiling, the call's GEMM launches (2: an input gradient's left-over columns run as a second
+    launch) and that launch's splits. glu: the fused GLU forward or the SwiGLU epilogue of the
+    backward; lora: some weight has LoRA terms; blocksize: the largest block size; nested: the
     fused GLU forward's weights carry nested statistics."""
     ns_arr = (ctypes.c_int64 * len(ns))(*ns)
-    out = (ctypes.c_int32 * 4)()
+    out = (ctypes.c_int32 * 6)()
     flags = (_lib.PLAN_GLU if glu else 0) | (_lib.PLAN_LORA if lora else 0) | (_lib.PLAN_NO_SPLIT if no_split else 0)
-    flags |= _lib.PLAN_NESTED if nested else 0
+    flags |= (_lib.PLAN_NESTED if nested else 0) | _lib.PLAN_PARTS
     check(lib().dk_nf4_linear_plan(1 if backward else 0, m, k, ns_arr, len(ns), flags, blocksize, out))
-    return dict(rows_blocks=out[0], waves=out[1], splits=out[2], kernel=_lib.PLAN_KERNELS[out[3]])
+    return dict(rows_blocks=out[0], waves=out[1], splits=out[2], kernel=_lib.PLAN_KERNELS[out[3]],
+                launches=out[4], splits_second=out[5])
 
 
 def linear_backward(items, m, k, dx=None, dx_fp32=False, lora_rank=0):

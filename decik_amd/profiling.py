@@ -118,7 +118,7 @@ def counter_summary(run_dirs_prefixes, title, commands, match=r"dk::"):
     return "\n".join(out) + "\n"
 
 
-def traffic(fetch_dir, write_dir, prefix, match, commands, launch=None):
+def traffic(fetch_dir, write_dir, prefix, match, commands, launch=None, plan=None, commit=None):
     def load(run_dir):
         rows = sorted(_rows(run_dir, prefix, "counter_collection"), key=lambda r: int(r["Dispatch_Id"]))
         rx = re.compile(match)
@@ -150,7 +150,8 @@ def traffic(fetch_dir, write_dir, prefix, match, commands, launch=None):
     return dict(note="HBM bytes per call of one launch: FETCH_SIZE and WRITE_SIZE (KiB per dispatch, mean over "
                      "the dispatches) of its kernels, scaled so that the fp32->fp16 conversion of 128 Mi values "
                      "reads 512 MiB and writes 256 MiB",
-                launch=launch, match=match, bytes_per_call=round(total), kernels=detail, commands=list(commands),
+                launch=launch, plan=plan, commit=commit, match=match, bytes_per_call=round(total), kernels=detail,
+                commands=list(commands),
                 calibration=dict(kernel=_short(cal[0], 100), fetch_kib=cal_f, write_kib=cal_w,
                                  fetch_scale=round(sf, 4), write_scale=round(sw, 4)))
 
@@ -176,6 +177,10 @@ def main(argv=None):
     f.add_argument("--match", required=True)
     f.add_argument("--command", action="append", required=True)
     f.add_argument("--launch", default=None, help="the launch kind bench.py names (its roofline reads the file)")
+    f.add_argument("--plan", default=None,
+                   help="JSON of the launch plan the counters were taken on (bench.py's mlp_plan(launch)): "
+                        "bench.py ignores the file once the planner picks another plan")
+    f.add_argument("--commit", default=None, help="the commit the counters were taken on")
     a = ap.parse_args(argv)
     if a.cmd == "trace":
         sys.stdout.write(trace_summary(a.dir, a.prefix, a.title, a.command, a.match))
@@ -183,7 +188,9 @@ def main(argv=None):
         runs = [tuple(r.rsplit(":", 1)) for r in a.runs]
         sys.stdout.write(counter_summary(runs, a.title, a.command, a.match))
     else:
-        json.dump(traffic(a.fetch_dir, a.write_dir, a.prefix, a.match, a.command, a.launch), sys.stdout, indent=1)
+        plan = json.loads(a.plan) if a.plan else None
+        json.dump(traffic(a.fetch_dir, a.write_dir, a.prefix, a.match, a.command, a.launch, plan, a.commit),
+                  sys.stdout, indent=1)
         sys.stdout.write("\n")
 
 

@@ -278,7 +278,10 @@ int dk_swiglu_bwd(const uint16_t* grad, const uint16_t* gate, const uint16_t* up
  * tuning. flags: DK_PLAN_GLU (forward: the fused GLU mode of dk_nf4_glu_fwd; backward: the SwiGLU
  * epilogue of dk_nf4_linear_bwd_swiglu), DK_PLAN_LORA (some group has LoRA terms),
  * DK_PLAN_NO_SPLIT (a single pass), DK_PLAN_NESTED (with DK_PLAN_GLU, forward: the weights carry
- * nested statistics). blocksize: the largest block size of the groups' weights.
+ * nested statistics), DK_PLAN_PARTS (out holds 6 values: out[4] = GEMM launches of the call, 2
+ * when an input gradient whose tiles overrun whole rounds of CUs runs its left-over columns as a
+ * second launch, and out[5] = that launch's contraction splits; out[0..3] then describe the
+ * first launch). blocksize: the largest block size of the groups' weights.
  * out[0] = 32-token row blocks per tile, out[1] = waves per work-group, out[2] = contraction
  * splits, out[3] = kernel (0 nf4_fwd_kernel, 1 nf4_fwd8_kernel, 2 no longer returned (an
  * earlier input-gradient kernel), 3 nf4_bwd8_kernel, 4 nf4_gemv_kernel (forward launches of one
@@ -292,6 +295,7 @@ int dk_swiglu_bwd(const uint16_t* grad, const uint16_t* gate, const uint16_t* up
 #define DK_PLAN_LORA 2
 #define DK_PLAN_NO_SPLIT 4
 #define DK_PLAN_NESTED 8
+#define DK_PLAN_PARTS 16
 int dk_nf4_linear_plan(int backward, int64_t m, int64_t k, const int64_t* ns, int ngroups, int flags,
                        int blocksize, int32_t* out);
 

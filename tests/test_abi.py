@@ -180,10 +180,23 @@ def test_launch_plans():
             os.environ["DECIK_SMALL_M"] = old_sm
     glu = launch_plan(False, 830, 1536, [8960, 8960], glu=True)
     assert glu["splits"] == 1 and glu["kernel"] == "nf4_fwd8_kernel"
+    # nested statistics in the fused GLU forward: eight-wave variants only (at every M)
+    for m in (1, 8, 64, 830):
+        assert launch_plan(False, m, 1536, [8960, 8960], glu=True, nested=True)["waves"] == 8
+    # an input gradient whose tiles overrun a round of CUs by a partial round runs the left-over
+    # columns as a second, split launch (7B down at 830 tokens: 296 tiles of 224 x 256); the MLP
+    # launches, and launches that fill whole rounds, stay one launch
+    down7 = launch_plan(True, 830, 18944, [3584])
+    assert down7["launches"] == 2 and down7["splits"] == 1 and down7["splits_second"] > 1
+    for m, k, ns in ((830, 1536, [8960, 8960]), (830, 8960, [1536]), (8192, 3584, [3584]), (830, 3584, [18944])):
+        assert launch_plan(True, m, k, ns)["launches"] == 1
+    arr = (ctypes.c_int64 * 1)(3584)
+    need = _lib.lib().dk_nf4_linear_bwd_workspace(830, 18944, arr, 1)
+    assert need == down7["splits_second"] * 830 * (18944 - 64 * 256) * 4
     # 64 and 128 token rows: the eight-wave forward kernel on 64- / 128-token tiles (two waves
     # per SIMD where the four-wave kernel's tiles left one)
-    assert launch_plan(False, 64, 3584, [18944]) == dict(rows_blocks=2, waves=8, splits=3, kernel="nf4_fwd8_kernel")
-    assert launch_plan(False, 128, 3584, [18944]) == dict(rows_blocks=4, waves=8, splits=3, kernel="nf4_fwd8_kernel")
+    assert launch_plan(False, 64, 3584, [18944]) == dict(rows_blocks=2, waves=8, splits=3, kernel="nf4_fwd8_kernel", launches=1, splits_second=0)
+    assert launch_plan(False, 128, 3584, [18944]) == dict(rows_blocks=4, waves=8, splits=3, kernel="nf4_fwd8_kernel", launches=1, splits_second=0)
     assert launch_plan(False, 64, 3584, [18944, 18944], glu=True)["rows_blocks"] == 2
     # k % blocksize != 0: the eight-wave forward kernel may not run
     assert launch_plan(False, 830, 1536, [8960], blocksize=1024)["kernel"] == "nf4_fwd_kernel"
@@ -192,7 +205,7 @@ def test_launch_plans():
     try:
         os.environ["DECIK_BWD_PLAN"] = "8,3,8"
         assert launch_plan(True, 830, 1536, [8960]) == dict(rows_blocks=8, waves=8, splits=3,
-                                                             kernel="nf4_bwd8_kernel")
+                                                             kernel="nf4_bwd8_kernel", launches=1, splits_second=0)
         # no SwiGLU epilogue with 8 token blocks: the forced plan does not apply
         assert launch_plan(True, 830, 1536, [8960], glu=True)["rows_blocks"] != 8
         # variants that spilled registers are not offered: a forced plan naming one is ignored
@@ -200,7 +213,7 @@ def test_launch_plans():
         assert launch_plan(True, 830, 1536, [8960])["rows_blocks"] != 9
         os.environ["DECIK_BWD_PLAN"] = "4,2,8,256"
         assert launch_plan(True, 830, 1536, [8960]) == dict(rows_blocks=4, waves=8, splits=2,
-                                                             kernel="nf4_bwd8_kernel")
+                                                             kernel="nf4_bwd8_kernel", launches=1, splits_second=0)
         # the retired four-wave input-gradient variants are not offered: a forced plan naming one
         # is ignored
         os.environ["DECIK_BWD_PLAN"] = "2,1,4"
