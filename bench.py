@@ -169,6 +169,7 @@ def bench_mlp(steps, warmup, device, n_sets=None, only=None):
         t1.record()
         torch.cuda.synchronize()
         ms_step = t0.elapsed_time(t1) / steps
+    graph_ms = graph_mlp_steps(step, n_sets) if only is None else None
     # Per-launch timing: each launch kind back to back (same inputs as one step, weight sets
     # rotating), HIP events on the launch stream around the loop. Unlike events between the
     # launches of one step, this excludes host-side gaps, so the average matches the kernel's
@@ -232,7 +233,43 @@ def bench_mlp(steps, warmup, device, n_sets=None, only=None):
         nf4._scales = saved_scales
     step_flops = sum(flops.values())
     return dict(ms_step=ms_step, launch_ms=launch_ms, flops=flops, symbol=symbol,
-                step_flops=step_flops, n_sets=n_sets, uncached_ms=uncached)
+                step_flops=step_flops, n_sets=n_sets, uncached_ms=uncached, graph_ms=graph_ms)
+
+
+def graph_mlp_steps(step, n_sets, reps=3):
+    """The MLP step (its six kernels) over every weight set, captured once in a HIP graph and
+    replayed: ms per step with the host's launch cost and the gaps between eager launches taken
+    out. The replay's last outputs must equal the same step run eagerly; None if capture fails."""
+    import torch
+
+    try:
+        g = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step(0)  # warm-up on the capture stream
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            outs = [step(i) for i in range(n_sets)]
+        g.replay()
+        torch.cuda.synchronize()
+        ref = step(n_sets - 1)
+        torch.cuda.synchronize()
+        if not (torch.equal(outs[-1][0], ref[0]) and torch.equal(outs[-1][1], ref[1])):
+            return None
+        times = []
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            g.replay()
+            b.record()
+            torch.cuda.synchronize()
+            times.append(a.elapsed_time(b) / n_sets)
+        del g, outs
+        return statistics.median(times)
+    except Exception:  # noqa: BLE001 - reported as null
+        return None
 
 
 def bench_dequant(iters, warmup, device, n_layers=24):
@@ -785,7 +822,7 @@ def fused_bytes(n, k, m):
     return nf4_bytes(n, k) + 2 * m * (n + k)
 
 
-def bench_c5(device, reps=3, min_bytes=512 << 20):
+def bench_c5(device, reps=3, min_bytes=512 << 20, m_list=C5_M, shapes=tuple(s[0] for s in QWEN7_SHAPES)):
     """Each 7B projection shape at every M: forward Y = X.W^T (the GEMV kernel at M = 1, the
     small-M kernel at M = 8, the MFMA kernels above) and, for M >= 64, the input gradient
     dX = dY.W. Enough copies of the weight to total more than 512 MB of NF4 data are called back
@@ -803,6 +840,8 @@ def bench_c5(device, reps=3, min_bytes=512 << 20):
 
     rows = []
     for si, (name, n, k) in enumerate(QWEN7_SHAPES):
+        if name not in shapes:
+            continue
         copies = max(2, min(600, -(-min_bytes // nf4_bytes(n, k))))
         base = seeded_fp16((n, k), 30_000 + si, 0.02, device)
         ws = []
@@ -810,7 +849,7 @@ def bench_c5(device, reps=3, min_bytes=512 << 20):
             # distinct weights (a sign flip of a seeded pattern per copy) so no two calls share lines
             ws.append(quantize_nf4(base if c % 2 == 0 else -base, blocksize=64, compress_statistics=True))
         del base
-        for m in C5_M:
+        for m in m_list:
             x = seeded_fp16((m, k), 31_000 + m, 1.0, device)
             dy = seeded_fp16((m, n), 32_000 + m, 1e-2, device)
             kinds = {"fwd": lambda p, q: nf4.linear_forward(x, [dict(packed=p, qs=q)])[0]}
@@ -926,9 +965,13 @@ def main():
     ap.add_argument("--configs", default="c3,c4,c5",
                     help="comma-separated subset of c3, c4, c5 to run besides the headline MLP step")
     ap.add_argument("--only", default=None,
-                    choices=["fwd_gate_up", "fwd_down", "bwd_down", "bwd_gate_up", "dequant"],
+                    choices=["fwd_gate_up", "fwd_down", "bwd_down", "bwd_gate_up", "dequant", "c5"],
                     help="time only this launch kind, or the standalone dequantization (for counter runs); "
                          "prints its roofline only")
+    ap.add_argument("--c5-m", default=",".join(str(m) for m in C5_M),
+                    help="token counts of the Qwen2.5-7B sweep (C5)")
+    ap.add_argument("--c5-shapes", default=",".join(s[0] for s in QWEN7_SHAPES),
+                    help="projections of the Qwen2.5-7B sweep (C5): q/o, k/v, gate/up, down")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also convert 128 Mi fp32 values to fp16 three times: one elementwise "
                          "kernel of known traffic (512 MiB read, 256 MiB written), to scale "
@@ -952,6 +995,15 @@ def main():
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
 
+    c5_m = tuple(int(v) for v in args.c5_m.split(",") if v.strip())
+    c5_shapes = tuple(v.strip() for v in args.c5_shapes.split(",") if v.strip())
+    if args.only == "c5":
+        # counter runs of the 7B sweep alone (the small-M kernels' traffic)
+        if args.copy_probe:
+            copy_probe(device)
+        with no_gc():
+            print(json.dumps(dict(only="c5", c5_qwen7b_sweep=bench_c5(device, m_list=c5_m, shapes=c5_shapes))))
+        return
     if args.only == "dequant":
         if args.copy_probe:
             copy_probe(device)
@@ -980,7 +1032,7 @@ def main():
         torch.cuda.empty_cache()
     if "c5" in configs:
         with no_gc():
-            c5 = bench_c5(device)
+            c5 = bench_c5(device, m_list=c5_m, shapes=c5_shapes)
         torch.cuda.empty_cache()
 
     # Dominant launch: the fused GEMM call with the largest time. Its kernels: the GEMM kernel,
@@ -1023,6 +1075,11 @@ def main():
                  for k, v in mlp["launch_ms"].items()},
         kernels_uncached_nested={k: dict(ms=round(v, 4), tflops=round(mlp["flops"][k] / (v * 1e-3) / 1e12, 1))
                                  for k, v in mlp["uncached_ms"].items()},
+        graph_step=None if mlp["graph_ms"] is None else dict(
+            ms_per_step=round(mlp["graph_ms"], 4),
+            tflops=round(mlp["step_flops"] / (mlp["graph_ms"] * 1e-3) / 1e12, 2),
+            note="the same step captured once in a HIP graph (one step per weight set) and replayed; "
+                 "value stays the eager step"),
     )
     if c3 is not None:
         line["c3_attention_step"] = c3

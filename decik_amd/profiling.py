@@ -7,6 +7,7 @@ This module reduces them to short markdown tables (or, for the traffic of one la
   python -m decik_amd.profiling trace <dir> <prefix> --title T --command C [--match RE]
   python -m decik_amd.profiling counters <dir> <prefix> --title T --command C [--match RE]
   python -m decik_amd.profiling traffic <fetch_dir> <write_dir> <prefix> --match RE --command C --command C
+  python -m decik_amd.profiling traffic-table <fetch_dir:write_dir:prefix:label> ... --title T --command C ...
 
 `trace`: rocprofv3's own per-kernel totals, then every matching kernel by launch shape (grid):
 launches, median / mean / min duration, VGPRs, LDS. `counters`: per kernel and grid the mean of
@@ -14,7 +15,8 @@ each counter over its dispatches and the usual ratios (VALU and LDS instructions
 busy share, wait share). `traffic`: HBM bytes per dispatch of the launch matched by RE (its most
 frequent kernel and grid, plus the split-K reduction dispatched right after it) from FETCH_SIZE
 and WRITE_SIZE, each scaled by what the counter reads for the fp32 -> fp16 conversion of 128 Mi
-values that bench.py --copy-probe runs (512 MiB read, 256 MiB written).
+values that bench.py --copy-probe runs (512 MiB read, 256 MiB written). `traffic-table`: the same
+scaled bytes for every matching kernel and grid of several pass pairs, as a markdown table.
 """
 
 import argparse
@@ -156,6 +158,37 @@ def traffic(fetch_dir, write_dir, prefix, match, commands, launch=None, plan=Non
                                  fetch_scale=round(sf, 4), write_scale=round(sw, 4)))
 
 
+def traffic_table(runs, title, commands, match):
+    """Markdown table of HBM bytes per dispatch of every (kernel, grid) matching `match` in
+    several FETCH_SIZE / WRITE_SIZE pass pairs (runs: (fetch_dir, write_dir, prefix, label)), each
+    pass scaled by its own fp32 -> fp16 conversion probe (bench.py --copy-probe)."""
+    out = [f"# rocprofv3 HBM traffic: {title}", "", "Commands (from /tmp, TMPDIR=/tmp; one pass each):", "", "```"]
+    out += list(commands) + ["```", "",
+                             "Bytes per dispatch: FETCH_SIZE and WRITE_SIZE (KiB, mean over the dispatches of "
+                             "the kernel and grid), scaled so that the fp32 -> fp16 conversion of 128 Mi values "
+                             "reads 512 MiB and writes 256 MiB.", "",
+                             "| run | kernel | grid | dispatches | read MB | written MB | total MB |",
+                             "|---|---|---:|---:|---:|---:|---:|"]
+    rx = re.compile(match)
+    for fetch_dir, write_dir, prefix, label in runs:
+        per = []
+        for d in (fetch_dir, write_dir):
+            acc = collections.defaultdict(list)
+            for r in _rows(d, prefix, "counter_collection"):
+                acc[(r["Kernel_Name"], int(r["Grid_Size"]))].append(float(r["Counter_Value"]))
+            per.append(acc)
+        fetch, write = per
+        cal = max((k for k in fetch if "float16_copy" in k[0]), key=lambda k: max(fetch[k]))
+        sf, sw = (512 * 1024) / max(fetch[cal]), (256 * 1024) / max(write[cal])
+        for k in sorted(fetch, key=lambda k: (k[0], k[1])):
+            if not rx.search(k[0]) or k not in write:
+                continue
+            f = statistics.fmean(fetch[k]) * 1024 * sf / 1e6
+            w = statistics.fmean(write[k]) * 1024 * sw / 1e6
+            out.append(f"| {label} | `{_short(k[0], 60)}` | {k[1]} | {len(fetch[k])} | {f:.2f} | {w:.2f} | {f + w:.2f} |")
+    return "\n".join(out) + "\n"
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(prog="python -m decik_amd.profiling")
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -181,9 +214,16 @@ def main(argv=None):
                    help="JSON of the launch plan the counters were taken on (bench.py's mlp_plan(launch)): "
                         "bench.py ignores the file once the planner picks another plan")
     f.add_argument("--commit", default=None, help="the commit the counters were taken on")
+    tt = sub.add_parser("traffic-table")
+    tt.add_argument("runs", nargs="+", help="fetch_dir:write_dir:prefix:label of each pass pair")
+    tt.add_argument("--title", required=True)
+    tt.add_argument("--command", action="append", required=True)
+    tt.add_argument("--match", default=r"dk::")
     a = ap.parse_args(argv)
     if a.cmd == "trace":
         sys.stdout.write(trace_summary(a.dir, a.prefix, a.title, a.command, a.match))
+    elif a.cmd == "traffic-table":
+        sys.stdout.write(traffic_table([tuple(r.split(":", 3)) for r in a.runs], a.title, a.command, a.match))
     elif a.cmd == "counters":
         runs = [tuple(r.rsplit(":", 1)) for r in a.runs]
         sys.stdout.write(counter_summary(runs, a.title, a.command, a.match))
