@@ -4,6 +4,7 @@
 #include <mutex>
 #include <set>
 #include <tuple>
+#include <unordered_map>
 #include <string>
 
 #include "dk_internal.h"
@@ -91,7 +92,10 @@ int num_cus() {
     static std::mutex mu;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDevs) return 256;
+    thread_local int t_dev = -1, t_cus = 0;  // this thread's last device: no lock on the planner's hot path
+    if (dev == t_dev) return t_cus;
     std::lock_guard<std::mutex> lock(mu);
+    t_dev = dev;
     if (cus[dev] == 0) {
         hipDeviceProp_t prop;
         if (hipGetDeviceProperties(&prop, dev) == hipSuccess && prop.multiProcessorCount > 0)
@@ -99,7 +103,48 @@ int num_cus() {
         else
             cus[dev] = 256;
     }
+    t_cus = cus[dev];
     return cus[dev];
+}
+
+// Plans are pure functions of their arguments, the device's CU count and the tuning variables
+// (DECIK_FWD_PLAN, DECIK_BWD_PLAN, DECIK_SMALL_M), and a plan evaluates hundreds of (variant,
+// splits) estimates: every launch and workspace query would repeat them. PlanMemo keeps them per
+// argument list (cleared past 4096 entries).
+template <typename P>
+class PlanMemo {
+  public:
+    template <typename F>
+    P get(const std::string& key, F compute) {
+        {
+            std::lock_guard<std::mutex> lock(mu_);
+            const auto it = map_.find(key);
+            if (it != map_.end()) return it->second;
+        }
+        const P p = compute();
+        std::lock_guard<std::mutex> lock(mu_);
+        if (map_.size() >= 4096) map_.clear();
+        map_.emplace(key, p);
+        return p;
+    }
+
+  private:
+    std::mutex mu_;
+    std::unordered_map<std::string, P> map_;
+};
+
+std::string plan_key(char kind, std::initializer_list<int64_t> vals, const int64_t* ns, int ngroups) {
+    std::string key(1, kind);
+    auto add = [&key](int64_t v) { key.append(reinterpret_cast<const char*>(&v), sizeof v); };
+    for (const int64_t v : vals) add(v);
+    for (int g = 0; g < ngroups; ++g) add(ns[g]);
+    add(num_cus());
+    for (const char* var : {"DECIK_FWD_PLAN", "DECIK_BWD_PLAN", "DECIK_SMALL_M"}) {
+        const char* v = std::getenv(var);
+        key.push_back('|');
+        if (v != nullptr) key.append(v);
+    }
+    return key;
 }
 
 int pad8(int g) { return (g + 7) & ~7; }
@@ -264,8 +309,8 @@ static_assert(kFwdVariants[kNumFwd4Variants - 1].waves == 4 && kFwdVariants[kNum
 // needs the finished sums). fwd8_ok: the eight-wave kernel may run (see above). fwd4_ok: the
 // four-wave kernel may run (not for GLU launches on nested statistics: its GLU waves mix the two
 // weights' rows and keep one code2 table).
-GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool glu, bool fwd8_ok,
-                  bool no_split = false, int min_splits = 1, bool fwd4_ok = true) {
+GemmPlan plan_fwd_compute(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool glu, bool fwd8_ok,
+                          bool no_split, int min_splits, bool fwd4_ok) {
     GemmPlan p{};
     p.steps = (int)((k + kFwdBK - 1) / kFwdBK);
     p.n_tiles = 0;
@@ -298,8 +343,8 @@ GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool glu
 
 // swiglu: the SwiGLU epilogue of dk_nf4_linear_bwd_swiglu (never split; the variants that have it).
 // max_partial_bytes: the split-K partial slabs must fit in that many bytes.
-GemmPlan plan_bwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool swiglu, bool no_split = false,
-                  int64_t max_partial_bytes = INT64_MAX) {
+GemmPlan plan_bwd_compute(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool swiglu, bool no_split,
+                          int64_t max_partial_bytes) {
     GemmPlan p{};
     p.steps = 0;
     for (int g = 0; g < ngroups; ++g) p.steps += (int)((ns[g] + kBwdBC - 1) / kBwdBC);
@@ -318,6 +363,20 @@ GemmPlan plan_bwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool swi
     p.m_tiles = (int)((m + kRowUnit * p.mt - 1) / (kRowUnit * p.mt));
     finish_plan(p, m, k);
     return p;
+}
+
+GemmPlan plan_fwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool glu, bool fwd8_ok,
+                  bool no_split = false, int min_splits = 1, bool fwd4_ok = true) {
+    static PlanMemo<GemmPlan> memo;
+    return memo.get(plan_key('f', {m, k, glu, fwd8_ok, no_split, min_splits, fwd4_ok}, ns, ngroups),
+                    [&] { return plan_fwd_compute(m, k, ns, ngroups, glu, fwd8_ok, no_split, min_splits, fwd4_ok); });
+}
+
+GemmPlan plan_bwd(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool swiglu, bool no_split = false,
+                  int64_t max_partial_bytes = INT64_MAX) {
+    static PlanMemo<GemmPlan> memo;
+    return memo.get(plan_key('b', {m, k, swiglu, no_split, max_partial_bytes}, ns, ngroups),
+                    [&] { return plan_bwd_compute(m, k, ns, ngroups, swiglu, no_split, max_partial_bytes); });
 }
 
 // Input-gradient launches whose tiles overrun whole rounds of resident work-groups by a partial
@@ -341,8 +400,8 @@ const VariantCost* bwd_variant(int mt) {
     return &kBwdVariants[0];
 }
 
-BwdParts plan_bwd_parts(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool swiglu,
-                        int64_t max_partial_bytes = INT64_MAX) {
+BwdParts plan_bwd_parts_compute(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool swiglu,
+                                int64_t max_partial_bytes) {
     BwdParts r;
     r.a = plan_bwd(m, k, ns, ngroups, swiglu, false, max_partial_bytes);
     const char* forced = std::getenv("DECIK_BWD_PLAN");
@@ -372,11 +431,18 @@ int64_t workspace_bytes(const BwdParts& p) {
     return std::max(workspace_bytes(p.a), p.two ? workspace_bytes(p.b) : (int64_t)0);
 }
 
+BwdParts plan_bwd_parts(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool swiglu,
+                        int64_t max_partial_bytes = INT64_MAX) {
+    static PlanMemo<BwdParts> memo;
+    return memo.get(plan_key('p', {m, k, swiglu, max_partial_bytes}, ns, ngroups),
+                    [&] { return plan_bwd_parts_compute(m, k, ns, ngroups, swiglu, max_partial_bytes); });
+}
+
 // nf4_skinny_kernel (forward, m <= kSkinnyMaxM): 64-row groups; contraction splits while the
 // launch still has at most one work-group per CU and every split keeps at least two 128-wide
 // super-steps per wave (16 per work-group). no_split: a single pass (no workspace).
 constexpr int kSkinnyRows = 64, kSkinnyStep = 128, kSkinnyWaves = 8;
-GemmPlan plan_skinny(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool no_split = false) {
+GemmPlan plan_skinny_compute(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool no_split) {
     GemmPlan p{};
     int64_t rgroups = 0, ncols = 0;
     for (int g = 0; g < ngroups; ++g) {
@@ -402,6 +468,12 @@ GemmPlan plan_skinny(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool 
     p.waves = kSkinnyWaves;
     finish_plan(p, m, ncols);
     return p;
+}
+
+GemmPlan plan_skinny(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool no_split = false) {
+    static PlanMemo<GemmPlan> memo;
+    return memo.get(plan_key('s', {m, k, no_split}, ns, ngroups),
+                    [&] { return plan_skinny_compute(m, k, ns, ngroups, no_split); });
 }
 
 // Forward launches of at most kSkinnyMaxM token rows without LoRA terms or the GLU epilogue run

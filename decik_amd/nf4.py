@@ -256,6 +256,43 @@ def linear_backward(items, m, k, dx=None, dx_fp32=False, lora_rank=0):
     return dx
 
 
+def _forward_one(x2, packed, qs, bias16):
+    """linear_forward of one weight without LoRA terms (NF4Linear's call): the same launch with
+    less Python per call (an eager step makes one per projection and direction)."""
+    dev = x2.device
+    m, k = x2.shape
+    n = int(qs.shape[0])
+    w, kp = _lib.DESCS.get(packed, qs, dev, _scales)
+    out = torch.empty((m, n), dtype=torch.float16, device=dev)
+    groups = (LinearFwdGroup * 1)()
+    g = groups[0]
+    g.w = w
+    if bias16 is not None:
+        g.bias = bias16.data_ptr()
+    g.y = out.data_ptr()
+    g.ldy = n
+    ws, ws_bytes = _lib.WORKSPACE.get(_workspace_need(True, m, k, (n,)), dev)
+    check(lib().dk_nf4_linear_fwd(x2.data_ptr(), m, k, x2.stride(0), groups, 1, 0, ptr(ws), ws_bytes,
+                                  stream_of(dev)))
+    return out
+
+
+def _backward_one(g2, packed, qs, k):
+    """linear_backward of one weight without LoRA terms (NF4Linear's input gradient)."""
+    dev = g2.device
+    m = g2.shape[0]
+    w, kp = _lib.DESCS.get(packed, qs, dev, _scales)
+    dx = torch.empty((m, k), dtype=torch.float16, device=dev)
+    groups = (LinearBwdGroup * 1)()
+    g = groups[0]
+    g.w = w
+    g.dy = g2.data_ptr()
+    g.lddy = g2.stride(0)
+    ws, ws_bytes = _lib.WORKSPACE.get(_workspace_need(False, m, k, (int(qs.shape[0]),)), dev)
+    check(lib().dk_nf4_linear_bwd(groups, 1, m, k, dx.data_ptr(), k, 0, 0, ptr(ws), ws_bytes, stream_of(dev)))
+    return dx
+
+
 def _fwd_group(g, it, dev, keep):
     qs = it["qs"]
     w, kp = _lib.DESCS.get(it["packed"], qs, dev, _scales)
@@ -338,8 +375,7 @@ class NF4Linear(torch.autograd.Function):
         ctx.x_shape = x16.shape
         warmup.wait()
         if _fusable(x16, packed, quant_state, bias16) and x16.numel() > 0:
-            (y,) = linear_forward(x16.contiguous(), [dict(packed=packed, qs=quant_state,
-                                                          bias=bias16)])
+            y = _forward_one(_rows(x16.contiguous()), packed, quant_state, bias16)
             return y.reshape(*x16.shape[:-1], y.shape[-1])
         weight = dequantize_nf4(packed, quant_state)
         return torch.nn.functional.linear(x16, weight, bias16)
@@ -352,9 +388,7 @@ class NF4Linear(torch.autograd.Function):
             qs = ctx.quant_state
             k = ctx.x_shape[-1]
             if fused_ok(qs, k) and _aligned(g16) and g16.numel() > 0:
-                m = g16.numel() // g16.shape[-1]
-                grad_x = linear_backward([dict(packed=ctx.packed, qs=qs, dy=g16)], m, k)
-                grad_x = grad_x.reshape(ctx.x_shape)
+                grad_x = _backward_one(_rows(g16), ctx.packed, qs, k).reshape(ctx.x_shape)
             else:
                 weight = dequantize_nf4(ctx.packed, qs)
                 grad_x = torch.matmul(g16, weight)
