@@ -299,3 +299,26 @@ def test_scale_cache_version_key_tracks_statistics():
     assert k1 != k0
     qs.absmax = qs.absmax.clone()
     assert _lib._version_key(qs) != k1
+
+
+def test_plan_memo_follows_the_tuning_variables(monkeypatch):
+    """Plans are memoized per argument list; a forced plan (DECIK_FWD_PLAN / DECIK_BWD_PLAN) set
+    or cleared between calls is seen by the next call, and the memo gives the same plan again."""
+    from decik_amd.nf4 import launch_plan
+
+    monkeypatch.delenv("DECIK_FWD_PLAN", raising=False)
+    monkeypatch.delenv("DECIK_BWD_PLAN", raising=False)
+    base = launch_plan(False, 830, 1536, [1536])
+    assert launch_plan(False, 830, 1536, [1536]) == base
+    monkeypatch.setenv("DECIK_FWD_PLAN", "4,2")
+    forced = launch_plan(False, 830, 1536, [1536])
+    assert forced["rows_blocks"] == 4 and forced["splits"] == 2
+    monkeypatch.setenv("DECIK_FWD_PLAN", "7,3")
+    assert launch_plan(False, 830, 1536, [1536])["rows_blocks"] == 7
+    monkeypatch.delenv("DECIK_FWD_PLAN")
+    assert launch_plan(False, 830, 1536, [1536]) == base
+    bwd = launch_plan(True, 830, 1536, [1536])
+    monkeypatch.setenv("DECIK_BWD_PLAN", "4,1")
+    assert launch_plan(True, 830, 1536, [1536])["splits"] == 1
+    monkeypatch.delenv("DECIK_BWD_PLAN")
+    assert launch_plan(True, 830, 1536, [1536]) == bwd
