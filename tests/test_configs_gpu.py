@@ -227,3 +227,22 @@ def test_c5_down_input_gradient_two_launches(dx_fp32, qwen7b_weights, device, mo
     ref = O.linear_dx_ref(dy[rows].cpu().numpy(), w16)
     assert_close(dx[rows], ref, what="7B down dX, two launches")
     assert_close(dx[rows][:, 16384:], ref[:, 16384:], what="7B down dX, remainder columns")
+
+
+def test_c5_down_input_gradient_two_launches_lora(qwen7b_weights, device):
+    """The two-launch input gradient with a rank-16 LoRA term: each launch adds GU . A for its own
+    columns (split 0 of the second launch), against the oracle."""
+    from decik_amd.nf4 import linear_backward
+
+    packed, qs, w16 = qwen7b_weights["down"]
+    n, k = (int(v) for v in qs.shape)
+    m, r = 830, 16
+    dy = randn16((m, n), seed=741, device=device, std=1e-2)
+    gu = randn16((m, r), seed=742, device=device, std=0.05)
+    a = randn16((r, k), seed=743, device=device, std=0.05)
+    dx = linear_backward([dict(packed=packed, qs=qs, dy=dy, lora_gu=gu, lora_a=a)], m, k, lora_rank=r)
+    torch.cuda.synchronize()
+    rows = np.arange(0, m, 11)
+    ref = O.linear_dx_ref(dy[rows].cpu().numpy(), w16) + gu[rows].float().cpu().numpy() @ a.float().cpu().numpy()
+    assert_close(dx[rows], ref, what="7B down dX + LoRA, two launches")
+    assert_close(dx[rows][:, 16384:], ref[:, 16384:], what="7B down dX + LoRA, remainder columns")

@@ -106,3 +106,24 @@ def test_noalloc_input_gradient_matches_allocating_entry(device):
     items = [(gate[0], gate[1], dg)]
     assert torch.equal(_run(items, 300, 1536, False, noalloc=False), _run(items, 300, 1536, False, noalloc=True))
     assert _lib.lib().dk_last_error() == b""
+
+
+def test_noalloc_two_launch_input_gradient(device):
+    """The 7B down-projection input gradient at 830 tokens runs as two launches (the left-over
+    columns split): its partials fit the scratch, so the static entry runs the same two launches
+    and gives the same bits, fp16 and fp32."""
+    from decik_amd.nf4 import launch_plan
+
+    assert launch_plan(True, 830, 18944, [3584])["launches"] == 2
+    assert 0 < _workspace_need(830, 18944, [3584]) <= 64 << 20
+    down = make_weight((3584, 18944), seed=311, device=device)
+    dy = randn16((830, 3584), seed=312, device=device, std=1e-2)
+    items = [(down[0], down[1], dy)]
+    for dx_fp32 in (False, True):
+        a = _run(items, 830, 18944, dx_fp32, noalloc=False)
+        b = _run(items, 830, 18944, dx_fp32, noalloc=True)
+        assert not torch.isnan(b.float()).any()
+        assert torch.equal(a, b)
+    rows = np.arange(0, 830, 37)
+    ref = O._f64(dy[torch.as_tensor(rows, device=device)].cpu().numpy()) @ O._f64(down[2])
+    assert_close(b[torch.as_tensor(rows, device=device)], ref.astype(np.float32), what="noalloc two launches")
