@@ -639,10 +639,26 @@ def bench_c3(steps, warmup, device):
             b.record()
             torch.cuda.synchronize()
             blocks.append(a.elapsed_time(b) / steps)
+        # the same eager steps with autograd's backward on the calling thread instead of its
+        # per-device worker thread (torch.autograd.set_multithreading_enabled(False)): the
+        # difference is the engine's thread hand-off, a host cost of torch, not of these kernels
+        single = []
+        with torch.autograd.set_multithreading_enabled(False):
+            for _ in range(3):
+                torch.cuda.synchronize()
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                for i in range(steps):
+                    fn(layers[i % n_sets])
+                    clear()
+                b.record()
+                torch.cuda.synchronize()
+                single.append(a.elapsed_time(b) / steps)
         launches, busy = count_kernels(lambda fn=fn: (fn(layers[-1]), clear()))
         graph_ms, graph_note = graph_steps(step_grads(forward), layers)
         res[name] = dict(ms=statistics.median(blocks), spread=(min(blocks), max(blocks)), launches=launches,
-                         busy_us=busy, graph_ms=graph_ms, graph_note=graph_note)
+                         busy_us=busy, graph_ms=graph_ms, graph_note=graph_note,
+                         single_ms=statistics.median(single))
     gemm = 2 * sum(gemm_flops(n, k) for name, n, k in QWEN15_SHAPES if name in ("q", "k", "v", "o"))
     lora_f = sum(2 * M * LORA_R * (HIDDEN + n) + 2 * M * LORA_R * (2 * HIDDEN + 2 * n) for n in (1536, 256))
     out = dict(workload="Qwen2.5-1.5B attention projections, one layer fwd+bwd, M=830 (8 packed sequences): "
@@ -653,6 +669,7 @@ def bench_c3(steps, warmup, device):
     for name, r in res.items():
         out[name] = dict(ms=round(r["ms"], 4), ms_range=[round(v, 4) for v in r["spread"]],
                          tflops=round((gemm + lora_f) / (r["ms"] * 1e-3) / 1e12, 1),
+                         backward_on_caller_ms=round(r["single_ms"], 4),
                          launches=r["launches"],
                          gpu_busy_ms=None if r["busy_us"] is None else round(r["busy_us"] / 1e3, 4),
                          graph_ms=None if r["graph_ms"] is None else round(r["graph_ms"], 4),
@@ -667,7 +684,10 @@ def bench_c3(steps, warmup, device):
         out["gpu_busy_speedup"] = round(res["reference_order"]["busy_us"] / res["fused"]["busy_us"], 3)
     out["note"] = ("ms: eager steps back to back (HIP events), bound by the host's Python and launch "
                    "overhead at this size: median of five blocks of steps (ms_range: the fastest and "
-                   "slowest block); gpu_busy_ms: the kernels' summed durations in one profiled step; "
+                   "slowest block); backward_on_caller_ms: the same eager steps with autograd's backward "
+                   "on the calling thread (torch.autograd.set_multithreading_enabled(False)), the "
+                   "difference being torch's hand-off to its device thread; gpu_busy_ms: the kernels' "
+                   "summed durations in one profiled step; "
                    "graph_ms: the same step over every layer's weights captured once in a HIP graph "
                    "(forward + torch.autograd.grad) and replayed, median of three replays, each "
                    "replay's last gradients equal to the eager step's bit for bit")
