@@ -114,10 +114,16 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
     const int cs0 = split * a.csteps_per_split;
     const int cs1 = min(a.csteps, cs0 + a.csteps_per_split);
 
+    // nested statistics: this thread's entry of every group's code2 table, written to LDS with the
+    // first group's code book, once that group's first loads are issued (one memory round trip
+    // for both; buffer loads of uniform pointers, which indexed loads would fetch and wait for)
+    float c2v[kMaxGroups] = {};
     if constexpr (NESTED) {
-        for (int gg = 0; gg < a.ngroups; ++gg)
-            if (tid < 256) ((float*)smem)[256 * gg + tid] = a.g[gg].w.code2[tid];
+#pragma unroll
+        for (int gg = 0; gg < kMaxGroups; ++gg)
+            if (gg < a.ngroups && tid < 256) c2v[gg] = bloadf(make_rsrc(sgpr(a.g[gg].w.code2), 1024u), 4u * tid);
     }
+    bool tables_written = false;
     uint8_t* wring = dring + DRING + wave * (3 * kB8WSlot);
     float* stab = (float*)(dring + DRING + kB8Waves * 3 * kB8WSlot + wave * kB8ScaleBytes);
     // this lane's transposed reads (slices j, j + 1 for even j): row 32 g + 8 j + (lane % 16) of
@@ -212,12 +218,11 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
         const uint32_t bs_shift = sgpr((uint32_t)G.w.bs_shift), bs2_shift = sgpr((uint32_t)G.w.bs2_shift);
         const float offset = NESTED ? *G.w.offset : 0.0f;
         const float* c2 = (const float*)smem + 256 * gi;
-        {
-            // the previous group's readers are past the barrier that ended its loop; this
-            // group's prologue barrier publishes the new book
-            const float* book = G.w.code;
-            if (tid < 256) lutT[tid] = float2_t{book[tid & 15], book[tid >> 4]};
-        }
+        // this group's code book: loaded here, written to LDS once the group's first steps are in
+        // flight (the previous group's readers are past the barrier that ended its loop; this
+        // group's prologue barrier publishes the new book)
+        const rsrc_t bkr = make_rsrc(sgpr(G.w.code), 64u);
+        const float book_lo = bloadf(bkr, 4u * (tid & 15)), book_hi = bloadf(bkr, 4u * ((tid >> 4) & 15));
 
         // Loads use per-lane offsets fixed for the group (bit 31 set where the lane's data lies
         // outside the tile or the weight: it reads zeros) against buffer descriptors whose base
@@ -331,6 +336,15 @@ __global__ __launch_bounds__(kB8Threads, 1) void nf4_bwd8_kernel(const BwdArgs a
         load_step(t0, 0, 0, true);
         load_step(t0 + 1, DBUF, kB8WSlot, t0 + 1 < t1);
         load_step(t0 + 2, 2 * DBUF, 2 * kB8WSlot, t0 + 2 < t1);
+        if (tid < 256) lutT[tid] = float2_t{book_lo, book_hi};
+        if constexpr (NESTED) {
+            if (!tables_written) {
+#pragma unroll
+                for (int gg = 0; gg < kMaxGroups; ++gg)
+                    if (gg < a.ngroups && tid < 256) ((float*)smem)[256 * gg + tid] = c2v[gg];
+                tables_written = true;
+            }
+        }
         wait_vmcnt<2 * NL>();
         lds_barrier();  // dY(t0) from every wave, code tables
         scales_1(0);

@@ -110,15 +110,23 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
     const int ks0 = split * a.ksteps_per_split;
     const int ks1 = min(a.ksteps, ks0 + a.ksteps_per_split);
 
-    {
-        const float* book = a.g[glu ? (tid >> 8) : gi].w.code;
-        lut2[tid] = float2_t{book[(tid >> 4) & 15], book[tid & 15]};
-    }
+    // this thread's code-book entry and code2 entry (GLU: threads 256..511 bring the up weight's
+    // table; the waves of each weight index their own), written to LDS once the ring's first
+    // loads are issued, so that the two memory round trips overlap
+    // (the table pointers are picked from uniform ones: indexed by thread, they would be fetched
+    // by a vector load and waited for before the tables themselves)
+    // (read through buffer descriptors of uniform pointers: indexed by thread, the pointers would
+    // be fetched by a vector load and waited for before the tables themselves)
+    const bool up_half = glu && tid >= 256;
+    const rsrc_t bk0 = make_rsrc(sgpr(glu ? a.g[0].w.code : W.code), 64u);
+    const rsrc_t bk1 = make_rsrc(sgpr(a.g[glu ? 1 : 0].w.code), 64u);
+    const float book_hi = bloadf(up_half ? bk1 : bk0, 4u * ((tid >> 4) & 15));
+    const float book_lo = bloadf(up_half ? bk1 : bk0, 4u * (tid & 15));
+    float c2v = 0.0f;
     if constexpr (NESTED) {
-        // GLU: threads 256..511 bring the up weight's table (the waves of each weight index
-        // their own)
-        if (glu) c2[tid] = a.g[tid >> 8].w.code2[tid & 255];
-        else if (tid < 256) c2[tid] = W.code2[tid];
+        const rsrc_t c0 = make_rsrc(sgpr(glu ? a.g[0].w.code2 : W.code2), 1024u);
+        const rsrc_t c1 = make_rsrc(sgpr(a.g[glu ? 1 : 0].w.code2), 1024u);
+        if (glu || tid < 256) c2v = bloadf(up_half ? c1 : c0, 4u * (tid & 255));
     }
     const float* const c2w = c2 + (glu ? 256 * (wave >> 2) : 0);  // this wave's weight's table
     const float offset = NESTED ? *W.offset : 0.0f;
@@ -225,6 +233,16 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
 #pragma unroll
     for (int i = 0; i < MB; ++i) acc[i] = float16_t{};
 
+    // Ring buffers: step t uses X buffer rx0 (byte offset in the X ring) and weight slot rw0;
+    // step t + 1 uses rx1 / rw1; step t + 3 reuses step t's.
+    int rx0 = 0, rw0 = 0, rx1 = XBUF, rw1 = wslot_bytes, rx2 = 2 * XBUF, rw2 = 2 * wslot_bytes;
+    // Prologue: two steps and the slice-3 parts of the third in flight (issued before the LoRA
+    // term, whose loads then share their round trip); the wait for the first follows the LoRA term.
+    load_step(ks0, 0, 0, true);
+    load_step(ks0 + 1, XBUF, wslot_bytes, ks0 + 1 < ks1);
+#pragma unroll
+    for (int i = 0; i < NP; i += 4) load_part(spread_part(i, XPT), ks0 + 2, rx2, rw2, ks0 + 2 < ks1);
+
     // LoRA term s * U.B^T first (split 0 only), as in nf4_fwd_kernel, for this wave's weight.
     {
         const int R = (G.lora_u != nullptr && split == 0) ? sgpr(a.lora_rank) : 0;
@@ -244,14 +262,10 @@ __global__ __launch_bounds__(kF8Threads, 1) void nf4_fwd8_kernel(const FwdArgs a
         }
     }
 
-    // Ring buffers: step t uses X buffer rx0 (byte offset in the X ring) and weight slot rw0;
-    // step t + 1 uses rx1 / rw1; step t + 3 reuses step t's.
-    int rx0 = 0, rw0 = 0, rx1 = XBUF, rw1 = wslot_bytes, rx2 = 2 * XBUF, rw2 = 2 * wslot_bytes;
-    // Prologue: two steps and the slice-3 parts of the third in flight; wait for the first.
-    load_step(ks0, 0, 0, true);
-    load_step(ks0 + 1, XBUF, wslot_bytes, ks0 + 1 < ks1);
-#pragma unroll
-    for (int i = 0; i < NP; i += 4) load_part(spread_part(i, XPT), ks0 + 2, rx2, rw2, ks0 + 2 < ks1);
+    // the code book and code2 table (their loads have landed: they are older than the ring's)
+    lut2[tid] = float2_t{book_hi, book_lo};
+    if constexpr (NESTED)
+        if (glu || tid < 256) c2[tid] = c2v;
     wait_vmcnt<NL + L3>();
     lds_barrier();
 
