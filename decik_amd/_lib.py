@@ -246,7 +246,9 @@ class DescCache:
             scales = SCALES.get(packed, qs, device) if qs.nested else None
         else:
             scales = scales_of(packed, qs, device)
-        key = id(qs)
+        # one entry per weight and form (cached scales or its own statistics), so that calls
+        # alternating between the two reuse both descriptors
+        key = (id(qs), scales is None)
         ver = (id(packed), packed.data_ptr(), device.index, id(scales), id(qs.code), int(qs.blocksize),
                tuple(id(t) if isinstance(t, torch.Tensor) else float(t) for t in _stats(qs)))
         with self._lock:

@@ -438,17 +438,29 @@ BwdParts plan_bwd_parts(int64_t m, int64_t k, const int64_t* ns, int ngroups, bo
                     [&] { return plan_bwd_parts_compute(m, k, ns, ngroups, swiglu, max_partial_bytes); });
 }
 
-// nf4_skinny_kernel (forward, m <= kSkinnyMaxM): 64-row groups; contraction splits while the
-// launch still has at most one work-group per CU and every split keeps at least two 128-wide
+// nf4_skinny_kernel (forward, m <= kSkinnyMaxM): row groups of 4 tiles of 16 rows, or of 5 or 6
+// where that is the fewest that keep the row groups to one per CU: a weight of more 64-row groups
+// than CUs would otherwise run a second round of only its left-over groups, as long as the first
+// (7B gate: 296 groups of 64 rows on 256 CUs, 237 of 80); contraction splits while the launch
+// still has at most one work-group per CU and every split keeps at least two 128-wide
 // super-steps per wave (16 per work-group). no_split: a single pass (no workspace).
-constexpr int kSkinnyRows = 64, kSkinnyStep = 128, kSkinnyWaves = 8;
+constexpr int kSkinnyStep = 128, kSkinnyWaves = 8;
+int64_t skinny_row_groups(const int64_t* ns, int ngroups, int row_tiles) {
+    int64_t rgroups = 0;
+    for (int g = 0; g < ngroups; ++g) rgroups += (ns[g] + 16 * row_tiles - 1) / (16 * row_tiles);
+    return rgroups;
+}
+int skinny_row_tiles(const int64_t* ns, int ngroups) {
+    for (int rt = 4; rt <= 6; ++rt)
+        if (skinny_row_groups(ns, ngroups, rt) <= num_cus()) return rt;
+    return 4;
+}
 GemmPlan plan_skinny_compute(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool no_split) {
     GemmPlan p{};
-    int64_t rgroups = 0, ncols = 0;
-    for (int g = 0; g < ngroups; ++g) {
-        rgroups += (ns[g] + kSkinnyRows - 1) / kSkinnyRows;
-        ncols += ns[g];
-    }
+    p.row_tiles = skinny_row_tiles(ns, ngroups);
+    const int64_t rgroups = skinny_row_groups(ns, ngroups, p.row_tiles);
+    int64_t ncols = 0;
+    for (int g = 0; g < ngroups; ++g) ncols += ns[g];
     p.steps = (int)((k + kSkinnyStep - 1) / kSkinnyStep);
     // split the contraction as far as the work-groups still fit one per CU and every split keeps
     // at least two super-steps (all splits non-empty). Weights of few row groups (k/v) gain most
@@ -482,18 +494,15 @@ GemmPlan plan_skinny(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool 
 // 18 us against 25, q/o 10 against 16), and at two rows on all but the long contraction of down;
 // from 3 rows on the skinny kernel wins (7B gate at 8 rows: 28 us against 39 for the MFMA
 // kernels). DECIK_SMALL_M = gemv / skinny forces one of them for launches both may take.
-// Past 16 rows (two 16-token blocks a work-group), weights of more 64-row groups than CUs go to
-// the MFMA kernels: the skinny kernel's second round then holds few work-groups (7B gate, 296
-// groups: 38.8 / 39.6 us at 24 / 32 rows against 34.2 / 34.9 on 64-token MFMA tiles).
+// Past 16 rows (two 16-token blocks a work-group), weights of more row groups than CUs (even at
+// 6 tiles a group) go to the MFMA kernels: the skinny kernel's second round would hold few
+// work-groups (7B gate, 296 groups of 64 rows: 38.8 / 39.6 us at 24 / 32 rows against 34.2 /
+// 34.9 on 64-token MFMA tiles).
 bool small_m_forward(int64_t m, bool glu, bool lora, const int64_t* ns, int ngroups) {
     if (glu || lora || m < 1 || m > kSkinnyMaxM) return false;
     const char* forced = std::getenv("DECIK_FWD_PLAN");
     if (forced != nullptr && *forced != 0) return false;
-    if (m > 16) {
-        int64_t rgroups = 0;
-        for (int g = 0; g < ngroups; ++g) rgroups += (ns[g] + kSkinnyRows - 1) / kSkinnyRows;
-        if (rgroups > num_cus()) return false;
-    }
+    if (m > 16 && skinny_row_groups(ns, ngroups, skinny_row_tiles(ns, ngroups)) > num_cus()) return false;
     return true;
 }
 bool gemv_requested(int64_t m, int64_t k) {
@@ -750,10 +759,11 @@ static int linear_fwd_impl(const std::string& name, const uint16_t* x, int64_t m
         const int64_t need = workspace_bytes(p);
         if (need > 0 && (workspace == nullptr || workspace_bytes_ < need || !aligned(workspace, 256)))
             return fail(name + ": workspace too small (need " + std::to_string(need) + " bytes)");
+        const int rows = 16 * p.row_tiles;
         int rg = 0;
         for (int g = 0; g < ngroups; ++g) {
             a.g[g].tile_begin = rg;
-            rg += (int)((ns[g] + kSkinnyRows - 1) / kSkinnyRows);
+            rg += (int)((ns[g] + rows - 1) / rows);
         }
         a.splits = p.splits;
         a.ksteps = p.steps;
@@ -761,7 +771,7 @@ static int linear_fwd_impl(const std::string& name, const uint16_t* x, int64_t m
         if (need > 0) a.partials = static_cast<float*>(workspace);
         const int64_t wgs = (int64_t)rg * p.splits;
         if (wgs > INT32_MAX / 2) return fail(name + ": problem too large");
-        if (check_hip(launch_skinny(a, (int)wgs, st), "dk_nf4_linear_fwd small-M launch")) return 1;
+        if (check_hip(launch_skinny(a, p.row_tiles, (int)wgs, st), "dk_nf4_linear_fwd small-M launch")) return 1;
         if (p.splits <= 1) return 0;
         ReduceArgs r{};
         r.partials = a.partials;

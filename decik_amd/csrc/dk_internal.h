@@ -149,6 +149,7 @@ struct GemmPlan {
     int splits;
     int steps_per_split;
     int64_t partial_floats;  // fp32 partial slabs (splits > 1)
+    int row_tiles;           // nf4_skinny_kernel: 16-row tiles per work-group (4 to 6)
 };
 
 hipError_t launch_fwd(const FwdArgs& a, int mb, int grid, hipStream_t s);
@@ -161,11 +162,11 @@ bool gemv_fits(int64_t k);
 // waves per work-group of a GEMV launch (k must fit: gemv_fits)
 int gemv_waves(int64_t m, int64_t k, int64_t nrows);
 // Forward launches of few token rows (no LoRA terms, no GLU epilogue): nf4_skinny_kernel. A
-// work-group owns 64 weight rows; a.splits work-groups share them along the contraction, each
-// covering a.ksteps_per_split 128-wide super-steps; g[].tile_begin = each group's first 64-row
-// group. splits > 1: fp32 partial slabs, then splitk_reduce_kernel.
+// work-group owns 16 * row_tiles weight rows (row_tiles 4 to 6); a.splits work-groups share them
+// along the contraction, each covering a.ksteps_per_split 128-wide super-steps; g[].tile_begin =
+// each group's first row group. splits > 1: fp32 partial slabs, then splitk_reduce_kernel.
 constexpr int kSkinnyMaxM = 32;
-hipError_t launch_skinny(const FwdArgs& a, int grid, hipStream_t s);
+hipError_t launch_skinny(const FwdArgs& a, int row_tiles, int grid, hipStream_t s);
 // 8-wave forward kernel (32 weight rows x 32*mb tokens per wave), mb = 8 or 9
 hipError_t launch_fwd8(const FwdArgs& a, int mb, int grid, hipStream_t s);
 // 8-wave input-gradient kernel (32 output columns x 32*mb tokens per wave), mb = 2, 4, 7 or 8;

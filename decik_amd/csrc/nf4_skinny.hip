@@ -5,8 +5,10 @@
 // is padded only to 16 (MT = 1) or 32 (MT = 2) and the kernel is organised around the weight
 // stream:
 //
-// - A work-group (8 waves) owns 64 weight rows (4 row tiles of 16) and one contiguous range of
-//   the contraction (split-K over work-groups only where the rows alone cannot fill the GPU).
+// - A work-group (8 waves) owns RT row tiles of 16 weight rows (RT = 4; 5 or 6 where 64-row
+//   groups would overrun one work-group per CU, so that a tall weight runs in one round instead of
+//   two whose second is mostly idle) and one contiguous range of the contraction (split-K over
+//   work-groups only where the rows alone cannot fill the GPU).
 //   Its waves take the range's 128-wide super-steps in turn, so every wave streams whole rows
 //   and the fp32 tiles of the 8 waves are summed through LDS in wave order at the end.
 // - Per super-step a lane loads 16 contiguous packed bytes (32 weights, one block: blocks are
@@ -25,16 +27,17 @@ namespace dk {
 
 constexpr int kSkWaves = 8;
 constexpr int kSkThreads = 64 * kSkWaves;
-constexpr int kSkRows = 64;    // weight rows per work-group (4 tiles of 16)
 constexpr int kSkStep = 128;   // contraction per super-step
-constexpr int kSkPad = kSkRows + 1;
 
-__host__ __device__ constexpr size_t skinny_smem_bytes(int mt) {
-    return (size_t)kSkWaves * 16 * mt * kSkPad * 4;  // the waves' fp32 tiles for the reduction
+// the waves' fp32 tiles for the reduction (rows padded to 16 RT + 1 floats)
+__host__ __device__ constexpr size_t skinny_smem_bytes(int mt, int rt) {
+    return (size_t)kSkWaves * 16 * mt * (16 * rt + 1) * 4;
 }
 
-template <int MT, bool NESTED>
+template <int MT, bool NESTED, int RT>
 __global__ __launch_bounds__(kSkThreads) void nf4_skinny_kernel(const FwdArgs a) {
+    constexpr int kSkRows = 16 * RT;  // weight rows per work-group
+    constexpr int kSkPad = kSkRows + 1;
     __shared__ float2_t lut2[256];  // byte-pair code book of this work-group's weight
     __shared__ float c2[256];       // nested statistics: the code2 table
     extern __shared__ __attribute__((aligned(16))) float red[];
@@ -69,10 +72,10 @@ __global__ __launch_bounds__(kSkThreads) void nf4_skinny_kernel(const FwdArgs a)
     const uint32_t bs_shift = W.bs_shift, bs2_shift = W.bs2_shift;
 
     // this lane's rows (A row i of tile r) and token rows (B column i of token block b)
-    uint32_t wbase[4];
-    bool rok[4];
+    uint32_t wbase[RT];
+    bool rok[RT];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < RT; ++r) {
         const int row = n0 + 16 * r + i;
         rok[r] = row < N;
         wbase[r] = (uint32_t)(rok[r] ? row : 0) * (uint32_t)K + 32u * (uint32_t)g;  // flat element index
@@ -85,24 +88,24 @@ __global__ __launch_bounds__(kSkThreads) void nf4_skinny_kernel(const FwdArgs a)
     const int s0 = split * a.ksteps_per_split;
     const int s1 = min(total, s0 + a.ksteps_per_split);
 
-    float4_t acc[4][MT];
+    float4_t acc[RT][MT];
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+    for (int r = 0; r < RT; ++r)
 #pragma unroll
         for (int b = 0; b < MT; ++b) acc[r][b] = float4_t{};
 
     // loads of one super-step: packed bytes and block scale of each row, X of each token block
     struct Step {
-        u32x4_t p[4];
-        float s[4];
-        uint32_t q8[4];  // nested: absmax codes (the scale is completed after the wait)
+        u32x4_t p[RT];
+        float s[RT];
+        uint32_t q8[RT];  // nested: absmax codes (the scale is completed after the wait)
         u32x4_t x[MT][4];
     };
     auto load = [&](int ss, Step& st) __attribute__((always_inline)) {
         const int k = ss * kSkStep + 32 * g;
         const bool kok = ss < s1 && k < K;  // K % 32 == 0: a lane's 32 k are wholly in or out
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
+        for (int r = 0; r < RT; ++r) {
             const uint32_t el = wbase[r] + (uint32_t)ss * kSkStep;
             st.p[r] = bload128(wrs, off_if(kok && rok[r], el >> 1));
             const uint32_t blk = el >> bs_shift;
@@ -121,7 +124,7 @@ __global__ __launch_bounds__(kSkThreads) void nf4_skinny_kernel(const FwdArgs a)
     };
     auto compute = [&](const Step& st) __attribute__((always_inline)) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
+        for (int r = 0; r < RT; ++r) {
             float s = st.s[r];
             if constexpr (NESTED) s = c2[st.q8[r]] * s + offset;  // two roundings (no contraction)
             if (!rok[r]) s = 0.0f;
@@ -167,7 +170,7 @@ __global__ __launch_bounds__(kSkThreads) void nf4_skinny_kernel(const FwdArgs a)
     // lane holds D[4 g + r'][i] of tile r, token block b: weight row n0 + 16 r + 4 g + r',
     // token 16 b + i. Stage as red[wave][token][row] (rows padded to 65 floats).
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+    for (int r = 0; r < RT; ++r)
 #pragma unroll
         for (int b = 0; b < MT; ++b)
 #pragma unroll
@@ -191,20 +194,31 @@ __global__ __launch_bounds__(kSkThreads) void nf4_skinny_kernel(const FwdArgs a)
     }
 }
 
-template <int MT, bool NESTED>
+template <int MT, bool NESTED, int RT>
 static hipError_t launch_skinny_t(const FwdArgs& a, int grid, hipStream_t s) {
-    const hipError_t e = allow_dynamic_lds((const void*)nf4_skinny_kernel<MT, NESTED>, skinny_smem_bytes(MT));
+    const size_t lds = skinny_smem_bytes(MT, RT);
+    const hipError_t e = allow_dynamic_lds((const void*)nf4_skinny_kernel<MT, NESTED, RT>, lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((nf4_skinny_kernel<MT, NESTED>), dim3(grid), dim3(kSkThreads), skinny_smem_bytes(MT), s, a);
+    hipLaunchKernelGGL((nf4_skinny_kernel<MT, NESTED, RT>), dim3(grid), dim3(kSkThreads), lds, s, a);
     return hipGetLastError();
 }
 
-hipError_t launch_skinny(const FwdArgs& a, int grid, hipStream_t s) {
+template <int RT>
+static hipError_t launch_skinny_rt(const FwdArgs& a, int grid, hipStream_t s) {
+    if (a.m <= 16) return a.nested ? launch_skinny_t<1, true, RT>(a, grid, s) : launch_skinny_t<1, false, RT>(a, grid, s);
+    return a.nested ? launch_skinny_t<2, true, RT>(a, grid, s) : launch_skinny_t<2, false, RT>(a, grid, s);
+}
+
+hipError_t launch_skinny(const FwdArgs& a, int row_tiles, int grid, hipStream_t s) {
     if (a.m < 1 || a.m > kSkinnyMaxM || a.glu) return hipErrorInvalidValue;
     for (int g = 0; g < a.ngroups; ++g)
         if (a.g[g].lora_u != nullptr) return hipErrorInvalidValue;
-    if (a.m <= 16) return a.nested ? launch_skinny_t<1, true>(a, grid, s) : launch_skinny_t<1, false>(a, grid, s);
-    return a.nested ? launch_skinny_t<2, true>(a, grid, s) : launch_skinny_t<2, false>(a, grid, s);
+    switch (row_tiles) {
+        case 4: return launch_skinny_rt<4>(a, grid, s);
+        case 5: return launch_skinny_rt<5>(a, grid, s);
+        case 6: return launch_skinny_rt<6>(a, grid, s);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace dk

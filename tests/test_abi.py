@@ -159,11 +159,21 @@ def test_launch_plans():
     assert launch_plan(False, 1, 8960, [1536])["waves"] == 4
     for m in (3, 8, 16):
         assert launch_plan(False, m, 3584, [18944])["kernel"] == "nf4_skinny_kernel"
-    # past 16 rows, a weight of more 64-row groups than CUs (7B gate: 296) takes the MFMA kernel
-    assert launch_plan(False, 32, 3584, [18944])["kernel"] == "nf4_fwd8_kernel"
+    # past 16 rows, the small-M kernel keeps weights whose row groups fit one work-group per CU
+    # (7B gate: 296 groups of 64 rows, 237 of 80 on 256 CUs); taller ones (24592 rows: 257 groups
+    # of 96) take the MFMA kernels
+    assert launch_plan(False, 32, 3584, [18944])["kernel"] == "nf4_skinny_kernel"
+    assert launch_plan(False, 32, 3584, [24592])["kernel"] == "nf4_fwd8_kernel"
+    assert launch_plan(False, 16, 3584, [24592])["kernel"] == "nf4_skinny_kernel"
     assert launch_plan(False, 32, 18944, [3584])["kernel"] == "nf4_skinny_kernel"
     assert launch_plan(False, 8, 3584, [18944])["splits"] == 1
     assert launch_plan(False, 8, 18944, [3584])["splits"] > 1
+    # nested statistics as stored for unsplit small-M launches, cached fp32 scales otherwise
+    from decik_amd import nf4 as _nf4
+    assert _nf4._forward_scales(8, 3584, [18944]) is _nf4._own_statistics
+    assert _nf4._forward_scales(8, 3584, [512]) is _nf4._scales        # split: cached
+    assert _nf4._forward_scales(1, 3584, [18944]) is _nf4._scales      # GEMV
+    assert _nf4._forward_scales(830, 3584, [18944]) is _nf4._scales    # MFMA kernels
     # few row groups (7B k/v: 8 groups of 64 rows, 28 super-steps): split down to two super-steps
     assert launch_plan(False, 8, 3584, [512])["splits"] == 14
     assert launch_plan(False, 33, 3584, [18944])["kernel"] != "nf4_skinny_kernel"

@@ -164,6 +164,53 @@ def test_skinny_small_m(m, nested, blocksize, device, raw_statistics, skinny):
         assert_close(y, ref, what=f"skinny m={m} nested={nested} bs={blocksize}")
 
 
+@pytest.mark.parametrize("m", [3, 8, 17, 32])
+@pytest.mark.parametrize("ns", [(16408, 64), (20496,)])
+@pytest.mark.parametrize("raw", [False, True])
+def test_skinny_tall_weights(m, ns, raw, device, monkeypatch):
+    """Weights of more 64-row groups than a 256-CU device has CUs: the small-M kernel takes row
+    groups of 80 (16408 + 64 rows: 206 + 1 groups) or 96 rows (20496: 214 groups, 257 of 80) so
+    that they run in one round; the last group of each weight is partial, and at 17-32 token rows
+    the kernel is still chosen (one round)."""
+    from decik_amd import nf4
+    from decik_amd.nf4 import launch_plan, linear_forward
+
+    if raw:
+        monkeypatch.setattr(nf4, "_scales", lambda packed, qs, device: None)
+    k = 256
+    assert launch_plan(False, m, k, list(ns))["kernel"] == "nf4_skinny_kernel"
+    x = randn16((m, k), seed=180 + m, device=device)
+    items, refs = [], []
+    for i, n in enumerate(ns):
+        packed, qs, w16 = make_weight((n, k), seed=181 + i, device=device)
+        b = randn16((n,), seed=183 + i, device=device, std=0.1)
+        items.append(dict(packed=packed, qs=qs, bias=b))
+        refs.append(O.linear_ref(x.cpu().numpy(), w16, b.cpu().numpy()))
+    ys = linear_forward(x, items)
+    for y, ref in zip(ys, refs):
+        assert_close(y, ref, what=f"skinny tall m={m} ns={ns} raw={raw}")
+
+
+@pytest.mark.parametrize("m", [3, 8, 24])
+def test_small_m_statistics_forms_same_bits(m, device, monkeypatch):
+    """Unsplit small-M launches read nested statistics as stored (the default for them), split ones
+    and the MFMA kernels the cached fp32 scales: both forms give the same dequantized weights and
+    the same sums, so the outputs are equal bit for bit."""
+    from decik_amd import nf4
+    from decik_amd.nf4 import linear_forward
+
+    k, n = 512, 16408
+    assert nf4._forward_scales(m, k, [n]) is nf4._own_statistics
+    packed, qs, w16 = make_weight((n, k), seed=190, device=device)
+    assert qs.nested
+    x = randn16((m, k), seed=191 + m, device=device)
+    (y_raw,) = linear_forward(x, [dict(packed=packed, qs=qs)])
+    monkeypatch.setattr(nf4, "_own_statistics", nf4._scales)
+    (y_cached,) = linear_forward(x, [dict(packed=packed, qs=qs)])
+    assert torch.equal(y_raw, y_cached)
+    assert_close(y_raw, O.linear_ref(x.cpu().numpy(), w16), what=f"small-M raw m={m}")
+
+
 @pytest.mark.parametrize("m", [1, 8, 32])
 @pytest.mark.parametrize("raw", [False, True])
 def test_skinny_split_k(m, raw, device, monkeypatch, skinny):
