@@ -505,15 +505,21 @@ bool small_m_forward(int64_t m, bool glu, bool lora, const int64_t* ns, int ngro
     if (m > 16 && skinny_row_groups(ns, ngroups, skinny_row_tiles(ns, ngroups)) > num_cus()) return false;
     return true;
 }
-bool gemv_requested(int64_t m, int64_t k) {
+bool gemv_requested(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
     if (m > kGemvMaxM || !gemv_fits(k)) return false;
     const char* v = std::getenv("DECIK_SMALL_M");
     if (v != nullptr && std::string(v) == "gemv") return true;
     if (v != nullptr && std::string(v) == "skinny") return false;
-    // two rows of a long contraction: the small-M kernel's split is faster for the 7B down
-    // projection (k = 18944: 23.7 vs 35.1 us graph-replayed), the GEMV for the 1.5B one (k = 8960:
-    // 8.6 vs 10.8 us)
-    return m == 1 || k <= 12288;
+    if (m == 1) return true;
+    // Two rows: the GEMV's second dot product per weight costs in proportion to the weight, the
+    // small-M kernel hardly depends on the row count, so large launches take the small-M kernel.
+    // Graph-replayed at two rows, GEMV against small-M kernel: 7B gate 21.3-21.6 against 17.4 us
+    // (67.9M weights), 1.5B gate 8.1 against 8.8 (13.8M), 7B q/o 7.5 against 11.1 (12.8M); a
+    // long contraction also favours the small-M kernel's split (7B down, k = 18944: 23.7 against
+    // 35.1; the 1.5B down, k = 8960: 8.6 against 10.5 on the GEMV).
+    int64_t weights = 0;
+    for (int g = 0; g < ngroups; ++g) weights += ns[g] * k;
+    return k <= 12288 && weights < (int64_t(1) << 25);
 }
 
 
@@ -626,7 +632,7 @@ int dk_nf4_linear_plan(int backward, int64_t m, int64_t k, const int64_t* ns, in
             }
         }
         kernel = 3;  // nf4_bwd8_kernel
-    } else if (small_m_forward(m, glu, lora, ns, ngroups) && gemv_requested(m, k)) {
+    } else if (small_m_forward(m, glu, lora, ns, ngroups) && gemv_requested(m, k, ns, ngroups)) {
         p = GemmPlan{};
         int64_t nrows = 0;
         for (int g = 0; g < ngroups; ++g) nrows += ns[g];
@@ -754,7 +760,7 @@ static int linear_fwd_impl(const std::string& name, const uint16_t* x, int64_t m
         a.ncols = (int32_t)ncols;
         if (ncols > INT32_MAX / 2) return fail(name + ": problem too large");
         const hipStream_t st = static_cast<hipStream_t>(stream);
-        if (gemv_requested(m, k)) return check_hip(launch_gemv(a, st), "dk_nf4_linear_fwd GEMV launch");
+        if (gemv_requested(m, k, ns, ngroups)) return check_hip(launch_gemv(a, st), "dk_nf4_linear_fwd GEMV launch");
         const GemmPlan p = plan_skinny(m, k, ns, ngroups, no_split);
         const int64_t need = workspace_bytes(p);
         if (need > 0 && (workspace == nullptr || workspace_bytes_ < need || !aligned(workspace, 256)))

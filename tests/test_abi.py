@@ -142,8 +142,11 @@ def test_launch_plans():
     assert sw["kernel"] == "nf4_bwd8_kernel" and sw["rows_blocks"] <= 4
     # at most 32 token rows, no LoRA, no GLU epilogue: the small-M kernel, split along the
     # contraction only where the rows cannot fill the GPU
-    for m in (1, 2):
-        assert launch_plan(False, m, 3584, [18944])["kernel"] == "nf4_gemv_kernel"
+    assert launch_plan(False, 1, 3584, [18944])["kernel"] == "nf4_gemv_kernel"
+    # two rows: the GEMV below 2^25 weights, the small-M kernel above (7B gate: 67.9M)
+    assert launch_plan(False, 2, 3584, [18944])["kernel"] == "nf4_skinny_kernel"
+    assert launch_plan(False, 2, 1536, [8960])["kernel"] == "nf4_gemv_kernel"
+    assert launch_plan(False, 2, 3584, [3584])["kernel"] == "nf4_gemv_kernel"
     # forward split-K with few outputs: each split lengthens the reduction's chain of dependent
     # loads, so these split less than the slab bytes alone would have them (7B k/v, q/o at 64 tokens)
     assert launch_plan(False, 64, 3584, [512])["splits"] == 14
