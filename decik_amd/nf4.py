@@ -395,8 +395,10 @@ def _fusable(x16, packed, qs, bias16):
 
 
 class NF4Linear(torch.autograd.Function):
-    """F.linear(x, dequant(W), bias) with fp16 x; the input gradient is dY . dequant(W), as
-    bitsandbytes' MatMul4Bit (the weight itself is frozen). Both directions are one fused launch."""
+    """Autograd op of a frozen NF4 projection (solution/nf4.py:88-104): forward Y = X.W^T + b on
+    fp16 activations, backward dX = dY.W only (no weight or bias gradient). Each direction is a
+    single launch that decodes the packed weight tile by tile on the fly; no fp16 copy of W is
+    ever materialised on the fused path."""
 
     @staticmethod
     def forward(ctx, x16, packed, bias16, quant_state):

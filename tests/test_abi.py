@@ -214,6 +214,16 @@ def test_launch_plans():
     # k % blocksize != 0: the eight-wave forward kernel may not run
     assert launch_plan(False, 830, 1536, [8960], blocksize=1024)["kernel"] == "nf4_fwd_kernel"
     assert launch_plan(True, 830, 1536, [8960, 8960], no_split=True)["splits"] == 1
+    # few token rows without a workspace (the GLU entry's two-launch fallback): the small-M kernel
+    # runs unsplit, though it would split these launches when a workspace is allowed
+    for m, k, ns in ((8, 1024, [256, 256]), (24, 1536, [1536, 1536])):
+        assert launch_plan(False, m, k, ns)["splits"] > 1
+        assert launch_plan(False, m, k, ns, no_split=True) == dict(
+            rows_blocks=1 if m <= 16 else 2, waves=8, splits=1, kernel="nf4_skinny_kernel", launches=1, splits_second=0)
+    # the RoPE epilogue lives in the split-K reduction: a contraction of exactly two 64-wide steps
+    # still gets a two-split plan (a workspace of two fp32 slabs), never a single pass
+    qkv = (ctypes.c_int64 * 3)(1536, 256, 256)
+    assert _lib.lib().dk_nf4_linear_rope_fwd_workspace(64, 128, qkv, 3) == 2 * 64 * 2048 * 4
     old = os.environ.get("DECIK_BWD_PLAN")
     try:
         os.environ["DECIK_BWD_PLAN"] = "8,3,8"

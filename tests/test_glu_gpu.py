@@ -151,6 +151,42 @@ def test_glu_forward_narrow_blocks_take_two_launches(device):
     del keep
 
 
+@pytest.mark.parametrize("blocksize", [32, 64])
+@pytest.mark.parametrize("m,n,k", [(8, 256, 1024), (24, 1536, 1536)])
+def test_glu_forward_few_rows_without_workspace(m, n, k, blocksize, device, monkeypatch):
+    """The GLU entry takes no workspace. At 8 and 24 token rows with no forced plan, raw nested
+    statistics take the one-launch GLU kernel (blocksize 64) and 32-element blocks the grouped
+    launch plus the SwiGLU kernel, whose small-M forward would split these shapes when a workspace
+    is allowed: it must run them in a single pass. Gate and up meet the bar against the oracle and
+    h is the SwiGLU of the returned gate and up, bit for bit."""
+    from decik_amd._lib import lib, ptr, stream_of
+    from decik_amd.swiglu import swiglu_fwd
+
+    monkeypatch.delenv("DECIK_FWD_PLAN", raising=False)
+    monkeypatch.delenv("DECIK_SMALL_M", raising=False)
+    pg, qg, wg = make_weight((n, k), seed=91 + m, device=device, blocksize=blocksize)
+    pu, qu, wu = make_weight((n, k), seed=92 + m, device=device, blocksize=blocksize)
+    x = randn16((m, k), seed=93 + m, device=device)
+    g = torch.empty((m, n), dtype=torch.float16, device=device)
+    u = torch.empty_like(g)
+    h = torch.empty_like(g)
+    groups, keep = _glu_groups([(pg, qg), (pu, qu)], [g, u], n, device)
+    assert groups[0].w.nested == 1 and groups[1].w.nested == 1
+    rc = lib().dk_nf4_glu_fwd(ptr(x), m, k, k, groups, 0, ptr(h), n, stream_of(device))
+    assert rc == 0, lib().dk_last_error()
+    g2, u2, h2 = _separate_glu(x, dict(packed=pg, qs=qg), dict(packed=pu, qs=qu))
+    torch.cuda.synchronize()
+    xn = x.cpu().numpy()
+    assert_close(g, O.linear_ref(xn, wg, None), what=f"gate {m}x{n}x{k} bs {blocksize}")
+    assert_close(u, O.linear_ref(xn, wu, None), what=f"up {m}x{n}x{k} bs {blocksize}")
+    assert torch.equal(h, swiglu_fwd(g, u))
+    if blocksize == 32:
+        # the fallback is the separate path itself (the same small-M kernel, unsplit here)
+        assert_close(g2, O.linear_ref(xn, wg, None), what="separate gate")
+        assert torch.equal(h2, swiglu_fwd(g2, u2))
+    del keep
+
+
 BWD_SHAPES = [(830, 1536, 8960), (64, 264, 256), (17, 96, 128)]  # (M, N, K): W [N, K], dY [M, N]
 
 

@@ -133,3 +133,40 @@ def test_rope_entry_rejects_bad_shapes(device):
     c = torch.ones((64, 24), dtype=torch.float32, device=device)
     with pytest.raises(_lib.DecikError, match="head_dim"):
         nf4.linear_rope_forward(x, items, c, c, 24, 3)
+
+
+@pytest.mark.parametrize("plan", [None, "2,2,8"])
+def test_fused_rope_shortest_contraction(plan, device, monkeypatch):
+    """k = 128 is two 64-wide steps, the shortest contraction the RoPE epilogue (which lives in the
+    split-K reduction) takes: with no forced plan the planner must still give it two splits. The
+    output meets the bar against the oracle (projection rounded to fp16, then RoPE), and under one
+    forced plan equals the projection followed by the RoPE kernel, bit for bit."""
+    from decik_amd import nf4
+    from decik_amd.rope import rope_qk_forward
+
+    if plan is None:
+        monkeypatch.delenv("DECIK_FWD_PLAN", raising=False)
+    else:
+        monkeypatch.setenv("DECIK_FWD_PLAN", plan)
+    m, k, h, hk, d = 64, 128, 2, 1, 64
+    lengths = [40, 24]
+    c, s = rope_tables(lengths, d)
+    ct, st = torch.from_numpy(c).to(device), torch.from_numpy(s).to(device)
+    items, w16s = [], []
+    for i, n in enumerate((h * d, hk * d, hk * d)):
+        packed, qs, w16 = make_weight((n, k), seed=860 + i, device=device)
+        items.append(dict(packed=packed, qs=qs, bias=randn16((n,), seed=870 + i, device=device, std=0.1)))
+        w16s.append(w16)
+    x = randn16((m, k), seed=880, device=device)
+    q_rot, k_rot, v = nf4.linear_rope_forward(x, items, ct, st, d, 3)
+    torch.cuda.synchronize()
+    xn = x.cpu().numpy()
+    refs = [O.linear_ref(xn, w, it["bias"].cpu().numpy()) for w, it in zip(w16s, items)]
+    rq, rk = O.rope_fwd_ref(refs[0].astype(np.float16), None, refs[1].astype(np.float16), c, s, h, hk)
+    assert_close(q_rot, rq.astype(np.float32), what="q rotated, k = 128")
+    assert_close(k_rot, rk.astype(np.float32), what="k rotated, k = 128")
+    assert_close(v, refs[2], what="v, k = 128")
+    if plan is not None:
+        q, kk, v2 = nf4.linear_forward(x, items)
+        rq2, rk2 = rope_qk_forward(q, None, kk, ct, st, h, hk)
+        assert torch.equal(q_rot, rq2) and torch.equal(k_rot, rk2) and torch.equal(v, v2)
