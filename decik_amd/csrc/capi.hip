@@ -689,7 +689,8 @@ static int linear_fwd_impl(const std::string& name, const uint16_t* x, int64_t m
     if (m < 0 || k <= 0 || (k % 32) != 0)
         return fail(name + ": k must be a positive multiple of 32");
     if (m > INT32_MAX / 2 || k > INT32_MAX / 2) return fail(name + ": m or k too large");
-    if (x == nullptr || !aligned(x, 16) || ldx < k || (ldx % 8) != 0)
+    // zero token rows: nothing is read or written, and row pointers may be NULL
+    if (m > 0 && (x == nullptr || !aligned(x, 16) || ldx < k || (ldx % 8) != 0))
         return fail(name + ": x must be 16-byte aligned with ldx >= k, ldx % 8 == 0");
     if (lora_rank != 0 && lora_rank != 16 && lora_rank != 32)
         return fail(name + ": lora_rank must be 0, 16 or 32");
@@ -714,11 +715,11 @@ static int linear_fwd_impl(const std::string& name, const uint16_t* x, int64_t m
         if (G.w.blocksize < 64 || k % 64 != 0) a.wide_stats = 1;
         const bool roped = rope != nullptr && ((rope->mask >> g) & 1);
         if (roped) {
-            if (rope->out == nullptr || rope->out[g] == nullptr || !aligned(rope->out[g], 16) ||
+            if ((m > 0 && (rope->out == nullptr || rope->out[g] == nullptr || !aligned(rope->out[g], 16))) ||
                 G.w.n % rope->head_dim != 0)
                 return fail(name + ": a rotated group needs a 16-byte aligned head-major output and n % head_dim == 0");
-        } else if ((G.y == nullptr && !glu) ||
-                   (G.y != nullptr && (!aligned(G.y, 16) || G.ldy < G.w.n || (G.ldy % 8) != 0))) {
+        } else if (m > 0 && ((G.y == nullptr && !glu) ||
+                             (G.y != nullptr && (!aligned(G.y, 16) || G.ldy < G.w.n || (G.ldy % 8) != 0)))) {
             return fail(name + ": y must be 16-byte aligned with ldy >= n, ldy % 8 == 0");
         }
         if (G.lora_u != nullptr && (lora_rank == 0 || G.lora_b == nullptr))
@@ -880,12 +881,12 @@ int dk_nf4_glu_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
                    const dk_linear_fwd_group* groups, int lora_rank, uint16_t* h, int64_t ldh,
                    void* stream) {
     g_error.clear();
-    if (groups == nullptr || h == nullptr) return fail("dk_nf4_glu_fwd: groups and h are required");
+    if (groups == nullptr || (h == nullptr && m > 0)) return fail("dk_nf4_glu_fwd: groups and h are required");
     const dk_nf4_weight& wg = groups[0].w;
     const dk_nf4_weight& wu = groups[1].w;
     if (wg.n != wu.n || wg.k != wu.k) return fail("dk_nf4_glu_fwd: gate and up shapes differ");
     const int64_t n = wg.n;
-    if (!aligned(h, 16) || ldh < n || (ldh % 8) != 0)
+    if (m > 0 && (!aligned(h, 16) || ldh < n || (ldh % 8) != 0))
         return fail("dk_nf4_glu_fwd: h must be 16-byte aligned with ldh >= n, ldh % 8 == 0");
     const bool fused = wg.nested == wu.nested && wg.blocksize == wu.blocksize && wg.blocksize >= 64 &&
                        k % 64 == 0;
@@ -893,12 +894,13 @@ int dk_nf4_glu_fwd(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
         return linear_fwd_impl("dk_nf4_glu_fwd", x, m, k, ldx, groups, 2, lora_rank, nullptr, 0, stream,
                                h, ldh, true);
     // other statistics: gate and up by the grouped launch (one pass), then the SwiGLU kernel
-    if (groups[0].y == nullptr || groups[1].y == nullptr || groups[0].ldy != n || groups[1].ldy != n ||
-        ldh != n)
+    if (m > 0 && (groups[0].y == nullptr || groups[1].y == nullptr || groups[0].ldy != n ||
+                  groups[1].ldy != n || ldh != n))
         return fail("dk_nf4_glu_fwd: narrow-block or mixed-statistics weights need gate and up outputs, all rows contiguous");
     if (linear_fwd_impl("dk_nf4_glu_fwd", x, m, k, ldx, groups, 2, lora_rank, nullptr, 0, stream, nullptr,
                         0, true))
         return 1;
+    if (m == 0) return 0;
     return check_hip(launch_swiglu_fwd(reinterpret_cast<const _Float16*>(groups[0].y),
                                        reinterpret_cast<const _Float16*>(groups[1].y),
                                        reinterpret_cast<_Float16*>(h), m * n, static_cast<hipStream_t>(stream)),
@@ -960,7 +962,7 @@ static int linear_bwd_impl(const std::string& name, const dk_linear_bwd_group* g
     if (m < 0 || k <= 0 || (k % 32) != 0)
         return fail(name + ": k must be a positive multiple of 32");
     if (m > INT32_MAX / 2 || k > INT32_MAX / 2) return fail(name + ": m or k too large");
-    if (sw == nullptr && (dx == nullptr || !aligned(dx, 16) || lddx < k || (lddx % 8) != 0))
+    if (sw == nullptr && m > 0 && (dx == nullptr || !aligned(dx, 16) || lddx < k || (lddx % 8) != 0))
         return fail(name + ": dx must be 16-byte aligned with lddx >= k, lddx % 8 == 0");
     if (lora_rank != 0 && lora_rank != 16 && lora_rank != 32)
         return fail(name + ": lora_rank must be 0, 16 or 32");
@@ -979,7 +981,7 @@ static int linear_bwd_impl(const std::string& name, const dk_linear_bwd_group* g
         if (nested >= 0 && nested != G.w.nested)
             return fail(name + ": all groups must be nested or all plain");
         nested = G.w.nested;
-        if (G.dy == nullptr || !aligned(G.dy, 16) || G.lddy < G.w.n || (G.lddy % 8) != 0)
+        if (m > 0 && (G.dy == nullptr || !aligned(G.dy, 16) || G.lddy < G.w.n || (G.lddy % 8) != 0))
             return fail(name + ": dy must be 16-byte aligned with lddy >= n, lddy % 8 == 0");
         if (G.lora_gu != nullptr && (lora_rank == 0 || G.lora_a == nullptr || !aligned(G.lora_gu, 16)))
             return fail(name + ": LoRA needs lora_rank > 0, lora_a and 16-byte aligned gu");
@@ -1096,10 +1098,10 @@ int dk_nf4_linear_bwd_swiglu(const dk_linear_bwd_group* group, int64_t m, int64_
                              const uint16_t* gate, const uint16_t* up, int64_t ldgu, uint16_t* dgate,
                              uint16_t* dup, int64_t ldd, void* stream) {
     g_error.clear();
-    if (gate == nullptr || up == nullptr || dgate == nullptr || dup == nullptr)
+    if (m > 0 && (gate == nullptr || up == nullptr || dgate == nullptr || dup == nullptr))
         return fail("dk_nf4_linear_bwd_swiglu: gate, up, dgate and dup are required");
-    if (!aligned(gate, 16) || !aligned(up, 16) || !aligned(dgate, 16) || !aligned(dup, 16) || ldgu < k ||
-        ldd < k || (ldgu % 8) != 0 || (ldd % 8) != 0)
+    if (m > 0 && (!aligned(gate, 16) || !aligned(up, 16) || !aligned(dgate, 16) || !aligned(dup, 16) ||
+                  ldgu < k || ldd < k || (ldgu % 8) != 0 || (ldd % 8) != 0))
         return fail("dk_nf4_linear_bwd_swiglu: gate/up/dgate/dup must be 16-byte aligned, row strides >= k and % 8 == 0");
     const SwigluBwdOut sw{gate, up, ldgu, dgate, dup, ldd};
     return linear_bwd_impl("dk_nf4_linear_bwd_swiglu", group, 1, m, k, nullptr, 0, 0, lora_rank, nullptr, 0,

@@ -115,8 +115,8 @@ def _forward_scales(m, k, ns):
     nested weights go as stored (0.516 bytes per weight against 0.5625 with fp32 scales; 7B gate
     at 3-32 rows 10-14% faster); split launches re-read statistics per split and take the cached
     scales (raw: 2-6% slower on the 7B k/v and Qwen2.5-1.5B down projections). Remembered per
-    shape and tuning variables."""
-    if m > 32:
+    shape and tuning variables. An empty batch launches nothing: any form does."""
+    if m > 32 or m < 1:
         return _scales
     key = (m, k, tuple(ns), os.environ.get("DECIK_FWD_PLAN"), os.environ.get("DECIK_SMALL_M"))
     raw = _RAW.get(key)

@@ -7,6 +7,9 @@
  * hipStream_t (NULL = the default stream). Every entry point returns 0 on success and a
  * non-zero code on error; dk_last_error() then describes the error (per calling thread).
  * The library never allocates device memory: split-K workspaces are passed in.
+ * The fused linear entries (forward, GLU forward, RoPE forward, input gradient with or without
+ * the SwiGLU epilogue) accept m = 0 token rows: the shapes and descriptors are still checked,
+ * nothing is launched, and the activation / output pointers may then be NULL.
  *
  * Reference interfaces replaced (tokha-t/decik, Python + Triton):
  *   dk_nf4_dequant / dk_nf4_dequant_batched  <- skc_nf4_dequant_kernel + dequantize_nf4

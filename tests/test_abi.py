@@ -116,6 +116,42 @@ def test_forward_rejects_rows_not_multiple_of_8(m):
     assert rc != 0 and b"multiple of 8" in L.dk_last_error()
 
 
+def test_zero_token_rows_are_a_no_op():
+    """m = 0 (an empty batch, which the reference's dequantize + F.linear path accepts): every fused
+    linear entry checks shapes and descriptors, launches nothing and returns 0, with NULL
+    activation and output pointers and any row strides (an empty tensor's strides carry no
+    meaning: the gradient of a sum is an expanded tensor of stride 0); a bad shape is still
+    rejected."""
+    from decik_amd import _lib
+
+    L = _lib.lib()
+    g = (_lib.LinearFwdGroup * 2)()
+    for i in range(2):
+        g[i].w = _fake_weight(64, 1536)
+        g[i].y, g[i].ldy = None, 0
+    assert L.dk_nf4_linear_fwd(None, 0, 1536, 0, g, 2, 0, None, 0, None) == 0
+    assert L.dk_nf4_glu_fwd(None, 0, 1536, 0, g, 0, None, 0, None) == 0
+    heads = (ctypes.c_void_p * 2)(None, None)
+    tab = ctypes.c_void_p(256)
+    assert L.dk_nf4_linear_rope_fwd(None, 0, 1536, 0, g, 2, 0, tab, tab, 64, 1, heads, None, 0, None) == 0
+    b = (_lib.LinearBwdGroup * 2)()
+    for i in range(2):
+        b[i].w = _fake_weight(64, 1536)
+        b[i].dy, b[i].lddy = None, 0
+    assert L.dk_nf4_linear_bwd(b, 2, 0, 1536, None, 0, 0, 0, None, 0, None) == 0
+    assert L.dk_nf4_linear_bwd_swiglu(b, 0, 1536, 0, None, None, 0, None, None, 0, None) == 0
+    rc = L.dk_nf4_linear_fwd(None, 0, 1000, 1000, g, 1, 0, None, 0, None)
+    assert rc != 0 and b"multiple of 32" in L.dk_last_error()
+    # one row: the row checks apply again
+    rc = L.dk_nf4_linear_fwd(ctypes.c_void_p(16), 1, 1536, 0, g, 1, 0, None, 0, None)
+    assert rc != 0 and b"ldx >= k" in L.dk_last_error()
+    rc = L.dk_nf4_linear_bwd(b, 1, 1, 1536, ctypes.c_void_p(16), 1536, 0, 0, None, 0, None)
+    assert rc != 0 and b"dy must be" in L.dk_last_error()
+    g[1].w = _fake_weight(60, 1536)
+    rc = L.dk_nf4_glu_fwd(None, 0, 1536, 1536, g, 0, None, 64, None)
+    assert rc != 0 and b"shapes differ" in L.dk_last_error()
+
+
 def test_workspace_sizes():
     from decik_amd import _lib
 

@@ -226,3 +226,42 @@ def test_large_m_planned_launches(device):
     dx = linear_backward([dict(packed=pg, qs=qg, dy=dg), dict(packed=pu, qs=qu, dy=du)], m, k, dx_fp32=True)
     ref = dg.float() @ wg32 + du.float() @ wu32
     assert_close(dx, ref.cpu().numpy(), max_rel=1e-4, mean_rel=1e-5, what="large-M grouped bwd")
+
+
+def test_empty_token_batches(device):
+    """Zero token rows: NF4Linear (forward and backward, with and without leading dims), the
+    fused linear entries and the GLU forward return empty outputs and launch nothing; the C
+    entries accept m = 0 with valid shapes and return 0."""
+    from decik_amd._lib import LinearBwdGroup, LinearFwdGroup, lib, ptr, stream_of, weight_desc
+    from decik_amd.nf4 import NF4Linear, glu_forward, linear_backward, linear_forward
+
+    n, k = 256, 512
+    packed, qs, _ = make_weight((n, k), seed=5, device=device)
+    for shape in ((0, k), (3, 0, k)):
+        x = torch.zeros(shape, dtype=torch.float16, device=device, requires_grad=True)
+        y = NF4Linear.apply(x, packed, None, qs)
+        assert y.shape == shape[:-1] + (n,)
+        y.sum().backward()
+        assert x.grad.shape == shape
+    x0 = torch.zeros((0, k), dtype=torch.float16, device=device)
+    (y0,) = linear_forward(x0, [dict(packed=packed, qs=qs)])
+    assert y0.shape == (0, n)
+    dx0 = linear_backward([dict(packed=packed, qs=qs, dy=torch.zeros((0, n), dtype=torch.float16, device=device))], 0, k)
+    assert dx0.shape == (0, k)
+    g, u, h = glu_forward(x0, dict(packed=packed, qs=qs), dict(packed=packed, qs=qs))
+    assert g.shape == u.shape == h.shape == (0, n)
+    w, keep = weight_desc(packed, qs, device)
+    fg = (LinearFwdGroup * 1)()
+    fg[0].w = w
+    out = torch.empty((1, n), dtype=torch.float16, device=device)
+    fg[0].y, fg[0].ldy = out.data_ptr(), n
+    xs = torch.zeros((1, k), dtype=torch.float16, device=device)
+    assert lib().dk_nf4_linear_fwd(ptr(xs), 0, k, k, fg, 1, 0, None, 0, stream_of(device)) == 0
+    bg = (LinearBwdGroup * 1)()
+    bg[0].w = w
+    dys = torch.zeros((1, n), dtype=torch.float16, device=device)
+    bg[0].dy, bg[0].lddy = dys.data_ptr(), n
+    dxs = torch.empty((1, k), dtype=torch.float16, device=device)
+    assert lib().dk_nf4_linear_bwd(bg, 1, 0, k, ptr(dxs), k, 0, 0, None, 0, stream_of(device)) == 0
+    torch.cuda.synchronize()
+    del keep

@@ -106,6 +106,20 @@ def test_recomputed_mlp_reference_signature_and_fallback(bnb, device):
         assert_close(x.grad, ref["dx"], what=f"dX hidden={hidden}")
 
 
+def test_recomputed_mlp_empty_batch(bnb, device):
+    """An empty token batch through RecomputedMLP (as the reference's dequantize + F.linear chain
+    takes it): empty fp16 output, empty fp32 input gradient, no error."""
+    from decik_amd.mlp import RecomputedMLP
+
+    mods = [_module(bnb, s, 80 + i, device)[0] for i, s in enumerate(((8960, 1536), (8960, 1536), (1536, 8960)))]
+    for shape in ((0, 1536), (2, 0, 1536)):
+        x = torch.zeros(shape, dtype=torch.float32, device=device, requires_grad=True)
+        out = RecomputedMLP.apply(x, *mods)
+        assert out.shape == shape and out.dtype == torch.float16
+        out.float().sum().backward()
+        assert x.grad.shape == shape and x.grad.dtype == torch.float32
+
+
 @pytest.mark.parametrize("packed", [True, False])
 def test_lora_pair_from_norm(packed, device):
     """LoRAPairFromNorm with the reference's 19 arguments, packed-mask and unpacked paths
