@@ -236,6 +236,93 @@ def bench_mlp(steps, warmup, device, n_sets=None, only=None):
                 step_flops=step_flops, n_sets=n_sets, uncached_ms=uncached, graph_ms=graph_ms)
 
 
+def bench_mlp_gpu_baselines(steps, warmup, device, our_ms):
+    """The same MLP block on the same GPU without the fused kernels, for scale:
+
+    reference_algorithm -- the reference's RecomputedMLP step as it computes it
+        (solution/mlp.py:62-110): every weight dequantized to fp16 before each use (3 + 3 per
+        step; this library's dequantization kernel stands in for skc_nf4_dequant_kernel, bit for
+        bit), fp16 F.linear / matmul on torch (hipBLASLt), the SwiGLU kernels, gate/up recomputed
+        in the backward (8 GEMMs), dX as two fp16 products summed in fp32.
+    fp16_library_gemms -- the fused step's six products (gate/up forward, down forward, down
+        input gradient, gate/up input gradient) as plain fp16 torch GEMMs on weights dequantized
+        once before timing, plus the SwiGLU kernels: the vendor library's rate at these shapes
+        with no dequantization in the step at all.
+    Both rotate over weight sets larger than the 256 MB Infinity Cache, as the fused step does
+    (fp16 weights: 27.5 MB a projection). Time per step = K eager steps between two events."""
+    import torch
+    import torch.nn.functional as F
+
+    from decik_amd import nf4
+    from decik_amd.swiglu import swiglu_bwd, swiglu_fwd
+
+    x = seeded_fp16((M, HIDDEN), 1001, 1.0, device)
+    dy = seeded_fp16((M, HIDDEN), 1002, 1e-2, device)
+    n_sets = 4  # 4 x 82.6 MB of fp16 weights for the library GEMMs (330 MB > the Infinity Cache)
+    layers = make_layers(max(n_sets, mlp_weight_sets()), ["gate", "up", "down"], device)
+    n_ref = len(layers)
+
+    def ref_step(i):
+        L = layers[i % n_ref]
+        wg = nf4.dequantize_nf4(*L["gate"])
+        gate = F.linear(x, wg)
+        wu = nf4.dequantize_nf4(*L["up"])
+        up = F.linear(x, wu)
+        h = swiglu_fwd(gate, up)
+        del gate, up
+        wd = nf4.dequantize_nf4(*L["down"])
+        out = F.linear(h, wd)
+        wd = nf4.dequantize_nf4(*L["down"])
+        gh = torch.matmul(dy, wd)
+        wg = nf4.dequantize_nf4(*L["gate"])
+        gate = F.linear(x, wg)
+        wu = nf4.dequantize_nf4(*L["up"])
+        up = F.linear(x, wu)
+        dgate, dup = swiglu_bwd(gh, gate, up, out=(gate, up))
+        dx = torch.matmul(dgate, wg).float() + torch.matmul(dup, wu).float()
+        return out, dx
+
+    w16 = [{n: nf4.dequantize_nf4(*layers[s][n]) for n in ("gate", "up", "down")} for s in range(n_sets)]
+
+    def lib_step(i):
+        W = w16[i % n_sets]
+        gate = F.linear(x, W["gate"])
+        up = F.linear(x, W["up"])
+        h = swiglu_fwd(gate, up)
+        out = F.linear(h, W["down"])
+        gh = torch.matmul(dy, W["down"])
+        dgate, dup = swiglu_bwd(gh, gate, up, out=(gate, up))
+        dx = torch.matmul(dgate, W["gate"]).float() + torch.matmul(dup, W["up"]).float()
+        return out, dx
+
+    def timed(step, sets):
+        for i in range(max(warmup, sets)):
+            step(i)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(steps):
+            step(i)
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / steps
+
+    flops = 3 * gemm_flops(INTER, HIDDEN) * 2  # the fused step's six products
+    res = {}
+    # launches per step: dequantizations + GEMMs + the two SwiGLU kernels + two fp32 casts and their sum
+    for name, step, sets, launches, gemms in (("reference_algorithm", ref_step, n_ref, 6 + 8 + 2 + 3, 8),
+                                              ("fp16_library_gemms", lib_step, n_sets, 6 + 2 + 3, 6)):
+        ms = timed(step, sets)
+        res[name] = dict(ms_per_step=round(ms, 4), tflops=round(flops / (ms * 1e-3) / 1e12, 1),
+                         fused_speedup=round(ms / our_ms, 3), launches=launches, gemms=gemms)
+    del w16, layers
+    torch.cuda.empty_cache()
+    res["note"] = ("tflops: the fused step's 137.1 GFLOP (6 products) over each step's time; the "
+                   "reference's step does 8 products (gate/up recomputed) and 6 whole-weight "
+                   "dequantizations; fused_speedup = that step's time / the fused step's")
+    return res
+
+
 def graph_mlp_steps(step, n_sets, reps=3):
     """The MLP step (its six kernels) over every weight set, captured once in a HIP graph and
     replayed: ms per step with the host's launch cost and the gaps between eager launches taken
@@ -1034,6 +1121,11 @@ def main():
         return
     with no_gc():
         mlp = bench_mlp(args.steps, args.warmup, device, only=args.only)
+    baselines = None
+    if args.only is None and not args.skip_configs:
+        torch.cuda.empty_cache()
+        with no_gc():
+            baselines = bench_mlp_gpu_baselines(args.steps, args.warmup, device, mlp["ms_step"])
     if args.copy_probe:
         copy_probe(device)
     with no_gc():
@@ -1101,6 +1193,8 @@ def main():
             note="the same step captured once in a HIP graph (one step per weight set) and replayed; "
                  "value stays the eager step"),
     )
+    if baselines is not None:
+        line["gpu_baselines"] = baselines
     if c3 is not None:
         line["c3_attention_step"] = c3
     if c4 is not None:
