@@ -1086,7 +1086,7 @@ def main():
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, "
+        print(f"bench.py: measures one GPU only (asked for --gpus {args.gpus}, "
               f"WORLD_SIZE={world}); the NF4 path needs no collectives and is not run on several GPUs.",
               file=sys.stderr)
         sys.exit(2)

@@ -1,7 +1,8 @@
 /*
  * CPU oracle for the NF4 dequantization path. TEST INFRASTRUCTURE ONLY: only tests/,
- * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load this library, and only as
- * the checker (or, in bench.py, as the timed CPU baseline). The product path never calls it.
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load this library, and only to
+ * produce expected results (or, in bench.py, as the timed CPU baseline). The product path never
+ * calls it.
  *
  * Restates the reference kernel skc_nf4_dequant_kernel (solution/nf4.py:27-48) on the CPU:
  *   for the packed byte b at flat byte offset i:
