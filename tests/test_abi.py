@@ -381,3 +381,49 @@ def test_plan_memo_follows_the_tuning_variables(monkeypatch):
     assert launch_plan(True, 830, 1536, [1536])["splits"] == 1
     monkeypatch.delenv("DECIK_BWD_PLAN")
     assert launch_plan(True, 830, 1536, [1536]) == bwd
+
+
+def test_workspace_queries_cover_every_plan():
+    """Property test of the planner (host-only): for random launch shapes, every plan the forward
+    and input-gradient entries may choose -- with or without LoRA terms, any block size, the GLU
+    and SwiGLU forms -- fits the workspace the matching query reports (a plan needing more made
+    a call fail with 'workspace too small'), no-split plans never split, and every split gets work."""
+    from hypothesis import HealthCheck, given, settings
+    from hypothesis import strategies as st
+
+    from decik_amd import _lib
+    from decik_amd.nf4 import launch_plan
+
+    L = _lib.lib()
+
+    @settings(max_examples=250, deadline=None, suppress_health_check=[HealthCheck.too_slow])
+    @given(m=st.one_of(st.integers(1, 40), st.integers(41, 9000)),
+           k=st.integers(1, 640).map(lambda v: 32 * v),
+           ns=st.lists(st.integers(1, 3000).map(lambda v: 8 * v), min_size=1, max_size=4),
+           blocksize=st.sampled_from([32, 64, 128, 256]))
+    def check(m, k, ns, blocksize):
+        arr = (ctypes.c_int64 * len(ns))(*ns)
+        fwd_ws = L.dk_nf4_linear_fwd_workspace(m, k, arr, len(ns))
+        bwd_ws = L.dk_nf4_linear_bwd_workspace(m, k, arr, len(ns))
+        ncols = sum(ns)
+        steps64 = -(-k // 64)
+        for lora in (False, True):
+            p = launch_plan(False, m, k, ns, lora=lora, blocksize=blocksize)
+            assert 1 <= p["splits"] <= max(steps64, 1)
+            if p["splits"] > 1:
+                assert fwd_ws >= p["splits"] * m * ncols * 4, (m, k, ns, blocksize, lora, p, fwd_ws)
+            assert launch_plan(False, m, k, ns, lora=lora, no_split=True, blocksize=blocksize)["splits"] == 1
+        if len(ns) == 2 and ns[0] == ns[1]:
+            assert launch_plan(False, m, k, ns, glu=True, blocksize=blocksize)["splits"] == 1
+        b = launch_plan(True, m, k, ns, blocksize=blocksize)
+        assert b["splits"] >= 1 and b["launches"] in (1, 2)
+        if b["launches"] == 1 and b["splits"] > 1:
+            assert bwd_ws >= b["splits"] * m * k * 4, (m, k, ns, blocksize, b, bwd_ws)
+        if b["launches"] == 2 and b["splits_second"] > 1:
+            # the left-over columns' own split launch: its slabs (fewer columns than k) need a workspace
+            assert bwd_ws > 0, (m, k, ns, blocksize, b)
+        assert launch_plan(True, m, k, ns, no_split=True, blocksize=blocksize)["splits"] == 1
+        if len(ns) == 1:
+            assert launch_plan(True, m, k, ns, glu=True, blocksize=blocksize)["splits"] == 1
+
+    check()
