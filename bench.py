@@ -823,9 +823,10 @@ def stack_flops(n_layers):
 
 def bench_c4(steps, warmup, device, n_layers=28):
     """One training step of the 28-layer stack (solution/varlen.py:254-257 -> attn.py:396-418,
-    mlp.py:62-110): per layer forward q/k/v with LoRA q/v (one fused launch, U from
-    dk_lora_down), o, gate+up+SwiGLU, down; backward down with the SwiGLU backward, gate+up, o,
-    q/k/v with the LoRA input-gradient terms (GU, dA, dB from dk_lora_bwd). Attention and the
+    mlp.py:62-110): per layer forward q/k/v with LoRA q/v (one fused launch, U of both adapters
+    from one dk_lora_down_group launch), o, gate+up+SwiGLU, down; backward down with the SwiGLU
+    backward, gate+up, o, q/k/v with the LoRA input-gradient terms (GU, dB of both adapters in one
+    launch and dA in another, dk_lora_bwd_group). Attention and the
     norms are outside this path: each layer's attention output and MLP input are fixed synthetic
     tensors; gate/up are kept from the forward (no recompute). Also timed: the same step with U
     and GU precomputed (the dequant-GEMM launches alone)."""
@@ -846,7 +847,7 @@ def bench_c4(steps, warmup, device, n_layers=28):
     def layer_step(L, li, lora_kernels):
         (aq, bq), (av, bv) = L["q_lora"], L["v_lora"]
         if lora_kernels:
-            uq, uv = lora.lora_down(x, aq), lora.lora_down(x, av)
+            uq, uv = lora.lora_down_group([(x, aq, None, None), (x, av, None, None)])
         else:
             uq, uv = pre[li][0], pre[li][1]
         items = [dict(packed=L["q"][0], qs=L["q"][1], bias=L["q_bias"], lora_u=uq, lora_b=bq, lora_scale=s),
@@ -868,8 +869,8 @@ def bench_c4(steps, warmup, device, n_layers=28):
                              dict(packed=L["up"][0], qs=L["up"][1], dy=dup)], M, HIDDEN)
         nf4.linear_backward([dict(packed=L["o"][0], qs=L["o"][1], dy=dy)], M, HIDDEN)
         if lora_kernels:
-            guq, _, _ = lora.lora_grads(dq, uq, x, bq, s)
-            guv, _, _ = lora.lora_grads(dkv, uv, x, bv, s)
+            (guq, _, _), (guv, _, _) = lora.lora_grads_group([dict(dy16=dq, u16=uq, x=x, b16=bq, scaling=s),
+                                                              dict(dy16=dkv, u16=uv, x=x, b16=bv, scaling=s)])
         else:
             guq, guv = pre[li][2], pre[li][3]
         nf4.linear_backward([dict(packed=L["q"][0], qs=L["q"][1], dy=dq, lora_gu=guq, lora_a=aq),
@@ -905,8 +906,8 @@ def bench_c4(steps, warmup, device, n_layers=28):
     return dict(
         workload=f"Qwen2.5-1.5B {n_layers} layers x {{q,k,v,o,gate,up,down}} NF4 (bs 64, double quant) + "
                  f"LoRA r=16 on q/v, M={M}, one training step: 8 fused dequant-GEMM launches per layer "
-                 f"({7 * n_layers} forward + {7 * n_layers} input-gradient GEMMs) + 6 LoRA side launches "
-                 f"(U of q and v; GU with dB, then dA, of q and v)",
+                 f"({7 * n_layers} forward + {7 * n_layers} input-gradient GEMMs) + 3 LoRA side launches "
+                 f"(U of q and v in one; GU with dB of q and v in one, then dA of q and v in one)",
         ms_per_step=round(res["step"], 4), dequant_gemm_ms=round(res["gemm_only"], 4),
         dequant_gemm_share=round(res["gemm_only"] / res["step"], 4),
         tflops=round((base + lora_f) / (res["step"] * 1e-3) / 1e12, 1),

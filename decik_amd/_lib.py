@@ -44,6 +44,13 @@ class LinearBwdGroup(ctypes.Structure):
                 ("reserved", c_i32)]
 
 
+class LoraBranch(ctypes.Structure):
+    """dk_lora_branch: one adapter of a grouped LoRA call (dk_lora_down_group, dk_lora_bwd_group)."""
+    _fields_ = [("x", c_vp), ("keep_bits", c_vp), ("keep_scale", c_vp), ("a", c_vp), ("u", c_vp),
+                ("dy", c_vp), ("b", c_vp), ("gu", c_vp), ("da", c_vp), ("db", c_vp),
+                ("ldx", c_i64), ("lddy", c_i64), ("n", c_i64), ("scale", c_f32), ("x_fp32", c_i32)]
+
+
 EXPORTS = {
     "dk_nf4_dequant": ([ctypes.POINTER(NF4Weight), c_vp, c_vp], c_i32),
     "dk_nf4_dequant_batched": ([ctypes.POINTER(NF4Weight), ctypes.POINTER(c_vp), c_i32, c_vp], c_i32),
@@ -73,6 +80,8 @@ EXPORTS = {
                              c_f32, c_vp, c_vp, c_vp, c_vp], c_i32),
     "dk_lora_bwd": ([c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_i32, c_f32, c_vp,
                      c_vp, c_vp, c_vp], c_i32),
+    "dk_lora_down_group": ([ctypes.POINTER(LoraBranch), c_i32, c_i64, c_i64, c_i32, c_vp], c_i32),
+    "dk_lora_bwd_group": ([ctypes.POINTER(LoraBranch), c_i32, c_i64, c_i64, c_i32, c_vp], c_i32),
     "dk_lora_keep_pack": ([c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp], c_i32),
     "dk_lora_dropout_inputs": ([c_vp, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp], c_i32),
     "dk_lora_input_grad": ([c_vp, c_vp, c_vp, c_vp, c_f32, c_f32, c_vp, c_i64, c_i64, c_vp], c_i32),

@@ -1110,48 +1110,107 @@ int dk_nf4_linear_bwd_swiglu(const dk_linear_bwd_group* group, int64_t m, int64_
 
 }  // extern "C"
 
-// dk_lora_down / dk_lora_down_dropout: x fp16 or fp32 (x32), keep null or packed dropout bits
+// The LoRA entries: every branch is checked as the per-branch entries check it, then handed to the
+// grouped launchers (one branch for dk_lora_down / dk_lora_bwd and their dropout forms).
+static int lora_check_common(const std::string& who, int rank, int64_t m, int64_t k) {
+    if (rank != 16 && rank != 32) return fail(who + ": rank must be 16 or 32");
+    if (m < 0 || k <= 0) return fail(who + ": bad shapes");
+    return 0;
+}
+
+// x fp16 or fp32 (x32), keep null or packed dropout bits
+static int lora_down_check(const std::string& who, const LoraBranch& b, int64_t m, int64_t k, int rank) {
+    if ((k % 8) != 0 || b.ldx < k || (b.ldx % 8) != 0) return fail(who + ": k and ldx must be multiples of 8");
+    if (b.x == nullptr || b.a == nullptr || b.u == nullptr || !aligned(b.x, 16) || !aligned(b.a, 16))
+        return fail(who + ": x and a must be 16-byte aligned");
+    if (b.keep != nullptr && b.keep_scale == nullptr) return fail(who + ": keep bits need keep_scale");
+    // 32-bit byte offsets (with a 32-row margin for the tile past the last row)
+    if ((m + 32) * b.ldx * (b.x32 ? 4 : 2) >= INT32_MAX || k * rank * 2 >= INT32_MAX || (m + 32) * (k / 8) >= INT32_MAX)
+        return fail(who + ": tensors too large");
+    return 0;
+}
+
+static int lora_bwd_check(const std::string& who, const LoraBranch& b, int64_t m, int64_t k, int rank) {
+    const int64_t n = b.n;
+    if (n <= 0 || b.lddy < n || b.ldx < k) return fail(who + ": bad shapes");
+    if (b.dy == nullptr || b.u == nullptr || b.x == nullptr || b.b == nullptr || b.gu == nullptr)
+        return fail(who + ": null pointer");
+    if (!aligned(b.u, 16) || !aligned(b.b, 16) || !aligned(b.gu, 16) || !aligned(b.dy, 16) ||
+        !aligned(b.x, b.x32 ? 4 : 2))
+        return fail(who + ": dy, u, b, gu must be 16-byte aligned (x aligned to its element)");
+    if ((n % 8) != 0 || (b.lddy % 8) != 0) return fail(who + ": n and lddy must be multiples of 8");
+    if (b.keep != nullptr && (b.keep_scale == nullptr || (k % 8) != 0))
+        return fail(who + ": keep bits need keep_scale and k % 8 == 0");
+    // 32-bit byte offsets (with a 32-row margin for the tile past the last row)
+    if ((m + 32) * b.lddy * 2 >= INT32_MAX || (m + 32) * b.ldx * (b.x32 ? 4 : 2) >= INT32_MAX ||
+        (m + 32) * rank * 2 >= INT32_MAX || n * rank * 2 >= INT32_MAX || (m + 32) * (k / 8) >= INT32_MAX)
+        return fail(who + ": tensors too large");
+    return 0;
+}
+
+static LoraBranch lora_branch(const void* x, bool x32, int64_t ldx, const uint8_t* keep, const float* keep_scale) {
+    LoraBranch b{};
+    b.x = x;
+    b.x32 = x32;
+    b.ldx = ldx;
+    b.keep = keep;
+    b.keep_scale = keep_scale;
+    return b;
+}
+
 static int lora_down_impl(const std::string& who, const void* x, bool x32, int64_t m, int64_t k, int64_t ldx,
                           const uint8_t* keep, const float* keep_scale, const uint16_t* a, int rank, uint16_t* u,
                           void* stream) {
-    if (rank != 16 && rank != 32) return fail(who + ": rank must be 16 or 32");
-    if (m < 0 || k <= 0 || (k % 8) != 0 || ldx < k || (ldx % 8) != 0)
-        return fail(who + ": k and ldx must be multiples of 8");
-    if (x == nullptr || a == nullptr || u == nullptr || !aligned(x, 16) || !aligned(a, 16))
-        return fail(who + ": x and a must be 16-byte aligned");
-    if (keep != nullptr && keep_scale == nullptr) return fail(who + ": keep bits need keep_scale");
-    // 32-bit byte offsets (with a 32-row margin for the tile past the last row)
-    if ((m + 32) * ldx * (x32 ? 4 : 2) >= INT32_MAX || k * rank * 2 >= INT32_MAX || (m + 32) * (k / 8) >= INT32_MAX)
-        return fail(who + ": tensors too large");
-    return check_hip(launch_lora_down(x, x32, m, k, ldx, keep, keep_scale, reinterpret_cast<const _Float16*>(a),
-                                      rank, reinterpret_cast<_Float16*>(u), static_cast<hipStream_t>(stream)),
-                     (who + " launch").c_str());
+    if (lora_check_common(who, rank, m, k)) return 1;
+    LoraBranch b = lora_branch(x, x32, ldx, keep, keep_scale);
+    b.a = reinterpret_cast<const _Float16*>(a);
+    b.u = reinterpret_cast<_Float16*>(u);
+    if (lora_down_check(who, b, m, k, rank)) return 1;
+    return check_hip(launch_lora_down(&b, 1, m, k, rank, static_cast<hipStream_t>(stream)), (who + " launch").c_str());
 }
 
 static int lora_bwd_impl(const std::string& who, const uint16_t* dy, int64_t lddy, const uint16_t* u, const void* x,
                          bool x32, int64_t ldx, const uint8_t* keep, const float* keep_scale, const uint16_t* b,
                          int64_t m, int64_t n, int64_t k, int rank, float scale, uint16_t* gu, float* da, float* db,
                          void* stream) {
-    if (rank != 16 && rank != 32) return fail(who + ": rank must be 16 or 32");
-    if (m < 0 || n <= 0 || k <= 0 || lddy < n || ldx < k)
-        return fail(who + ": bad shapes");
-    if (dy == nullptr || u == nullptr || x == nullptr || b == nullptr || gu == nullptr)
-        return fail(who + ": null pointer");
-    if (!aligned(u, 16) || !aligned(b, 16) || !aligned(gu, 16) || !aligned(dy, 16) || !aligned(x, x32 ? 4 : 2))
-        return fail(who + ": dy, u, b, gu must be 16-byte aligned (x aligned to its element)");
-    if ((n % 8) != 0 || (lddy % 8) != 0) return fail(who + ": n and lddy must be multiples of 8");
-    if (keep != nullptr && (keep_scale == nullptr || (k % 8) != 0))
-        return fail(who + ": keep bits need keep_scale and k % 8 == 0");
-    // 32-bit byte offsets (with a 32-row margin for the tile past the last row)
-    if ((m + 32) * lddy * 2 >= INT32_MAX || (m + 32) * ldx * (x32 ? 4 : 2) >= INT32_MAX ||
-        (m + 32) * rank * 2 >= INT32_MAX || n * rank * 2 >= INT32_MAX || (m + 32) * (k / 8) >= INT32_MAX)
-        return fail(who + ": tensors too large");
-    return check_hip(launch_lora_bwd(reinterpret_cast<const _Float16*>(dy), lddy,
-                                     reinterpret_cast<const _Float16*>(u), x, x32, ldx, keep, keep_scale,
-                                     reinterpret_cast<const _Float16*>(b), m, n, k, rank, scale,
-                                     reinterpret_cast<_Float16*>(gu), da, db,
-                                     static_cast<hipStream_t>(stream)),
-                     (who + " launch").c_str());
+    if (lora_check_common(who, rank, m, k)) return 1;
+    LoraBranch br = lora_branch(x, x32, ldx, keep, keep_scale);
+    br.dy = reinterpret_cast<const _Float16*>(dy);
+    br.lddy = lddy;
+    br.n = n;
+    br.u = const_cast<_Float16*>(reinterpret_cast<const _Float16*>(u));
+    br.b = reinterpret_cast<const _Float16*>(b);
+    br.scale = scale;
+    br.gu = reinterpret_cast<_Float16*>(gu);
+    br.da = da;
+    br.db = db;
+    if (lora_bwd_check(who, br, m, k, rank)) return 1;
+    return check_hip(launch_lora_bwd(&br, 1, m, k, rank, static_cast<hipStream_t>(stream)), (who + " launch").c_str());
+}
+
+// The branches of a grouped call as the launchers take them (every one checked).
+static int lora_group(const std::string& who, const dk_lora_branch* in, int nb, int64_t m, int64_t k, int rank,
+                      bool backward, LoraBranch* out) {
+    if (in == nullptr || nb < 1 || nb > kLoraMaxBranches) return fail(who + ": need 1..4 branches");
+    if (lora_check_common(who, rank, m, k)) return 1;
+    for (int i = 0; i < nb; ++i) {
+        const dk_lora_branch& s = in[i];
+        LoraBranch b = lora_branch(s.x, s.x_fp32 != 0, s.ldx, s.keep_bits, s.keep_scale);
+        b.a = reinterpret_cast<const _Float16*>(s.a);
+        b.u = reinterpret_cast<_Float16*>(s.u);
+        b.dy = reinterpret_cast<const _Float16*>(s.dy);
+        b.lddy = s.lddy;
+        b.n = s.n;
+        b.b = reinterpret_cast<const _Float16*>(s.b);
+        b.gu = reinterpret_cast<_Float16*>(s.gu);
+        b.da = s.da;
+        b.db = s.db;
+        b.scale = s.scale;
+        const std::string w = who + " branch " + std::to_string(i);
+        if (backward ? lora_bwd_check(w, b, m, k, rank) : lora_down_check(w, b, m, k, rank)) return 1;
+        out[i] = b;
+    }
+    return 0;
 }
 
 extern "C" {
@@ -1184,6 +1243,24 @@ int dk_lora_bwd_dropout(const uint16_t* dy, int64_t lddy, const uint16_t* u, con
     g_error.clear();
     return lora_bwd_impl("dk_lora_bwd_dropout", dy, lddy, u, x, x_fp32 != 0, ldx, keep_bits, keep_scale, b, m, n,
                          k, rank, scale, gu, da, db, stream);
+}
+
+int dk_lora_down_group(const dk_lora_branch* branches, int nbranches, int64_t m, int64_t k, int rank,
+                       void* stream) {
+    g_error.clear();
+    LoraBranch br[kLoraMaxBranches];
+    if (lora_group("dk_lora_down_group", branches, nbranches, m, k, rank, false, br)) return 1;
+    return check_hip(launch_lora_down(br, nbranches, m, k, rank, static_cast<hipStream_t>(stream)),
+                     "dk_lora_down_group launch");
+}
+
+int dk_lora_bwd_group(const dk_lora_branch* branches, int nbranches, int64_t m, int64_t k, int rank,
+                      void* stream) {
+    g_error.clear();
+    LoraBranch br[kLoraMaxBranches];
+    if (lora_group("dk_lora_bwd_group", branches, nbranches, m, k, rank, true, br)) return 1;
+    return check_hip(launch_lora_bwd(br, nbranches, m, k, rank, static_cast<hipStream_t>(stream)),
+                     "dk_lora_bwd_group launch");
 }
 
 int dk_lora_keep_pack(const uint8_t* keep_q, const uint8_t* keep_v, uint8_t* bits_q, uint8_t* bits_v,

@@ -177,12 +177,29 @@ hipError_t launch_splitk_reduce(const ReduceArgs& a, hipStream_t s);
 // LoRA and SwiGLU helpers.
 // x: fp16 or fp32 (x32) [m, ldx]; keep: packed dropout bits [m, k / 8] with keep_scale a device
 // fp32 scalar, or null (no dropout)
-hipError_t launch_lora_down(const void* x, bool x32, int64_t m, int64_t k, int64_t ldx, const uint8_t* keep,
-                            const float* keep_scale, const _Float16* a, int rank, _Float16* u, hipStream_t s);
-hipError_t launch_lora_bwd(const _Float16* dy, int64_t lddy, const _Float16* u, const void* x, bool x32,
-                           int64_t ldx, const uint8_t* keep, const float* keep_scale, const _Float16* b,
-                           int64_t m, int64_t n, int64_t k, int rank, float scale, _Float16* gu, float* da,
-                           float* db, hipStream_t s);
+// Several branches (the q and v adapters of one layer) share a launch of each product: every
+// branch takes its own range of work-groups, which compute what a launch of that branch alone
+// computes, in the same order.
+constexpr int kLoraMaxBranches = 4;
+struct LoraBranch {
+    const void* x;           // the branch input (fp16, or fp32 with x32), [m, ldx]
+    const uint8_t* keep;     // packed dropout bits [m, k / 8] or null
+    const float* keep_scale; // device scalar 1 / (1 - p) with keep
+    const _Float16* a;       // A [rank, k] (down: U = X.A^T)
+    _Float16* u;             // U [m, rank]: written by the down product, read by the backward
+    const _Float16* dy;      // backward: dY [m, n], row stride lddy
+    const _Float16* b;       // backward: B [n, rank]
+    _Float16* gu;            // backward: GU [m, rank]
+    float* da;               // backward: dA fp32 [rank, k] or null
+    float* db;               // backward: dB fp32 [n, rank] or null
+    int64_t ldx, lddy, n;
+    float scale;             // backward: the LoRA scaling s
+    bool x32;
+};
+// All branches share m, k and the rank; a launch per kind of input (fp16 / fp32, with or without
+// dropout) where they differ.
+hipError_t launch_lora_down(const LoraBranch* br, int nbr, int64_t m, int64_t k, int rank, hipStream_t s);
+hipError_t launch_lora_bwd(const LoraBranch* br, int nbr, int64_t m, int64_t k, int rank, hipStream_t s);
 hipError_t launch_lora_keep_pack(const uint8_t* kq, const uint8_t* kv, uint8_t* bq, uint8_t* bv,
                                  int64_t nbytes, hipStream_t s);
 hipError_t launch_lora_dropout_inputs(const void* x, bool x32, const uint8_t* bq, const uint8_t* bv,

@@ -11,7 +11,9 @@
 // and GU, 16 weight rows for dB, 16 columns of A for dA) and all r rank columns; its waves take
 // the 32-wide contraction chunks in turn and their fp32 tiles are summed through LDS in wave
 // order, so the summation order is fixed (no atomics) and every call gives the same bits.
-// GU and dB are one launch (both read dY); dA, which needs GU, is a second one.
+// GU and dB are one launch (both read dY); dA, which needs GU, is a second one. The LoRA branches
+// of one layer (q and v) share each launch: a job table gives every branch its own range of
+// work-groups (a branch's tiles are those of a launch of it alone, so the bits are the same).
 //
 // X, as lora_down and lora_da read it, is the branch's input: fp16 or fp32 storage, optionally
 // through dropout (LoRAPairFromNorm's packed path, solution/attn.py:153-165, 219-223, 241-243):
@@ -150,19 +152,65 @@ __device__ __forceinline__ half8_t x_col8(const XInput& in, int mm, int col, boo
     return drop_round<KEEP>(xf, bits, in.scale);
 }
 
+// Job tables of the grouped launches (kernel arguments): branch j owns the work-groups
+// [start[j], start[j + 1]), and each of its work-groups computes what it computes in a launch of
+// that branch alone.
+struct DownJob {
+    const void* x;
+    const uint8_t* keep;
+    const float* keep_scale;
+    const _Float16* a;
+    _Float16* u;
+    int ldx;
+};
+struct GuDbJob {
+    const _Float16* dy;
+    const _Float16* u;
+    const _Float16* b;
+    _Float16* gu;
+    float* db;
+    float scale;
+    int lddy, n;
+};
+struct DaJob {
+    const _Float16* gu;
+    const void* x;
+    const uint8_t* keep;
+    const float* keep_scale;
+    float* da;
+    int ldx;
+};
+template <typename J>
+struct Jobs {
+    J j[kLoraMaxBranches];
+    int start[kLoraMaxBranches + 1];
+    int nj, m, k;
+};
+
+// this work-group's branch (uniform) and its work-group index within the branch's range
+template <typename J>
+__device__ __forceinline__ int job_of(const Jobs<J>& jobs, int* local) {
+    int jb = 0;
+#pragma unroll
+    for (int q = 1; q < kLoraMaxBranches; ++q)
+        if (q < jobs.nj && (int)blockIdx.x >= jobs.start[q]) jb = q;
+    *local = (int)blockIdx.x - jobs.start[jb];
+    return __builtin_amdgcn_readfirstlane(jb);
+}
+
 // U[m, t] = fp16(sum_k X[m, k] A[t, k]): A operand X (16 tokens), B operand A^T (rows of A).
 template <int R, bool X32, bool KEEP>
-__global__ __launch_bounds__(kLoraThreads) void lora_down_kernel(const void* __restrict__ x, int m, int k,
-                                                                 int ldx, const uint8_t* __restrict__ keep,
-                                                                 const float* __restrict__ keep_scale,
-                                                                 const _Float16* __restrict__ a,
-                                                                 _Float16* __restrict__ u) {
+__global__ __launch_bounds__(kLoraThreads) void lora_down_kernel(const Jobs<DownJob> jobs) {
     __shared__ float red[kLoraWaves * 16 * R];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int i = lane & 15, g = lane >> 4;
-    const int m0 = blockIdx.x * 16;
-    const XInput xin = x_input<X32, KEEP>(x, m, k, ldx, keep, keep_scale);
-    const rsrc_t ar = make_rsrc(a, (uint32_t)R * (uint32_t)k * 2u);
+    int tile;
+    const DownJob& J = jobs.j[job_of(jobs, &tile)];
+    const int m = jobs.m, k = jobs.k;
+    const int m0 = tile * 16;
+    const XInput xin = x_input<X32, KEEP>(J.x, m, k, J.ldx, J.keep, J.keep_scale);
+    const rsrc_t ar = make_rsrc(J.a, (uint32_t)R * (uint32_t)k * 2u);
+    _Float16* const u = J.u;
     const bool rok = m0 + i < m;
     float4_t acc[R / 16];
 #pragma unroll
@@ -191,25 +239,26 @@ __global__ __launch_bounds__(kLoraThreads) void lora_down_kernel(const void* __r
     }
 }
 
-// Work-groups [0, m_tiles): GU tiles, GU[m, t] = fp16(s sum_n dY[m, n] B[n, t]);
-// work-groups [m_tiles, m_tiles + n_tiles): dB tiles, dB[n, t] = s sum_m dY[m, n] U[m, t].
+// A branch's work-groups [0, m_tiles): GU tiles, GU[m, t] = fp16(s sum_n dY[m, n] B[n, t]);
+// the next ones (when it wants dB): dB tiles, dB[n, t] = s sum_m dY[m, n] U[m, t].
 template <int R>
-__global__ __launch_bounds__(kLoraThreads) void lora_gu_db_kernel(const _Float16* __restrict__ dy, int lddy,
-                                                                  const _Float16* __restrict__ u,
-                                                                  const _Float16* __restrict__ b, int m, int n,
-                                                                  float scale, int m_tiles,
-                                                                  _Float16* __restrict__ gu,
-                                                                  float* __restrict__ db) {
+__global__ __launch_bounds__(kLoraThreads) void lora_gu_db_kernel(const Jobs<GuDbJob> jobs) {
     __shared__ float red[kLoraWaves * 16 * R];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int i = lane & 15, g = lane >> 4;
-    const rsrc_t dr = make_rsrc(dy, (uint32_t)(((int64_t)(m - 1) * lddy + n) * 2));
+    int tile;
+    const GuDbJob& J = jobs.j[job_of(jobs, &tile)];
+    const int m = jobs.m, n = J.n, lddy = J.lddy;
+    const int m_tiles = (m + 15) / 16;
+    const float scale = J.scale;
+    const rsrc_t dr = make_rsrc(J.dy, (uint32_t)(((int64_t)(m - 1) * lddy + n) * 2));
     float4_t acc[R / 16];
 #pragma unroll
     for (int h = 0; h < R / 16; ++h) acc[h] = float4_t{};
-    if ((int)blockIdx.x < m_tiles) {
-        const int m0 = blockIdx.x * 16;
-        const rsrc_t br = make_rsrc(b, (uint32_t)n * (uint32_t)R * 2u);
+    if (tile < m_tiles) {
+        const int m0 = tile * 16;
+        const rsrc_t br = make_rsrc(J.b, (uint32_t)n * (uint32_t)R * 2u);
+        _Float16* const gu = J.gu;
         const bool rok = m0 + i < m;
         const int nc = (n + 31) >> 5;
         for (int c = wave; c < nc; c += 2 * kLoraWaves) {
@@ -235,9 +284,10 @@ __global__ __launch_bounds__(kLoraThreads) void lora_gu_db_kernel(const _Float16
         }
         return;
     }
+    float* const db = J.db;
     if (db == nullptr) return;
-    const int n0 = ((int)blockIdx.x - m_tiles) * 16;
-    const rsrc_t ur = make_rsrc(u, (uint32_t)m * (uint32_t)R * 2u);
+    const int n0 = (tile - m_tiles) * 16;
+    const rsrc_t ur = make_rsrc(J.u, (uint32_t)m * (uint32_t)R * 2u);
     const bool cok = n0 + i < n;
     const int mc = (m + 31) >> 5;
     for (int c = wave; c < mc; c += 2 * kLoraWaves) {
@@ -267,17 +317,17 @@ __global__ __launch_bounds__(kLoraThreads) void lora_gu_db_kernel(const _Float16
 // dA[t, k] = sum_m GU[m, t] X[m, k]: work-group = 16 columns k (all R rows t); A operand GU^T,
 // B operand X, both gathered along the token dimension.
 template <int R, bool X32, bool KEEP>
-__global__ __launch_bounds__(kLoraThreads) void lora_da_kernel(const _Float16* __restrict__ gu,
-                                                               const void* __restrict__ x, int ldx,
-                                                               const uint8_t* __restrict__ keep,
-                                                               const float* __restrict__ keep_scale, int m,
-                                                               int k, float* __restrict__ da) {
+__global__ __launch_bounds__(kLoraThreads) void lora_da_kernel(const Jobs<DaJob> jobs) {
     __shared__ float red[kLoraWaves * 16 * R];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int i = lane & 15, g = lane >> 4;
-    const int k0 = blockIdx.x * 16;
-    const rsrc_t gr = make_rsrc(gu, (uint32_t)m * (uint32_t)R * 2u);
-    const XInput xin = x_input<X32, KEEP>(x, m, k, ldx, keep, keep_scale);
+    int tile;
+    const DaJob& J = jobs.j[job_of(jobs, &tile)];
+    const int m = jobs.m, k = jobs.k;
+    const int k0 = tile * 16;
+    const rsrc_t gr = make_rsrc(J.gu, (uint32_t)m * (uint32_t)R * 2u);
+    const XInput xin = x_input<X32, KEEP>(J.x, m, k, J.ldx, J.keep, J.keep_scale);
+    float* const da = J.da;
     const bool cok = k0 + i < k;
     // acc[h]: D[t = 16 h + 4 g + r][k0 + i]
     float4_t acc[R / 16];
@@ -318,53 +368,97 @@ __global__ __launch_bounds__(kLoraThreads) void lora_da_kernel(const _Float16* _
 #define DK_XIN_CASES(X, R)                                                                             \
     X(R, false, false) X(R, false, true) X(R, true, false) X(R, true, true)
 
-hipError_t launch_lora_down(const void* x, bool x32, int64_t m, int64_t k, int64_t ldx, const uint8_t* keep,
-                            const float* keep_scale, const _Float16* a, int rank, _Float16* u, hipStream_t s) {
-    if (m == 0) return hipSuccess;
-    const dim3 grid((unsigned)((m + 15) / 16));
-    const bool kp = keep != nullptr;
+// the kind of a branch's input: fp16 / fp32, with or without dropout (one kernel instance each)
+static int input_kind(const LoraBranch& b) { return (b.x32 ? 2 : 0) + (b.keep != nullptr ? 1 : 0); }
+
+hipError_t launch_lora_down(const LoraBranch* br, int nbr, int64_t m, int64_t k, int rank, hipStream_t s) {
+    if (m == 0 || nbr == 0) return hipSuccess;
+    if (nbr > kLoraMaxBranches) return hipErrorInvalidValue;
+    const int m_tiles = (int)((m + 15) / 16);
+    for (int kind = 0; kind < 4; ++kind) {
+        Jobs<DownJob> jobs{};
+        jobs.m = (int)m;
+        jobs.k = (int)k;
+        int blocks = 0;
+        for (int b = 0; b < nbr; ++b) {
+            if (input_kind(br[b]) != kind) continue;
+            jobs.j[jobs.nj] = DownJob{br[b].x, br[b].keep, br[b].keep_scale, br[b].a, br[b].u, (int)br[b].ldx};
+            jobs.start[jobs.nj++] = blocks;
+            blocks += m_tiles;
+        }
+        if (jobs.nj == 0) continue;
+        jobs.start[jobs.nj] = blocks;
+        const bool x32 = (kind & 2) != 0, kp = (kind & 1) != 0;
+        hipError_t e = hipErrorInvalidValue;
 #define X(R, X32, KEEP)                                                                                \
     if (rank == R && x32 == X32 && kp == KEEP) {                                                       \
-        hipLaunchKernelGGL((lora_down_kernel<R, X32, KEEP>), grid, dim3(kLoraThreads), 0, s, x, (int)m, \
-                           (int)k, (int)ldx, keep, keep_scale, a, u);                                  \
-        return hipGetLastError();                                                                      \
-    }
-    DK_XIN_CASES(X, 16)
-    DK_XIN_CASES(X, 32)
-#undef X
-    return hipErrorInvalidValue;
-}
-
-hipError_t launch_lora_bwd(const _Float16* dy, int64_t lddy, const _Float16* u, const void* x, bool x32,
-                           int64_t ldx, const uint8_t* keep, const float* keep_scale, const _Float16* b,
-                           int64_t m, int64_t n, int64_t k, int rank, float scale, _Float16* gu, float* da,
-                           float* db, hipStream_t s) {
-    if (m == 0) return hipSuccess;
-    const int m_tiles = (int)((m + 15) / 16);
-    const int n_tiles = db != nullptr ? (int)((n + 15) / 16) : 0;
-    const bool kp = keep != nullptr;
-    hipError_t e = hipErrorInvalidValue;
-#define X(R)                                                                                           \
-    if (rank == R) {                                                                                   \
-        hipLaunchKernelGGL((lora_gu_db_kernel<R>), dim3(m_tiles + n_tiles), dim3(kLoraThreads), 0, s,  \
-                           dy, (int)lddy, u, b, (int)m, (int)n, scale, m_tiles, gu, db);               \
+        hipLaunchKernelGGL((lora_down_kernel<R, X32, KEEP>), dim3(blocks), dim3(kLoraThreads), 0, s, jobs); \
         e = hipGetLastError();                                                                         \
     }
-    X(16)
-    X(32)
+        DK_XIN_CASES(X, 16)
+        DK_XIN_CASES(X, 32)
 #undef X
-    if (e != hipSuccess || da == nullptr) return e;
-    const dim3 grid((unsigned)((k + 15) / 16));
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_lora_bwd(const LoraBranch* br, int nbr, int64_t m, int64_t k, int rank, hipStream_t s) {
+    if (m == 0 || nbr == 0) return hipSuccess;
+    if (nbr > kLoraMaxBranches) return hipErrorInvalidValue;
+    const int m_tiles = (int)((m + 15) / 16);
+    // GU and dB of every branch: one launch (no dependence on the input's kind)
+    {
+        Jobs<GuDbJob> jobs{};
+        jobs.m = (int)m;
+        jobs.k = (int)k;
+        int blocks = 0;
+        for (int b = 0; b < nbr; ++b) {
+            const LoraBranch& B = br[b];
+            jobs.j[jobs.nj] = GuDbJob{B.dy, B.u, B.b, B.gu, B.db, B.scale, (int)B.lddy, (int)B.n};
+            jobs.start[jobs.nj++] = blocks;
+            blocks += m_tiles + (B.db != nullptr ? (int)((B.n + 15) / 16) : 0);
+        }
+        jobs.start[jobs.nj] = blocks;
+        hipError_t e = hipErrorInvalidValue;
+#define X(R)                                                                                           \
+    if (rank == R) {                                                                                   \
+        hipLaunchKernelGGL((lora_gu_db_kernel<R>), dim3(blocks), dim3(kLoraThreads), 0, s, jobs);      \
+        e = hipGetLastError();                                                                         \
+    }
+        X(16)
+        X(32)
+#undef X
+        if (e != hipSuccess) return e;
+    }
+    // dA (needs GU) of the branches that want it: one launch per kind of input
+    const int k_tiles = (int)((k + 15) / 16);
+    for (int kind = 0; kind < 4; ++kind) {
+        Jobs<DaJob> jobs{};
+        jobs.m = (int)m;
+        jobs.k = (int)k;
+        int blocks = 0;
+        for (int b = 0; b < nbr; ++b) {
+            if (br[b].da == nullptr || input_kind(br[b]) != kind) continue;
+            jobs.j[jobs.nj] = DaJob{br[b].gu, br[b].x, br[b].keep, br[b].keep_scale, br[b].da, (int)br[b].ldx};
+            jobs.start[jobs.nj++] = blocks;
+            blocks += k_tiles;
+        }
+        if (jobs.nj == 0) continue;
+        jobs.start[jobs.nj] = blocks;
+        const bool x32 = (kind & 2) != 0, kp = (kind & 1) != 0;
+        hipError_t e = hipErrorInvalidValue;
 #define X(R, X32, KEEP)                                                                                \
     if (rank == R && x32 == X32 && kp == KEEP) {                                                       \
-        hipLaunchKernelGGL((lora_da_kernel<R, X32, KEEP>), grid, dim3(kLoraThreads), 0, s, gu, x,      \
-                           (int)ldx, keep, keep_scale, (int)m, (int)k, da);                            \
-        return hipGetLastError();                                                                      \
+        hipLaunchKernelGGL((lora_da_kernel<R, X32, KEEP>), dim3(blocks), dim3(kLoraThreads), 0, s, jobs); \
+        e = hipGetLastError();                                                                         \
     }
-    DK_XIN_CASES(X, 16)
-    DK_XIN_CASES(X, 32)
+        DK_XIN_CASES(X, 16)
+        DK_XIN_CASES(X, 32)
 #undef X
-    return hipErrorInvalidValue;
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 }  // namespace dk

@@ -19,6 +19,7 @@ masks: dk_lora_keep_pack, dk_lora_dropout_inputs, dk_lora_up, dk_lora_input_grad
 import torch
 
 from . import nf4 as _nf4
+from . import _lib
 from ._lib import check, lib, ptr, stream_of
 
 
@@ -74,6 +75,64 @@ def lora_grads(dy16, u16, x, b16, scaling, want_da=True, want_db=True, keep_bits
                                     ptr(b16), m, n, k, r, float(scaling), ptr(gu), ptr(da), ptr(db),
                                     stream_of(dev)))
     return gu, da, db
+
+
+def lora_down_group(branches):
+    """U of every branch, [M, r] fp16 each, for branches that share the token count, the input width
+    and the rank (the q and v adapters of a layer): one launch (one per kind of input where the
+    kinds differ) instead of one per branch, with the same bits as lora_down branch by branch
+    (dk_lora_down_group). branches: list of (x, a16, keep_bits, keep_scale), as lora_down takes
+    them."""
+    n = len(branches)
+    arr = (_lib.LoraBranch * n)()
+    keep, us = [], []
+    m = k = r = None
+    for i, (x, a16, keep_bits, keep_scale) in enumerate(branches):
+        x2 = x.reshape(-1, x.shape[-1])
+        m, k = x2.shape
+        r = a16.shape[0]
+        bits, sc = _keep_args(x2, keep_bits, keep_scale)
+        u = torch.empty((m, r), dtype=torch.float16, device=x.device)
+        arr[i].x, arr[i].ldx, arr[i].x_fp32 = x2.data_ptr(), x2.stride(0), int(x2.dtype == torch.float32)
+        arr[i].keep_bits, arr[i].keep_scale = ptr(bits), ptr(sc)
+        arr[i].a, arr[i].u = a16.data_ptr(), u.data_ptr()
+        keep += [x2, bits, sc, a16]
+        us.append(u)
+    check(lib().dk_lora_down_group(arr, n, m, k, r, stream_of(branches[0][0].device)))
+    return us
+
+
+def lora_grads_group(branches):
+    """lora_grads of every branch, [(GU, dA, dB), ...], for branches that share the token count,
+    the input width and the rank: GU and dB of all branches in one launch, dA in another (one per
+    kind of input where the kinds differ), the same bits as lora_grads branch by branch
+    (dk_lora_bwd_group). branches: list of dicts with dy16, u16, x, b16, scaling and optional
+    want_da, want_db (default True), keep_bits, keep_scale."""
+    n = len(branches)
+    arr = (_lib.LoraBranch * n)()
+    keep, outs = [], []
+    m = k = r = None
+    for i, br in enumerate(branches):
+        dy2 = br["dy16"].reshape(-1, br["dy16"].shape[-1])
+        x2 = br["x"].reshape(-1, br["x"].shape[-1])
+        u16, b16 = br["u16"], br["b16"]
+        m, nn = dy2.shape
+        k = x2.shape[1]
+        r = u16.shape[1]
+        dev = dy2.device
+        bits, sc = _keep_args(x2, br.get("keep_bits"), br.get("keep_scale"))
+        gu = torch.empty((m, r), dtype=torch.float16, device=dev)
+        da = torch.empty((r, k), dtype=torch.float32, device=dev) if br.get("want_da", True) else None
+        db = torch.empty((nn, r), dtype=torch.float32, device=dev) if br.get("want_db", True) else None
+        e = arr[i]
+        e.x, e.ldx, e.x_fp32 = x2.data_ptr(), x2.stride(0), int(x2.dtype == torch.float32)
+        e.keep_bits, e.keep_scale = ptr(bits), ptr(sc)
+        e.u, e.dy, e.lddy, e.n, e.b = u16.data_ptr(), dy2.data_ptr(), dy2.stride(0), nn, b16.data_ptr()
+        e.gu, e.da, e.db, e.scale = gu.data_ptr(), ptr(da), ptr(db), float(br["scaling"])
+        keep += [dy2, x2, bits, sc, u16, b16]
+        outs.append((gu, da, db))
+    check(lib().dk_lora_bwd_group(arr, n, m, k, r, stream_of(branches[0]["dy16"].device)))
+    return outs
 
 
 def pack_keep(keep_q, keep_v):
@@ -176,34 +235,33 @@ class _QVDropout:
 def _qv_lora_forward(x, drop, adapters, scalings):
     """(out_q, out_v, u_q, u_v): out = fp16(fp16(U . B^T) * s), U = fp16(X . A^T) per branch, with
     X the branch's dropped-out fp16 input (solution/attn.py:224-228)."""
-    outs, us = [], []
-    for x16, (a, b), s in zip(drop.inputs(x, True), adapters, scalings):
-        u = lora_down(x16, a.to(torch.float16).contiguous())
-        outs.append(lora_up(u, b.to(torch.float16).t().contiguous()) * s)
-        us.append(u)
+    xs = drop.inputs(x, True)
+    us = lora_down_group([(x16, a.to(torch.float16).contiguous(), None, None) for x16, (a, _) in zip(xs, adapters)])
+    outs = [lora_up(u, b.to(torch.float16).t().contiguous()) * s for u, (_, b), s in zip(us, adapters, scalings)]
     lead = x.shape[:-1]
     return outs[0].reshape(*lead, -1), outs[1].reshape(*lead, -1), us[0], us[1]
 
 
 def _qv_lora_backward(x, drop, adapters, scalings, us, grads):
-    """(dX fp32 in x's shape, [dA_q, dB_q, dA_v, dB_v] in the adapters' dtypes). Per branch the
-    fused dk_lora_bwd gives GU = fp16(s * dY . B), dB = s * dY^T . U and dA = GU^T . X in fp32
-    (the products autograd forms, solution/attn.py:251-257); GU . A is the branch's input gradient
-    before its dropout. A branch that received no gradient contributes zeros, formed as the
+    """(dX fp32 in x's shape, [dA_q, dB_q, dA_v, dB_v] in the adapters' dtypes). For both branches
+    at once dk_lora_bwd_group gives GU = fp16(s * dY . B), dB = s * dY^T . U and dA = GU^T . X in
+    fp32 (the products autograd forms, solution/attn.py:251-257); GU . A is the branch's input
+    gradient before its dropout. A branch that received no gradient contributes zeros, formed as the
     reference forms them."""
     xs = drop.inputs(x, False)
     rows = xs[0].shape[0]
-    adapter_grads, input_grads = [], []
+    branches = []
     for x16, (a, b), s, u, g in zip(xs, adapters, scalings, us, grads):
-        a16 = a.to(torch.float16).contiguous()
         b16 = b.to(torch.float16).contiguous()
         if g is None:
             g16 = torch.zeros((rows, b16.shape[0]), dtype=torch.float16, device=x.device)
         else:
             g16 = g.to(torch.float16).reshape(rows, -1).contiguous()
-        gu, da, db = lora_grads(g16, u, x16, b16, s)
+        branches.append(dict(dy16=g16, u16=u, x=x16, b16=b16, scaling=s))
+    adapter_grads, input_grads = [], []
+    for (gu, da, db), (a, b) in zip(lora_grads_group(branches), adapters):
         adapter_grads += [da.to(a.dtype), db.to(b.dtype)]
-        input_grads.append(lora_up(gu, a16))
+        input_grads.append(lora_up(gu, a.to(torch.float16).contiguous()))
     return drop.input_grad(input_grads).view(x.shape), adapter_grads
 
 
@@ -304,15 +362,21 @@ def _qkv_forward_items(x2, x16, projections):
         # one launch runs one rank (its LoRA slices and the U / B row strides)
         raise ValueError(f"QKV projection: LoRA ranks differ within one launch: {sorted(ranks)}")
     items, saved, rank = [], [], 0
-    for p in projections:
-        it = dict(packed=p["packed"], qs=p["qs"], bias=p.get("bias"))
+    downs, adapters = [], {}
+    for i, p in enumerate(projections):
         if p.get("lora_a") is not None:
             a16 = p["lora_a"].to(torch.float16).contiguous()
-            b16 = p["lora_b"].to(torch.float16).contiguous()
+            adapters[i] = (a16, p["lora_b"].to(torch.float16).contiguous())
             if p.get("keep_bits") is not None:
-                u = lora_down(x2, a16, p["keep_bits"], p["keep_scale"])
+                downs.append((x2, a16, p["keep_bits"], p["keep_scale"]))
             else:
-                u = lora_down(x16, a16)
+                downs.append((x16, a16, None, None))
+    us = iter(lora_down_group(downs) if downs else [])  # every branch's U in one launch
+    for i, p in enumerate(projections):
+        it = dict(packed=p["packed"], qs=p["qs"], bias=p.get("bias"))
+        if i in adapters:
+            a16, b16 = adapters[i]
+            u = next(us)
             it.update(lora_u=u, lora_b=b16, lora_scale=p["scaling"])
             rank = a16.shape[0]
             saved.append((u, a16, b16))
@@ -328,7 +392,7 @@ def _qkv_backward(x2, x16, projections, saved, grads, rank):
     gradient masked in the GEMM's epilogue with 1 / (1 - p) (skc_lora_input_grad_kernel's
     scale, solution/attn.py:262-266)."""
     m, k = x2.shape
-    items, adapter_grads = [], []
+    items, branches = [], []
     for p, sv, g in zip(projections, saved, grads):
         if g is None:
             g = torch.zeros((m, int(p["qs"].shape[0])), dtype=torch.float16, device=x2.device)
@@ -337,14 +401,21 @@ def _qkv_backward(x2, x16, projections, saved, grads, rank):
         if sv is not None:
             u, a16, b16 = sv
             if p.get("keep_bits") is not None:
-                gu, da, db = lora_grads(g16, u, x2, b16, p["scaling"], keep_bits=p["keep_bits"],
-                                        keep_scale=p["keep_scale"])
+                branches.append(dict(dy16=g16, u16=u, x=x2, b16=b16, scaling=p["scaling"],
+                                     keep_bits=p["keep_bits"], keep_scale=p["keep_scale"]))
                 it.update(lora_keep=p["keep_bits"], lora_keep_scale=1.0 / (1.0 - float(p["p"])))
             else:
-                gu, da, db = lora_grads(g16, u, x16, b16, p["scaling"])
-            it.update(lora_gu=gu, lora_a=a16)
-            adapter_grads += [da.to(p["lora_a"].dtype), db.to(p["lora_b"].dtype)]
+                branches.append(dict(dy16=g16, u16=u, x=x16, b16=b16, scaling=p["scaling"]))
+            it.update(lora_a=a16)
         items.append(it)
+    # GU, dB and dA of every branch: one launch per product
+    grads_of = iter(lora_grads_group(branches) if branches else [])
+    adapter_grads = []
+    for p, sv, it in zip(projections, saved, items):
+        if sv is not None:
+            gu, da, db = next(grads_of)
+            it["lora_gu"] = gu
+            adapter_grads += [da.to(p["lora_a"].dtype), db.to(p["lora_b"].dtype)]
     grad_x = _nf4.linear_backward(items, m, k, dx_fp32=x2.dtype == torch.float32, lora_rank=rank)
     return grad_x, adapter_grads
 

@@ -32,6 +32,8 @@
  *                                               backward (solution/mlp.py:95, 104)
  *   dk_lora_down / dk_lora_bwd                <- the rank-r products of LoRAPairFromNorm
  *                                               (solution/attn.py:225-227, 251-257)
+ *   dk_lora_down_group / dk_lora_bwd_group    <- the same products of LoRAPairFromNorm's q and v
+ *                                               branches, one launch for both (attn.py:206-273)
  *   dk_lora_down_dropout / dk_lora_bwd_dropout <- the same with skc_lora_inputs_kernel fused in
  *     + dk_linear_bwd_group.lora_keep            and skc_lora_input_grad_kernel in the input-
  *                                               gradient GEMM (solution/attn.py:153-180, 206-273)
@@ -229,6 +231,34 @@ int dk_lora_bwd_dropout(const uint16_t* dy, int64_t lddy, const uint16_t* u, con
                         int64_t ldx, const uint8_t* keep_bits, const float* keep_scale, const uint16_t* b,
                         int64_t m, int64_t n, int64_t k, int rank, float scale, uint16_t* gu, float* da,
                         float* db, void* stream);
+
+/* One LoRA branch (one adapter: q or v) of a grouped call. */
+typedef struct dk_lora_branch {
+    const void* x;            /* the branch input, fp16 (x_fp32 = 0) or fp32 [m, k], row stride ldx */
+    const uint8_t* keep_bits; /* NULL, or packed dropout keep bits [m, k / 8] (as above)        */
+    const float* keep_scale;  /* device fp32 scalar 1 / (1 - p) with keep_bits                 */
+    const uint16_t* a;        /* A fp16 [rank, k]                                               */
+    uint16_t* u;              /* U fp16 [m, rank]: written by _down, read by _bwd               */
+    const uint16_t* dy;       /* _bwd: dY fp16 [m, n], row stride lddy                          */
+    const uint16_t* b;        /* _bwd: B fp16 [n, rank]                                         */
+    uint16_t* gu;             /* _bwd: GU fp16 [m, rank] out                                    */
+    float* da;                /* _bwd: dA fp32 [rank, k] out, or NULL                           */
+    float* db;                /* _bwd: dB fp32 [n, rank] out, or NULL                           */
+    int64_t ldx, lddy, n;
+    float scale;              /* _bwd: the LoRA scaling s                                       */
+    int32_t x_fp32;
+} dk_lora_branch;
+
+/* dk_lora_down_dropout / dk_lora_bwd_dropout for 1..4 branches that share m, k and the rank (the
+ * q and v adapters of one layer, LoRAPairFromNorm's two branches, solution/attn.py:206-273): each
+ * product of every branch in one launch (one per kind of input -- fp16 / fp32, with / without
+ * dropout -- where the branches' kinds differ) instead of one launch per branch, with the same
+ * bits as the per-branch calls. _down reads x, keep_bits, keep_scale, a and writes u; _bwd reads
+ * every field but a and writes gu, da, db. */
+int dk_lora_down_group(const dk_lora_branch* branches, int nbranches, int64_t m, int64_t k, int rank,
+                       void* stream);
+int dk_lora_bwd_group(const dk_lora_branch* branches, int nbranches, int64_t m, int64_t k, int rank,
+                      void* stream);
 
 /* LoRA dropout (the packed-mask path of LoRAPairFromNorm). Masks are bool bytes (0/1), rows x width
  * row-major, width % 8 == 0; bits are [rows, width / 8]. */

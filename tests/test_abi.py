@@ -41,18 +41,21 @@ def test_struct_layout_matches_c(tmp_path):
 
     src = tmp_path / "layout.c"
     src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "decik_nf4.h"\n'
-                   "int main(void){printf(\"%zu %zu %zu %zu %zu %zu %zu %zu\\n\","
+                   "int main(void){printf(\"%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\\n\","
                    "sizeof(dk_nf4_weight), offsetof(dk_nf4_weight, n), offsetof(dk_nf4_weight, nested),"
                    "sizeof(dk_linear_fwd_group), offsetof(dk_linear_fwd_group, lora_scale),"
                    "offsetof(dk_linear_fwd_group, y), sizeof(dk_linear_bwd_group),"
-                   "offsetof(dk_linear_bwd_group, lora_a));return 0;}\n")
+                   "offsetof(dk_linear_bwd_group, lora_a), sizeof(dk_lora_branch),"
+                   "offsetof(dk_lora_branch, ldx), offsetof(dk_lora_branch, scale),"
+                   "offsetof(dk_lora_branch, x_fp32));return 0;}\n")
     exe = tmp_path / "layout"
     subprocess.run(["gcc", "-I", os.path.dirname(HEADER), "-o", str(exe), str(src)], check=True)
     got = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True,
                                           check=True).stdout.split()]
-    W, F, B = _lib.NF4Weight, _lib.LinearFwdGroup, _lib.LinearBwdGroup
+    W, F, B, R = _lib.NF4Weight, _lib.LinearFwdGroup, _lib.LinearBwdGroup, _lib.LoraBranch
     want = [ctypes.sizeof(W), W.n.offset, W.nested.offset, ctypes.sizeof(F), F.lora_scale.offset,
-            F.y.offset, ctypes.sizeof(B), B.lora_a.offset]
+            F.y.offset, ctypes.sizeof(B), B.lora_a.offset, ctypes.sizeof(R), R.ldx.offset, R.scale.offset,
+            R.x_fp32.offset]
     assert got == want
 
 

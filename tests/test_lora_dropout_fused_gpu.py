@@ -207,3 +207,37 @@ def test_qkv_rope_projection_with_dropout_matches_unfused(device):
 
     for a, b in zip(run(True), run(False)):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("r", [16, 32])
+@pytest.mark.parametrize("m,k", [(830, 1536), (37, 96)])
+def test_grouped_lora_launches_equal_per_branch(r, m, k, device):
+    """dk_lora_down_group / dk_lora_bwd_group (every branch's product in one launch, one per kind of
+    input): the same bits as the per-branch calls, for four branches of every input kind (fp16 or
+    fp32, with or without dropout), different output widths n, and dA / dB left out of some."""
+    from decik_amd.lora import lora_down, lora_down_group, lora_grads, lora_grads_group, pack_keep
+
+    kq, kv = _masks(m, k, 0.3, 41, device)
+    bq, bv = pack_keep(kq, kv)
+    sq = torch.tensor(1.0 / 0.7, dtype=torch.float32, device=device)
+    x16 = _x(m, k, torch.float16, device, 42)
+    x32 = _x(m, k, torch.float32, device, 43)
+    spec = [(x16, None, None, 1536, True, True), (x32, bq, sq, 256, True, True),
+            (x16, bv, sq, 512, False, True), (x32, None, None, 264, True, False)]
+    downs, ref_u, branches, ref_g = [], [], [], []
+    for i, (x, bits, sc, n, want_da, want_db) in enumerate(spec):
+        a, b = adapters(n, k, 44 + i, device, r=r)
+        downs.append((x, a, bits, sc))
+        ref_u.append(lora_down(x, a, bits, sc))
+        dy = randn16((m, n), seed=50 + i, device=device, std=1e-2)
+        branches.append(dict(dy16=dy, u16=ref_u[-1], x=x, b16=b, scaling=2.0, want_da=want_da, want_db=want_db,
+                             keep_bits=bits, keep_scale=sc))
+        ref_g.append(lora_grads(dy, ref_u[-1], x, b, 2.0, want_da, want_db, keep_bits=bits, keep_scale=sc))
+    us = lora_down_group(downs)
+    got = lora_grads_group(branches)
+    torch.cuda.synchronize()
+    for u, ru in zip(us, ref_u):
+        assert torch.equal(u, ru)
+    for g, rg in zip(got, ref_g):
+        for t, rt in zip(g, rg):
+            assert (t is None and rt is None) or torch.equal(t, rt)
