@@ -150,8 +150,8 @@ def bench_mlp(steps, warmup, device, n_sets=None, only=None):
                                   dict(packed=u[0], qs=u[1], dy=dup)], M, HIDDEN)
         return out, dx
 
-    # setup: one pass over every weight set fills the per-weight block-scale cache (computed once
-    # per frozen weight) before the warm-up steps
+    # setup: one pass over every weight set fills the per-weight descriptor cache before the
+    # warm-up steps
     for i in range(n_sets):
         step(i)
     torch.cuda.synchronize()
@@ -205,12 +205,12 @@ def bench_mlp(steps, warmup, device, n_sets=None, only=None):
         torch.cuda.synchronize()
         per[kind] = a.elapsed_time(b) / steps
     launch_ms = per
-    # The same launches on the raw double-quant statistics (no cached fp32 block scales): each
-    # kernel then decodes code2[q] * absmax2 + offset per block itself, and the GLU forward runs as
-    # the grouped launch plus the SwiGLU kernel (its fused epilogue takes plain statistics only).
-    uncached = {}
-    saved_scales = nf4._scales
-    nf4._scales = lambda packed, qs, device: None
+    # The same launches on the derived fp32 block scales (dk_nf4_block_scales, computed once per
+    # frozen weight before timing) instead of the statistics as stored: each kernel then loads one
+    # fp32 scale per block instead of an absmax code and forming code2[q] * absmax2 + offset.
+    cached = {}
+    saved_form = nf4._tiled_scales
+    nf4._tiled_scales = nf4._scales
     try:
         if only is not None:
             launches = []  # counter runs (--only) time the cached launch alone
@@ -228,12 +228,12 @@ def bench_mlp(steps, warmup, device, n_sets=None, only=None):
                 one(kind, i)
             b.record()
             torch.cuda.synchronize()
-            uncached[kind] = a.elapsed_time(b) / steps
+            cached[kind] = a.elapsed_time(b) / steps
     finally:
-        nf4._scales = saved_scales
+        nf4._tiled_scales = saved_form
     step_flops = sum(flops.values())
     return dict(ms_step=ms_step, launch_ms=launch_ms, flops=flops, symbol=symbol,
-                step_flops=step_flops, n_sets=n_sets, uncached_ms=uncached, graph_ms=graph_ms)
+                step_flops=step_flops, n_sets=n_sets, cached_ms=cached, graph_ms=graph_ms)
 
 
 def bench_mlp_gpu_baselines(steps, warmup, device, our_ms):
@@ -707,7 +707,7 @@ def bench_c3(steps, warmup, device):
     res = {}
     for name, forward in (("fused", fused), ("reference_order", reference_order)):
         fn = step(forward)
-        for i in range(n_sets):  # fills every weight's block-scale cache
+        for i in range(n_sets):  # fills every weight's descriptor cache
             fn(layers[i])
             clear()
         for i in range(warmup):
@@ -887,7 +887,7 @@ def bench_c4(steps, warmup, device, n_layers=28):
         (aq, bq), (av, bv) = L["q_lora"], L["v_lora"]
         uq, uv = lora.lora_down(x, aq), lora.lora_down(x, av)
         pre[li] = (uq, uv, lora.lora_grads(dq, uq, x, bq, s)[0], lora.lora_grads(dkv, uv, x, bv, s)[0])
-    step()  # fills the block-scale cache of every weight
+    step()  # fills the descriptor cache of every weight
     torch.cuda.synchronize()
     res = {}
     for name, lk in (("step", True), ("gemm_only", False)):
@@ -964,7 +964,7 @@ def bench_c5(device, reps=3, min_bytes=512 << 20, m_list=C5_M, shapes=tuple(s[0]
             if m >= 64:
                 kinds["bwd"] = lambda p, q: nf4.linear_backward([dict(packed=p, qs=q, dy=dy)], m, k)
             for d, call in kinds.items():
-                for p, q in ws:  # fills every block-scale cache and the workspace
+                for p, q in ws:  # fills the descriptor and block-scale caches and the workspace
                     call(p, q)
                 torch.cuda.synchronize()
                 ref = call(*ws[-1]).clone()
@@ -1011,7 +1011,8 @@ def bench_c5(device, reps=3, min_bytes=512 << 20, m_list=C5_M, shapes=tuple(s[0]
             torch.cuda.empty_cache()
         del ws
         torch.cuda.empty_cache()
-    return dict(workload="Qwen2.5-7B projections (NF4 bs 64, double quant, cached fp32 block scales), each shape "
+    return dict(workload="Qwen2.5-7B projections (NF4 bs 64, double quant; statistics as stored, fp32 block scales for "
+                         "the GEMV and split small-M launches), each shape "
                          "and M: back-to-back calls over weight copies totalling > 512 MB (weights from HBM), "
                          "replayed from a HIP graph",
                 shapes={name: [n, k] for name, n, k in QWEN7_SHAPES},
@@ -1026,7 +1027,10 @@ def mlp_plan(kind):
 
     args = {"fwd_gate_up": (False, HIDDEN, [INTER, INTER], True), "fwd_down": (False, INTER, [HIDDEN], False),
             "bwd_down": (True, INTER, [HIDDEN], True), "bwd_gate_up": (True, HIDDEN, [INTER, INTER], False)}[kind]
-    return nf4.launch_plan(args[0], M, args[1], args[2], glu=args[3])
+    plan = nf4.launch_plan(args[0], M, args[1], args[2], glu=args[3])
+    # the form in which the kernels read nested statistics (the bytes a launch moves depend on it)
+    plan["statistics"] = "fp32 block scales" if nf4._tiled_scales is nf4._scales else "as stored"
+    return plan
 
 
 def load_traffic(kind):
@@ -1178,16 +1182,17 @@ def main():
                              "down [1536,8960], blocksize 64, double quant; X [830,1536]; SwiGLU; "
                              "dX through W; gate/up kept from the forward",
                     m=M, hidden=HIDDEN, intermediate=INTER, weight_sets=mlp["n_sets"],
-                    block_scales="fp32 scale of every 64-weight block cached per frozen weight (4 B per 64 "
-                                 "weights: +12.5% of the packed bytes, 0.5 bit/weight), computed once "
-                                 "before timing; kernels_uncached_nested times the raw double-quant path"),
+                    block_scales="bitsandbytes' double-quant statistics as stored (uint8 absmax codes, "
+                                 "fp32 absmax2 and offset), each block's scale formed in the kernels; "
+                                 "kernels_cached_scales times the same launches on fp32 block scales "
+                                 "derived once per frozen weight (+12.5% of the packed bytes)"),
         roofline=roofline,
         measured_peaks=peaks,
         kernels={k: dict(ms=round(v, 4),
                          tflops=round(mlp["flops"][k] / (v * 1e-3) / 1e12, 1) if mlp["flops"][k] else None)
                  for k, v in mlp["launch_ms"].items()},
-        kernels_uncached_nested={k: dict(ms=round(v, 4), tflops=round(mlp["flops"][k] / (v * 1e-3) / 1e12, 1))
-                                 for k, v in mlp["uncached_ms"].items()},
+        kernels_cached_scales={k: dict(ms=round(v, 4), tflops=round(mlp["flops"][k] / (v * 1e-3) / 1e12, 1))
+                               for k, v in mlp["cached_ms"].items()},
         graph_step=None if mlp["graph_ms"] is None else dict(
             ms_per_step=round(mlp["graph_ms"], 4),
             tflops=round(mlp["step_flops"] / (mlp["graph_ms"] * 1e-3) / 1e12, 2),

@@ -210,12 +210,15 @@ def test_launch_plans():
     assert launch_plan(False, 32, 18944, [3584])["kernel"] == "nf4_skinny_kernel"
     assert launch_plan(False, 8, 3584, [18944])["splits"] == 1
     assert launch_plan(False, 8, 18944, [3584])["splits"] > 1
-    # nested statistics as stored for unsplit small-M launches, cached fp32 scales otherwise
+    # nested statistics as stored for the MFMA kernels and unsplit small-M launches, cached fp32
+    # scales for the GEMV and split small-M launches
     from decik_amd import nf4 as _nf4
     assert _nf4._forward_scales(8, 3584, [18944]) is _nf4._own_statistics
     assert _nf4._forward_scales(8, 3584, [512]) is _nf4._scales        # split: cached
     assert _nf4._forward_scales(1, 3584, [18944]) is _nf4._scales      # GEMV
-    assert _nf4._forward_scales(830, 3584, [18944]) is _nf4._scales    # MFMA kernels
+    assert _nf4._forward_scales(830, 3584, [18944]) is _nf4._tiled_scales  # MFMA kernels
+    assert _nf4._forward_scales(32, 3584, [24592]) is _nf4._tiled_scales   # MFMA kernels at 32 rows
+    assert _nf4._tiled_scales(None, None, None) is None                 # ... read the statistics as stored
     # few row groups (7B k/v: 8 groups of 64 rows, 28 super-steps): split down to two super-steps
     assert launch_plan(False, 8, 3584, [512])["splits"] == 14
     assert launch_plan(False, 33, 3584, [18944])["kernel"] != "nf4_skinny_kernel"
@@ -314,8 +317,9 @@ def test_no_bit_cast_of_vector_elements():
 
 def test_descriptor_cache_follows_the_scales_hook():
     """DESCS keys a cached NF4Weight on the scales it was built with: describing a nested weight
-    by its raw statistics (a hook returning None, as the raw-statistics tests and the bench's
-    uncached timing do) and then by block scales gives two different descriptors, each reused
+    by its raw statistics (a hook returning None, as the MFMA launches' default does) and then by
+    block scales (the GEMV's form, and the bench's cached-scales timing) gives two different
+    descriptors, each reused
     while nothing changes; new scales (what the scales cache hands out after an in-place change
     of the statistics) or a replaced statistics tensor rebuild it."""
     import torch

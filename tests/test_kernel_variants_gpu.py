@@ -16,7 +16,8 @@ CASES = [(True, 64), (True, 128), (True, 256), (False, 32)]
 
 @pytest.fixture
 def raw_statistics(monkeypatch):
-    """Describe nested weights to the kernels as they are (no cached block scales)."""
+    """Describe nested weights to every kernel as they are (no cached block scales, also for the
+    GEMV and split small-M launches)."""
     from decik_amd import nf4
 
     monkeypatch.setattr(nf4, "_scales", lambda packed, qs, device: None)
@@ -193,9 +194,9 @@ def test_skinny_tall_weights(m, ns, raw, device, monkeypatch):
 
 @pytest.mark.parametrize("m", [3, 8, 24])
 def test_small_m_statistics_forms_same_bits(m, device, monkeypatch):
-    """Unsplit small-M launches read nested statistics as stored (the default for them), split ones
-    and the MFMA kernels the cached fp32 scales: both forms give the same dequantized weights and
-    the same sums, so the outputs are equal bit for bit."""
+    """Unsplit small-M launches read nested statistics as stored (the default for them, as for the
+    MFMA kernels), split ones and the GEMV the cached fp32 scales: both forms give the same
+    dequantized weights and the same sums, so the outputs are equal bit for bit."""
     from decik_amd import nf4
     from decik_amd.nf4 import linear_forward
 
@@ -384,3 +385,53 @@ def test_small_tile_forward(plan, m, device, monkeypatch):
     g, up, h = glu_forward(x, gi, ui)
     g2, u2 = linear_forward(x, [gi, ui])
     assert torch.equal(g, g2) and torch.equal(up, u2) and torch.equal(h, swiglu_fwd(g2, u2))
+
+
+@pytest.mark.parametrize("m", [64, 830])
+def test_mfma_launches_statistics_forms_same_bits(m, device, monkeypatch):
+    """The MFMA launches read nested statistics as stored by default (_tiled_scales); on the
+    derived fp32 block scales instead they give the same bits: forward (several weights, bias,
+    LoRA), input gradient (with a LoRA term), the GLU forward, the SwiGLU backward and the RoPE
+    forward."""
+    from decik_amd import nf4
+    from decik_amd.lora import lora_down
+    from test_rope_gpu import rope_tables
+
+    k, r = 1536, 16
+    pq, qq, _ = make_weight((1536, k), seed=210, device=device)
+    pk, qk, _ = make_weight((256, k), seed=211, device=device)
+    pg, qg, _ = make_weight((1024, k), seed=212, device=device)
+    pu, qu, _ = make_weight((1024, k), seed=213, device=device)
+    pd, qd, _ = make_weight((k, 1024), seed=214, device=device)
+    assert qq.nested and qd.nested
+    x = randn16((m, k), seed=215, device=device)
+    bias = randn16((1536,), seed=216, device=device, std=0.1)
+    a = randn16((r, k), seed=217, device=device, std=0.05)
+    lb = randn16((1536, r), seed=218, device=device, std=0.05)
+    dyq = randn16((m, 1536), seed=219, device=device, std=1e-2)
+    dyk = randn16((m, 256), seed=220, device=device, std=1e-2)
+    dyd = randn16((m, k), seed=221, device=device, std=1e-2)
+    gu = randn16((m, r), seed=222, device=device, std=1e-2)
+    c, s = rope_tables([m], 128)
+    cos, sin = torch.from_numpy(c).to(device), torch.from_numpy(s).to(device)
+
+    def run():
+        u = lora_down(x, a)
+        items = [dict(packed=pq, qs=qq, bias=bias, lora_u=u, lora_b=lb, lora_scale=2.0), dict(packed=pk, qs=qk)]
+        out = list(nf4.linear_forward(x, items, lora_rank=r))
+        out += nf4.linear_forward(x, [dict(packed=pq, qs=qq), dict(packed=pk, qs=qk)])
+        out.append(nf4.linear_backward([dict(packed=pq, qs=qq, dy=dyq, lora_gu=gu, lora_a=a),
+                                        dict(packed=pk, qs=qk, dy=dyk)], m, k, lora_rank=r))
+        g, up, h = nf4.glu_forward(x, dict(packed=pg, qs=qg), dict(packed=pu, qs=qu))
+        out += [g, up, h]
+        out += list(nf4.linear_backward_swiglu(dict(packed=pd, qs=qd, dy=dyd), g.clone(), up.clone()))
+        out += nf4.linear_rope_forward(x, [dict(packed=pq, qs=qq), dict(packed=pk, qs=qk)], cos, sin, 128, 3)
+        return out
+
+    as_stored = run()
+    monkeypatch.setattr(nf4, "_tiled_scales", nf4._scales)
+    cached = run()
+    torch.cuda.synchronize()
+    assert len(as_stored) == len(cached) == 12
+    for i, (t1, t2) in enumerate(zip(as_stored, cached)):
+        assert torch.equal(t1, t2), i
