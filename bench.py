@@ -209,6 +209,12 @@ def bench_mlp(steps, warmup, device, n_sets=None, only=None):
     # frozen weight before timing) instead of the statistics as stored: each kernel then loads one
     # fp32 scale per block instead of an absmax code and forming code2[q] * absmax2 + offset.
     cached = {}
+    from decik_amd import _lib
+
+    for L in layers:  # the derived scales exist before timing (computed once per frozen weight)
+        for name in ("gate", "up", "down"):
+            _lib.SCALES.get(L[name][0], L[name][1], device)
+    torch.cuda.synchronize()
     saved_form = nf4._tiled_scales
     nf4._tiled_scales = nf4._scales
     try:
