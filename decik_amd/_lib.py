@@ -235,8 +235,8 @@ SCALES = ScaleCache()
 
 
 class DescCache:
-    """The NF4Weight descriptor the fused GEMMs take for a (packed, QuantState) pair -- with the
-    cached block scales for a nested weight -- built once and reused while it stays valid: the
+    """The NF4Weight descriptor the fused GEMMs take for a (packed, QuantState) pair -- with its
+    statistics as stored or with the cached block scales of a nested weight -- built once and reused while it stays valid: the
     same packed tensor, statistics tensors and scales (compared by identity; the entry keeps them
     alive, so an identity is not reused meanwhile). An in-place change of the statistics leaves
     the descriptor's pointers valid; the scales cache notices it and hands out new scales, which

@@ -97,51 +97,23 @@ def _rows(x):
 
 
 def _scales(packed, qs, device):
-    """Cached fp32 block scales of a nested weight for the fused GEMMs (None for plain ones)."""
+    """Cached fp32 block scales of a nested weight (None for plain ones): the derived form of its
+    statistics, which _launch_scales can switch the fused launches to."""
     return _lib.SCALES.get(packed, qs, device) if qs.nested else None
 
 
-def _own_statistics(packed, qs, device):
-    """No cached scales: the kernels read a nested weight's statistics as stored."""
+def _launch_scales(packed, qs, device):
+    """The form in which every fused launch reads a nested weight's statistics: as stored (an
+    absmax code per block, the code2 table in LDS, code2[q] * absmax2 + offset formed per block
+    in the kernel with the reference's two roundings), not the derived fp32 block scales of
+    _scales. Both forms give the same bits. Measured against the cached scales (graph-replayed,
+    weights from HBM): the MFMA launches of the Qwen2.5 1.5B and 7B projections at 64-8192 token
+    rows from 0.9% slower to 4.7% faster (0.516 bytes of weight and statistics per weight instead
+    of 0.5625), the 1.5B MLP step 2% faster; the GEMV at one or two rows from 1.5% slower to 3.5%
+    faster; split small-M launches from 3.7% slower (7B k/v at 8 rows) to 2.4% faster (7B down at
+    24 rows). Reading them as stored keeps no derived copy (+12.5% of the packed bytes); this hook
+    is where a caller (or the bench's cached-scales timing) switches to the derived form."""
     return None
-
-
-def _tiled_scales(packed, qs, device):
-    """The statistics form of the MFMA (tiled) launches: a nested weight's statistics as stored
-    (an absmax code per block, code2 in LDS, code2[q] * absmax2 + offset formed per block in the
-    kernel, the reference's two roundings). Against the cached fp32 block scales on the Qwen2.5
-    1.5B and 7B launches at 64-8192 token rows (graph-replayed, weights from HBM): from 0.9%
-    slower to 4.7% faster (0.516 instead of 0.5625 bytes per weight), the 1.5B MLP step unchanged,
-    and no derived copy of the statistics is kept (+12.5% of the packed bytes). Both forms give
-    the same bits."""
-    return None
-
-
-_FORM = {}
-
-
-def _forward_scales(m, k, ns):
-    """The block-scale form for a forward launch without LoRA terms. The MFMA kernels take the
-    statistics as stored (_tiled_scales). So does a launch of few token rows that the small-M
-    kernel runs unsplit: it reads every packed byte once and is bound by HBM (7B gate at 3-32 rows
-    10-14% faster than on fp32 scales). The GEMV and split small-M launches take the cached scales:
-    a split re-reads statistics per split (raw: 2-6% slower on the 7B k/v and Qwen2.5-1.5B down
-    projections), and the GEMV measured no gain from them. Remembered per shape and tuning
-    variables. An empty batch launches nothing: any form does."""
-    if m > 32 or m < 1:
-        return _tiled_scales
-    key = (m, k, tuple(ns), os.environ.get("DECIK_FWD_PLAN"), os.environ.get("DECIK_SMALL_M"))
-    form = _FORM.get(key)
-    if form is None:
-        plan = launch_plan(False, m, k, list(ns))
-        if plan["kernel"] == "nf4_skinny_kernel":
-            form = "raw" if plan["splits"] == 1 else "cached"
-        else:
-            form = "cached" if plan["kernel"] == "nf4_gemv_kernel" else "tiled"
-        if len(_FORM) > 4096:
-            _FORM.clear()
-        _FORM[key] = form
-    return {"raw": _own_statistics, "cached": _scales}.get(form, _tiled_scales)
 
 
 _NEED = {}
@@ -175,8 +147,7 @@ def linear_forward(x16, items, lora_rank=0):
     m, k = x2.shape
     groups = (LinearFwdGroup * len(items))()
     keep, outs, ns = [x2], [], []
-    # LoRA terms keep a launch on the MFMA kernels
-    scales_of = _tiled_scales if lora_rank else _forward_scales(m, k, [int(it["qs"].shape[0]) for it in items])
+    scales_of = _launch_scales
     for g, it in enumerate(items):
         qs = it["qs"]
         n = int(qs.shape[0])
@@ -277,7 +248,7 @@ def linear_backward(items, m, k, dx=None, dx_fp32=False, lora_rank=0):
     keep, ns = [dx], []
     for g, it in enumerate(items):
         qs = it["qs"]
-        w, kp = _lib.DESCS.get(it["packed"], qs, dev, _tiled_scales)
+        w, kp = _lib.DESCS.get(it["packed"], qs, dev, _launch_scales)
         keep += kp
         dy = _rows(it["dy"])
         groups[g].w = w
@@ -307,7 +278,7 @@ def _forward_one(x2, packed, qs, bias16):
     dev = x2.device
     m, k = x2.shape
     n = int(qs.shape[0])
-    w, kp = _lib.DESCS.get(packed, qs, dev, _forward_scales(m, k, (n,)))
+    w, kp = _lib.DESCS.get(packed, qs, dev, _launch_scales)
     out = torch.empty((m, n), dtype=torch.float16, device=dev)
     groups = (LinearFwdGroup * 1)()
     g = groups[0]
@@ -326,7 +297,7 @@ def _backward_one(g2, packed, qs, k):
     """linear_backward of one weight without LoRA terms (NF4Linear's input gradient)."""
     dev = g2.device
     m = g2.shape[0]
-    w, kp = _lib.DESCS.get(packed, qs, dev, _tiled_scales)
+    w, kp = _lib.DESCS.get(packed, qs, dev, _launch_scales)
     dx = torch.empty((m, k), dtype=torch.float16, device=dev)
     groups = (LinearBwdGroup * 1)()
     g = groups[0]
@@ -340,7 +311,7 @@ def _backward_one(g2, packed, qs, k):
 
 def _fwd_group(g, it, dev, keep):
     qs = it["qs"]
-    w, kp = _lib.DESCS.get(it["packed"], qs, dev, _tiled_scales)
+    w, kp = _lib.DESCS.get(it["packed"], qs, dev, _launch_scales)
     keep += kp
     g.w = w
     bias = it.get("bias")
@@ -386,7 +357,7 @@ def linear_backward_swiglu(item, gate, up, out=None, lora_rank=0):
     assert gate.is_contiguous() and up.is_contiguous() and dgate.is_contiguous() and dup.is_contiguous()
     groups = (LinearBwdGroup * 1)()
     qs = item["qs"]
-    w, kp = _lib.DESCS.get(item["packed"], qs, dev, _tiled_scales)
+    w, kp = _lib.DESCS.get(item["packed"], qs, dev, _launch_scales)
     keep = list(kp)
     dy = _rows(item["dy"])
     groups[0].w = w

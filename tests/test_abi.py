@@ -210,15 +210,9 @@ def test_launch_plans():
     assert launch_plan(False, 32, 18944, [3584])["kernel"] == "nf4_skinny_kernel"
     assert launch_plan(False, 8, 3584, [18944])["splits"] == 1
     assert launch_plan(False, 8, 18944, [3584])["splits"] > 1
-    # nested statistics as stored for the MFMA kernels and unsplit small-M launches, cached fp32
-    # scales for the GEMV and split small-M launches
+    # every fused launch reads nested statistics as stored (no derived block scales)
     from decik_amd import nf4 as _nf4
-    assert _nf4._forward_scales(8, 3584, [18944]) is _nf4._own_statistics
-    assert _nf4._forward_scales(8, 3584, [512]) is _nf4._scales        # split: cached
-    assert _nf4._forward_scales(1, 3584, [18944]) is _nf4._scales      # GEMV
-    assert _nf4._forward_scales(830, 3584, [18944]) is _nf4._tiled_scales  # MFMA kernels
-    assert _nf4._forward_scales(32, 3584, [24592]) is _nf4._tiled_scales   # MFMA kernels at 32 rows
-    assert _nf4._tiled_scales(None, None, None) is None                 # ... read the statistics as stored
+    assert _nf4._launch_scales(None, None, None) is None
     # few row groups (7B k/v: 8 groups of 64 rows, 28 super-steps): split down to two super-steps
     assert launch_plan(False, 8, 3584, [512])["splits"] == 14
     assert launch_plan(False, 33, 3584, [18944])["kernel"] != "nf4_skinny_kernel"

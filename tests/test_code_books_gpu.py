@@ -55,13 +55,14 @@ def test_glu_forward(plan, device, monkeypatch):
 @pytest.mark.parametrize("plan", ["2,1,8", "2,2,8", "4,1,8", "4,2,8", "7,2,8"])
 @pytest.mark.parametrize("nested,raw", [(True, False), (True, True), (False, False)])
 def test_grouped_input_gradient(plan, nested, raw, device, monkeypatch):
-    """raw: nested weights described by their double-quant statistics (no cached block scales)."""
+    """raw: nested weights described by their double-quant statistics (the default); otherwise by
+    the derived fp32 block scales."""
     from decik_amd import nf4
     from decik_amd.nf4 import linear_backward
 
     monkeypatch.setenv("DECIK_BWD_PLAN", plan)
-    if raw:
-        monkeypatch.setattr(nf4, "_scales", lambda packed, qs, device: None)
+    if not raw:
+        monkeypatch.setattr(nf4, "_launch_scales", nf4._scales)
     (p1, q1, w1), (p2, q2, w2) = _two_books(device, 256, 200, 512, nested=nested)
     d1 = randn16((130, 256), seed=312, device=device, std=1e-2)
     d2 = randn16((130, 200), seed=313, device=device, std=1e-2)

@@ -183,12 +183,15 @@ def test_unsupported_k_takes_reference_algorithm(device):
     assert_close(x.grad, ref_dx, what="odd k dx")
 
 
-def test_scale_cache_follows_in_place_updates(device):
-    """The fused GEMMs reuse cached block scales of a nested weight; changing a statistics
-    tensor in place (its version counter moves) makes the next call recompute them."""
-    from decik_amd import _lib
+def test_scale_cache_follows_in_place_updates(device, monkeypatch):
+    """Fused GEMMs switched to the derived fp32 block scales reuse the cached scales of a nested
+    weight; changing a statistics tensor in place (its version counter moves) makes the next call
+    recompute them."""
+    from decik_amd import _lib, nf4
     from decik_amd.nf4 import linear_forward
     from helpers import oracle_state
+
+    monkeypatch.setattr(nf4, "_launch_scales", nf4._scales)
 
     packed, qs, w16 = make_weight((512, 1024), seed=91, device=device)
     x = randn16((64, 1024), seed=92, device=device)

@@ -16,11 +16,11 @@ CASES = [(True, 64), (True, 128), (True, 256), (False, 32)]
 
 @pytest.fixture
 def raw_statistics(monkeypatch):
-    """Describe nested weights to every kernel as they are (no cached block scales, also for the
-    GEMV and split small-M launches)."""
+    """Describe nested weights to every kernel as they are (no derived block scales: the default,
+    made explicit here)."""
     from decik_amd import nf4
 
-    monkeypatch.setattr(nf4, "_scales", lambda packed, qs, device: None)
+    monkeypatch.setattr(nf4, "_launch_scales", lambda packed, qs, device: None)
 
 
 @pytest.mark.parametrize("plan", ["4,1,4", "2,3,4", "2,3,8", "4,1,8", "7,2,8", "8,1,8", "9,2,8"])
@@ -176,8 +176,8 @@ def test_skinny_tall_weights(m, ns, raw, device, monkeypatch):
     from decik_amd import nf4
     from decik_amd.nf4 import launch_plan, linear_forward
 
-    if raw:
-        monkeypatch.setattr(nf4, "_scales", lambda packed, qs, device: None)
+    if not raw:  # the derived fp32 block scales instead of the statistics as stored
+        monkeypatch.setattr(nf4, "_launch_scales", nf4._scales)
     k = 256
     assert launch_plan(False, m, k, list(ns))["kernel"] == "nf4_skinny_kernel"
     x = randn16((m, k), seed=180 + m, device=device)
@@ -194,19 +194,18 @@ def test_skinny_tall_weights(m, ns, raw, device, monkeypatch):
 
 @pytest.mark.parametrize("m", [3, 8, 24])
 def test_small_m_statistics_forms_same_bits(m, device, monkeypatch):
-    """Unsplit small-M launches read nested statistics as stored (the default for them, as for the
-    MFMA kernels), split ones and the GEMV the cached fp32 scales: both forms give the same
-    dequantized weights and the same sums, so the outputs are equal bit for bit."""
+    """Small-M launches read nested statistics as stored (the default for every launch) or, through
+    the hook, the derived fp32 scales: both forms give the same dequantized weights and the same
+    sums, so the outputs are equal bit for bit."""
     from decik_amd import nf4
     from decik_amd.nf4 import linear_forward
 
     k, n = 512, 16408
-    assert nf4._forward_scales(m, k, [n]) is nf4._own_statistics
     packed, qs, w16 = make_weight((n, k), seed=190, device=device)
     assert qs.nested
     x = randn16((m, k), seed=191 + m, device=device)
     (y_raw,) = linear_forward(x, [dict(packed=packed, qs=qs)])
-    monkeypatch.setattr(nf4, "_own_statistics", nf4._scales)
+    monkeypatch.setattr(nf4, "_launch_scales", nf4._scales)
     (y_cached,) = linear_forward(x, [dict(packed=packed, qs=qs)])
     assert torch.equal(y_raw, y_cached)
     assert_close(y_raw, O.linear_ref(x.cpu().numpy(), w16), what=f"small-M raw m={m}")
@@ -222,8 +221,8 @@ def test_skinny_split_k(m, raw, device, monkeypatch, skinny):
     from decik_amd import nf4
     from decik_amd.nf4 import launch_plan, linear_forward
 
-    if raw:
-        monkeypatch.setattr(nf4, "_scales", lambda packed, qs, device: None)
+    if not raw:  # the derived fp32 block scales instead of the statistics as stored
+        monkeypatch.setattr(nf4, "_launch_scales", nf4._scales)
     plan = launch_plan(False, m, 8192, [128, 64])
     assert plan["kernel"] == "nf4_skinny_kernel" and plan["splits"] > 1
     x = randn16((m, 8192), seed=170 + m, device=device)
@@ -370,14 +369,11 @@ def test_small_tile_forward(plan, m, device, monkeypatch):
     lb = randn16((320, r), seed=196, device=device, std=0.05)
     u = lora_down(x, a)
     items = [dict(packed=p1, qs=q1, bias=b1, lora_u=u, lora_b=lb, lora_scale=2.0), dict(packed=p2, qs=q2, bias=b2)]
-    raw = nf4._scales
-    monkeypatch.setattr(nf4, "_scales", lambda packed, qs, device: None)
-    y1, y2 = linear_forward(x, items, lora_rank=r)
+    y1, y2 = linear_forward(x, items, lora_rank=r)  # statistics as stored
     xn = x.cpu().numpy()
     lora = O.lora_fwd_ref(xn, a.cpu().numpy(), lb.cpu().numpy(), 2.0)[1]
     assert_close(y1, O.linear_ref(xn, w1, b1.cpu().numpy()) + lora, what=f"first weight, plan {plan}, m={m}")
     assert_close(y2, O.linear_ref(xn, w2, b2.cpu().numpy()), what=f"second weight, plan {plan}, m={m}")
-    monkeypatch.setattr(nf4, "_scales", raw)
     # the GLU launch never splits: the separate launches it must equal run unsplit too
     monkeypatch.setenv("DECIK_FWD_PLAN", plan.split(",")[0] + ",1,8")
     p3, q3, _ = make_weight((200, k), seed=197, device=device)
@@ -389,7 +385,7 @@ def test_small_tile_forward(plan, m, device, monkeypatch):
 
 @pytest.mark.parametrize("m", [64, 830])
 def test_mfma_launches_statistics_forms_same_bits(m, device, monkeypatch):
-    """The MFMA launches read nested statistics as stored by default (_tiled_scales); on the
+    """The MFMA launches read nested statistics as stored by default (_launch_scales); on the
     derived fp32 block scales instead they give the same bits: forward (several weights, bias,
     LoRA), input gradient (with a LoRA term), the GLU forward, the SwiGLU backward and the RoPE
     forward."""
@@ -429,7 +425,7 @@ def test_mfma_launches_statistics_forms_same_bits(m, device, monkeypatch):
         return out
 
     as_stored = run()
-    monkeypatch.setattr(nf4, "_tiled_scales", nf4._scales)
+    monkeypatch.setattr(nf4, "_launch_scales", nf4._scales)
     cached = run()
     torch.cuda.synchronize()
     assert len(as_stored) == len(cached) == 12
