@@ -17,10 +17,10 @@
 //   e * (k / 32) + p, so the lanes of a wave (consecutive chunks, consecutive p) read
 //   consecutive 16-byte slots -- no LDS bank conflicts -- where the natural order would put 64
 //   bytes between neighbouring lanes.
-// - Each chunk's dot products (fp32) go to an LDS slot; a wave then sums each row's slots in a
-//   fixed order (lane l: slots l, l + 64, ...; then a butterfly across the lanes), adds the bias,
-//   rounds once to fp16 and stores. The summation order depends only on k: every call gives the
-//   same bits.
+// - Each chunk's dot products (fp32) go to an LDS slot; 16 lanes of a wave then sum each row's
+//   slots in a fixed order (lane j: slots j, j + 16, ...; then four DPP steps across the 16), add
+//   the bias, round once to fp16 and store. The summation order depends only on k: every call
+//   gives the same bits.
 // - Dequantization as in the other kernels: byte-pair code book in LDS (one 8-byte read per
 //   packed byte), fp32 multiply by the block scale, one fp16 rounding: the reference's bits.
 #include "dk_internal.h"
@@ -37,8 +37,24 @@ static size_t gemv_smem_bytes(int mt, int k, int chunks) {
     return 256 * sizeof(float) + (size_t)mt * k * 2 + (size_t)mt * chunks * sizeof(float);
 }
 
+// x plus the x of the lane that DPP control CTRL names (all rows and banks, no bound control)
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float x) {
+    const int o = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false);
+    return x + __builtin_bit_cast(float, o);
+}
+
+// The sum of v over the 16 lanes of a DPP row: every lane of the row receives a sum of all 16,
+// each in a fixed order (pairs, then quads, then across quads).
+__device__ __forceinline__ float row16_sum(float v) {
+    v = dpp_add<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+    v = dpp_add<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+    v = dpp_add<0x124>(v);  // row_ror:4
+    return dpp_add<0x128>(v);  // row_ror:8
+}
+
 template <int MT, bool NESTED, int CPT, int TH>
-__global__ __launch_bounds__(TH) void nf4_gemv_kernel(const FwdArgs a, const int rows_per_wg) {
+__global__ __launch_bounds__(TH) void nf4_gemv_kernel(const FwdArgs a, const int rows_per_wg, const uint32_t cpr_inv) {
     // byte-pair code book (static: its address is a constant the LDS reads take as an offset)
     __shared__ float2_t lut2[256];
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -62,27 +78,10 @@ __global__ __launch_bounds__(TH) void nf4_gemv_kernel(const FwdArgs a, const int
     const int nch = rows * cpr;             // chunks of this work-group
     const uint32_t c0 = (uint32_t)n0 * (uint32_t)cpr;  // first chunk (flat over the weight)
 
-    // Load order (vector memory operations complete in order): the code-book entries of this
-    // thread, X of every token row straight into LDS (no registers), then the thread's chunk loads
-    // and block scales, all issued before any is used; waiting until only the chunk loads are
-    // outstanding then covers the code book and X.
-    const float b_hi = W.code[(tid & 255) >> 4], b_lo = W.code[tid & 15];
-    const float c2v = NESTED ? W.code2[tid & 255] : 0.0f;
-    const float offset = NESTED ? *W.offset : 0.0f;
-    {
-        const uint32_t xbytes = (uint32_t)K * 2u;
-        for (int m = 0; m < MT; ++m) {
-            const rsrc_t xr = make_rsrc(a.x + (int64_t)min(m, M - 1) * a.ldx, m < M ? xbytes : 0u);
-            for (uint32_t o = 1024u * (uint32_t)wave; o < xbytes; o += 1024u * (TH / 64))
-                if (o + 16u * (uint32_t)lane < xbytes) {  // rows past m: zeros (descriptor of size 0)
-                    // slot s = e * cpr + p holds piece e of k-range p: source bytes 16 (4 p + e)
-                    const uint32_t sl = (o >> 4) + (uint32_t)lane, e = sl / (uint32_t)cpr;
-                    const uint32_t src = (4u * (sl - e * (uint32_t)cpr) + e) * 16u;
-                    bload128_lds(xr, (uint8_t*)xs + (size_t)m * xbytes + o, src);
-                }
-        }
-    }
-    asm volatile("" ::: "memory");  // the chunk loads stay behind the X loads (the wait below counts on it)
+    // Load order: the thread's chunk loads and block statistics first, so that the HBM round trip
+    // starts before anything else; then its code-book entries and X of every token row, straight
+    // into LDS (no registers), which arrive while the chunks are in flight. Vector memory
+    // operations complete in order: one wait for all of them precedes the code book's LDS writes.
     const rsrc_t wrs = make_rsrc(W.packed, W.packed_bytes);
     const rsrc_t ars = make_rsrc(NESTED ? (const void*)W.absmax8 : (const void*)W.absmaxf, W.absmax_bytes);
     const rsrc_t a2rs = make_rsrc(W.absmax2, NESTED ? W.absmax2_bytes : 0u);
@@ -104,11 +103,28 @@ __global__ __launch_bounds__(TH) void nf4_gemv_kernel(const FwdArgs a, const int
             s[i] = bloadf(ars, off_if(ok, blk * 4u));
         }
     }
+    asm volatile("" ::: "memory");  // the chunk loads go out first
+    const float b_hi = W.code[(tid & 255) >> 4], b_lo = W.code[tid & 15];
+    const float c2v = NESTED ? W.code2[tid & 255] : 0.0f;
+    const float offset = NESTED ? *W.offset : 0.0f;
+    {
+        // slot e * cpr + p of a token row holds its 16-byte piece e of k-range p (source bytes
+        // 16 (4 p + e)): each load instruction of a wave fills 64 consecutive slots of one piece
+        const uint32_t xbytes = (uint32_t)K * 2u;
+        for (int m = 0; m < MT; ++m) {
+            const rsrc_t xr = make_rsrc(a.x + (int64_t)min(m, M - 1) * a.ldx, m < M ? xbytes : 0u);
+            uint8_t* xm = (uint8_t*)xs + (size_t)m * xbytes;
+            for (int p0 = 64 * wave; p0 < cpr; p0 += TH)
+                if (p0 + lane < cpr)  // rows past m: zeros (descriptor of size 0)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        bload128_lds(xr, xm + (size_t)(e * cpr + p0) * 16, (4u * (uint32_t)(p0 + lane) + (uint32_t)e) * 16u);
+        }
+    }
 
     // code book and nested code2 table; the barrier (without the release fence of
-    // __syncthreads, which would wait for the chunk loads too) then publishes every wave's share
-    // of them and of X
-    wait_vmcnt<(NESTED ? 3 : 2) * CPT>();
+    // __syncthreads) then publishes every wave's share of them and of X
+    wait_vmcnt<0>();
     if (tid < 256) {
         lut2[tid] = float2_t{b_hi, b_lo};
         if constexpr (NESTED) c2[tid] = c2v;
@@ -116,8 +132,10 @@ __global__ __launch_bounds__(TH) void nf4_gemv_kernel(const FwdArgs a, const int
     lds_barrier();
 
     // k-range p (chunk within its row) of the thread's chunk i: advanced by 256 chunks a step
-    int pk = tid % cpr;
-    const int dp = TH % cpr;
+    // tid % cpr and TH % cpr without a division: cpr_inv = ceil(2^20 / cpr), exact for
+    // numerators below 512 while cpr <= 2048 (the error term n (cpr_inv cpr - 2^20) stays below 2^20)
+    int pk = tid - (int)__umul24((uint32_t)cpr, __umul24((uint32_t)tid, cpr_inv) >> 20);
+    const int dp = TH - cpr * (int)(((uint32_t)TH * cpr_inv) >> 20);
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
         const int c = tid + TH * i;
@@ -142,7 +160,7 @@ __global__ __launch_bounds__(TH) void nf4_gemv_kernel(const FwdArgs a, const int
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 // packed byte 4 e + q: weights 32 p + 8 e + 2 q (high nibble) and + 1
-                const float2_t cv = *(const float2_t*)((const char*)lut2 + (((w >> (8 * q)) & 0xFFu) << 3));
+                const float2_t cv = *(const float2_t*)((const char*)lut2 + byte_x8(w, q));
                 const half2_t w2 = __builtin_bit_cast(half2_t, pack_half2(cv.x * sc, cv.y * sc));
 #pragma unroll
                 for (int m = 0; m < MT; ++m) {
@@ -161,17 +179,33 @@ __global__ __launch_bounds__(TH) void nf4_gemv_kernel(const FwdArgs a, const int
     }
     lds_barrier();
 
-    // each row's sum in a fixed order: lane l adds slots l, l + 64, ... of the row, then a butterfly
-    for (int r = wave; r < rows; r += TH / 64) {
+    // each row's sum in a fixed order: a wave sums four rows at once, 16 lanes each; lane j of a
+    // row adds its slots j, j + 16, ... in turn, then the 16 lanes combine in four DPP steps
+    // (lane j with lanes j ^ 1, j ^ 2, then rotations by 4 and 8 within the 16), and lane 0 of
+    // the 16 stores. The order depends only on k.
+    const int sub = lane >> 4, j16 = lane & 15;
+    for (int r0 = 4 * wave; r0 < rows; r0 += TH / 16) {
+        const int r = r0 + sub;
         float v[MT];
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
             v[m] = 0.0f;
-            for (int j = lane; j < cpr; j += 64) v[m] += part[m * nch + r * cpr + j];
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) v[m] += __shfl_xor(v[m], o, 64);
+            if (r < rows) {
+                // four reads in flight at a time, added in slot order
+                const float* pr = part + m * nch + r * cpr;
+                int q = j16;
+                for (; q + 48 < cpr; q += 64) {
+                    const float t0 = pr[q], t1 = pr[q + 16], t2 = pr[q + 32], t3 = pr[q + 48];
+                    v[m] += t0;
+                    v[m] += t1;
+                    v[m] += t2;
+                    v[m] += t3;
+                }
+                for (; q < cpr; q += 16) v[m] += pr[q];
+            }
+            v[m] = row16_sum(v[m]);
         }
-        if (lane == 0) {
+        if (j16 == 0 && r < rows) {
             const int n = n0 + r;
             const float b = G.bias != nullptr ? (float)G.bias[n] : 0.0f;
 #pragma unroll
@@ -265,7 +299,8 @@ static hipError_t launch_gemv_th(const FwdArgs& a, int rows, int grid, hipStream
     const size_t lds = gemv_smem_bytes(MT, a.k, rows * (a.k >> 5));
     const hipError_t e = allow_dynamic_lds((const void*)nf4_gemv_kernel<MT, NESTED, CPT, TH>, lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((nf4_gemv_kernel<MT, NESTED, CPT, TH>), dim3(grid), dim3(TH), lds, s, a, rows);
+    const uint32_t cpr = (uint32_t)(a.k >> 5), cpr_inv = ((1u << 20) + cpr - 1) / cpr;
+    hipLaunchKernelGGL((nf4_gemv_kernel<MT, NESTED, CPT, TH>), dim3(grid), dim3(TH), lds, s, a, rows, cpr_inv);
     return hipGetLastError();
 }
 
