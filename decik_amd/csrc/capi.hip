@@ -492,8 +492,8 @@ GemmPlan plan_skinny(int64_t m, int64_t k, const int64_t* ns, int ngroups, bool 
 // the GEMV kernel (at most kGemvMaxM rows) or nf4_skinny_kernel, unless DECIK_FWD_PLAN forces an
 // MFMA plan. Measured on Qwen2.5-7B shapes: at one row the GEMV is faster on every shape (gate
 // 18 us against 25, q/o 10 against 16), and at two rows on all but the long contraction of down;
-// from 3 rows on the skinny kernel wins (7B gate at 8 rows: 28 us against 39 for the MFMA
-// kernels). DECIK_SMALL_M = gemv / skinny forces one of them for launches both may take.
+// from 3 rows on the skinny kernel wins on all but small weights (gemv_requested; 7B gate at 8
+// rows: 28 us against 39 for the MFMA kernels). DECIK_SMALL_M = gemv / skinny forces one of them for launches both may take.
 // Past 16 rows (two 16-token blocks a work-group), weights of more row groups than CUs (even at
 // 6 tiles a group) go to the MFMA kernels: the skinny kernel's second round would hold few
 // work-groups (7B gate, 296 groups of 64 rows: 38.8 / 39.6 us at 24 / 32 rows against 34.2 /
@@ -506,7 +506,7 @@ bool small_m_forward(int64_t m, bool glu, bool lora, const int64_t* ns, int ngro
     return true;
 }
 bool gemv_requested(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
-    if (m > kGemvMaxM || !gemv_fits(k)) return false;
+    if (!gemv_fits(m, k)) return false;
     const char* v = std::getenv("DECIK_SMALL_M");
     if (v != nullptr && std::string(v) == "gemv") return true;
     if (v != nullptr && std::string(v) == "skinny") return false;
@@ -519,7 +519,16 @@ bool gemv_requested(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
     // 35.1; the 1.5B down, k = 8960: 8.6 against 10.5 on the GEMV).
     int64_t weights = 0;
     for (int g = 0; g < ngroups; ++g) weights += ns[g] * k;
-    return k <= 12288 && weights < (int64_t(1) << 25);
+    if (m == 2) return k <= 12288 && weights < (int64_t(1) << 25);
+    // 3-8 rows (the GEMV computes 4 or 8): small weights, whose small-M launches are bound by
+    // their fixed cost (a split and its reduction launch), while X of the computed rows stays
+    // within 32 KB of LDS per work-group. Graph-replayed, GEMV against small-M kernel, us:
+    // 1.5B k/v 4.3-4.5 / 6.3 against 8.1 / 8.3 at 3-4 / 8 rows, 1.5B q/o 4.9-5.0 / 6.9 against
+    // 8.4-8.6, the 1.5B q/k/v launch 5.1-5.3 / 7.1 against 8.6-8.8, 7B k/v 5.2 against 9.2 at
+    // 3-4 rows (11.6 against 9.4 at 8: X of 8 rows 56 KB); larger weights lose (7B q/o 11.9
+    // against 11.0, 7B gate 26 against 18, at 3 rows).
+    const int64_t mt = m <= 4 ? 4 : 8;
+    return weights < (int64_t(1) << 23) && mt * k * 2 <= 32768;
 }
 
 

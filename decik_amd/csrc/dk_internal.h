@@ -153,12 +153,13 @@ struct GemmPlan {
 };
 
 hipError_t launch_fwd(const FwdArgs& a, int mb, int grid, hipStream_t s);
-// GEMV for launches of at most kGemvMaxM token rows (no LoRA terms, no GLU epilogue, no split)
-constexpr int kGemvMaxM = 2;  // measured: the MFMA kernels are faster from 3 token rows on 7B shapes
+// GEMV for launches of at most kGemvMaxM token rows (no LoRA terms, no GLU epilogue, no split),
+// computed for 1, 2, 4 or 8 rows
+constexpr int kGemvMaxM = 8;
 // a: the groups' tile_begin fields become their first work-group. gemv_fits: the GEMV takes
-// this contraction length.
+// m token rows at this contraction length.
 hipError_t launch_gemv(FwdArgs& a, hipStream_t s);
-bool gemv_fits(int64_t k);
+bool gemv_fits(int64_t m, int64_t k);
 // waves per work-group of a GEMV launch (k must fit: gemv_fits)
 int gemv_waves(int64_t m, int64_t k, int64_t nrows);
 // Forward launches of few token rows (no LoRA terms, no GLU epilogue): nf4_skinny_kernel. A

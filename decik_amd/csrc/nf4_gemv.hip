@@ -145,17 +145,24 @@ __global__ __launch_bounds__(TH) void nf4_gemv_kernel(const FwdArgs a, const int
         pk += dp;
         if (pk >= cpr) pk -= cpr;
         // the 32 X values of this chunk for every token row: dword j of piece e holds
-        // X[32 p + 8 e + 2 j] and X[32 p + 8 e + 2 j + 1]
-        u32x4_t xv[MT][4];
+        // X[32 p + 8 e + 2 j] and X[32 p + 8 e + 2 j + 1]. One or two token rows: all four
+        // pieces read up front; more rows: piece by piece (16 registers a row otherwise)
+        constexpr bool kXAll = MT <= 2;
+        u32x4_t xv[kXAll ? MT : 1][4];
+        if constexpr (kXAll)
 #pragma unroll
-        for (int m = 0; m < MT; ++m)
+            for (int m = 0; m < MT; ++m)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) xv[m][e] = *(const u32x4_t*)(xs + m * K + (e * cpr + pc) * 8);
+                for (int e = 0; e < 4; ++e) xv[m][e] = *(const u32x4_t*)(xs + m * K + (e * cpr + pc) * 8);
         float acc[MT];
 #pragma unroll
         for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
+            u32x4_t xe[MT];
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+                xe[m] = kXAll ? xv[kXAll ? m : 0][e] : *(const u32x4_t*)(xs + m * K + (e * cpr + pc) * 8);
             const uint32_t w = p[i][e];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -166,7 +173,7 @@ __global__ __launch_bounds__(TH) void nf4_gemv_kernel(const FwdArgs a, const int
                 for (int m = 0; m < MT; ++m) {
                     // elements copied to a scalar first: hipcc compiles __builtin_bit_cast of a
                     // vector element v[j] as element 0 whatever j is
-                    const uint32_t xq = xv[m][e][q];
+                    const uint32_t xq = xe[m][q];
                     acc[m] = __builtin_amdgcn_fdot2(w2, __builtin_bit_cast(half2_t, xq), acc[m], false);
                 }
             }
@@ -240,12 +247,15 @@ static GemvShape gemv_shape_bound(int k) {
     return best;
 }
 
-// Whether the GEMV takes a launch of contraction k (a row must fit one work-group's loads, X of
-// two token rows and the sums must fit LDS).
-bool gemv_fits(int64_t k) {
-    if (k <= 0 || k % 32 != 0 || k > kGemvThreads * kGemvMaxChunks * 32) return false;
+// Token rows a launch of m rows is computed for (X rows past m read as zeros)
+static int gemv_mt(int64_t m) { return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8; }
+
+// Whether the GEMV takes a launch of m token rows and contraction k (a row must fit one
+// work-group's loads, X of the token rows and the sums must fit LDS).
+bool gemv_fits(int64_t m, int64_t k) {
+    if (m < 1 || m > kGemvMaxM || k <= 0 || k % 32 != 0 || k > kGemvThreads * kGemvMaxChunks * 32) return false;
     const GemvShape sh = gemv_shape_bound((int)k);
-    return sh.rows >= 1 && gemv_smem_bytes(kGemvMaxM, (int)k, sh.rows * (int)(k >> 5)) <= 158 * 1024;
+    return sh.rows >= 1 && gemv_smem_bytes(gemv_mt(m), (int)k, sh.rows * (int)(k >> 5)) <= 158 * 1024;
 }
 
 // The shape of a launch of `nrows` weight rows and mt token rows. Every work-group stages X
@@ -328,27 +338,29 @@ static hipError_t launch_gemv_cpt(const FwdArgs& a, const GemvShape& sh, int gri
 }
 
 int gemv_waves(int64_t m, int64_t k, int64_t nrows) {
-    return gemv_shape((int)k, nrows, (int)m).threads / 64;
+    return gemv_shape((int)k, nrows, gemv_mt(m)).threads / 64;
 }
 
 // a: the groups' tile_begin fields are overwritten with their first work-group
 hipError_t launch_gemv(FwdArgs& a, hipStream_t s) {
-    if (a.m < 1 || a.m > kGemvMaxM || a.glu || !gemv_fits(a.k)) return hipErrorInvalidValue;
+    if (a.glu || !gemv_fits(a.m, a.k)) return hipErrorInvalidValue;
     for (int g = 0; g < a.ngroups; ++g)
         if (a.g[g].lora_u != nullptr) return hipErrorInvalidValue;
     int64_t nrows = 0;
     for (int g = 0; g < a.ngroups; ++g) nrows += a.g[g].w.n;
-    const GemvShape sh = gemv_shape(a.k, nrows, a.m);
+    const int mt = gemv_mt(a.m);
+    const GemvShape sh = gemv_shape(a.k, nrows, mt);
     int grid = 0;
     for (int g = 0; g < a.ngroups; ++g) {
         a.g[g].tile_begin = grid;
         grid += (int)((a.g[g].w.n + sh.rows - 1) / sh.rows);
     }
-    if (a.m == 1)
-        return a.nested ? launch_gemv_cpt<1, true>(a, sh, grid, s)
-                        : launch_gemv_cpt<1, false>(a, sh, grid, s);
-    return a.nested ? launch_gemv_cpt<2, true>(a, sh, grid, s)
-                    : launch_gemv_cpt<2, false>(a, sh, grid, s);
+    switch (mt) {
+        case 1: return a.nested ? launch_gemv_cpt<1, true>(a, sh, grid, s) : launch_gemv_cpt<1, false>(a, sh, grid, s);
+        case 2: return a.nested ? launch_gemv_cpt<2, true>(a, sh, grid, s) : launch_gemv_cpt<2, false>(a, sh, grid, s);
+        case 4: return a.nested ? launch_gemv_cpt<4, true>(a, sh, grid, s) : launch_gemv_cpt<4, false>(a, sh, grid, s);
+        default: return a.nested ? launch_gemv_cpt<8, true>(a, sh, grid, s) : launch_gemv_cpt<8, false>(a, sh, grid, s);
+    }
 }
 
 }  // namespace dk

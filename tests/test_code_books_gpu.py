@@ -71,15 +71,17 @@ def test_grouped_input_gradient(plan, nested, raw, device, monkeypatch):
     assert_close(dx, ref, max_rel=1e-4, mean_rel=1e-5, what=f"two books, plan {plan}, nested={nested} raw={raw}")
 
 
-@pytest.mark.parametrize("m,small", [(1, "gemv"), (2, "gemv"), (8, None)])
+@pytest.mark.parametrize("m,small", [(1, "gemv"), (2, "gemv"), (4, None), (8, "skinny")])
 def test_small_m_forward(m, small, device, monkeypatch):
+    """Two weights with different code books in one small-M launch: GEMV (forced, or the planner's
+    choice for these small weights at 4 rows) and the small-M MFMA kernel."""
     from decik_amd.nf4 import launch_plan, linear_forward
 
     if small is not None:
         monkeypatch.setenv("DECIK_SMALL_M", small)
     (p1, q1, w1), (p2, q2, w2) = _two_books(device, 256, 264, 1024)
     plan = launch_plan(False, m, 1024, [256, 264])
-    assert plan["kernel"] == ("nf4_gemv_kernel" if small else "nf4_skinny_kernel")
+    assert plan["kernel"] == ("nf4_skinny_kernel" if small == "skinny" else "nf4_gemv_kernel")
     x = randn16((m, 1024), seed=314 + m, device=device)
     y1, y2 = linear_forward(x, [dict(packed=p1, qs=q1), dict(packed=p2, qs=q2)])
     xn = x.cpu().numpy()

@@ -168,7 +168,7 @@ def test_skinny_small_m(m, nested, blocksize, device, raw_statistics, skinny):
 @pytest.mark.parametrize("m", [3, 8, 17, 32])
 @pytest.mark.parametrize("ns", [(16408, 64), (20496,)])
 @pytest.mark.parametrize("raw", [False, True])
-def test_skinny_tall_weights(m, ns, raw, device, monkeypatch):
+def test_skinny_tall_weights(m, ns, raw, device, monkeypatch, skinny):
     """Weights of more 64-row groups than a 256-CU device has CUs: the small-M kernel takes row
     groups of 80 (16408 + 64 rows: 206 + 1 groups) or 96 rows (20496: 214 groups, 257 of 80) so
     that they run in one round; the last group of each weight is partial, and at 17-32 token rows
@@ -260,6 +260,32 @@ def test_gemv_small_m(m, nested, blocksize, device, raw_statistics, gemv):
     ys = linear_forward(x, items)
     for y, ref in zip(ys, refs):
         assert_close(y, ref, what=f"gemv m={m} nested={nested} bs={blocksize}")
+
+
+@pytest.mark.parametrize("m", [3, 4, 5, 8])
+@pytest.mark.parametrize("k", [1056, 3584])
+def test_gemv_more_rows(m, k, device, raw_statistics, monkeypatch):
+    """The GEMV computed for four or eight token rows (m = 3, 5: rows past m read as zeros and
+    are not stored), sent there on purpose: three weights with bias in one launch against the
+    oracle, and the same bits on a second call."""
+    import torch
+
+    from decik_amd.nf4 import launch_plan, linear_forward
+
+    monkeypatch.setenv("DECIK_SMALL_M", "gemv")
+    assert launch_plan(False, m, k, [320, 64, 64])["kernel"] == "nf4_gemv_kernel"
+    items, refs = [], []
+    x = randn16((m, k), seed=160 + m, device=device)
+    for i, n in enumerate((320, 64, 64)):
+        packed, qs, w16 = make_weight((n, k), seed=161 + i + k, device=device)
+        b = randn16((n,), seed=165 + i, device=device, std=0.1)
+        items.append(dict(packed=packed, qs=qs, bias=b))
+        refs.append(O.linear_ref(x.cpu().numpy(), w16, b.cpu().numpy()))
+    ys = linear_forward(x, items)
+    for y, ref in zip(ys, refs):
+        assert_close(y, ref, what=f"gemv m={m} k={k}")
+    for y, y2 in zip(ys, linear_forward(x, items)):
+        assert torch.equal(y, y2)
 
 
 @pytest.mark.parametrize("m", [1, 2])

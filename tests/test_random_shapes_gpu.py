@@ -59,7 +59,8 @@ def test_random_input_gradient(m, n, k, nested, bs, seed, plan, device, monkeypa
                  what=f"bwd m={m} n={n} k={k_in} nested={nested} bs={bs} plan={plan}")
 
 
-# Few token rows (the decoding regime: GEMV at 1-2 rows, the small-M kernel at 3-32, split along
+# Few token rows (the decoding regime: GEMV at 1-2 rows and at 3-8 on small weights, the small-M
+# kernel otherwise up to 32 rows, split along
 # the contraction where the rows cannot fill the GPU), with contractions up to 20480 so that X of
 # long rows takes the GEMV's eight-wave work-groups.
 _RNG_S = np.random.default_rng(20261203)
@@ -86,6 +87,8 @@ def test_random_small_m_forward(m, n, k, nested, bs, seed, device):
     kernel = launch_plan(False, m, k, [n], blocksize=bs)["kernel"]
     if m <= 2 and (m == 1 or k <= 12288):
         assert kernel == "nf4_gemv_kernel"
+    elif m <= 8 and n * k < 2 ** 23 and (4 if m <= 4 else 8) * k * 2 <= 32768:
+        assert kernel == "nf4_gemv_kernel"  # 3-8 rows on small weights
     else:
         assert kernel == ("nf4_fwd8_kernel" if m > 16 and (n + 63) // 64 > 256 else "nf4_skinny_kernel")
     packed, qs, w16 = make_weight((n, k), seed=seed, device=device, nested=nested, blocksize=bs)
