@@ -153,8 +153,8 @@ struct GemmPlan {
 };
 
 hipError_t launch_fwd(const FwdArgs& a, int mb, int grid, hipStream_t s);
-// GEMV for launches of at most kGemvMaxM token rows (no LoRA terms, no GLU epilogue, no split),
-// computed for 1, 2, 4 or 8 rows
+// GEMV for launches of at most kGemvMaxM token rows (no LoRA terms, no GLU epilogue, no split);
+// a work-group computes 1, 2 or 4 of them
 constexpr int kGemvMaxM = 8;
 // a: the groups' tile_begin fields become their first work-group. gemv_fits: the GEMV takes
 // m token rows at this contraction length.

@@ -1,10 +1,12 @@
-// Fused NF4 dequant x fp16 product for launches with one or two token rows: the same
+// Fused NF4 dequant x fp16 product for launches with one to eight token rows: the same
 // Y = X.W^T + bias as nf4_fwd_kernel (solution/nf4.py:93-96) in the decoding regime, where the
 // call is bound by streaming the packed weight from HBM once. The MFMA kernels pad such launches
 // to 32-token tiles and dequantize every weight for one useful multiply-add; here each weight is
 // dequantized once and used for every token in fp32 dot products (v_dot2_f32_f16).
 //
 // The kernel is organised around keeping as much of the weight in flight as HBM needs:
+// - Token rows: a work-group computes one, two or four (MT); launches of five to eight rows take
+//   two work-groups per row range, one per four token rows, so that X stays four rows of LDS.
 // - A work-group (four waves; eight where X of long rows would limit a CU to 12 waves) owns
 //   `rows` consecutive weight rows of one group. Their packed bytes are contiguous ([n, k / 2]
 //   row-major), so the work-group streams one contiguous range of 16-byte chunks (32 weights of
@@ -54,13 +56,19 @@ __device__ __forceinline__ float row16_sum(float v) {
 }
 
 template <int MT, bool NESTED, int CPT, int TH>
-__global__ __launch_bounds__(TH) void nf4_gemv_kernel(const FwdArgs a, const int rows_per_wg, const uint32_t cpr_inv) {
+__global__ __launch_bounds__(TH) void nf4_gemv_kernel(const FwdArgs a, const int rows_per_wg, const uint32_t cpr_inv,
+                                                       const int tg_shift) {
     // byte-pair code book (static: its address is a constant the LDS reads take as an offset)
     __shared__ float2_t lut2[256];
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     float* c2 = (float*)smem;                        // nested: code2 table
     _Float16* xs = (_Float16*)(smem + 256 * 4);      // [MT][k], transposed 16-byte pieces
-    const int K = a.k, M = a.m;
+    // token groups: with tg_shift = 1, work-groups 2 b and 2 b + 1 take the same weight rows for
+    // token rows 0..MT-1 and MT..2 MT-1 (X of MT rows per work-group)
+    const int tg = (int)blockIdx.x & ((1 << tg_shift) - 1);
+    const int bid = (int)blockIdx.x >> tg_shift;
+    const int K = a.k, M = min(MT, a.m - MT * tg);
+    const _Float16* const xg = a.x + (int64_t)(MT * tg) * a.ldx;
     float* part = (float*)(xs + MT * K);             // [MT][rows * cpr]
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -68,11 +76,11 @@ __global__ __launch_bounds__(TH) void nf4_gemv_kernel(const FwdArgs a, const int
     int gi = 0;
 #pragma unroll
     for (int q = 1; q < kMaxGroups; ++q)
-        if (q < a.ngroups && (int)blockIdx.x >= a.g[q].tile_begin) gi = q;
+        if (q < a.ngroups && bid >= a.g[q].tile_begin) gi = q;
     const FwdGroupDev& G = a.g[gi];
     const NF4Dev& W = G.w;
     const int N = (int)W.n;
-    const int n0 = ((int)blockIdx.x - G.tile_begin) * rows_per_wg;
+    const int n0 = (bid - G.tile_begin) * rows_per_wg;
     const int rows = min(rows_per_wg, N - n0);
     const int cpr = K >> 5;                 // chunks per row
     const int nch = rows * cpr;             // chunks of this work-group
@@ -112,7 +120,7 @@ __global__ __launch_bounds__(TH) void nf4_gemv_kernel(const FwdArgs a, const int
         // 16 (4 p + e)): each load instruction of a wave fills 64 consecutive slots of one piece
         const uint32_t xbytes = (uint32_t)K * 2u;
         for (int m = 0; m < MT; ++m) {
-            const rsrc_t xr = make_rsrc(a.x + (int64_t)min(m, M - 1) * a.ldx, m < M ? xbytes : 0u);
+            const rsrc_t xr = make_rsrc(xg + (int64_t)min(m, M - 1) * a.ldx, m < M ? xbytes : 0u);
             uint8_t* xm = (uint8_t*)xs + (size_t)m * xbytes;
             for (int p0 = 64 * wave; p0 < cpr; p0 += TH)
                 if (p0 + lane < cpr)  // rows past m: zeros (descriptor of size 0)
@@ -217,7 +225,7 @@ __global__ __launch_bounds__(TH) void nf4_gemv_kernel(const FwdArgs a, const int
             const float b = G.bias != nullptr ? (float)G.bias[n] : 0.0f;
 #pragma unroll
             for (int m = 0; m < MT; ++m)
-                if (m < M) G.y[(int64_t)m * G.ldy + n] = to_half(v[m] + b);
+                if (m < M) G.y[(int64_t)(MT * tg + m) * G.ldy + n] = to_half(v[m] + b);
         }
     }
 }
@@ -247,8 +255,9 @@ static GemvShape gemv_shape_bound(int k) {
     return best;
 }
 
-// Token rows a launch of m rows is computed for (X rows past m read as zeros)
-static int gemv_mt(int64_t m) { return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8; }
+// Token rows a work-group of a launch of m rows computes (X rows past m read as zeros); past
+// four rows two work-groups share each weight row range, one per four token rows
+static int gemv_mt(int64_t m) { return m <= 1 ? 1 : m <= 2 ? 2 : 4; }
 
 // Whether the GEMV takes a launch of m token rows and contraction k (a row must fit one
 // work-group's loads, X of the token rows and the sums must fit LDS).
@@ -305,34 +314,35 @@ static GemvShape gemv_shape(int k, int64_t nrows, int mt) {
 }
 
 template <int MT, bool NESTED, int CPT, int TH>
-static hipError_t launch_gemv_th(const FwdArgs& a, int rows, int grid, hipStream_t s) {
+static hipError_t launch_gemv_th(const FwdArgs& a, int rows, int grid, int tg_shift, hipStream_t s) {
     const size_t lds = gemv_smem_bytes(MT, a.k, rows * (a.k >> 5));
     const hipError_t e = allow_dynamic_lds((const void*)nf4_gemv_kernel<MT, NESTED, CPT, TH>, lds);
     if (e != hipSuccess) return e;
     const uint32_t cpr = (uint32_t)(a.k >> 5), cpr_inv = ((1u << 20) + cpr - 1) / cpr;
-    hipLaunchKernelGGL((nf4_gemv_kernel<MT, NESTED, CPT, TH>), dim3(grid), dim3(TH), lds, s, a, rows, cpr_inv);
+    hipLaunchKernelGGL((nf4_gemv_kernel<MT, NESTED, CPT, TH>), dim3(grid << tg_shift), dim3(TH), lds, s, a, rows, cpr_inv,
+                       tg_shift);
     return hipGetLastError();
 }
 
 template <int MT, bool NESTED, int CPT>
-static hipError_t launch_gemv_t(const FwdArgs& a, const GemvShape& sh, int grid, hipStream_t s) {
+static hipError_t launch_gemv_t(const FwdArgs& a, const GemvShape& sh, int grid, int tg_shift, hipStream_t s) {
     if constexpr (CPT >= 4)  // eight-wave shapes take at least 4 loads per thread
-        if (sh.threads == 2 * kGemvThreads) return launch_gemv_th<MT, NESTED, CPT, 2 * kGemvThreads>(a, sh.rows, grid, s);
+        if (sh.threads == 2 * kGemvThreads) return launch_gemv_th<MT, NESTED, CPT, 2 * kGemvThreads>(a, sh.rows, grid, tg_shift, s);
     if (sh.threads != kGemvThreads) return hipErrorInvalidValue;
-    return launch_gemv_th<MT, NESTED, CPT, kGemvThreads>(a, sh.rows, grid, s);
+    return launch_gemv_th<MT, NESTED, CPT, kGemvThreads>(a, sh.rows, grid, tg_shift, s);
 }
 
 template <int MT, bool NESTED>
-static hipError_t launch_gemv_cpt(const FwdArgs& a, const GemvShape& sh, int grid, hipStream_t s) {
+static hipError_t launch_gemv_cpt(const FwdArgs& a, const GemvShape& sh, int grid, int tg_shift, hipStream_t s) {
     switch (sh.cpt) {
-        case 1: return launch_gemv_t<MT, NESTED, 1>(a, sh, grid, s);
-        case 2: return launch_gemv_t<MT, NESTED, 2>(a, sh, grid, s);
-        case 3: return launch_gemv_t<MT, NESTED, 3>(a, sh, grid, s);
-        case 4: return launch_gemv_t<MT, NESTED, 4>(a, sh, grid, s);
-        case 5: return launch_gemv_t<MT, NESTED, 5>(a, sh, grid, s);
-        case 6: return launch_gemv_t<MT, NESTED, 6>(a, sh, grid, s);
-        case 7: return launch_gemv_t<MT, NESTED, 7>(a, sh, grid, s);
-        case 8: return launch_gemv_t<MT, NESTED, 8>(a, sh, grid, s);
+        case 1: return launch_gemv_t<MT, NESTED, 1>(a, sh, grid, tg_shift, s);
+        case 2: return launch_gemv_t<MT, NESTED, 2>(a, sh, grid, tg_shift, s);
+        case 3: return launch_gemv_t<MT, NESTED, 3>(a, sh, grid, tg_shift, s);
+        case 4: return launch_gemv_t<MT, NESTED, 4>(a, sh, grid, tg_shift, s);
+        case 5: return launch_gemv_t<MT, NESTED, 5>(a, sh, grid, tg_shift, s);
+        case 6: return launch_gemv_t<MT, NESTED, 6>(a, sh, grid, tg_shift, s);
+        case 7: return launch_gemv_t<MT, NESTED, 7>(a, sh, grid, tg_shift, s);
+        case 8: return launch_gemv_t<MT, NESTED, 8>(a, sh, grid, tg_shift, s);
         default: return hipErrorInvalidValue;
     }
 }
@@ -355,11 +365,11 @@ hipError_t launch_gemv(FwdArgs& a, hipStream_t s) {
         a.g[g].tile_begin = grid;
         grid += (int)((a.g[g].w.n + sh.rows - 1) / sh.rows);
     }
+    const int tg_shift = a.m > 4 ? 1 : 0;
     switch (mt) {
-        case 1: return a.nested ? launch_gemv_cpt<1, true>(a, sh, grid, s) : launch_gemv_cpt<1, false>(a, sh, grid, s);
-        case 2: return a.nested ? launch_gemv_cpt<2, true>(a, sh, grid, s) : launch_gemv_cpt<2, false>(a, sh, grid, s);
-        case 4: return a.nested ? launch_gemv_cpt<4, true>(a, sh, grid, s) : launch_gemv_cpt<4, false>(a, sh, grid, s);
-        default: return a.nested ? launch_gemv_cpt<8, true>(a, sh, grid, s) : launch_gemv_cpt<8, false>(a, sh, grid, s);
+        case 1: return a.nested ? launch_gemv_cpt<1, true>(a, sh, grid, 0, s) : launch_gemv_cpt<1, false>(a, sh, grid, 0, s);
+        case 2: return a.nested ? launch_gemv_cpt<2, true>(a, sh, grid, 0, s) : launch_gemv_cpt<2, false>(a, sh, grid, 0, s);
+        default: return a.nested ? launch_gemv_cpt<4, true>(a, sh, grid, tg_shift, s) : launch_gemv_cpt<4, false>(a, sh, grid, tg_shift, s);
     }
 }
 

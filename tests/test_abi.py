@@ -213,19 +213,20 @@ def test_launch_plans():
     # every fused launch reads nested statistics as stored (no derived block scales)
     from decik_amd import nf4 as _nf4
     assert _nf4._launch_scales(None, None, None) is None
-    # few row groups (7B k/v: 8 groups of 64 rows, 28 super-steps): split down to two super-steps
-    assert launch_plan(False, 8, 3584, [512])["splits"] == 14
-    # 3-8 rows: small weights take the GEMV (computed for 4 or 8 rows) while X of those rows fits
+    # 3-8 rows: small weights take the GEMV (4 token rows a work-group) while X of 4 rows fits
     # 32 KB; larger weights and longer rows the small-M kernel
     assert launch_plan(False, 3, 3584, [512])["kernel"] == "nf4_gemv_kernel"  # 7B k/v
     assert launch_plan(False, 8, 1536, [1536, 256, 256])["kernel"] == "nf4_gemv_kernel"  # 1.5B q/k/v
     assert launch_plan(False, 3, 3584, [3584])["kernel"] == "nf4_skinny_kernel"  # 7B q/o
-    assert launch_plan(False, 5, 3584, [512])["kernel"] == "nf4_skinny_kernel"  # X of 8 rows: 56 KB
+    assert launch_plan(False, 8, 3584, [512])["kernel"] == "nf4_gemv_kernel"  # 7B k/v, two token groups
+    assert launch_plan(False, 5, 8960, [256])["kernel"] == "nf4_skinny_kernel"  # X of 4 rows: 70 KB
     assert launch_plan(False, 33, 3584, [18944])["kernel"] != "nf4_skinny_kernel"
     assert launch_plan(False, 1, 3584, [18944], lora=True)["kernel"] not in ("nf4_skinny_kernel", "nf4_gemv_kernel")
     old_sm = os.environ.get("DECIK_SMALL_M")
     try:
         os.environ["DECIK_SMALL_M"] = "skinny"
+        # few row groups (7B k/v: 8 groups of 64 rows, 28 super-steps): split down to two super-steps
+        assert launch_plan(False, 8, 3584, [512])["splits"] == 14
         assert launch_plan(False, 1, 3584, [18944])["kernel"] == "nf4_skinny_kernel"
         assert launch_plan(False, 3, 3584, [18944])["kernel"] == "nf4_skinny_kernel"
     finally:
@@ -258,7 +259,7 @@ def test_launch_plans():
     assert launch_plan(True, 830, 1536, [8960, 8960], no_split=True)["splits"] == 1
     # few token rows without a workspace (the GLU entry's two-launch fallback): the small-M kernel
     # runs unsplit, though it would split these launches when a workspace is allowed
-    for m, k, ns in ((8, 3584, [512, 512]), (24, 1536, [1536, 1536])):
+    for m, k, ns in ((8, 8960, [256, 256]), (24, 1536, [1536, 1536])):
         assert launch_plan(False, m, k, ns)["splits"] > 1
         assert launch_plan(False, m, k, ns, no_split=True) == dict(
             rows_blocks=1 if m <= 16 else 2, waves=8, splits=1, kernel="nf4_skinny_kernel", launches=1, splits_second=0)

@@ -87,7 +87,7 @@ def test_random_small_m_forward(m, n, k, nested, bs, seed, device):
     kernel = launch_plan(False, m, k, [n], blocksize=bs)["kernel"]
     if m <= 2 and (m == 1 or k <= 12288):
         assert kernel == "nf4_gemv_kernel"
-    elif m <= 8 and n * k < 2 ** 23 and (4 if m <= 4 else 8) * k * 2 <= 32768:
+    elif m <= 8 and n * k < 2 ** 23 and 4 * k * 2 <= 32768:
         assert kernel == "nf4_gemv_kernel"  # 3-8 rows on small weights
     else:
         assert kernel == ("nf4_fwd8_kernel" if m > 16 and (n + 63) // 64 > 256 else "nf4_skinny_kernel")
