@@ -133,13 +133,14 @@ def test_eight_wave_backward_three_groups_lora(plan, device, monkeypatch):
 
 @pytest.fixture
 def gemv(monkeypatch):
-    """Forward launches of 1-2 token rows take the GEMV kernel (the default; DECIK_SMALL_M unset)."""
+    """Forward launches of 1-2 token rows (3-8 on small weights) take the GEMV kernel (the
+    default; DECIK_SMALL_M unset)."""
     monkeypatch.delenv("DECIK_SMALL_M", raising=False)
 
 
 @pytest.fixture
 def skinny(monkeypatch):
-    """Send every small-M forward launch, 1-2 token rows included, to the skinny kernel."""
+    """Send every small-M forward launch, 1-8 token rows included, to the skinny kernel."""
     monkeypatch.setenv("DECIK_SMALL_M", "skinny")
 
 
@@ -242,7 +243,7 @@ def test_skinny_split_k(m, raw, device, monkeypatch, skinny):
 @pytest.mark.parametrize("m", [1, 2])
 @pytest.mark.parametrize("nested,blocksize", CASES)
 def test_gemv_small_m(m, nested, blocksize, device, raw_statistics, gemv):
-    """The GEMV kernel (forward launches of at most 2 token rows without LoRA terms): three
+    """The GEMV kernel (forward launches of 1-2 token rows without LoRA terms): three
     weights in one launch (q/k/v-like, with bias; each weight's last work-group holds fewer
     rows), statistics read raw, k = 1056 (rows of 33 16-byte chunks: a work-group's chunk range
     and its X pieces wrap across rows at odd positions)."""
