@@ -220,6 +220,10 @@ def test_launch_plans():
     assert launch_plan(False, 3, 3584, [3584])["kernel"] == "nf4_skinny_kernel"  # 7B q/o
     assert launch_plan(False, 8, 3584, [512])["kernel"] == "nf4_gemv_kernel"  # 7B k/v, two token groups
     assert launch_plan(False, 5, 8960, [256])["kernel"] == "nf4_skinny_kernel"  # X of 4 rows: 70 KB
+    # 3-4 rows: long rows up to 2^24 weights too (1.5B down), not 7B q/o or larger
+    assert launch_plan(False, 4, 8960, [1536])["kernel"] == "nf4_gemv_kernel"
+    assert launch_plan(False, 3, 3584, [3584])["kernel"] == "nf4_skinny_kernel"
+    assert launch_plan(False, 3, 8192, [3584])["kernel"] == "nf4_skinny_kernel"
     assert launch_plan(False, 33, 3584, [18944])["kernel"] != "nf4_skinny_kernel"
     assert launch_plan(False, 1, 3584, [18944], lora=True)["kernel"] not in ("nf4_skinny_kernel", "nf4_gemv_kernel")
     old_sm = os.environ.get("DECIK_SMALL_M")

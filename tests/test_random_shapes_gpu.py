@@ -79,16 +79,22 @@ SMALL += [(1, 3584, 18944, True, 64, 8100), (1, 200, 20480, False, 32, 8101), (2
 
 
 @pytest.mark.parametrize("m,n,k,nested,bs,seed", SMALL)
-def test_random_small_m_forward(m, n, k, nested, bs, seed, device):
+def test_random_small_m_forward(m, n, k, nested, bs, seed, device, monkeypatch):
     import torch
 
     from decik_amd.nf4 import launch_plan, linear_forward
 
     kernel = launch_plan(False, m, k, [n], blocksize=bs)["kernel"]
+    monkeypatch.setenv("DECIK_SMALL_M", "gemv")  # whether the GEMV can take the launch at all
+    fits = launch_plan(False, m, k, [n], blocksize=bs)["kernel"] == "nf4_gemv_kernel"
+    monkeypatch.delenv("DECIK_SMALL_M")
+    w = n * k
     if m <= 2 and (m == 1 or k <= 12288):
         assert kernel == "nf4_gemv_kernel"
-    elif m <= 8 and n * k < 2 ** 23 and 4 * k * 2 <= 32768:
-        assert kernel == "nf4_gemv_kernel"  # 3-8 rows on small weights
+    elif 3 <= m <= 4 and fits and w <= 2 ** 24 and (w < 2 ** 23 or k >= 4096):
+        assert kernel == "nf4_gemv_kernel"  # 3-4 rows: small weights, or long rows up to 2^24
+    elif 5 <= m <= 8 and fits and w < 2 ** 23 and 4 * k * 2 <= 32768:
+        assert kernel == "nf4_gemv_kernel"  # 5-8 rows on small weights
     else:
         assert kernel == ("nf4_fwd8_kernel" if m > 16 and (n + 63) // 64 > 256 else "nf4_skinny_kernel")
     packed, qs, w16 = make_weight((n, k), seed=seed, device=device, nested=nested, blocksize=bs)
