@@ -519,7 +519,9 @@ bool gemv_requested(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
     // 35.1; the 1.5B down, k = 8960: 8.6 against 10.5 on the GEMV).
     int64_t weights = 0;
     for (int g = 0; g < ngroups; ++g) weights += ns[g] * k;
-    if (m == 2) return k <= 12288 && weights < (int64_t(1) << 25);
+    // Long rows at two rows: up to 2^24 weights the GEMV still wins ([256, 20480] 8.2 against
+    // 11.0 us, [1024, 16384] 9.0 against 11.7); the 7B down projection (67.9M) does not.
+    if (m == 2) return weights < (int64_t(1) << 25) && (k <= 12288 || weights <= (int64_t(1) << 24));
     // 3-8 rows (a GEMV work-group computes 4; past 4 rows two work-groups share each weight row
     // range): small weights, whose small-M launches are bound by their fixed cost (a split and
     // its reduction launch). At 3-4 rows also weights of up to 2^24 with long rows (k >= 4096),

@@ -182,7 +182,10 @@ def test_launch_plans():
     # at most 32 token rows, no LoRA, no GLU epilogue: the small-M kernel, split along the
     # contraction only where the rows cannot fill the GPU
     assert launch_plan(False, 1, 3584, [18944])["kernel"] == "nf4_gemv_kernel"
-    # two rows: the GEMV below 2^25 weights, the small-M kernel above (7B gate: 67.9M)
+    # two rows: the GEMV below 2^25 weights (k <= 12288, any k up to 2^24 weights), the small-M
+    # kernel above (7B gate: 67.9M)
+    assert launch_plan(False, 2, 20480, [256])["kernel"] == "nf4_gemv_kernel"
+    assert launch_plan(False, 2, 18944, [3584])["kernel"] == "nf4_skinny_kernel"
     assert launch_plan(False, 2, 3584, [18944])["kernel"] == "nf4_skinny_kernel"
     assert launch_plan(False, 2, 1536, [8960])["kernel"] == "nf4_gemv_kernel"
     assert launch_plan(False, 2, 3584, [3584])["kernel"] == "nf4_gemv_kernel"

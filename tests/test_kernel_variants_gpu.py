@@ -314,9 +314,9 @@ def test_gemv_short_k_no_bias(m, device, gemv):
 @pytest.mark.parametrize("m", [1, 2])
 def test_gemv_long_k(m, device, monkeypatch):
     """A long contraction (k = 18944, the 7B down projection's: 592 chunks a row, three rows a
-    work-group of eight waves, X staged whole in LDS; two token rows are sent to the GEMV on
-    purpose, the planner would take the small-M MFMA kernel): 40 rows against the oracle, and the
-    same bits on a second call (the row sums run in a fixed order)."""
+    work-group of eight waves, X staged whole in LDS; sent to the GEMV explicitly, which the
+    planner also picks for a weight this small): 40 rows against the oracle, and the same bits
+    on a second call (the row sums run in a fixed order)."""
     import torch
 
     from decik_amd.nf4 import launch_plan, linear_forward

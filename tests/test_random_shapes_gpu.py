@@ -89,7 +89,7 @@ def test_random_small_m_forward(m, n, k, nested, bs, seed, device, monkeypatch):
     fits = launch_plan(False, m, k, [n], blocksize=bs)["kernel"] == "nf4_gemv_kernel"
     monkeypatch.delenv("DECIK_SMALL_M")
     w = n * k
-    if m <= 2 and (m == 1 or k <= 12288):
+    if m == 1 or (m == 2 and fits and w < 2 ** 25 and (k <= 12288 or w <= 2 ** 24)):
         assert kernel == "nf4_gemv_kernel"
     elif 3 <= m <= 4 and fits and w <= 2 ** 24 and (w < 2 ** 23 or k >= 4096):
         assert kernel == "nf4_gemv_kernel"  # 3-4 rows: small weights, or long rows up to 2^24
