@@ -524,22 +524,24 @@ bool gemv_requested(int64_t m, int64_t k, const int64_t* ns, int ngroups) {
     if (m == 2) return weights < (int64_t(1) << 25) && (k <= 12288 || weights <= (int64_t(1) << 24));
     // 3-8 rows (a GEMV work-group computes 4; past 4 rows two work-groups share each weight row
     // range): small weights, whose small-M launches are bound by their fixed cost (a split and
-    // its reduction launch). At 3-4 rows also weights of up to 2^24 with long rows (k >= 4096),
-    // which the small-M kernel splits: graph-replayed, GEMV against small-M kernel, us: 1.5B down
-    // [1536, 8960] 10.4-10.7 against 11.5, [2048, 8192] 10.1 against 12.3, [1024, 12288] 10.3-10.4
+    // its reduction launch). At 3-4 rows every weight of up to 2^24: graph-replayed, GEMV against
+    // small-M kernel, us: 7B q/o 9.3 against 11.2, 1.5B gate 8.6 against 8.9, 1.5B down [1536,
+    // 8960] 10.4-10.7 against 11.5, [2048, 8192] 10.1 against 12.3, [1024, 12288] 10.3-10.4
     // against 10.9-11.0, [896, 4864] 7.9-8.1 against 8.9-9.0 ([3584, 8192], 2^24.8 weights: 17.7
     // against 15.1-15.2). Past 4 rows, X of 4 rows must stay within 32 KB of LDS per work-group. Graph-replayed, GEMV against small-M kernel, us:
     // 1.5B k/v 4.3-4.5 / 6.3 against 8.1 / 8.3 at 3-4 / 8 rows, 1.5B q/o 4.9-5.0 / 6.9 against
     // 8.4-8.6, the 1.5B q/k/v launch 5.1-5.3 / 7.1 against 8.6-8.8, 7B k/v 5.2 against 9.2 at
     // 3-4 rows (11.6 against 9.4 at 8: X of 8 rows 56 KB); larger weights lose (7B q/o 11.9
     // against 11.0, 7B gate 26 against 18, at 3 rows).
-    if (m <= 4) return weights <= (int64_t(1) << 24) && (weights < (int64_t(1) << 23) || k >= 4096);
+    if (m <= 4) return weights <= (int64_t(1) << 24);
     return weights < (int64_t(1) << 23) && 4 * k * 2 <= 32768;
 }
 
 
 
 }  // namespace
+
+int device_cus() { return num_cus(); }
 
 hipError_t allow_dynamic_lds(const void* fn, size_t bytes) {
     static std::mutex mu;

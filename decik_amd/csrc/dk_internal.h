@@ -160,6 +160,8 @@ constexpr int kGemvMaxM = 8;
 // m token rows at this contraction length.
 hipError_t launch_gemv(FwdArgs& a, hipStream_t s);
 bool gemv_fits(int64_t m, int64_t k);
+// CUs of the current device (256 where no device answers)
+int device_cus();
 // waves per work-group of a GEMV launch (k must fit: gemv_fits)
 int gemv_waves(int64_t m, int64_t k, int64_t nrows);
 // Forward launches of few token rows (no LoRA terms, no GLU epilogue): nf4_skinny_kernel. A

@@ -275,7 +275,7 @@ bool gemv_fits(int64_t m, int64_t k) {
 // on MI355X at one token (us, against the previous 4-8-load rule): 7B gate 17.0 -> 15.3, k/v
 // 5.5 -> 3.7, q/o 7.6 -> 6.3; Qwen2.5-1.5B gate 8.4 -> 6.7, down 8.9 -> 7.1, q/o 6.4 -> 4.3,
 // k/v 6.0 -> 3.7. The row sums keep their order whatever the shape: the same bits.
-static GemvShape gemv_shape(int k, int64_t nrows, int mt) {
+static GemvShape gemv_shape(int k, int64_t nrows, int mt, int tgroups) {
     const int cpr = k >> 5;
     GemvShape fewest{0, 0}, most{0, 0};
     double most_fill = -1.0;
@@ -295,8 +295,26 @@ static GemvShape gemv_shape(int k, int64_t nrows, int mt) {
         }
     }
     if (most.cpt == 0) return gemv_shape_bound(k);
-    const GemvShape pick = (nrows + most.rows - 1) / most.rows >= 1024 ? most : fewest;
+    GemvShape pick = (nrows + most.rows - 1) / most.rows >= 1024 ? most : fewest;
     if (gemv_smem_bytes(mt, k, pick.rows * cpr) > 158 * 1024) return gemv_shape_bound(k);
+    if (mt >= 4) {
+        // Four token rows: every work-group stages X of four rows (8 k bytes), so the LDS bounds
+        // how many a CU holds; from the pick up, the fewest loads per thread whose work-groups
+        // run in one round. Graph-replayed at 4 rows: 7B q/o 12.4 -> 9.3 us (4 rows a
+        // work-group instead of 2: 896 work-groups of 39 KB instead of 1792 of 35 KB).
+        const int cus = device_cus();
+        for (int cpt = pick.cpt; cpt <= kGemvMaxChunks; ++cpt) {
+            const int rows = kGemvThreads * cpt / cpr;
+            if (rows < 1 || (double)rows * cpr < 0.75 * kGemvThreads * cpt) continue;
+            const size_t lds = gemv_smem_bytes(mt, k, rows * cpr) + 256 * sizeof(float2_t);  // + code book
+            if (lds > 158 * 1024) break;
+            const int64_t per_cu = std::min<int64_t>(32 / (kGemvThreads / 64), (int64_t)(160 * 1024 / lds));
+            if ((nrows + rows - 1) / rows * tgroups <= per_cu * cus) {
+                pick = GemvShape{cpt, rows};
+                break;
+            }
+        }
+    }
     if (gemv_smem_bytes(mt, k, pick.rows * cpr) > kGemvWideLds) {
         // X of long rows limits the work-groups a CU holds (three four-wave work-groups, 12 waves,
         // from 40 KB): eight-wave work-groups with at least 4 loads per thread and 85% fill double
@@ -348,7 +366,7 @@ static hipError_t launch_gemv_cpt(const FwdArgs& a, const GemvShape& sh, int gri
 }
 
 int gemv_waves(int64_t m, int64_t k, int64_t nrows) {
-    return gemv_shape((int)k, nrows, gemv_mt(m)).threads / 64;
+    return gemv_shape((int)k, nrows, gemv_mt(m), m > 4 ? 2 : 1).threads / 64;
 }
 
 // a: the groups' tile_begin fields are overwritten with their first work-group
@@ -359,7 +377,7 @@ hipError_t launch_gemv(FwdArgs& a, hipStream_t s) {
     int64_t nrows = 0;
     for (int g = 0; g < a.ngroups; ++g) nrows += a.g[g].w.n;
     const int mt = gemv_mt(a.m);
-    const GemvShape sh = gemv_shape(a.k, nrows, mt);
+    const GemvShape sh = gemv_shape(a.k, nrows, mt, a.m > 4 ? 2 : 1);
     int grid = 0;
     for (int g = 0; g < a.ngroups; ++g) {
         a.g[g].tile_begin = grid;

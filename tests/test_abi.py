@@ -220,12 +220,12 @@ def test_launch_plans():
     # 32 KB; larger weights and longer rows the small-M kernel
     assert launch_plan(False, 3, 3584, [512])["kernel"] == "nf4_gemv_kernel"  # 7B k/v
     assert launch_plan(False, 8, 1536, [1536, 256, 256])["kernel"] == "nf4_gemv_kernel"  # 1.5B q/k/v
-    assert launch_plan(False, 3, 3584, [3584])["kernel"] == "nf4_skinny_kernel"  # 7B q/o
+    assert launch_plan(False, 6, 3584, [3584])["kernel"] == "nf4_skinny_kernel"  # 7B q/o
     assert launch_plan(False, 8, 3584, [512])["kernel"] == "nf4_gemv_kernel"  # 7B k/v, two token groups
     assert launch_plan(False, 5, 8960, [256])["kernel"] == "nf4_skinny_kernel"  # X of 4 rows: 70 KB
-    # 3-4 rows: long rows up to 2^24 weights too (1.5B down), not 7B q/o or larger
+    # 3-4 rows: weights up to 2^24 (1.5B down, 7B q/o), not larger
     assert launch_plan(False, 4, 8960, [1536])["kernel"] == "nf4_gemv_kernel"
-    assert launch_plan(False, 3, 3584, [3584])["kernel"] == "nf4_skinny_kernel"
+    assert launch_plan(False, 3, 3584, [3584])["kernel"] == "nf4_gemv_kernel"
     assert launch_plan(False, 3, 8192, [3584])["kernel"] == "nf4_skinny_kernel"
     assert launch_plan(False, 33, 3584, [18944])["kernel"] != "nf4_skinny_kernel"
     assert launch_plan(False, 1, 3584, [18944], lora=True)["kernel"] not in ("nf4_skinny_kernel", "nf4_gemv_kernel")

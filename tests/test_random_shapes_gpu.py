@@ -91,8 +91,8 @@ def test_random_small_m_forward(m, n, k, nested, bs, seed, device, monkeypatch):
     w = n * k
     if m == 1 or (m == 2 and fits and w < 2 ** 25 and (k <= 12288 or w <= 2 ** 24)):
         assert kernel == "nf4_gemv_kernel"
-    elif 3 <= m <= 4 and fits and w <= 2 ** 24 and (w < 2 ** 23 or k >= 4096):
-        assert kernel == "nf4_gemv_kernel"  # 3-4 rows: small weights, or long rows up to 2^24
+    elif 3 <= m <= 4 and fits and w <= 2 ** 24:
+        assert kernel == "nf4_gemv_kernel"  # 3-4 rows: weights up to 2^24
     elif 5 <= m <= 8 and fits and w < 2 ** 23 and 4 * k * 2 <= 32768:
         assert kernel == "nf4_gemv_kernel"  # 5-8 rows on small weights
     else:
