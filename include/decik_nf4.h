@@ -319,7 +319,7 @@ int dk_swiglu_bwd(const uint16_t* grad, const uint16_t* gate, const uint16_t* up
  * splits, out[3] = kernel (0 nf4_fwd_kernel, 1 nf4_fwd8_kernel, 2 no longer returned (an
  * earlier input-gradient kernel), 3 nf4_bwd8_kernel, 4 nf4_gemv_kernel (forward launches of one
  * token row, two with fewer than 2^25 weights and k <= 12288 (any k up to 2^24 weights), 3-4
- * with fewer than 2^23 weights or at most 2^24 and k >= 4096, 5-8 with fewer than 2^23 weights
+ * with at most 2^24 weights, 5-8 with fewer than 2^23 weights
  * and 8 k <= 32768, without LoRA terms or the GLU epilogue), 5
  * nf4_skinny_kernel (such launches of up to 32 token rows otherwise, but past 16 rows not for
  * weights of more 64-row groups than the device has CUs; out[2] is then its contraction splits); DECIK_SMALL_M = gemv / skinny picks one
